@@ -1,0 +1,242 @@
+/*
+ * forge_hip.h — C ABI of libforge_hip.so, the MI355X (gfx950) kernel library
+ * behind the drop-in `kernels.{swiglu,rope,cross_entropy,lora_mlp,lora_qkv}`
+ * Python modules.
+ *
+ * Conventions (all entry points):
+ *   - Plain device pointers, element counts and element strides; no framework
+ *     types.  The caller (PyTorch's caching allocator on the Python side) owns
+ *     every buffer; the library never allocates, frees or retains a pointer
+ *     past the call.
+ *   - Every launch is asynchronous on the caller's `stream` (a hipStream_t
+ *     passed as void*; NULL = the legacy default stream).  No host syncs.
+ *   - Return value: FORGE_OK (0) or a FORGE_ERR_* code; forge_last_error()
+ *     returns a message for the last failure on the calling thread.
+ *   - dtype codes: FORGE_DTYPE_*.
+ *
+ * Each declaration names the reference interface it replaces
+ * (paths relative to the Forge-researchlab/kernel-POCs root).
+ */
+#ifndef FORGE_HIP_H
+#define FORGE_HIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum {
+  FORGE_DTYPE_F32 = 0,
+  FORGE_DTYPE_F16 = 1,
+  FORGE_DTYPE_BF16 = 2,
+  FORGE_DTYPE_F64 = 3,
+};
+
+enum {
+  FORGE_OK = 0,
+  FORGE_ERR_INVALID = 1,     /* bad argument (shape, stride, alignment, dtype) */
+  FORGE_ERR_UNSUPPORTED = 2, /* valid request this build does not implement */
+  FORGE_ERR_HIP = 3,         /* HIP runtime error */
+};
+
+/* Library identity / diagnostics. */
+const char* forge_version(void);
+const char* forge_last_error(void);
+/* Number of gfx950 code objects linked in (0 means a broken build). */
+int forge_arch_ok(void);
+
+/* ------------------------------------------------------------------------
+ * SwiGLU
+ * ------------------------------------------------------------------------ */
+
+/* out[r, c] = (silu(gate[r, c] * gm) -> dtype) * up[r, c] * dm
+ * gate/up rows are `ld_in` elements apart (gate and up may be two halves of
+ * one packed [rows, 2*cols] row: up = gate + cols, ld_in = 2*cols).
+ * Replaces `_swiglu_forward_kernel` / `_swiglu_packed_forward_kernel`
+ * (kernels/swiglu/swiglu.py:60-82, 119-142) launched by `swiglu_forward` /
+ * `swiglu_packed_forward` (kernels/swiglu/swiglu.py:201-229, 265-292). */
+int forge_swiglu_fwd(int dtype, const void* gate, const void* up, int64_t ld_in,
+                     void* out, int64_t ld_out, int64_t rows, int64_t cols,
+                     float gate_multiplier, float down_multiplier, void* stream);
+
+/* dup = dout*dm*silu(gate*gm); dgate = dout*dm*up*dsilu(gate*gm)*gm.
+ * dgate/dup may alias gate/up (the reference's in-place default).
+ * Replaces `_swiglu_backward_kernel` / `_swiglu_packed_backward_kernel`
+ * (kernels/swiglu/swiglu.py:85-116, 145-176) launched by `swiglu_backward` /
+ * `swiglu_packed_backward` (kernels/swiglu/swiglu.py:232-262, 295-323). */
+int forge_swiglu_bwd(int dtype, const void* dout, int64_t ld_dout,
+                     const void* gate, const void* up, int64_t ld_in,
+                     void* dgate, void* dup, int64_t ld_dgrad,
+                     int64_t rows, int64_t cols,
+                     float gate_multiplier, float down_multiplier, void* stream);
+
+/* ------------------------------------------------------------------------
+ * RoPE (half-split rotation, GQA: n_q % n_kv == 0)
+ * ------------------------------------------------------------------------ */
+
+/* Rotates Q [B, n_q, S, D] and K [B, n_kv, S, D] given by element strides
+ * (batch, head, seq; the D stride must be 1) into q_out/k_out (same
+ * convention).  cos/sin rows are [D] with the given batch/seq strides
+ * (batch stride 0 = broadcast); only the first D/2 entries of each row are
+ * read.  If `positions` (int64, [B*S]) is non-NULL the cos/sin row of token
+ * (b, s) is positions[b*S + s] instead of s.  backward != 0 rotates by -theta.
+ * Replaces `_forge_rope_v3_kernel` + `_launch_kernel`
+ * (kernels/rope/forge_rope_v3.py:32-132). */
+int forge_rope(int dtype,
+               const void* q, int64_t q_sb, int64_t q_sh, int64_t q_ss,
+               const void* k, int64_t k_sb, int64_t k_sh, int64_t k_ss,
+               void* q_out, int64_t qo_sb, int64_t qo_sh, int64_t qo_ss,
+               void* k_out, int64_t ko_sb, int64_t ko_sh, int64_t ko_ss,
+               const void* cos, int64_t cos_sb, int64_t cos_ss,
+               const void* sin, int64_t sin_sb, int64_t sin_ss,
+               const int64_t* positions,
+               int64_t batch, int64_t n_q, int64_t n_kv, int64_t seq_len,
+               int64_t head_dim, int backward, void* stream);
+
+/* ------------------------------------------------------------------------
+ * Cross-entropy (online softmax, dlogits written in place)
+ * ------------------------------------------------------------------------ */
+
+enum {
+  FORGE_CE_HAS_GRADIENTS = 1,
+  FORGE_CE_HAS_WEIGHT = 2,
+  FORGE_CE_HAS_SOFTCAP = 4,
+  FORGE_CE_RETURN_Z_LOSS = 8,
+  FORGE_CE_RETURN_ACCURACY = 16,
+  FORGE_CE_RETURN_PREDICTED = 32,
+  FORGE_CE_REDUCTION_MEAN = 64,
+};
+
+/* Per row of logits [n_rows, n_cols] (row stride ld): loss (fp32, [n_rows]),
+ * optional z_loss (fp32), token accuracy (fp32), predicted token (int64),
+ * and — with FORGE_CE_HAS_GRADIENTS — dloss/dlogits written over the logits
+ * (ignored rows are zero-filled).  weight (fp32 [n_cols]) is read only with
+ * FORGE_CE_HAS_WEIGHT.  Scalars follow the reference kernel's arguments.
+ * Replaces `forge_cross_entropy_kernel`
+ * (kernels/cross_entropy/experiments/v2/cross_entropy_kernel_v2.py:65-338)
+ * launched by `cross_entropy_forward` (same file :346-458). */
+int forge_ce_fwd(int dtype, void* logits, int64_t ld, int64_t n_rows, int64_t n_cols,
+                 const int64_t* target, int64_t target_stride,
+                 const float* weight,
+                 float* loss, float* z_loss, float* token_accuracy,
+                 int64_t* predicted_tokens,
+                 int64_t ignore_index, float n_non_ignore, float sum_non_ignore_weight,
+                 float weight_sum, float lse_square_scale, float label_smoothing,
+                 float softcap, int flags, void* stream);
+
+/* x[r, :] *= *grad_output (device fp32 scalar), in place.
+ * Replaces `_element_mul_kernel`
+ * (kernels/cross_entropy/experiments/v2/cross_entropy_kernel_v2.py:49-62). */
+int forge_ce_scale(int dtype, void* x, int64_t ld, int64_t n_rows, int64_t n_cols,
+                   const float* grad_output, void* stream);
+
+/* Sum of an fp32 vector into out[0] (fp32), deterministic two-level tree.
+ * Used for the loss reduction in place of `torch.sum(loss_1d)`
+ * (kernels/cross_entropy/experiments/v2/cross_entropy_kernel_v2.py:451). */
+int forge_sum_f32(const float* x, int64_t n, float* out, void* stream);
+
+/* ------------------------------------------------------------------------
+ * bf16 MFMA GEMM core (fp32 accumulation) with fused LoRA epilogues
+ * ------------------------------------------------------------------------ */
+
+/* Operand layouts. For A (M x K): ROW = [M][K] row-major (K contiguous),
+ * COL = [K][M] (M contiguous).  For B (K x N): COL = [N][K] (K contiguous,
+ * i.e. an nn.Linear weight used as W^T), ROW = [K][N] (N contiguous). */
+enum { FORGE_LAYOUT_ROW = 0, FORGE_LAYOUT_COL = 1 };
+
+/* One K-segment of a multi-segment product C = sum_s A_s @ B_s. */
+typedef struct forge_gemm_segment {
+  const void* a;  /* bf16 */
+  int64_t lda;
+  const void* b;  /* bf16 */
+  int64_t ldb;
+  int64_t k;      /* extent of this segment along K (multiple of 8) */
+} forge_gemm_segment;
+
+enum {
+  FORGE_EPI_STORE = 0,          /* C = alpha*acc + beta*C (C dtype = c_dtype) */
+  FORGE_EPI_ATOMIC_F32 = 1,     /* C(fp32) += alpha*acc  (split-K partials) */
+};
+
+/* C[M, N] = alpha * sum_s A_s @ B_s + beta * C.  A and B layouts are shared by
+ * all segments.  c_dtype is FORGE_DTYPE_BF16 or FORGE_DTYPE_F32.  split_k > 1
+ * (only with FORGE_EPI_ATOMIC_F32) partitions the K range across workgroups.
+ * Replaces the cuBLAS calls (`torch.matmul` / `addmm_`) of the LoRA paths:
+ * kernels/lora_mlp/experiments/v6/lora_mlp_kernel_v6.py:373-443, 623-653;
+ * kernels/lora_qkv/experiments/v4/lora_qkv_kernel_v4.py:248-287. */
+int forge_gemm(int64_t M, int64_t N, const forge_gemm_segment* segs, int n_segs,
+               int a_layout, int b_layout,
+               void* c, int64_t ldc, int c_dtype, float alpha, float beta,
+               int epilogue, int split_k, void* stream);
+
+/* ------------------------------------------------------------------------
+ * Fused LoRA entry points (bf16 storage, fp32 accumulation)
+ * ------------------------------------------------------------------------ */
+
+/* LoRA-MLP forward, gate and up projections with the SwiGLU epilogue:
+ *   e = X Wg^T + xa[:, :r] Bg^T,  g = X Wu^T + xa[:, r:2r] Bu^T,  h = silu(e) g
+ * X [M, H] (row pitch ldx), Wg/Wu [I, H] (pitch ldw), xa [M, 2r] holding
+ * (sg X Ag^T | su X Au^T) (pitch ld_xa; NULL or r = 0 disables LoRA),
+ * Bg/Bu [I, r] (pitch ldb).  Writes e, g, h [M, I] (pitch ld_out).
+ * Replaces phases 1-3 of `_v6_forward_impl`
+ * (kernels/lora_mlp/experiments/v6/lora_mlp_kernel_v6.py:373-415: two cuBLAS
+ * GEMMs + `_fused_lora_swiglu_kernel`, experiments/v3/lora_mlp_kernel_v3.py:45-138). */
+int forge_lora_mlp_gate_up(int64_t M, int64_t H, int64_t I, int64_t r,
+                           const void* x, int64_t ldx,
+                           const void* w_gate, const void* w_up, int64_t ldw,
+                           const void* xa, int64_t ld_xa,
+                           const void* b_gate, const void* b_up, int64_t ldb,
+                           void* e, void* g, void* h, int64_t ld_out, void* stream);
+
+/* LoRA-MLP backward through the down projection and SwiGLU:
+ *   DW = dY Wd + t Ad   (dY [M, H], Wd [H, I], t = sd dY Bd [M, r], Ad [r, I])
+ *   then in place: h_out = silu(e) g,  e <- df = DW silu(e),
+ *                  g <- de = DW g sig(e) (1 + e (1 - sig(e)))
+ * Replaces `matmul_lora(dY, W_down^T, ...)` + `_DWf_DW_dfg_kernel`
+ * (kernels/lora_mlp/experiments/v6/lora_mlp_kernel_v6.py:632-634;
+ * kernels/lora_mlp/reference/unsloth_baseline.py:34-55, 118-168). */
+int forge_lora_mlp_down_bwd(int64_t M, int64_t H, int64_t I, int64_t r,
+                            const void* dy, int64_t lddy,
+                            const void* w_down, int64_t ldwd,
+                            const void* t_d, int64_t ld_t,
+                            const void* a_down, int64_t ld_ad,
+                            void* h_out, void* e_df, void* g_de, int64_t ld, void* stream);
+
+/* LoRA-QKV forward with GQA-asymmetric widths and optional fused RoPE:
+ *   out[:, 0:hq]          = X Wq^T + xa[:, 0:r]   Bq^T   (rotated if apply_rope)
+ *   out[:, hq:hq+hkv]     = X Wk^T + xa[:, r:2r]  Bk^T   (rotated if apply_rope)
+ *   out[:, hq+hkv:hq+2hkv]= X Wv^T + xa[:, 2r:3r] Bv^T
+ * xa holds (sq X Aq^T | sk X Ak^T | sv X Av^T).  RoPE (head_dim 64 or 128)
+ * uses bf16 cos/sin tables [*, head_dim] with row pitch cs_ld and row
+ * positions[m] for token m (NULL: m).  Q/K are rounded to bf16 before the
+ * rotation, as in the unfused path.
+ * Replaces `lora_qkv_v2_3` (kernels/lora_qkv/experiments/v2/lora_qkv_kernel_v2_3.py
+ * :177-267: one cuBLAS GEMM + `_fused_qkv_epilogue_packed_kernel`) followed by
+ * the caller's RoPE (forge/forge/patching/kernels/lora.py:250-264). */
+int forge_lora_qkv_rope(int64_t M, int64_t K, int64_t hq, int64_t hkv, int64_t r,
+                        const void* x, int64_t ldx,
+                        const void* w_q, const void* w_k, const void* w_v, int64_t ldw,
+                        const void* xa, int64_t ld_xa,
+                        const void* b_q, const void* b_k, const void* b_v, int64_t ldb,
+                        void* out, int64_t ld_out,
+                        const void* cos, const void* sin, int64_t cs_ld,
+                        const int64_t* positions, int64_t head_dim, int apply_rope,
+                        void* stream);
+
+/* Rank-r LoRA-A projections of one input, one GEMM:
+ *   out[:, p*r:(p+1)*r] = scales[p] * X @ A_p^T     for p < n_proj (<= 4)
+ * X [M, K] (row pitch ldx), A_p [r, K] (pitch lda), out [M, n_proj*r] bf16.
+ * scales is a host array.  Replaces the LoRA-A GEMMs X @ A^T of the
+ * reference (the stacked [W; A_g; A_u] cuBLAS call,
+ * kernels/lora_mlp/experiments/v6/lora_mlp_kernel_v6.py:373-381, and
+ * `XA_all = X @ A_packed^T`, kernels/lora_qkv/experiments/v4/lora_qkv_kernel_v4.py:260). */
+int forge_lora_a(int64_t M, int64_t K, int64_t r, int n_proj, const void* x, int64_t ldx,
+                 const void* const* a_mats, int64_t lda, const float* scales, void* out,
+                 int64_t ld_out, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* FORGE_HIP_H */

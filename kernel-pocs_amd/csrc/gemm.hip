@@ -1,0 +1,145 @@
+// Host launchers for the MFMA GEMM core: the generic forge_gemm entry point
+// and the fused LoRA entry points (LoRA-MLP gate/up + SwiGLU, LoRA-MLP
+// down-projection backward + SwiGLU backward, LoRA-QKV + RoPE).
+#include "gemm_core.h"
+
+namespace fgemm {
+
+// Tile configurations.
+enum Cfg {
+  CFG_BIG = 0,       // 256 x 256, 2 x 2 waves (128 x 128 per wave)
+  CFG_SKINNY_N = 1,  // 256 x 32, 4 x 1 waves: N <= 32-ish (rank-r outputs)
+  CFG_SKINNY_M = 2,  // 32 x 256, 1 x 4 waves: M <= 32-ish (LoRA A gradients)
+};
+
+template <int BM, int BN, int WM, int WN, int AL, int BL, int BMODE, int EPI>
+static int launch_cfg(const GemmArgs& a, hipStream_t s) {
+  constexpr int OUT_BN = (BMODE == B_DUAL) ? BN / 2 : BN;
+  const int64_t tm = (a.M + BM - 1) / BM;
+  const int64_t tn = (a.N + OUT_BN - 1) / OUT_BN;
+  if (tm * tn > 0x7fffffffLL) return forge_set_error(FORGE_ERR_INVALID, "gemm: too many tiles");
+  dim3 grid((unsigned)(tm * tn), 1, (unsigned)a.split_k);
+  gemm_kernel<BM, BN, WM, WN, AL, BL, BMODE, EPI><<<grid, WM * WN * 64, 0, s>>>(a);
+  FORGE_CHECK_LAUNCH();
+  return FORGE_OK;
+}
+
+template <int AL, int BL, int BMODE, int EPI>
+static int launch_layout(int cfg, const GemmArgs& a, hipStream_t s) {
+  switch (cfg) {
+    case CFG_BIG: return launch_cfg<256, 256, 2, 2, AL, BL, BMODE, EPI>(a, s);
+    case CFG_SKINNY_N:
+      if constexpr (BMODE == B_SINGLE) return launch_cfg<256, 32, 4, 1, AL, BL, BMODE, EPI>(a, s);
+      break;
+    case CFG_SKINNY_M:
+      if constexpr (BMODE == B_SINGLE) return launch_cfg<32, 256, 1, 4, AL, BL, BMODE, EPI>(a, s);
+      break;
+  }
+  return forge_set_error(FORGE_ERR_UNSUPPORTED, "gemm: tile config %d", cfg);
+}
+
+template <int EPI>
+static int launch_epi(int cfg, int al, int bl, const GemmArgs& a, hipStream_t s) {
+  if (al == ROW && bl == COL) return launch_layout<ROW, COL, B_SINGLE, EPI>(cfg, a, s);
+  if (al == ROW && bl == ROW) return launch_layout<ROW, ROW, B_SINGLE, EPI>(cfg, a, s);
+  if (al == COL && bl == ROW) return launch_layout<COL, ROW, B_SINGLE, EPI>(cfg, a, s);
+  if (al == COL && bl == COL) return launch_layout<COL, COL, B_SINGLE, EPI>(cfg, a, s);
+  return forge_set_error(FORGE_ERR_INVALID, "gemm: layout");
+}
+
+// Picks a tile shape from the output shape.
+static int pick_cfg(int64_t M, int64_t N) {
+  if (N <= 64 && M > N) return CFG_SKINNY_N;
+  if (M <= 64 && N > M) return CFG_SKINNY_M;
+  return CFG_BIG;
+}
+
+static int check_segs(const GemmArgs& a, int al, int bl) {
+  if (a.n_segs < 1 || a.n_segs > MAX_SEGS)
+    return forge_set_error(FORGE_ERR_INVALID, "gemm: 1..%d segments", MAX_SEGS);
+  for (int i = 0; i < a.n_segs; ++i) {
+    const Seg& s = a.segs[i];
+    if (s.k < 0 || s.k % 8 != 0)
+      return forge_set_error(FORGE_ERR_INVALID, "gemm: segment %d K=%lld must be a multiple of 8", i,
+                             (long long)s.k);
+    if (!aligned16(s.a) || (s.b && !aligned16(s.b)) || (s.b2 && !aligned16(s.b2)))
+      return forge_set_error(FORGE_ERR_INVALID, "gemm: segment %d operand not 16-byte aligned", i);
+    if (s.lda % 8 != 0 || s.ldb % 8 != 0)
+      return forge_set_error(FORGE_ERR_INVALID, "gemm: segment %d leading dims must be multiples of 8", i);
+    (void)al;
+    (void)bl;
+  }
+  return FORGE_OK;
+}
+
+int run(int cfg, int al, int bl, int epi, const GemmArgs& a, hipStream_t s) {
+  if (int e = check_segs(a, al, bl)) return e;
+  // transposed-operand tiles are fetched as 8-row blocks of 16-byte vectors
+  if (al == COL && a.M % 8 != 0)
+    return forge_set_error(FORGE_ERR_INVALID, "gemm: A^T layout needs M %% 8 == 0 (M=%lld)", (long long)a.M);
+  if (bl == ROW && a.N % 8 != 0)
+    return forge_set_error(FORGE_ERR_INVALID, "gemm: [K][N] B layout needs N %% 8 == 0 (N=%lld)", (long long)a.N);
+  if (a.M == 0 || a.N == 0) return FORGE_OK;
+  if (cfg < 0) cfg = pick_cfg(a.M, a.N);
+  switch (epi) {
+    case EPI_STORE_BF16: return launch_epi<EPI_STORE_BF16>(cfg, al, bl, a, s);
+    case EPI_STORE_F32: return launch_epi<EPI_STORE_F32>(cfg, al, bl, a, s);
+    case EPI_ATOMIC_F32: return launch_epi<EPI_ATOMIC_F32>(cfg, al, bl, a, s);
+    case EPI_SWIGLU_BWD:
+      if (al == ROW && bl == ROW) return launch_layout<ROW, ROW, B_SINGLE, EPI_SWIGLU_BWD>(CFG_BIG, a, s);
+      break;
+    case EPI_SWIGLU_FWD:
+      if (al == ROW && bl == COL) return launch_layout<ROW, COL, B_DUAL, EPI_SWIGLU_FWD>(CFG_BIG, a, s);
+      break;
+    case EPI_ROPE:
+      if (al == ROW && bl == COL) return launch_layout<ROW, COL, B_SINGLE, EPI_ROPE>(CFG_BIG, a, s);
+      break;
+  }
+  return forge_set_error(FORGE_ERR_UNSUPPORTED, "gemm: epilogue %d with layouts (%d, %d)", epi, al, bl);
+}
+
+}  // namespace fgemm
+
+using namespace fgemm;
+
+extern "C" int forge_gemm(int64_t M, int64_t N, const forge_gemm_segment* segs, int n_segs,
+                          int a_layout, int b_layout, void* c, int64_t ldc, int c_dtype,
+                          float alpha, float beta, int epilogue, int split_k, void* stream) {
+  if (M < 0 || N < 0) return forge_set_error(FORGE_ERR_INVALID, "gemm: negative shape");
+  if (n_segs < 1 || n_segs > MAX_SEGS)
+    return forge_set_error(FORGE_ERR_INVALID, "gemm: 1..%d segments", MAX_SEGS);
+  if (split_k < 1) split_k = 1;
+  GemmArgs a = {};
+  a.M = M;
+  a.N = N;
+  a.n_segs = n_segs;
+  for (int i = 0; i < n_segs; ++i) {
+    a.segs[i].a = (const __bf16*)segs[i].a;
+    a.segs[i].lda = segs[i].lda;
+    a.segs[i].b = (const __bf16*)segs[i].b;
+    a.segs[i].b2 = nullptr;
+    a.segs[i].ldb = segs[i].ldb;
+    a.segs[i].k = segs[i].k;
+    a.segs[i].n_lo = 0;
+    a.segs[i].n_hi = N;
+  }
+  a.split_k = split_k;
+  a.ep.c = c;
+  a.ep.ldc = ldc;
+  a.ep.alpha = alpha;
+  a.ep.beta = beta;
+  int epi;
+  if (epilogue == FORGE_EPI_ATOMIC_F32) {
+    if (c_dtype != FORGE_DTYPE_F32)
+      return forge_set_error(FORGE_ERR_INVALID, "gemm: atomic epilogue needs an fp32 C");
+    epi = EPI_ATOMIC_F32;
+  } else if (epilogue == FORGE_EPI_STORE) {
+    if (split_k != 1) return forge_set_error(FORGE_ERR_INVALID, "gemm: split_k needs the atomic epilogue");
+    if (c_dtype == FORGE_DTYPE_BF16) epi = EPI_STORE_BF16;
+    else if (c_dtype == FORGE_DTYPE_F32) epi = EPI_STORE_F32;
+    else return forge_set_error(FORGE_ERR_UNSUPPORTED, "gemm: C dtype %d", c_dtype);
+  } else {
+    return forge_set_error(FORGE_ERR_INVALID, "gemm: epilogue %d", epilogue);
+  }
+  return run(-1, a_layout, b_layout, epi, a, (hipStream_t)stream);
+}

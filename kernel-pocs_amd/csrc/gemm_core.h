@@ -1,0 +1,479 @@
+// bf16 MFMA GEMM core for gfx950 (CDNA4), fp32 accumulation.
+//
+// C[M, N] = sum over K-segments s of A_s[M, K_s] @ B_s[K_s, N], with a fused
+// epilogue.  Multi-segment K is how the LoRA terms ride along the base GEMM:
+//     X W^T + s (X A^T) B^T  =  [X | s X A^T] @ [W | B]^T
+// so the rank-r update costs one extra (zero-padded) K tile instead of a
+// separate kernel and another pass over the output.
+//
+// Tiling: BM x BN x 64 block tile, WAVES_M x WAVES_N waves, each wave owns a
+// (BM/WAVES_M) x (BN/WAVES_N) sub-tile computed with v_mfma_f32_32x32x16_bf16.
+// LDS holds both operands k-contiguous ([rows][64 + 8 pad] bf16, 144-byte row
+// pitch so the 16-byte fragment reads of 8 consecutive lanes hit distinct
+// banks), double-buffered: the global loads of tile k+1 are in flight while
+// the MFMAs of tile k run, one barrier per K tile.
+// Operands whose K dimension is not contiguous in memory (A^T, or a [K][N]
+// B) are loaded as 8x8 blocks of 16-byte vectors and transposed in registers
+// (v_perm_b32) before the LDS store, so both layouts feed the same LDS image.
+//
+// MFMA lane layouts (v_mfma_f32_32x32x16_bf16, 64 lanes):
+//   A operand: lane l holds A[row = l % 32][k = 8 * (l / 32) + 0..7]
+//   B operand: lane l holds B[k = 8 * (l / 32) + 0..7][col = l % 32]
+//   (A and B use the same k assignment, so the contraction is exact whatever
+//    order the hardware sums the 16 k values in)
+//   D: acc[r] (r = 0..15) of lane l is D[8 * (r / 4) + 4 * (l / 32) + r % 4][l % 32]
+#pragma once
+
+#include "common.h"
+
+namespace fgemm {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+constexpr int BK = 64;
+constexpr int LDS_PITCH = BK + 8;  // bf16 elements per LDS row
+
+enum Layout { ROW = 0, COL = 1 };
+
+// Output-row mapping of B-tile rows in "dual" mode: the tile's B rows come
+// alternately (in groups of 32) from two weights, so that a wave's N tiles
+// t = 0,1,2,3 are (gate cols c..c+31, up cols c..c+31, gate c+32.., up c+32..)
+// and the matching gate/up accumulators sit in the same lane and register.
+enum BMode { B_SINGLE = 0, B_DUAL = 1 };
+
+struct Seg {
+  const __bf16* a;
+  int64_t lda;
+  const __bf16* b;   // B rows of the tile (or the "gate" rows in dual mode)
+  const __bf16* b2;  // dual mode: the "up" rows (nullptr = zeros)
+  int64_t ldb;
+  int64_t k;         // K extent of the segment
+  int64_t n_lo, n_hi;  // output columns this segment applies to (B row = n - n_lo)
+};
+
+constexpr int MAX_SEGS = 6;
+
+enum Epi {
+  EPI_STORE_BF16 = 0,   // C = alpha*acc + beta*C
+  EPI_STORE_F32 = 1,
+  EPI_ATOMIC_F32 = 2,   // C += alpha*acc
+  EPI_SWIGLU_FWD = 3,   // dual: e, g, h = silu(e) * g
+  EPI_SWIGLU_BWD = 4,   // DW: (DW, e, g) -> (h, df, de) in place
+  EPI_ROPE = 5,         // QKV: rotate columns < rope_cols per head, store bf16
+};
+
+struct EpiArgs {
+  void* c;
+  int64_t ldc;
+  float alpha, beta;
+  // per-column-group scale for the STORE/ATOMIC epilogues: columns
+  // [g*alpha_group, (g+1)*alpha_group) use alphas[g] (alpha_group 0 = off)
+  int64_t alpha_group;
+  float alphas[4];
+  __bf16* e;   // SWIGLU: e buffer; SWIGLU_BWD: e in / df out
+  __bf16* g;   // SWIGLU: g buffer; SWIGLU_BWD: g in / de out
+  int64_t ld_eg;
+  const __bf16* cos;
+  const __bf16* sin;
+  int64_t cs_ld;             // cos/sin row pitch (elements)
+  const int64_t* positions;  // per output row (token); nullptr = row index
+  int64_t rope_cols;         // columns [0, rope_cols) are rotated
+  int head_dim;              // 64 or 128
+};
+
+struct GemmArgs {
+  int64_t M, N;  // N = output columns
+  int n_segs;
+  Seg segs[MAX_SEGS];
+  int split_k;   // number of K partitions (grid z)
+  EpiArgs ep;
+};
+
+__device__ __forceinline__ uint32_t perm_lo(uint32_t a, uint32_t b) {
+  // (a.lo16, b.lo16) -> low half from a, high half from b
+  return __builtin_amdgcn_perm(b, a, 0x05040100u);
+}
+__device__ __forceinline__ uint32_t perm_hi(uint32_t a, uint32_t b) {
+  return __builtin_amdgcn_perm(b, a, 0x07060302u);
+}
+
+// In-register transpose of an 8x8 block of 16-bit values.
+// in[i] holds row i (8 values, dword j = elements 2j, 2j+1).
+// out[j] holds column j (8 values: in[0][j], ..., in[7][j]).
+__device__ __forceinline__ void transpose8x8(const uint4 (&in)[8], uint4 (&out)[8]) {
+  uint32_t r[8][4];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) { r[i][0] = in[i].x; r[i][1] = in[i].y; r[i][2] = in[i].z; r[i][3] = in[i].w; }
+  // column c = 2*j + h (h = 0 low half, 1 high half of dword j)
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    uint32_t lo[4], hi[4];
+#pragma unroll
+    for (int p = 0; p < 4; ++p) {
+      lo[p] = perm_lo(r[2 * p][j], r[2 * p + 1][j]);  // (row 2p, row 2p+1) of column 2j
+      hi[p] = perm_hi(r[2 * p][j], r[2 * p + 1][j]);  // ... of column 2j+1
+    }
+    out[2 * j] = make_uint4(lo[0], lo[1], lo[2], lo[3]);
+    out[2 * j + 1] = make_uint4(hi[0], hi[1], hi[2], hi[3]);
+  }
+}
+
+// Tile loader: fetches a BROWS x BK operand tile from global memory into
+// registers, then writes it k-contiguous into LDS.
+//   KCONTIG: element (row, k) at base[row * ld + k]   (A ROW, B COL)
+//   !KCONTIG: element (row, k) at base[k * ld + row]  (A COL, B ROW)
+template <int BROWS, int NT, bool KCONTIG>
+struct TileLoader {
+  static constexpr int VPT = KCONTIG ? (BROWS * BK / 8 + NT - 1) / NT        // 16-byte vectors
+                                     : 8 * ((BROWS / 8) * (BK / 8) + NT - 1) / NT;  // 8 per 8x8 block
+  uint4 regs[VPT > 0 ? VPT : 1];
+
+  // Row source: base pointer for LDS row q (nullptr = zeros) and the number
+  // of valid k in this tile (k < kvalid).
+  template <class RowPtr>
+  __device__ __forceinline__ void load(RowPtr rowptr, int64_t ld, int64_t k0, int64_t kvalid) {
+    const int tid = threadIdx.x;
+    if constexpr (KCONTIG) {
+#pragma unroll
+      for (int i = 0; i < VPT; ++i) {
+        const int v = tid + i * NT;
+        const int q = v / (BK / 8);
+        const int kc = (v % (BK / 8)) * 8;
+        uint4 val = make_uint4(0, 0, 0, 0);
+        if (v < BROWS * BK / 8 && kc < kvalid) {
+          const __bf16* p = rowptr(q);
+          if (p) val = *reinterpret_cast<const uint4*>(p + (k0 + kc));
+        }
+        regs[i] = val;
+      }
+      (void)ld;
+    } else {
+      constexpr int NBLK = (BROWS / 8) * (BK / 8);
+#pragma unroll
+      for (int bi = 0; bi < VPT / 8; ++bi) {
+        const int blk = tid + bi * NT;
+        const int qb = (blk % (BROWS / 8)) * 8;  // rows qb..qb+7 (contiguous in memory)
+        const int kb = (blk / (BROWS / 8)) * 8;  // k rows kb..kb+7
+        uint4 in[8];
+        const __bf16* p = (blk < NBLK) ? rowptr(qb) : nullptr;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          in[i] = make_uint4(0, 0, 0, 0);
+          if (p && kb + i < kvalid) in[i] = *reinterpret_cast<const uint4*>(p + (k0 + kb + i) * ld);
+        }
+        uint4 out[8];
+        transpose8x8(in, out);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) regs[bi * 8 + i] = out[i];
+      }
+    }
+  }
+
+  __device__ __forceinline__ void store(__bf16* lds) {
+    const int tid = threadIdx.x;
+    if constexpr (KCONTIG) {
+#pragma unroll
+      for (int i = 0; i < VPT; ++i) {
+        const int v = tid + i * NT;
+        if (v < BROWS * BK / 8) {
+          const int q = v / (BK / 8);
+          const int kc = (v % (BK / 8)) * 8;
+          *reinterpret_cast<uint4*>(lds + q * LDS_PITCH + kc) = regs[i];
+        }
+      }
+    } else {
+      constexpr int NBLK = (BROWS / 8) * (BK / 8);
+#pragma unroll
+      for (int bi = 0; bi < VPT / 8; ++bi) {
+        const int blk = tid + bi * NT;
+        if (blk < NBLK) {
+          const int qb = (blk % (BROWS / 8)) * 8;
+          const int kb = (blk / (BROWS / 8)) * 8;
+#pragma unroll
+          for (int i = 0; i < 8; ++i)
+            *reinterpret_cast<uint4*>(lds + (qb + i) * LDS_PITCH + kb) = regs[bi * 8 + i];
+        }
+      }
+    }
+  }
+};
+
+__device__ __forceinline__ float silu_f(float x) { return x / (1.0f + __expf(-x)); }
+__device__ __forceinline__ float sigmoid_f(float x) { return 1.0f / (1.0f + __expf(-x)); }
+__device__ __forceinline__ float bf16r(float x) { return (float)(__bf16)x; }
+
+// XCD-aware tile order: consecutive workgroup ids land on different XCDs
+// (round-robin dispatch), so ids are regrouped so that each XCD walks a
+// contiguous range of the tile order; within it, tiles go in groups of
+// GROUP_M row-panels to share A and B panels in that XCD's L2.
+__device__ __forceinline__ void tile_coords(int64_t tiles_m, int64_t tiles_n, int& tm, int& tn) {
+  constexpr int NXCD = 8;
+  constexpr int GROUP_M = 8;
+  const int64_t total = tiles_m * tiles_n;
+  int64_t id = blockIdx.x;
+  if (total % NXCD == 0) {
+    const int64_t per = total / NXCD;
+    id = (id % NXCD) * per + id / NXCD;
+  }
+  const int64_t group_span = (int64_t)GROUP_M * tiles_n;
+  const int64_t g = id / group_span;
+  const int64_t first_m = g * GROUP_M;
+  const int64_t gm = (tiles_m - first_m) < GROUP_M ? (tiles_m - first_m) : GROUP_M;
+  const int64_t in = id % group_span;
+  tm = (int)(first_m + in % gm);
+  tn = (int)(in / gm);
+}
+
+template <int BM, int BN, int WAVES_M, int WAVES_N, int A_LAYOUT, int B_LAYOUT, int BMODE, int EPI>
+__global__ __launch_bounds__(WAVES_M * WAVES_N * 64) void gemm_kernel(GemmArgs args) {
+  constexpr int NT = WAVES_M * WAVES_N * 64;
+  constexpr int TM = BM / WAVES_M, TN = BN / WAVES_N;  // wave sub-tile
+  constexpr int FM = TM / 32, FN = TN / 32;            // 32x32 MFMA tiles per wave
+  static_assert(TM % 32 == 0 && TN % 32 == 0, "wave tile must be a multiple of 32");
+  static_assert(BMODE == B_SINGLE || TN == 128, "dual mode expects 128-row wave tiles");
+
+  __shared__ __attribute__((aligned(16))) __bf16 smem[2 * (BM + BN) * LDS_PITCH];
+  // stage b: A tile at smem + b*(BM+BN)*pitch, B tile right after it
+  auto As = [&](int b) { return smem + b * (BM + BN) * LDS_PITCH; };
+  auto Bs = [&](int b) { return smem + b * (BM + BN) * LDS_PITCH + BM * LDS_PITCH; };
+
+  const int64_t M = args.M;
+  // output columns covered by one tile (dual: BN B-rows -> BN/2 outputs)
+  constexpr int OUT_BN = (BMODE == B_DUAL) ? BN / 2 : BN;
+  const int64_t tiles_m = (M + BM - 1) / BM;
+  const int64_t tiles_n = (args.N + OUT_BN - 1) / OUT_BN;
+  int tmi, tni;
+  tile_coords(tiles_m, tiles_n, tmi, tni);
+  const int64_t m0 = (int64_t)tmi * BM;
+  const int64_t n0 = (int64_t)tni * OUT_BN;
+
+  const int lane = threadIdx.x % 64;
+  const int wave = threadIdx.x / 64;
+  const int wm = wave % WAVES_M;
+  const int wn = wave / WAVES_M;
+
+  // ---- K tiles of this workgroup (split-K partitions the flat tile list) ----
+  int seg_tiles[MAX_SEGS];
+  int total_tiles = 0;
+  for (int s = 0; s < args.n_segs; ++s) {
+    const Seg& sg = args.segs[s];
+    const bool active = sg.n_hi > n0 && sg.n_lo < n0 + OUT_BN;
+    seg_tiles[s] = active ? (int)((sg.k + BK - 1) / BK) : 0;
+    total_tiles += seg_tiles[s];
+  }
+  const int per = (total_tiles + args.split_k - 1) / args.split_k;
+  const int t_begin = blockIdx.z * per;
+  const int t_end = min(total_tiles, t_begin + per);
+
+  f32x16 acc[FM][FN];
+#pragma unroll
+  for (int i = 0; i < FM; ++i)
+#pragma unroll
+    for (int j = 0; j < FN; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+
+  TileLoader<BM, NT, A_LAYOUT == ROW> la;
+  TileLoader<BN, NT, B_LAYOUT == COL> lb;
+
+  // Resolves flat tile index t -> (segment, k0) and loads it into registers.
+  auto load_tile = [&](int t) {
+    int s = 0, base = 0;
+    while (s < args.n_segs && t >= base + seg_tiles[s]) { base += seg_tiles[s]; ++s; }
+    const Seg& sg = args.segs[s];
+    const int64_t k0 = (int64_t)(t - base) * BK;
+    const int64_t kvalid = sg.k - k0;
+    const __bf16* abase = sg.a;
+    const int64_t lda = sg.lda;
+    la.load(
+        [&](int q) -> const __bf16* {
+          const int64_t m = m0 + q;
+          if (m >= M) return nullptr;
+          return A_LAYOUT == ROW ? abase + m * lda : abase + m;
+        },
+        lda, k0, kvalid);
+    lb.load(
+        [&](int q) -> const __bf16* {
+          int64_t n;
+          const __bf16* bp;
+          if constexpr (BMODE == B_DUAL) {
+            const int t4 = (q % 128) / 32;
+            n = n0 + (q / 128) * 64 + (t4 / 2) * 32 + q % 32;
+            bp = (t4 % 2 == 0) ? sg.b : sg.b2;
+          } else {
+            n = n0 + q;
+            bp = sg.b;
+          }
+          if (!bp || n >= args.N || n < sg.n_lo || n >= sg.n_hi) return nullptr;
+          const int64_t nr = n - sg.n_lo;
+          return B_LAYOUT == COL ? bp + nr * sg.ldb : bp + nr;
+        },
+        sg.ldb, k0, kvalid);
+  };
+
+  if (t_begin < t_end) {
+    load_tile(t_begin);
+    la.store(As(0));
+    lb.store(Bs(0));
+    __syncthreads();
+    int buf = 0;
+    for (int t = t_begin; t < t_end; ++t) {
+      const bool more = t + 1 < t_end;
+      if (more) load_tile(t + 1);
+      const __bf16* a_s = As(buf) + (wm * TM + lane % 32) * LDS_PITCH + (lane / 32) * 8;
+      const __bf16* b_s = Bs(buf) + (wn * TN + lane % 32) * LDS_PITCH + (lane / 32) * 8;
+#pragma unroll
+      for (int ks = 0; ks < BK / 16; ++ks) {
+        bf16x8 af[FM], bfr[FN];
+#pragma unroll
+        for (int i = 0; i < FM; ++i) af[i] = *reinterpret_cast<const bf16x8*>(a_s + i * 32 * LDS_PITCH + ks * 16);
+#pragma unroll
+        for (int j = 0; j < FN; ++j) bfr[j] = *reinterpret_cast<const bf16x8*>(b_s + j * 32 * LDS_PITCH + ks * 16);
+#pragma unroll
+        for (int i = 0; i < FM; ++i)
+#pragma unroll
+          for (int j = 0; j < FN; ++j)
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[i], bfr[j], acc[i][j], 0, 0, 0);
+      }
+      if (more) {
+        la.store(As(buf ^ 1));
+        lb.store(Bs(buf ^ 1));
+      }
+      __syncthreads();
+      buf ^= 1;
+    }
+  }
+
+  // ---------------- epilogue ----------------
+  const EpiArgs& ep = args.ep;
+  const int64_t row_base = m0 + wm * TM + 4 * (lane / 32);
+  const int col_in = lane % 32;
+
+  if constexpr (EPI == EPI_STORE_BF16 || EPI == EPI_STORE_F32 || EPI == EPI_ATOMIC_F32) {
+#pragma unroll
+    for (int j = 0; j < FN; ++j) {
+      const int64_t n = n0 + wn * TN + j * 32 + col_in;
+      if (n >= args.N) continue;
+      float col_alpha = ep.alpha;
+      if (ep.alpha_group > 0) {
+        const int64_t grp = n / ep.alpha_group;
+        col_alpha = ep.alphas[grp < 4 ? grp : 3];
+      }
+#pragma unroll
+      for (int i = 0; i < FM; ++i) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int64_t m = row_base + i * 32 + 8 * (r / 4) + (r % 4);
+          if (m >= M) continue;
+          const float v = col_alpha * acc[i][j][r];
+          if constexpr (EPI == EPI_STORE_BF16) {
+            __bf16* cp = (__bf16*)ep.c + m * ep.ldc + n;
+            float o = v;
+            if (ep.beta != 0.f) o += ep.beta * (float)(*cp);
+            *cp = (__bf16)o;
+          } else if constexpr (EPI == EPI_STORE_F32) {
+            float* cp = (float*)ep.c + m * ep.ldc + n;
+            float o = v;
+            if (ep.beta != 0.f) o += ep.beta * (*cp);
+            *cp = o;
+          } else {
+            atomicAdd((float*)ep.c + m * ep.ldc + n, v);
+          }
+        }
+      }
+    }
+  } else if constexpr (EPI == EPI_SWIGLU_FWD) {
+    // wave tiles (0,1) and (2,3) are (gate, up) pairs for 32 output columns each
+#pragma unroll
+    for (int jp = 0; jp < FN / 2; ++jp) {
+      const int64_t n = n0 + wn * 64 + jp * 32 + col_in;
+      if (n >= args.N) continue;
+#pragma unroll
+      for (int i = 0; i < FM; ++i) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int64_t m = row_base + i * 32 + 8 * (r / 4) + (r % 4);
+          if (m >= M) continue;
+          const float e = acc[i][2 * jp][r];
+          const float g = acc[i][2 * jp + 1][r];
+          const int64_t off = m * ep.ld_eg + n;
+          ep.e[off] = (__bf16)e;
+          ep.g[off] = (__bf16)g;
+          ((__bf16*)ep.c)[m * ep.ldc + n] = (__bf16)(silu_f(e) * g);
+        }
+      }
+    }
+  } else if constexpr (EPI == EPI_SWIGLU_BWD) {
+    // Unsloth-style in-place SwiGLU backward on the DW = dY @ W_down tile:
+    //   f = silu(e) -> bf16, h = f*g, df = DW*f, de = (DW*g) * sig*(1 + e*(1-sig))
+#pragma unroll
+    for (int j = 0; j < FN; ++j) {
+      const int64_t n = n0 + wn * TN + j * 32 + col_in;
+      if (n >= args.N) continue;
+#pragma unroll
+      for (int i = 0; i < FM; ++i) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int64_t m = row_base + i * 32 + 8 * (r / 4) + (r % 4);
+          if (m >= M) continue;
+          const int64_t off = m * ep.ld_eg + n;
+          const float dw = bf16r(acc[i][j][r]);
+          const float e = (float)ep.e[off];
+          const float g = (float)ep.g[off];
+          const float se = sigmoid_f(e);
+          const float f = bf16r(se * e);
+          const float h = f * g;
+          const float df = dw * f;
+          const float dg = bf16r(dw * g);
+          const float de = dg * se * (1.0f + e * (1.0f - se));
+          ((__bf16*)ep.c)[m * ep.ldc + n] = (__bf16)h;
+          ep.e[off] = (__bf16)df;
+          ep.g[off] = (__bf16)de;
+        }
+      }
+    }
+  } else if constexpr (EPI == EPI_ROPE) {
+    // Each wave covers TN = 128 output columns aligned to a head boundary
+    // (head_dim 128: tiles 0,1 = lo half, 2,3 = hi half; head_dim 64: two
+    // heads, tiles (0,1) and (2,3)).
+    const int half_tiles = ep.head_dim / 64;  // partner distance in 32-col tiles
+#pragma unroll
+    for (int i = 0; i < FM; ++i) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int64_t m = row_base + i * 32 + 8 * (r / 4) + (r % 4);
+        if (m >= M) continue;
+        const int64_t pos = ep.positions ? ep.positions[m] : m;
+#pragma unroll
+        for (int j = 0; j < FN; ++j) {
+          const int64_t n = n0 + wn * TN + j * 32 + col_in;
+          if (n >= args.N) continue;
+          float v = acc[i][j][r];
+          if (n < ep.rope_cols) {
+            const int jj = j % (2 * half_tiles);
+            const bool lo = jj < half_tiles;
+            const int partner = lo ? j + half_tiles : j - half_tiles;
+            float pv = 0.f;
+#pragma unroll
+            for (int q = 0; q < FN; ++q)
+              if (q == partner) pv = acc[i][q][r];
+            const int d = (int)(n % ep.head_dim) % (ep.head_dim / 2);
+            const float c = (float)ep.cos[pos * ep.cs_ld + d];
+            const float s = (float)ep.sin[pos * ep.cs_ld + d];
+            // round the projection to bf16 first: RoPE is applied to the
+            // materialised Q/K in the unfused reference path
+            const float x = bf16r(v), xp = bf16r(pv);
+            v = lo ? x * c - xp * s : x * c + xp * s;
+          }
+          ((__bf16*)ep.c)[m * ep.ldc + n] = (__bf16)v;
+        }
+      }
+    }
+  }
+}
+
+// Launches one GEMM with tile config `cfg` (-1 = pick from the shape).
+int run(int cfg, int a_layout, int b_layout, int epi, const GemmArgs& a, hipStream_t s);
+
+}  // namespace fgemm

@@ -1,0 +1,140 @@
+// Fused LoRA entry points built on the MFMA GEMM core.
+//
+// LoRA-MLP (reference: kernels/lora_mlp/experiments/v6/lora_mlp_kernel_v6.py
+// :335-451 forward, :592-672 backward; math of
+// kernels/lora_mlp/reference/lora_mlp_pytorch.py:111-225):
+//   forward  e = X Wg^T + sg (X Ag^T) Bg^T,  g = X Wu^T + su (X Au^T) Bu^T,
+//            h = silu(e) * g                      -> forge_lora_mlp_gate_up
+//   backward DW = dY Wd + sd (dY Bd) Ad, then the in-place SwiGLU backward
+//            (DW, e, g) -> (h, df, de)            -> forge_lora_mlp_down_bwd
+// LoRA-QKV (reference: kernels/lora_qkv/experiments/v2/lora_qkv_kernel_v2_3.py
+// :177-267 + the caller's RoPE, forge/forge/patching/kernels/lora.py:250-264):
+//   [Q | K | V] = X [Wq; Wk; Wv]^T + per-projection LoRA, RoPE on Q and K
+//                                                  -> forge_lora_qkv_rope
+// The LoRA-A products (X A^T, dY B, ...) arrive pre-scaled by s from the
+// caller (computed with forge_gemm); the LoRA-B product rides along the base
+// GEMM as one more K segment.
+#include "gemm_core.h"
+
+using namespace fgemm;
+
+extern "C" int forge_lora_mlp_gate_up(int64_t M, int64_t H, int64_t I, int64_t r,
+                                      const void* x, int64_t ldx,
+                                      const void* w_gate, const void* w_up, int64_t ldw,
+                                      const void* xa, int64_t ld_xa,
+                                      const void* b_gate, const void* b_up, int64_t ldb,
+                                      void* e, void* g, void* h, int64_t ld_out, void* stream) {
+  if (M < 0 || H < 0 || I < 0 || r < 0) return forge_set_error(FORGE_ERR_INVALID, "lora_mlp_gate_up: shape");
+  GemmArgs a = {};
+  a.M = M;
+  a.N = I;
+  a.split_k = 1;
+  int ns = 0;
+  a.segs[ns++] = Seg{(const __bf16*)x, ldx, (const __bf16*)w_gate, (const __bf16*)w_up, ldw, H, 0, I};
+  if (r > 0 && xa) {
+    // gate rows take xa[:, :r] Bg^T, up rows take xa[:, r:2r] Bu^T
+    a.segs[ns++] = Seg{(const __bf16*)xa, ld_xa, (const __bf16*)b_gate, nullptr, ldb, r, 0, I};
+    a.segs[ns++] = Seg{(const __bf16*)xa + r, ld_xa, nullptr, (const __bf16*)b_up, ldb, r, 0, I};
+  }
+  a.n_segs = ns;
+  a.ep.c = h;
+  a.ep.ldc = ld_out;
+  a.ep.alpha = 1.f;
+  a.ep.e = (__bf16*)e;
+  a.ep.g = (__bf16*)g;
+  a.ep.ld_eg = ld_out;
+  if (r > 0 && xa && (ld_xa % 8 != 0 || r % 8 != 0))
+    return forge_set_error(FORGE_ERR_INVALID, "lora_mlp_gate_up: rank and ld_xa must be multiples of 8");
+  return run(-1, ROW, COL, EPI_SWIGLU_FWD, a, (hipStream_t)stream);
+}
+
+extern "C" int forge_lora_mlp_down_bwd(int64_t M, int64_t H, int64_t I, int64_t r,
+                                       const void* dy, int64_t lddy,
+                                       const void* w_down, int64_t ldwd,
+                                       const void* t_d, int64_t ld_t,
+                                       const void* a_down, int64_t ld_ad,
+                                       void* h_out, void* e_df, void* g_de, int64_t ld, void* stream) {
+  if (M < 0 || H < 0 || I < 0 || r < 0) return forge_set_error(FORGE_ERR_INVALID, "lora_mlp_down_bwd: shape");
+  GemmArgs a = {};
+  a.M = M;
+  a.N = I;
+  a.split_k = 1;
+  int ns = 0;
+  // DW[m, i] = sum_h dY[m, h] Wd[h, i]  (+ sum_j T[m, j] Ad[j, i]); B is [K][N]
+  a.segs[ns++] = Seg{(const __bf16*)dy, lddy, (const __bf16*)w_down, nullptr, ldwd, H, 0, I};
+  if (r > 0 && t_d) a.segs[ns++] = Seg{(const __bf16*)t_d, ld_t, (const __bf16*)a_down, nullptr, ld_ad, r, 0, I};
+  a.n_segs = ns;
+  a.ep.c = h_out;
+  a.ep.ldc = ld;
+  a.ep.alpha = 1.f;
+  a.ep.e = (__bf16*)e_df;
+  a.ep.g = (__bf16*)g_de;
+  a.ep.ld_eg = ld;
+  return run(-1, ROW, ROW, EPI_SWIGLU_BWD, a, (hipStream_t)stream);
+}
+
+extern "C" int forge_lora_qkv_rope(int64_t M, int64_t K, int64_t hq, int64_t hkv, int64_t r,
+                                   const void* x, int64_t ldx,
+                                   const void* w_q, const void* w_k, const void* w_v, int64_t ldw,
+                                   const void* xa, int64_t ld_xa,
+                                   const void* b_q, const void* b_k, const void* b_v, int64_t ldb,
+                                   void* out, int64_t ld_out,
+                                   const void* cos, const void* sin, int64_t cs_ld,
+                                   const int64_t* positions, int64_t head_dim, int apply_rope,
+                                   void* stream) {
+  if (M < 0 || K < 0 || hq < 0 || hkv < 0 || r < 0)
+    return forge_set_error(FORGE_ERR_INVALID, "lora_qkv_rope: shape");
+  if (apply_rope && !(head_dim == 64 || head_dim == 128))
+    return forge_set_error(FORGE_ERR_UNSUPPORTED, "lora_qkv_rope: head_dim %lld (64 or 128 fused)",
+                           (long long)head_dim);
+  if (apply_rope && (hq % 256 != 0 || hkv % 256 != 0))
+    return forge_set_error(FORGE_ERR_UNSUPPORTED,
+                           "lora_qkv_rope: projection widths must be multiples of 256 (got %lld, %lld)",
+                           (long long)hq, (long long)hkv);
+  GemmArgs a = {};
+  a.M = M;
+  a.N = hq + 2 * hkv;
+  a.split_k = 1;
+  int ns = 0;
+  const int64_t q1 = hq, k1 = hq + hkv, v1 = hq + 2 * hkv;
+  a.segs[ns++] = Seg{(const __bf16*)x, ldx, (const __bf16*)w_q, nullptr, ldw, K, 0, q1};
+  a.segs[ns++] = Seg{(const __bf16*)x, ldx, (const __bf16*)w_k, nullptr, ldw, K, q1, k1};
+  a.segs[ns++] = Seg{(const __bf16*)x, ldx, (const __bf16*)w_v, nullptr, ldw, K, k1, v1};
+  if (r > 0 && xa) {
+    a.segs[ns++] = Seg{(const __bf16*)xa, ld_xa, (const __bf16*)b_q, nullptr, ldb, r, 0, q1};
+    a.segs[ns++] = Seg{(const __bf16*)xa + r, ld_xa, (const __bf16*)b_k, nullptr, ldb, r, q1, k1};
+    a.segs[ns++] = Seg{(const __bf16*)xa + 2 * r, ld_xa, (const __bf16*)b_v, nullptr, ldb, r, k1, v1};
+  }
+  a.n_segs = ns;
+  a.ep.c = out;
+  a.ep.ldc = ld_out;
+  a.ep.alpha = 1.f;
+  a.ep.cos = (const __bf16*)cos;
+  a.ep.sin = (const __bf16*)sin;
+  a.ep.cs_ld = cs_ld;
+  a.ep.positions = positions;
+  a.ep.rope_cols = apply_rope ? k1 : 0;
+  a.ep.head_dim = (int)(head_dim > 0 ? head_dim : 128);
+  if (!apply_rope) return run(-1, ROW, COL, EPI_STORE_BF16, a, (hipStream_t)stream);
+  return run(-1, ROW, COL, EPI_ROPE, a, (hipStream_t)stream);
+}
+
+extern "C" int forge_lora_a(int64_t M, int64_t K, int64_t r, int n_proj, const void* x, int64_t ldx,
+                            const void* const* a_mats, int64_t lda, const float* scales, void* out,
+                            int64_t ld_out, void* stream) {
+  if (M < 0 || K < 0 || r <= 0 || n_proj < 1 || n_proj > 4)
+    return forge_set_error(FORGE_ERR_INVALID, "lora_a: shape (r > 0, 1 <= n_proj <= 4)");
+  GemmArgs a = {};
+  a.M = M;
+  a.N = r * n_proj;
+  a.split_k = 1;
+  a.n_segs = n_proj;
+  for (int p = 0; p < n_proj; ++p)
+    a.segs[p] = Seg{(const __bf16*)x, ldx, (const __bf16*)a_mats[p], nullptr, lda, K, p * r, (p + 1) * r};
+  a.ep.c = out;
+  a.ep.ldc = ld_out;
+  a.ep.alpha = 1.f;
+  a.ep.alpha_group = r;
+  for (int p = 0; p < 4; ++p) a.ep.alphas[p] = p < n_proj ? scales[p] : 1.f;
+  return run(-1, ROW, COL, EPI_STORE_BF16, a, (hipStream_t)stream);
+}

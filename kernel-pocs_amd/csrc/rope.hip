@@ -1,0 +1,177 @@
+// Rotary position embedding (half-split / rotate_half convention) for gfx950.
+//
+// Reference: kernels/rope/forge_rope_v3.py:32-96 (kernel) and :99-132
+// (launcher); the HF formula it is tested against is
+// kernels/rope/tests/test_v1.py:49-61:
+//     out = x * cos + rotate_half(x) * sin,   rotate_half(x) = cat(-x_hi, x_lo)
+// i.e. for j < D/2:  out_lo = lo*cos_j - hi*sin_j,  out_hi = hi*cos_j + lo*sin_j
+// (only the first D/2 cos/sin columns are read, as in the reference kernel).
+// Backward is the same rotation with -sin.
+//
+// Work decomposition: one work item = (token t, 16-byte column chunk c of the
+// lo half, group of HPT heads).  The item loads its cos/sin chunk once and
+// rotates that chunk in HPT heads (Q heads first, then K heads), so every
+// thread keeps 2*HPT independent 16-byte loads in flight.  Any element strides
+// for (batch, head, seq) are accepted, so the HF `transpose(1, 2)` view of a
+// [B, S, H, D] projection is rotated in place of memory order, with no copy.
+#include "common.h"
+
+namespace {
+
+constexpr int kBlock = 256;
+constexpr int kHPT = 8;  // heads per work item
+
+struct RopeArgs {
+  const void* q; int64_t q_sb, q_sh, q_ss;
+  const void* k; int64_t k_sb, k_sh, k_ss;
+  void* qo; int64_t qo_sb, qo_sh, qo_ss;
+  void* ko; int64_t ko_sb, ko_sh, ko_ss;
+  const void* cos; int64_t cos_sb, cos_ss;
+  const void* sin; int64_t sin_sb, sin_ss;
+  const int64_t* positions;
+  int64_t seq_len, n_q, n_heads, half, chunks, n_hgroups, n_items;
+  float sign;  // +1 forward, -1 backward
+};
+
+template <class T, int VEC>
+__global__ __launch_bounds__(kBlock) void rope_kernel(RopeArgs a) {
+  const int64_t stride = (int64_t)gridDim.x * kBlock;
+  for (int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x; i < a.n_items; i += stride) {
+    const int64_t c = i % a.chunks;
+    const int64_t rest = i / a.chunks;
+    const int64_t hg = rest % a.n_hgroups;
+    const int64_t t = rest / a.n_hgroups;
+    const int64_t b = t / a.seq_len;
+    const int64_t s = t - b * a.seq_len;
+    const int64_t pos = a.positions ? a.positions[t] : s;
+    const int64_t col = c * VEC;
+
+    float cs[VEC], sn[VEC];
+    {
+      const T* cp = (const T*)a.cos + b * a.cos_sb + pos * a.cos_ss + col;
+      const T* sp = (const T*)a.sin + b * a.sin_sb + pos * a.sin_ss + col;
+      if constexpr (VEC * sizeof(T) == 16) {
+        Vec16<T> cv = load16(cp), sv = load16(sp);
+#pragma unroll
+        for (int j = 0; j < VEC; ++j) { cs[j] = to_f32(cv.v[j]); sn[j] = a.sign * to_f32(sv.v[j]); }
+      } else {
+#pragma unroll
+        for (int j = 0; j < VEC; ++j) { cs[j] = to_f32(cp[j]); sn[j] = a.sign * to_f32(sp[j]); }
+      }
+    }
+
+    const int64_t h0 = hg * kHPT;
+    T lo[kHPT][VEC], hi[kHPT][VEC];
+#pragma unroll
+    for (int u = 0; u < kHPT; ++u) {
+      const int64_t h = h0 + u;
+      if (h < a.n_heads) {
+        const T* src = h < a.n_q
+                           ? (const T*)a.q + b * a.q_sb + h * a.q_sh + s * a.q_ss + col
+                           : (const T*)a.k + b * a.k_sb + (h - a.n_q) * a.k_sh + s * a.k_ss + col;
+        if constexpr (VEC * sizeof(T) == 16) {
+          Vec16<T> l = load16(src), r = load16(src + a.half);
+#pragma unroll
+          for (int j = 0; j < VEC; ++j) { lo[u][j] = l.v[j]; hi[u][j] = r.v[j]; }
+        } else {
+#pragma unroll
+          for (int j = 0; j < VEC; ++j) { lo[u][j] = src[j]; hi[u][j] = src[a.half + j]; }
+        }
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < kHPT; ++u) {
+      const int64_t h = h0 + u;
+      if (h < a.n_heads) {
+        T* dst = h < a.n_q ? (T*)a.qo + b * a.qo_sb + h * a.qo_sh + s * a.qo_ss + col
+                           : (T*)a.ko + b * a.ko_sb + (h - a.n_q) * a.ko_sh + s * a.ko_ss + col;
+        if constexpr (VEC * sizeof(T) == 16) {
+          Vec16<T> ol, oh;
+#pragma unroll
+          for (int j = 0; j < VEC; ++j) {
+            float x0 = to_f32(lo[u][j]), x1 = to_f32(hi[u][j]);
+            ol.v[j] = from_f32<T>(x0 * cs[j] - x1 * sn[j]);
+            oh.v[j] = from_f32<T>(x1 * cs[j] + x0 * sn[j]);
+          }
+          store16(dst, ol);
+          store16(dst + a.half, oh);
+        } else {
+#pragma unroll
+          for (int j = 0; j < VEC; ++j) {
+            float x0 = to_f32(lo[u][j]), x1 = to_f32(hi[u][j]);
+            dst[j] = from_f32<T>(x0 * cs[j] - x1 * sn[j]);
+            dst[a.half + j] = from_f32<T>(x1 * cs[j] + x0 * sn[j]);
+          }
+        }
+      }
+    }
+  }
+}
+
+template <class T>
+int launch(RopeArgs a, int64_t head_dim, bool all_aligned, hipStream_t s) {
+  constexpr int V = 16 / sizeof(T);
+  const bool vec = all_aligned && (a.half % V == 0);
+  const int vw = vec ? V : 1;
+  a.chunks = a.half / vw;
+  a.n_hgroups = (a.n_heads + kHPT - 1) / kHPT;
+  a.n_items = a.n_items * a.chunks * a.n_hgroups;  // n_items held the token count
+  int grid = grid_for(a.n_items, kBlock);
+  if (vec)
+    rope_kernel<T, V><<<grid, kBlock, 0, s>>>(a);
+  else
+    rope_kernel<T, 1><<<grid, kBlock, 0, s>>>(a);
+  FORGE_CHECK_LAUNCH();
+  (void)head_dim;
+  return FORGE_OK;
+}
+
+}  // namespace
+
+extern "C" int forge_rope(int dtype, const void* q, int64_t q_sb, int64_t q_sh, int64_t q_ss,
+                          const void* k, int64_t k_sb, int64_t k_sh, int64_t k_ss, void* q_out,
+                          int64_t qo_sb, int64_t qo_sh, int64_t qo_ss, void* k_out, int64_t ko_sb,
+                          int64_t ko_sh, int64_t ko_ss, const void* cos, int64_t cos_sb,
+                          int64_t cos_ss, const void* sin, int64_t sin_sb, int64_t sin_ss,
+                          const int64_t* positions, int64_t batch, int64_t n_q, int64_t n_kv,
+                          int64_t seq_len, int64_t head_dim, int backward, void* stream) {
+  if (batch < 0 || n_q < 0 || n_kv < 0 || seq_len < 0 || head_dim < 0)
+    return forge_set_error(FORGE_ERR_INVALID, "rope: negative shape");
+  if (head_dim % 2 != 0) return forge_set_error(FORGE_ERR_INVALID, "rope: head_dim must be even");
+  if (n_kv > 0 && n_q % n_kv != 0)
+    return forge_set_error(FORGE_ERR_INVALID, "rope: n_q %% n_kv != 0");
+  if (batch == 0 || seq_len == 0 || head_dim == 0 || (n_q + n_kv) == 0) return FORGE_OK;
+
+  RopeArgs a;
+  a.q = q; a.q_sb = q_sb; a.q_sh = q_sh; a.q_ss = q_ss;
+  a.k = k; a.k_sb = k_sb; a.k_sh = k_sh; a.k_ss = k_ss;
+  a.qo = q_out; a.qo_sb = qo_sb; a.qo_sh = qo_sh; a.qo_ss = qo_ss;
+  a.ko = k_out; a.ko_sb = ko_sb; a.ko_sh = ko_sh; a.ko_ss = ko_ss;
+  a.cos = cos; a.cos_sb = cos_sb; a.cos_ss = cos_ss;
+  a.sin = sin; a.sin_sb = sin_sb; a.sin_ss = sin_ss;
+  a.positions = positions;
+  a.seq_len = seq_len;
+  a.n_q = n_q;
+  a.n_heads = n_q + n_kv;
+  a.half = head_dim / 2;
+  a.n_items = batch * seq_len;
+  a.sign = backward ? -1.0f : 1.0f;
+
+  // 16-byte vectors need every base pointer and every non-unit stride aligned.
+  const size_t es = dtype_size(dtype);
+  const int64_t V = es ? (int64_t)(16 / es) : 1;
+  bool al = aligned16(q) && aligned16(k) && aligned16(q_out) && aligned16(k_out) &&
+            aligned16(cos) && aligned16(sin);
+  for (int64_t st : {q_sb, q_sh, q_ss, k_sb, k_sh, k_ss, qo_sb, qo_sh, qo_ss, ko_sb, ko_sh, ko_ss,
+                     cos_sb, cos_ss, sin_sb, sin_ss})
+    al = al && (st % V == 0);
+
+  hipStream_t s = (hipStream_t)stream;
+  switch (dtype) {
+    case FORGE_DTYPE_F32: return launch<float>(a, head_dim, al, s);
+    case FORGE_DTYPE_BF16: return launch<bf16_t>(a, head_dim, al, s);
+    case FORGE_DTYPE_F16: return launch<fp16_t>(a, head_dim, al, s);
+    case FORGE_DTYPE_F64: return launch<double>(a, head_dim, al, s);
+    default: return forge_set_error(FORGE_ERR_UNSUPPORTED, "rope: dtype %d", dtype);
+  }
+}

@@ -1,0 +1,186 @@
+"""Fused Q+K rotary embedding with GQA grouping on MI355X.
+
+Drop-in for kernels/rope/forge_rope_v3.py of Forge-researchlab/kernel-POCs:
+`ForgeRoPEv3Function` (same asserts, same `ctx.save_for_backward(cos, sin)`,
+backward = rotation by -theta), `apply_rope`, `ForgeRoPEv3` and
+`get_autotune_cache_for`.  The rotation runs in `forge_rope`
+(libforge_hip.so, csrc/rope.hip).
+
+Differences that keep values identical:
+  * Inputs with any (batch, head, seq) strides are rotated in place of memory
+    order, so HF's `transpose(1, 2)` view of a [B, S, H, D] projection costs
+    no `.contiguous()` copy (reference :179-180 copies).  Outputs are allocated
+    with `torch.empty_like`, i.e. in the input's memory layout.
+  * `apply_rope(..., positions=...)` (optional, int64 [B*S] or [B, S]) selects
+    the cos/sin row per token, for packed variable-length sequences.
+"""
+from __future__ import annotations
+
+import math
+from typing import Optional
+
+import torch
+
+from forge_hip import _lib as L
+
+# launch geometry of csrc/rope.hip (fixed; there is no autotuning)
+_BLOCK = 256
+_HEADS_PER_ITEM = 8
+
+
+def _rope_launch(q_in, k_in, q_out, k_out, cos, sin, backward_pass: bool, positions=None):
+    """Replaces `_launch_kernel` (kernels/rope/forge_rope_v3.py:99-132)."""
+    batch, n_q, seq_len, head_dim = q_in.shape
+    n_kv = k_in.shape[1]
+    assert n_q % n_kv == 0, f"V3 requires n_q % n_kv == 0 (got n_q={n_q}, n_kv={n_kv})."
+    L.require_gpu(q_in, k_in, cos, sin)
+
+    cos_has_batch = cos.shape[0] == batch
+    cos_sb = cos.stride(0) if cos_has_batch else 0
+    sin_sb = sin.stride(0) if cos_has_batch else 0
+    pos = None
+    if positions is not None:
+        pos = positions.reshape(-1).to(device=q_in.device, dtype=torch.int64).contiguous()
+        assert pos.numel() == batch * seq_len, "positions must have batch*seq_len entries"
+    L.check(
+        L.forge_rope(
+            L.dtype_code(q_in.dtype),
+            q_in.data_ptr(), q_in.stride(0), q_in.stride(1), q_in.stride(2),
+            k_in.data_ptr(), k_in.stride(0), k_in.stride(1), k_in.stride(2),
+            q_out.data_ptr(), q_out.stride(0), q_out.stride(1), q_out.stride(2),
+            k_out.data_ptr(), k_out.stride(0), k_out.stride(1), k_out.stride(2),
+            cos.data_ptr(), cos_sb, cos.stride(1),
+            sin.data_ptr(), sin_sb, sin.stride(1),
+            None if pos is None else pos.data_ptr(),
+            batch, n_q, n_kv, seq_len, head_dim, 1 if backward_pass else 0,
+            L.stream_of(q_in),
+        ),
+        "forge_rope",
+    )
+    return pos
+
+
+def _unit_last(t: torch.Tensor) -> torch.Tensor:
+    return t if t.stride(-1) == 1 else t.contiguous()
+
+
+def _cos_sin_like(cos: torch.Tensor, q: torch.Tensor) -> torch.Tensor:
+    # the reference kernel reads cos/sin as stored and computes in fp32; a
+    # table in another dtype than q is cast once so the kernel reads one type
+    return _unit_last(cos if cos.dtype == q.dtype else cos.to(q.dtype))
+
+
+def get_autotune_cache_for(q, k, cos, sin, backward_pass: bool = False):
+    """Diagnostic of kernels/rope/forge_rope_v3.py:135-158.  The HIP kernel has
+    one fixed launch shape, reported here in the same dict form."""
+    batch, n_q, seq_len, head_dim = q.shape
+    n_kv = k.shape[1]
+    chunk = 16 // q.element_size()
+    items = batch * seq_len * math.ceil((head_dim // 2) / chunk) * math.ceil((n_q + n_kv) / _HEADS_PER_ITEM)
+    return {
+        "num_warps": _BLOCK // 64,
+        "num_stages": 1,
+        "all_kwargs": {"block": _BLOCK, "heads_per_item": _HEADS_PER_ITEM, "work_items": items},
+    }
+
+
+def _rope_forward(ctx, q, k, cos, sin, positions):
+    assert q.dim() == 4
+    assert k.dim() == 4
+    assert cos.dim() == 3 and sin.dim() == 3
+
+    batch, n_q, seq_len, head_dim = q.shape
+    n_kv = k.shape[1]
+
+    assert k.shape == (batch, n_kv, seq_len, head_dim)
+    assert cos.shape[0] in (1, batch)
+    if positions is None:
+        assert cos.shape[1] == seq_len and cos.shape[2] == head_dim
+    else:
+        assert cos.shape[2] == head_dim
+    assert sin.shape == cos.shape
+    assert head_dim & (head_dim - 1) == 0
+
+    q = _unit_last(q)
+    k = _unit_last(k)
+    cos = _cos_sin_like(cos, q)
+    sin = _cos_sin_like(sin, q)
+
+    out_q = torch.empty_like(q)
+    out_k = torch.empty_like(k)
+    pos = _rope_launch(q, k, out_q, out_k, cos, sin, backward_pass=False, positions=positions)
+    ctx.save_for_backward(cos, sin)
+    ctx.positions = pos
+    return out_q, out_k
+
+
+def _rope_backward(ctx, dq, dk):
+    cos, sin = ctx.saved_tensors
+    dq = _unit_last(dq)
+    dk = _unit_last(dk)
+    dq_in = torch.empty_like(dq)
+    dk_in = torch.empty_like(dk)
+    _rope_launch(dq, dk, dq_in, dk_in, cos, sin, backward_pass=True, positions=ctx.positions)
+    return dq_in, dk_in
+
+
+class ForgeRoPEv3Function(torch.autograd.Function):
+    """kernels/rope/forge_rope_v3.py:161-200: forward(ctx, q, k, cos, sin),
+    saves (cos, sin), backward rotates the incoming grads by -theta."""
+
+    @staticmethod
+    def forward(ctx, q, k, cos, sin):
+        return _rope_forward(ctx, q, k, cos, sin, None)
+
+    @staticmethod
+    def backward(ctx, dq, dk):
+        dq_in, dk_in = _rope_backward(ctx, dq, dk)
+        return dq_in, dk_in, None, None
+
+
+class ForgeRoPEPositionsFunction(torch.autograd.Function):
+    """Same as ForgeRoPEv3Function with a per-token cos/sin row index
+    (int64 positions, B*S entries) for packed variable-length batches."""
+
+    @staticmethod
+    def forward(ctx, q, k, cos, sin, positions):
+        return _rope_forward(ctx, q, k, cos, sin, positions)
+
+    @staticmethod
+    def backward(ctx, dq, dk):
+        dq_in, dk_in = _rope_backward(ctx, dq, dk)
+        return dq_in, dk_in, None, None, None
+
+
+def apply_rope(q: torch.Tensor, k: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor,
+               positions: Optional[torch.Tensor] = None):
+    """kernels/rope/forge_rope_v3.py:203-210."""
+    if positions is None:
+        return ForgeRoPEv3Function.apply(q, k, cos, sin)
+    return ForgeRoPEPositionsFunction.apply(q, k, cos, sin, positions)
+
+
+class ForgeRoPEv3(torch.nn.Module):
+    """kernels/rope/forge_rope_v3.py:213-218."""
+
+    def __init__(self):
+        super().__init__()
+
+    def forward(self, q, k, cos, sin):
+        return apply_rope(q, k, cos, sin)
+
+
+def rope_cos_sin(positions: torch.Tensor, head_dim: int, base: float = 10000.0,
+                 dtype: torch.dtype = torch.bfloat16):
+    """cos/sin tables (len(positions), head_dim) for a configurable RoPE base,
+    built as in kernels/rope/tests/test_v1.py:68-88 (and the HF rotary
+    module): inv_freq = 1/base^(arange(0, D, 2)/D), freqs = pos*inv_freq in
+    fp32, emb = cat(freqs, freqs), then cos/sin cast to dtype."""
+    dev = positions.device
+    inv_freq = 1.0 / (base ** (torch.arange(0, head_dim, 2, device=dev).float() / head_dim))
+    freqs = positions.float().unsqueeze(1) * inv_freq.unsqueeze(0)
+    emb = torch.cat([freqs, freqs], dim=-1)
+    return emb.cos().to(dtype), emb.sin().to(dtype)
+
+
+__all__ = ["apply_rope", "ForgeRoPEv3Function", "ForgeRoPEPositionsFunction", "ForgeRoPEv3", "get_autotune_cache_for", "rope_cos_sin"]

@@ -1,0 +1,53 @@
+"""The C-ABI library loads and exports every entry point the header declares
+(CPU-only: no kernel is launched).  Argument errors are reported through the
+status code and forge_last_error() before any device work."""
+import ctypes
+import re
+from pathlib import Path
+
+from forge_hip import _lib as L
+
+HEADER = Path(__file__).resolve().parents[1] / "include" / "forge_hip.h"
+
+
+def _declared():
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(forge_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_header_declares_entry_points():
+    names = _declared()
+    assert "forge_swiglu_fwd" in names and "forge_lora_qkv_rope" in names
+    assert len(names) >= 13
+
+
+def test_library_exports_every_declared_symbol():
+    lib = ctypes.CDLL(str(L.LIB_PATH))
+    missing = [n for n in _declared() if not hasattr(lib, n)]
+    assert not missing, f"declared in forge_hip.h but not exported: {missing}"
+    assert sorted(L.EXPORTED) == sorted(_declared())
+
+
+def test_identity():
+    assert L.forge_version().startswith(b"forge-hip")
+    assert L.forge_arch_ok() == 1
+
+
+def test_status_codes_and_messages():
+    # unsupported dtype is rejected before any launch
+    rc = L.forge_swiglu_fwd(99, 16, 16, 8, 16, 8, 4, 8, 1.0, 1.0, None)
+    assert rc == 2 and b"dtype" in L.forge_last_error()
+    rc = L.forge_swiglu_fwd(0, 16, 16, 4, 16, 8, 4, 8, 1.0, 1.0, None)  # ld < cols
+    assert rc == 1
+    rc = L.forge_rope(2, *([16, 0, 0, 0] * 4), *([16, 0, 0] * 2), None, 1, 4, 3, 8, 128, 0, None)
+    assert rc == 1 and b"n_q" in L.forge_last_error()
+    rc = L.forge_ce_fwd(2, 16, 4, 2, 8, 16, 1, None, None, None, None, None, -100, *([0.0] * 6), 0, None)
+    assert rc == 1 and b"ld" in L.forge_last_error()
+    rc = L.forge_lora_qkv_rope(16, 64, 100, 256, 0, *([16] * 20)[:14], 16, 16, 8, None, 96, 1, None)
+    assert rc == 2
+
+
+def test_zero_size_calls_are_noops():
+    assert L.forge_swiglu_fwd(0, None, None, 0, None, 0, 0, 0, 1.0, 1.0, None) == 0
+    assert L.forge_ce_fwd(2, None, 0, 0, 0, None, 1, None, None, None, None, None, -100, *([0.0] * 6), 0, None) == 0

@@ -1,0 +1,99 @@
+"""MFMA GEMM core parity (forge_gemm through the C ABI) vs a float32 matmul
+of the same bf16 operands on the CPU.
+
+Covers every operand layout, the three tile configurations (big, skinny-N,
+skinny-M), ragged M/N edges, multi-segment K (the LoRA K-extension), beta,
+fp32 output and split-K with the atomic epilogue.  Tolerance: bf16 output
+2e-2 relative to the output scale; fp32 output 1e-3 (bf16 inputs, fp32
+accumulation, different summation order).
+"""
+import ctypes
+
+import pytest
+import torch
+
+from forge_hip import _lib as L
+
+
+def _operand(rows, k, layout, gen):
+    """Returns (device tensor as stored, logical [rows, k] fp32 CPU matrix)."""
+    x = torch.randn(rows, k, generator=gen).to(torch.bfloat16)
+    stored = x if layout == L.LAYOUT_ROW else x.t().contiguous()
+    return stored.cuda(), x.float()
+
+
+def _gemm(M, N, segs_host, a_layout, b_layout, c, c_dtype, alpha=1.0, beta=0.0, epi=L.EPI_STORE, split_k=1):
+    arr = (L.GemmSegment * len(segs_host))()
+    for i, (a, lda, b, ldb, k) in enumerate(segs_host):
+        arr[i] = L.GemmSegment(a.data_ptr(), lda, b.data_ptr(), ldb, k)
+    L.check(L.forge_gemm(M, N, arr, len(segs_host), a_layout, b_layout, c.data_ptr(), c.stride(0), c_dtype,
+                         alpha, beta, epi, split_k, L.stream_of(c)), "forge_gemm")
+
+
+# B layouts: COL = weight [N][K] (K contiguous), ROW = [K][N]
+def _b_operand(n, k, layout, gen):
+    w = torch.randn(n, k, generator=gen).to(torch.bfloat16)  # logical B^T = [N][K]
+    stored = w if layout == L.LAYOUT_COL else w.t().contiguous()
+    return stored.cuda(), w.float().t()  # logical B [K][N]
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("M,N,K", [(256, 256, 64), (296, 520, 264), (64, 1000, 136), (1000, 40, 512),
+                                   (16, 704, 1024), (2048, 2048, 512)])
+@pytest.mark.parametrize("a_layout", [0, 1])
+@pytest.mark.parametrize("b_layout", [0, 1])
+def test_gemm_layouts(M, N, K, a_layout, b_layout):
+    gen = torch.Generator().manual_seed(M * 7 + N + K)
+    a, A = _operand(M, K, a_layout, gen)
+    b, B = _b_operand(N, K, b_layout, gen)
+    lda = K if a_layout == L.LAYOUT_ROW else M
+    ldb = K if b_layout == L.LAYOUT_COL else N
+    c = torch.empty(M, N, dtype=torch.bfloat16, device="cuda")
+    _gemm(M, N, [(a, lda, b, ldb, K)], a_layout, b_layout, c, L.DTYPE_BF16)
+    ref = A @ B
+    scale = ref.abs().max()
+    torch.testing.assert_close(c.float().cpu() / scale, ref / scale, atol=2e-2, rtol=0)
+    # fp32 output is tighter
+    c32 = torch.empty(M, N, dtype=torch.float32, device="cuda")
+    _gemm(M, N, [(a, lda, b, ldb, K)], a_layout, b_layout, c32, L.DTYPE_F32)
+    torch.testing.assert_close(c32.cpu(), ref, atol=1e-3 * scale.item(), rtol=1e-3)
+
+
+@pytest.mark.gpu
+def test_gemm_segments_beta_alpha():
+    """C = alpha * (A0 B0 + A1 B1) + beta * C with a rank-16 second segment."""
+    gen = torch.Generator().manual_seed(5)
+    M, N, K0, K1 = 384, 320, 256, 16
+    a0, A0 = _operand(M, K0, 0, gen)
+    a1, A1 = _operand(M, K1, 0, gen)
+    b0, B0 = _b_operand(N, K0, 1, gen)
+    b1, B1 = _b_operand(N, K1, 1, gen)
+    c0 = torch.randn(M, N, generator=gen)
+    c = c0.cuda().contiguous()
+    _gemm(M, N, [(a0, K0, b0, K0, K0), (a1, K1, b1, K1, K1)], 0, 1, c, L.DTYPE_F32, alpha=0.5, beta=2.0)
+    ref = 0.5 * (A0 @ B0 + A1 @ B1) + 2.0 * c0
+    torch.testing.assert_close(c.cpu(), ref, atol=2e-3, rtol=1e-3)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("split", [1, 4, 7])
+def test_gemm_split_k_atomic(split):
+    """LoRA-A-gradient shape: [r, H] = T^T @ X with K = tokens."""
+    gen = torch.Generator().manual_seed(split)
+    r, H, T = 16, 512, 2048
+    t, Tm = _operand(r, T, 1, gen)  # A = T^T stored as [T][r]
+    x_stored = torch.randn(T, H, generator=gen).to(torch.bfloat16)
+    c = torch.zeros(r, H, dtype=torch.float32, device="cuda")
+    _gemm(r, H, [(t, r, x_stored.cuda(), H, T)], 1, 0, c, L.DTYPE_F32, epi=L.EPI_ATOMIC_F32, split_k=split)
+    ref = Tm @ x_stored.float()
+    torch.testing.assert_close(c.cpu(), ref, atol=1e-3 * ref.abs().max().item(), rtol=1e-3)
+
+
+def test_gemm_rejects_bad_segments_without_gpu():
+    """Argument validation happens on the host before any launch."""
+    seg = (L.GemmSegment * 1)()
+    seg[0] = L.GemmSegment(16, 8, 16, 8, 12)  # K not a multiple of 8
+    rc = L.forge_gemm(8, 8, seg, 1, 0, 1, 16, 8, L.DTYPE_BF16, 1.0, 0.0, L.EPI_STORE, 1, None)
+    assert rc == 1 and b"multiple of 8" in L.forge_last_error()
+    rc = L.forge_gemm(8, 8, seg, 0, 0, 1, 16, 8, L.DTYPE_BF16, 1.0, 0.0, L.EPI_STORE, 1, None)
+    assert rc == 1

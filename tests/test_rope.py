@@ -1,0 +1,167 @@
+"""RoPE parity: HIP kernel vs the CPU oracle (HF formula in fp32).
+
+Cases follow kernels/rope/tests/test_v1.py:122-340 (shapes incl. MHA/MQA,
+dtypes, backward, fp64 gradcheck, one-hot gradient) plus the BASELINE config
+(bf16 Q [4,4096,32,128], K [4,4096,8,128] in B,S,H,D memory passed as the
+HF transpose(1,2) view, bases 10000 and 500000) and varlen positions.
+Tolerances: fp32 1e-5, bf16/fp16 2e-2 (the oracle is fp32 math rounded once).
+"""
+import pytest
+import torch
+
+from kernels.rope import ForgeRoPEv3Function, apply_rope, rope_cos_sin
+from oracle.rope import cos_sin, hf_apply_rotary_pos_emb, rope_fwd_bwd
+
+SHAPES = [
+    ("demo_tiny", 2, 4, 2, 16, 64),
+    ("qwen25_0p5b_short", 1, 14, 2, 512, 64),
+    ("qwen3_8b_short", 4, 32, 8, 512, 128),
+    ("qwen3_8b_train", 2, 32, 8, 2048, 128),
+    ("mha_no_gqa", 2, 16, 16, 1024, 128),
+    ("mqa_extreme", 2, 8, 1, 1024, 128),
+]
+TOL = {torch.float32: 1e-5, torch.float16: 2e-2, torch.bfloat16: 2e-2, torch.float64: 1e-5}
+
+
+def _inputs(b, nq, nkv, s, d, dtype, base=10000.0, seed=0, bshd=False, cos_batched=False):
+    g = torch.Generator().manual_seed(seed)
+    if bshd:
+        q = torch.randn(b, s, nq, d, generator=g).to(dtype).transpose(1, 2)
+        k = torch.randn(b, s, nkv, d, generator=g).to(dtype).transpose(1, 2)
+    else:
+        q = torch.randn(b, nq, s, d, generator=g).to(dtype)
+        k = torch.randn(b, nkv, s, d, generator=g).to(dtype)
+    c, sn = cos_sin(torch.arange(s), d, base, dtype)
+    if cos_batched:
+        c, sn = c.unsqueeze(0).expand(b, -1, -1).contiguous(), sn.unsqueeze(0).expand(b, -1, -1).contiguous()
+    else:
+        c, sn = c.unsqueeze(0), sn.unsqueeze(0)
+    return q, k, c, sn
+
+
+def _close(a, b, dtype):
+    t = TOL[dtype]
+    torch.testing.assert_close(a.cpu(), b.cpu(), atol=t, rtol=t)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("label,b,nq,nkv,s,d", SHAPES)
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+def test_rope_forward_backward(label, b, nq, nkv, s, d, dtype):
+    q, k, c, sn = _inputs(b, nq, nkv, s, d, dtype)
+    dq = torch.randn(q.shape).to(dtype)
+    dk = torch.randn(k.shape).to(dtype)
+    rq, rk, rdq, rdk = rope_fwd_bwd(q, k, c, sn, dq, dk)
+    qg = q.cuda().requires_grad_(True)
+    kg = k.cuda().requires_grad_(True)
+    oq, ok = apply_rope(qg, kg, c.cuda(), sn.cuda())
+    _close(oq, rq, dtype)
+    _close(ok, rk, dtype)
+    (oq * dq.cuda()).sum().add((ok * dk.cuda()).sum()).backward()
+    _close(qg.grad, rdq, dtype)
+    _close(kg.grad, rdk, dtype)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("bshd", [False, True])
+@pytest.mark.parametrize("cos_batched", [False, True])
+def test_rope_layouts(bshd, cos_batched):
+    """Strided (HF transpose) inputs and per-batch cos/sin tables."""
+    dtype = torch.bfloat16
+    q, k, c, sn = _inputs(2, 8, 2, 64, 128, dtype, bshd=bshd, cos_batched=cos_batched, seed=5)
+    rq, rk = hf_apply_rotary_pos_emb(q.float(), k.float(), c.float(), sn.float())
+    oq, ok = apply_rope(q.cuda(), k.cuda(), c.cuda(), sn.cuda())
+    _close(oq, rq.to(dtype), dtype)
+    _close(ok, rk.to(dtype), dtype)
+    if bshd:  # output keeps the input's memory layout (no copy was made)
+        assert oq.stride() == q.stride()
+
+
+@pytest.mark.gpu
+def test_rope_gradcheck_fp64_and_one_hot():
+    """kernels/rope/tests/test_v1.py:273-340: fp64 gradcheck (fp32 math inside)
+    and the one-hot analytic check dq_lo = cos, dq_hi = -sin."""
+    b, nq, nkv, s, d = 2, 4, 2, 8, 32
+    q, k, c, sn = _inputs(b, nq, nkv, s, d, torch.float64)
+    q, k, c, sn = q.cuda(), k.cuda(), c.cuda(), sn.cuda()
+    q1 = q.clone().requires_grad_(True)
+    k1 = k.clone().requires_grad_(True)
+    oq, ok = apply_rope(q1, k1, c, sn)
+    g = torch.zeros_like(oq)
+    g[0, 0, 1, 0] = 1.0
+    (oq * g).sum().add((ok * torch.zeros_like(ok)).sum()).backward()
+    assert abs(q1.grad[0, 0, 1, 0].item() - c[0, 1, 0].item()) < 1e-5
+    assert abs(q1.grad[0, 0, 1, d // 2].item() + sn[0, 1, 0].item()) < 1e-5
+    q2 = q.clone().requires_grad_(True)
+    k2 = k.clone().requires_grad_(True)
+    assert torch.autograd.gradcheck(
+        lambda a, b_: ForgeRoPEv3Function.apply(a, b_, c, sn), (q2, k2),
+        eps=1e-3, atol=1e-2, rtol=1e-2, nondet_tol=1e-3,
+    )
+
+
+@pytest.mark.gpu
+def test_rope_varlen_positions():
+    """Packed variable-length sequences: positions restart at 0 per sequence
+    and select the cos/sin row per token."""
+    lens = [5, 17, 9]
+    pos = torch.cat([torch.arange(n) for n in lens])
+    T, nq, nkv, d = int(pos.numel()), 4, 2, 128
+    dtype = torch.bfloat16
+    g = torch.Generator().manual_seed(7)
+    q = torch.randn(1, nq, T, d, generator=g).to(dtype)
+    k = torch.randn(1, nkv, T, d, generator=g).to(dtype)
+    table_c, table_s = cos_sin(torch.arange(32), d, 500000.0, dtype)
+    c_tok, s_tok = table_c[pos].unsqueeze(0), table_s[pos].unsqueeze(0)
+    rq, rk = hf_apply_rotary_pos_emb(q.float(), k.float(), c_tok.float(), s_tok.float())
+    oq, ok = apply_rope(q.cuda(), k.cuda(), table_c.unsqueeze(0).cuda(), table_s.unsqueeze(0).cuda(),
+                        positions=pos.cuda())
+    _close(oq, rq.to(dtype), dtype)
+    _close(ok, rk.to(dtype), dtype)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("base", [10000.0, 500000.0])
+def test_rope_baseline_config(base):
+    """BASELINE configs[1] at full size.  The oracle checks the first 256
+    tokens of every batch; every token is checked by the size-independent
+    properties: backward(forward(x)) == x and per-pair norm preservation."""
+    B, S, NQ, NKV, D = 4, 4096, 32, 8, 128
+    dtype = torch.bfloat16
+    gen = torch.Generator(device="cuda").manual_seed(11)
+    q_bshd = torch.randn(B, S, NQ, D, device="cuda", generator=gen).to(dtype)
+    k_bshd = torch.randn(B, S, NKV, D, device="cuda", generator=gen).to(dtype)
+    q, k = q_bshd.transpose(1, 2), k_bshd.transpose(1, 2)
+    c, sn = cos_sin(torch.arange(S), D, base, dtype)
+    c, sn = c.unsqueeze(0).cuda(), sn.unsqueeze(0).cuda()
+    oq, ok = apply_rope(q, k, c, sn)
+    n = 256
+    rq, rk = hf_apply_rotary_pos_emb(q[:, :, :n].float().cpu(), k[:, :, :n].float().cpu(),
+                                     c[:, :n].float().cpu(), sn[:, :n].float().cpu())
+    _close(oq[:, :, :n], rq.to(dtype), dtype)
+    _close(ok[:, :, :n], rk.to(dtype), dtype)
+    # inverse rotation: the backward kernel applied to the forward output
+    bq, bk = ForgeRoPEv3Function.backward(_Ctx(c, sn), oq, ok)[:2]  # rotation by -theta
+    torch.testing.assert_close(bq.float(), q.float(), atol=3e-2, rtol=3e-2)
+    torch.testing.assert_close(bk.float(), k.float(), atol=3e-2, rtol=3e-2)
+    # norm of each (j, j + D/2) pair is preserved
+    def pair_norm(x):
+        x = x.float()
+        return x[..., : D // 2] ** 2 + x[..., D // 2:] ** 2
+    torch.testing.assert_close(pair_norm(oq), pair_norm(q), atol=5e-2, rtol=2e-2)
+
+
+class _Ctx:
+    def __init__(self, c, s):
+        self.saved_tensors = (c, s)
+        self.positions = None
+
+
+def test_rope_cos_sin_builder_matches_oracle():
+    """The package's configurable-base table builder equals the oracle's
+    (kernels/rope/tests/test_v1.py:75-83) on the CPU."""
+    for base in (10000.0, 500000.0):
+        pos = torch.arange(4096)
+        c, s = rope_cos_sin(pos, 128, base, torch.float32)
+        rc, rs = cos_sin(pos, 128, base, torch.float32)
+        assert torch.equal(c, rc) and torch.equal(s, rs)
