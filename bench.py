@@ -307,6 +307,143 @@ def bench_ce(args):
     return res
 
 
+def _gpu_params_mlp(H, I, r, alpha, gen):
+    """configs[3] initialisation on the GPU (same distributions as
+    oracle/lora_mlp.py make_params)."""
+    import torch
+
+    s = alpha / r
+    bf = torch.bfloat16
+
+    def W(o, i):
+        return (torch.randn(o, i, device="cuda", generator=gen) * 0.02).to(bf)
+
+    def A(i):
+        return ((torch.rand(r, i, device="cuda", generator=gen) * 2 - 1) / i ** 0.5).to(bf).requires_grad_(True)
+
+    def B(o):
+        return (torch.randn(o, r, device="cuda", generator=gen) * 0.01).to(bf).requires_grad_(True)
+
+    return (W(I, H), A(H), B(I), s, W(I, H), A(H), B(I), s, W(H, I), A(I), B(H), s)
+
+
+def bench_lora_mlp(args):
+    """LoRA MLP fwd+bwd, bf16, Llama-3-8B shape (M=8192, H=4096,
+    I=14336), r=16, alpha=32."""
+    import torch
+    from forge_hip import _lib as L
+    from kernels.lora_mlp.experiments.v6.lora_mlp_kernel_v6 import LoRAMLPv6
+    from kernels.lora_mlp._impl import mlp_forward
+    from oracle.lora_mlp import flops
+
+    M, H, I, r = 8192, 4096, 14336, 16
+    g = torch.Generator(device="cuda").manual_seed(3)
+    params = _gpu_params_mlp(H, I, r, 32, g)
+    X = torch.randn(1, M, H, device="cuda", generator=g).to(torch.bfloat16).requires_grad_(True)
+    dY = torch.randn(1, M, H, device="cuda", generator=g).to(torch.bfloat16)
+
+    def step(i):
+        out = LoRAMLPv6.apply(X, *params)
+        out.backward(dY)
+
+    ms, wall = time_steps(step, args.steps, args.warmup)
+    fl = flops(M, H, I, r)
+    tf = fl / (ms * 1e-3) / 1e12
+    # dominant kernel: the fused gate/up GEMM + SwiGLU epilogue
+    X2 = X.detach().reshape(M, H)
+    Wg, Ag, Bg, sg, Wu, Au, Bu, su = [t.detach() if isinstance(t, torch.Tensor) else t for t in params[:8]]
+    xa = torch.randn(M, 2 * r, device="cuda").to(torch.bfloat16)
+    e = torch.empty(M, I, device="cuda", dtype=torch.bfloat16)
+    gg, hh = torch.empty_like(e), torch.empty_like(e)
+    st = L.stream_of(X2)
+    launch_ms = time_launches(lambda i: L.forge_lora_mlp_gate_up(
+        M, H, I, r, X2.data_ptr(), H, Wg.data_ptr(), Wu.data_ptr(), H, xa.data_ptr(), 2 * r, Bg.data_ptr(),
+        Bu.data_ptr(), r, e.data_ptr(), gg.data_ptr(), hh.data_ptr(), I, st), max(args.steps, 10))
+    gu_flops = 4 * M * H * I + 4 * M * r * I
+    res = {
+        "config": {"workload": "lora_mlp_fwd_bwd", "dtype": "bf16", "M": M, "H": H, "I": I, "rank": r, "alpha": 32,
+                   "api": "LoRAMLPv6"},
+        "value": round(tf, 1), "unit": "TFLOP/s", "ms_per_step": round(ms, 4), "wall_ms_per_step": round(wall, 4),
+        "frac_of_mfma_peak": round(tf / BF16_PEAK_TFLOPS, 4), "algorithmic_flops_per_step": fl,
+        "launches_ms": {"forge_lora_mlp_gate_up": round(launch_ms, 4)},
+        "roofline": _roof("mfma", gu_flops / (launch_ms * 1e-3) / 1e12, BF16_PEAK_TFLOPS, "TFLOP/s",
+                          _traffic("lora_mlp_gate_up")),
+        "dtype": "bf16",
+    }
+    if not args.no_cpu_baseline:
+        from oracle.lora_mlp import fwd_bwd
+
+        ms_ = 64
+        cpu_params = [t.detach().cpu() if isinstance(t, torch.Tensor) else t for t in params]
+        Xc, dYc = X.detach()[:, :ms_].cpu(), dY[:, :ms_].cpu()
+        t = cpu_time(lambda: fwd_bwd(Xc, dYc, cpu_params, compute_dtype=torch.bfloat16), 3)
+        res["cpu_baseline"] = _cpu(flops(ms_, H, I, r) / t / 1e12, "TFLOP/s",
+                                   f"{ms_} of {M} tokens, reference LoRAMLP formulas in bf16, fwd+bwd, median of 3")
+    return res
+
+
+def bench_lora_qkv(args):
+    """fused LoRA QKV (GQA 32/8, head_dim 128, hidden 4096, r=64,
+    alpha=128) then RoPE (base 500000), 8 varlen sequences U[512, 4096]."""
+    import torch
+    from kernels.lora_qkv.experiments.v4.lora_qkv_kernel_v4 import lora_qkv_rope
+    from kernels.rope import rope_cos_sin
+    from oracle.lora_qkv import flops_per_token, positions_for, varlen_lengths
+
+    K, Hq, Hkv, D, r = 4096, 4096, 1024, 128, 64
+    lens = varlen_lengths(8, 512, 4096, seed=4)
+    pos = positions_for(lens).cuda()
+    T = int(pos.numel())
+    g = torch.Generator(device="cuda").manual_seed(4)
+    bf = torch.bfloat16
+
+    def W(o):
+        return (torch.randn(o, K, device="cuda", generator=g) * 0.02).to(bf)
+
+    def A():
+        return ((torch.rand(r, K, device="cuda", generator=g) * 2 - 1) / K ** 0.5).to(bf).requires_grad_(True)
+
+    def B(o):
+        return (torch.randn(o, r, device="cuda", generator=g) * 0.01).to(bf).requires_grad_(True)
+
+    s = 128 / r
+    Wq, Wk, Wv = W(Hq), W(Hkv), W(Hkv)
+    Aq, Bq, Ak, Bk, Av, Bv = A(), B(Hq), A(), B(Hkv), A(), B(Hkv)
+    X = torch.randn(T, K, device="cuda", generator=g).to(bf).requires_grad_(True)
+    dQ = torch.randn(T, Hq, device="cuda", generator=g).to(bf)
+    dK = torch.randn(T, Hkv, device="cuda", generator=g).to(bf)
+    dV = torch.randn(T, Hkv, device="cuda", generator=g).to(bf)
+    c, sn = rope_cos_sin(torch.arange(max(lens), device="cuda"), D, 500000.0, bf)
+
+    def step(i):
+        Q, K_, V = lora_qkv_rope(X, Wq, Aq, Bq, s, Wk, Ak, Bk, s, Wv, Av, Bv, s, c, sn, pos, D)
+        torch.autograd.backward((Q, K_, V), (dQ, dK, dV))
+
+    ms, wall = time_steps(step, args.steps, args.warmup)
+    fl = T * flops_per_token(K, Hq, Hkv, r)
+    tf = fl / (ms * 1e-3) / 1e12
+    res = {
+        "config": {"workload": "lora_qkv_rope_fwd_bwd", "dtype": "bf16", "tokens": T, "seq_lens": lens,
+                   "hidden": K, "q_heads": 32, "kv_heads": 8, "head_dim": D, "rank": r, "alpha": 128,
+                   "rope_base": 500000},
+        "value": round(tf, 1), "unit": "TFLOP/s", "ms_per_step": round(ms, 4), "wall_ms_per_step": round(wall, 4),
+        "frac_of_mfma_peak": round(tf / BF16_PEAK_TFLOPS, 4), "algorithmic_flops_per_step": fl,
+        "dtype": "bf16",
+    }
+    if not args.no_cpu_baseline:
+        from oracle.lora_qkv import qkv_rope_fwd_bwd
+
+        n = 64
+        cpu_p = [t.detach().cpu() if isinstance(t, torch.Tensor) else t
+                 for t in (Wq, Wk, Wv, Aq, Bq, s, Ak, Bk, s, Av, Bv, s)]
+        pc = pos[:n].cpu()
+        args_ = (X.detach()[:n].cpu(), dQ[:n].cpu(), dK[:n].cpu(), dV[:n].cpu(), cpu_p, c.cpu()[pc], sn.cpu()[pc], D)
+        t = cpu_time(lambda: qkv_rope_fwd_bwd(*args_, compute_dtype=torch.bfloat16), 3)
+        res["cpu_baseline"] = _cpu(n * flops_per_token(K, Hq, Hkv, r) / t / 1e12, "TFLOP/s",
+                                   f"{n} of {T} tokens, reference LoRAQKV + HF RoPE in bf16, fwd+bwd, median of 3")
+    return res
+
+
 def _roof(bound, achieved, peak, unit, traffic):
     return {"bound": bound, "achieved": round(achieved, 2), "peak": peak, "unit": unit,
             "frac": round(achieved / peak, 4), "traffic": traffic}
@@ -319,7 +456,8 @@ def _cpu(value, unit, sample):
             "sample": sample, "cpu_count": os.cpu_count()}
 
 
-BENCHES = {"swiglu": bench_swiglu, "rope": bench_rope, "ce": bench_ce}
+BENCHES = {"swiglu": bench_swiglu, "rope": bench_rope, "ce": bench_ce, "lora_mlp": bench_lora_mlp,
+           "lora_qkv": bench_lora_qkv}
 
 
 def main():

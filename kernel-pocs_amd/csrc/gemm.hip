@@ -59,15 +59,16 @@ static int check_segs(const GemmArgs& a, int al, int bl) {
     return forge_set_error(FORGE_ERR_INVALID, "gemm: 1..%d segments", MAX_SEGS);
   for (int i = 0; i < a.n_segs; ++i) {
     const Seg& s = a.segs[i];
-    if (s.k < 0 || s.k % 8 != 0)
+    // K-contiguous operands (A ROW, B COL) are fetched in 8-element chunks
+    // along K; transposed operands check every k row individually.
+    const bool kchunks = (al == ROW) || (bl == COL);
+    if (s.k < 0 || (kchunks && s.k % 8 != 0))
       return forge_set_error(FORGE_ERR_INVALID, "gemm: segment %d K=%lld must be a multiple of 8", i,
                              (long long)s.k);
     if (!aligned16(s.a) || (s.b && !aligned16(s.b)) || (s.b2 && !aligned16(s.b2)))
       return forge_set_error(FORGE_ERR_INVALID, "gemm: segment %d operand not 16-byte aligned", i);
     if (s.lda % 8 != 0 || s.ldb % 8 != 0)
       return forge_set_error(FORGE_ERR_INVALID, "gemm: segment %d leading dims must be multiples of 8", i);
-    (void)al;
-    (void)bl;
   }
   return FORGE_OK;
 }

@@ -136,5 +136,7 @@ extern "C" int forge_lora_a(int64_t M, int64_t K, int64_t r, int n_proj, const v
   a.ep.alpha = 1.f;
   a.ep.alpha_group = r;
   for (int p = 0; p < 4; ++p) a.ep.alphas[p] = p < n_proj ? scales[p] : 1.f;
-  return run(-1, ROW, COL, EPI_STORE_BF16, a, (hipStream_t)stream);
+  // 256 x 32 tiles: every tile covers at most two projections' columns and
+  // no MFMA work is spent on columns outside [0, n_proj * r)
+  return run(1 /* CFG_SKINNY_N */, ROW, COL, EPI_STORE_BF16, a, (hipStream_t)stream);
 }

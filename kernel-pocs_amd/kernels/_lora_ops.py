@@ -1,0 +1,95 @@
+"""Host-side helpers shared by the LoRA-MLP and LoRA-QKV modules.
+
+Thin wrappers over the MFMA GEMM entry points of libforge_hip.so
+(csrc/gemm.hip, csrc/lora.hip).  Operands are bf16 with unit stride in the
+last dimension and 16-byte aligned rows; every wrapper checks that and calls
+the library on torch's current stream.
+"""
+from __future__ import annotations
+
+import ctypes
+from typing import Optional, Sequence, Tuple
+
+import torch
+
+from forge_hip import _lib as L
+
+ROW, COL = L.LAYOUT_ROW, L.LAYOUT_COL
+
+
+def as_operand(t: torch.Tensor) -> torch.Tensor:
+    """A 2-D bf16 operand the kernels can read: unit last stride, row pitch a
+    multiple of 8 elements, 16-byte aligned base.  Copies only if needed."""
+    if t.dtype != torch.bfloat16:
+        raise TypeError(f"LoRA kernels compute in bf16, got {t.dtype}")
+    if t.dim() != 2:
+        t = t.reshape(-1, t.shape[-1])
+    ok = t.stride(-1) == 1 and (t.shape[0] <= 1 or t.stride(0) % 8 == 0) and t.data_ptr() % 16 == 0
+    return t if ok else t.contiguous()
+
+
+def ld(t: torch.Tensor) -> int:
+    return t.stride(0) if t.dim() == 2 and t.shape[0] > 1 else t.shape[-1]
+
+
+def gemm(M: int, N: int, segs: Sequence[Tuple[torch.Tensor, int, torch.Tensor, int, int]], a_layout: int,
+         b_layout: int, out: Optional[torch.Tensor] = None, alpha: float = 1.0, beta: float = 0.0,
+         out_dtype=torch.bfloat16, atomic: bool = False, split_k: int = 1, device=None) -> torch.Tensor:
+    """C[M, N] = alpha * sum_s A_s @ B_s (+ beta C).  segs: (A, lda, B, ldb, K).
+    atomic=True accumulates into a zero-initialised fp32 C over split_k
+    K partitions."""
+    dev = device if device is not None else segs[0][0].device
+    if out is None:
+        if atomic:
+            out = torch.zeros(M, N, dtype=torch.float32, device=dev)
+        else:
+            out = torch.empty(M, N, dtype=out_dtype, device=dev)
+    arr = (L.GemmSegment * len(segs))()
+    for i, (a, lda, b, ldb, k) in enumerate(segs):
+        arr[i] = L.GemmSegment(a.data_ptr(), int(lda), b.data_ptr(), int(ldb), int(k))
+    c_dtype = L.DTYPE_F32 if out.dtype == torch.float32 else L.DTYPE_BF16
+    L.check(
+        L.forge_gemm(M, N, arr, len(segs), a_layout, b_layout, out.data_ptr(), ld(out), c_dtype, float(alpha),
+                     float(beta), L.EPI_ATOMIC_F32 if atomic else L.EPI_STORE, int(split_k), L.stream_of(out)),
+        "forge_gemm",
+    )
+    return out
+
+
+def lora_a(x: torch.Tensor, mats: Sequence[torch.Tensor], scales: Sequence[float],
+           out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """[s_p * x @ A_p^T for p] concatenated along columns -> [M, n*r] bf16."""
+    M, K = x.shape
+    r = mats[0].shape[0]
+    n = len(mats)
+    if out is None:
+        out = torch.empty(M, n * r, dtype=torch.bfloat16, device=x.device)
+    mats = [as_operand(a) for a in mats]
+    ptrs = (ctypes.c_void_p * n)(*[a.data_ptr() for a in mats])
+    sc = (ctypes.c_float * n)(*[float(s) for s in scales])
+    L.check(
+        L.forge_lora_a(M, K, r, n, x.data_ptr(), ld(x), ptrs, ld(mats[0]), sc, out.data_ptr(), ld(out),
+                       L.stream_of(x)),
+        "forge_lora_a",
+    )
+    return out
+
+
+def split_k_for(k: int, tiles: int, target_wgs: int = 512, min_tiles_per_split: int = 4) -> int:
+    """Split count for a reduction over k (= tokens) with `tiles` output tiles:
+    aim for ~target_wgs workgroups, keep >= min_tiles_per_split K-tiles each."""
+    k_tiles = max(1, (k + 63) // 64)
+    split = max(1, min(target_wgs // max(1, tiles), k_tiles // min_tiles_per_split))
+    return split
+
+
+def grad_at_b(a_t: torch.Tensor, lda: int, b: torch.Tensor, ldb: int, rows: int, cols: int, k: int,
+              alpha: float = 1.0) -> torch.Tensor:
+    """alpha * A^T @ B where A is stored [k][rows] and B [k][cols] (both
+    row-major over the reduction dim k): the LoRA weight-gradient shape
+    (rank x features or features x rank, reduced over tokens).  fp32
+    split-K accumulation, returned as fp32 [rows, cols]."""
+    tiles_m = max(1, (rows + 255) // 256) if rows > 64 else 1
+    tiles_n = max(1, (cols + 255) // 256) if cols > 64 else 1
+    split = split_k_for(k, tiles_m * tiles_n)
+    return gemm(rows, cols, [(a_t, lda, b, ldb, k)], COL, ROW, alpha=alpha, atomic=True, split_k=split)

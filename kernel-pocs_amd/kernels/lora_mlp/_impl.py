@@ -1,0 +1,226 @@
+"""LoRA-MLP (LLaMA-style SwiGLU with LoRA on gate/up/down) on MI355X.
+
+Forward  (reference v6 `_v6_forward_impl`,
+kernels/lora_mlp/experiments/v6/lora_mlp_kernel_v6.py:335-451):
+  1. xa   = [sg X Ag^T | su X Au^T]                  forge_lora_a       [M, 2r]
+  2. e, g, h = gate/up GEMM + LoRA-B + SwiGLU        forge_lora_mlp_gate_up
+     (one MFMA GEMM: each tile computes gate and up columns together, h is
+      formed in registers, e and g (LoRA included) are saved for backward)
+  3. xd   = sd h Ad^T                                forge_lora_a       [M, r]
+  4. out  = h Wd^T + xd Bd^T                         forge_gemm (2 K segments)
+
+Backward (reference `LoRAMLPv6.backward`, :592-672, Unsloth-style in place;
+math of kernels/lora_mlp/reference/lora_mlp_pytorch.py:145-225):
+  1. td   = sd dY Bd                                 forge_gemm         [M, r]
+  2. DW = dY Wd + td Ad, fused in-place SwiGLU backward:
+     (DW, e, g) -> (h, df, de)                       forge_lora_mlp_down_bwd
+  3. dAd = td^T h,  dBd = sd dY^T (h Ad^T)           split-K forge_gemm
+  4. vu = su df Bu, vg = sg de Bg                    forge_gemm         [M, r]
+     dAu = vu^T X, dAg = vg^T X, dBu = su df^T (X Au^T), dBg = sg de^T (X Ag^T)
+  5. dX = df Wu + de Wg + vu Au + vg Ag              forge_gemm (4 K segments)
+The saved e/g buffers are overwritten by df/de in step 2 (the reference's
+in-place contract: backward is not re-entrant).
+"""
+from __future__ import annotations
+
+from typing import Optional, Tuple
+
+import torch
+import torch.nn.functional as F
+
+from forge_hip import _lib as L
+from kernels._lora_ops import COL, ROW, as_operand, gemm, grad_at_b, ld, lora_a
+
+
+def _w(t):
+    return None if t is None else as_operand(t)
+
+
+def mlp_forward(X2, W_gate, A_gate, B_gate, s_gate, W_up, A_up, B_up, s_up,
+                W_down, A_down, B_down, s_down, save_eg: bool = True):
+    """Returns (out [M, H], e [M, I], g [M, I]) (e, g None unless save_eg)."""
+    L.require_gpu(X2, W_gate, W_up, W_down)
+    X2 = as_operand(X2)
+    Wg, Wu, Wd = _w(W_gate), _w(W_up), _w(W_down)
+    M, H = X2.shape
+    I = Wg.shape[0]
+    has_lora = A_gate is not None and B_gate is not None
+    r = A_gate.shape[0] if has_lora else 0
+    dev = X2.device
+    e = torch.empty(M, I, dtype=torch.bfloat16, device=dev)
+    g = torch.empty(M, I, dtype=torch.bfloat16, device=dev)
+    h = torch.empty(M, I, dtype=torch.bfloat16, device=dev)
+    xa = None
+    Bg = Bu = None
+    if has_lora:
+        xa = lora_a(X2, [A_gate, A_up], [s_gate, s_up])
+        Bg, Bu = _w(B_gate), _w(B_up)
+    st = L.stream_of(X2)
+    L.check(
+        L.forge_lora_mlp_gate_up(
+            M, H, I, r, X2.data_ptr(), ld(X2), Wg.data_ptr(), Wu.data_ptr(), ld(Wg),
+            L.ptr(xa), 2 * r, L.ptr(Bg), L.ptr(Bu), r, e.data_ptr(), g.data_ptr(), h.data_ptr(), I, st),
+        "forge_lora_mlp_gate_up",
+    )
+    segs = [(h, I, Wd, ld(Wd), I)]
+    if has_lora and A_down is not None and B_down is not None:
+        xd = lora_a(h, [A_down], [s_down])
+        Bd = _w(B_down)
+        segs.append((xd, r, Bd, ld(Bd), r))
+    out = gemm(M, Wd.shape[0], segs, ROW, COL)
+    if not save_eg:
+        e = g = None
+    return out, e, g
+
+
+def mlp_backward(dY2, X2, e, g, W_gate, A_gate, B_gate, s_gate, W_up, A_up, B_up, s_up,
+                 W_down, A_down, B_down, s_down):
+    """Returns (dX [M, H], dAg, dBg, dAu, dBu, dAd, dBd).  e and g are
+    overwritten with df and de."""
+    dY2 = as_operand(dY2)
+    X2 = as_operand(X2)
+    Wg, Wu, Wd = _w(W_gate), _w(W_up), _w(W_down)
+    M, H = X2.shape
+    I = Wg.shape[0]
+    r = A_gate.shape[0]
+    dev = X2.device
+    Ag, Bg, Au, Bu, Ad, Bd = (_w(t) for t in (A_gate, B_gate, A_up, B_up, A_down, B_down))
+
+    # 1-2: DW = dY Wd + sd (dY Bd) Ad with the SwiGLU backward fused in place
+    td = gemm(M, r, [(dY2, ld(dY2), Bd, ld(Bd), H)], ROW, ROW, alpha=s_down)
+    h = torch.empty(M, I, dtype=torch.bfloat16, device=dev)
+    L.check(
+        L.forge_lora_mlp_down_bwd(M, H, I, r, dY2.data_ptr(), ld(dY2), Wd.data_ptr(), ld(Wd), td.data_ptr(), r,
+                                  Ad.data_ptr(), ld(Ad), h.data_ptr(), e.data_ptr(), g.data_ptr(), I,
+                                  L.stream_of(X2)),
+        "forge_lora_mlp_down_bwd",
+    )
+    df, de = e, g
+
+    # 3: down-projection LoRA grads
+    dAd = grad_at_b(td, r, h, I, r, I, M)                        # [r, I] = (sd dY Bd)^T h
+    u = lora_a(h, [Ad], [1.0])                                    # h Ad^T [M, r]
+    dBd = grad_at_b(dY2, ld(dY2), u, r, H, r, M, alpha=s_down)   # [H, r]
+
+    # 4: up / gate LoRA grads
+    v = torch.empty(M, 2 * r, dtype=torch.bfloat16, device=dev)  # [su df Bu | sg de Bg]
+    gemm(M, r, [(df, I, Bu, ld(Bu), I)], ROW, ROW, out=v[:, :r], alpha=s_up)
+    gemm(M, r, [(de, I, Bg, ld(Bg), I)], ROW, ROW, out=v[:, r:], alpha=s_gate)
+    dA_ug = grad_at_b(v, 2 * r, X2, ld(X2), 2 * r, H, M)         # [2r, H]: rows [dAu; dAg]
+    xa_ug = lora_a(X2, [Au, Ag], [1.0, 1.0])                     # [X Au^T | X Ag^T]
+    dBu = grad_at_b(df, I, xa_ug[:, :r], 2 * r, I, r, M, alpha=s_up)
+    dBg = grad_at_b(de, I, xa_ug[:, r:], 2 * r, I, r, M, alpha=s_gate)
+
+    # 5: dX
+    dX = gemm(M, H, [(df, I, Wu, ld(Wu), I), (de, I, Wg, ld(Wg), I),
+                     (v[:, :r], 2 * r, Au, ld(Au), r), (v[:, r:], 2 * r, Ag, ld(Ag), r)], ROW, ROW)
+    dt = A_gate.dtype
+    return (dX, dA_ug[r:].to(dt), dBg.to(dt), dA_ug[:r].to(dt), dBu.to(dt), dAd.to(dt), dBd.to(dt))
+
+
+def torch_forward(X, W_gate, A_gate, B_gate, s_gate, W_up, A_up, B_up, s_up, W_down, A_down, B_down, s_down):
+    """Plain-PyTorch forward the reference uses for float64 (gradcheck)
+    inputs (kernels/lora_mlp/experiments/v6/lora_mlp_kernel_v6.py:552-557)."""
+    e = X @ W_gate.t() + s_gate * ((X @ A_gate.t()) @ B_gate.t())
+    g = X @ W_up.t() + s_up * ((X @ A_up.t()) @ B_up.t())
+    h = F.silu(e) * g
+    out = h @ W_down.t() + s_down * ((h @ A_down.t()) @ B_down.t())
+    return out, e, g
+
+
+def torch_backward(dY, X, e, g, W_gate, A_gate, B_gate, s_gate, W_up, A_up, B_up, s_up,
+                   W_down, A_down, B_down, s_down):
+    """Plain-PyTorch backward the reference uses for float64 inputs
+    (kernels/lora_mlp/experiments/v6/lora_mlp_kernel_v6.py:608-628)."""
+    sig_e = torch.sigmoid(e.float()).to(e.dtype)
+    silu_e = e * sig_e
+    h = silu_e * g
+    DW = dY @ W_down + s_down * ((dY @ B_down) @ A_down)
+    d_downA = s_down * ((dY @ B_down).t() @ h)
+    d_downB = s_down * (dY.t() @ h @ A_down.t())
+    df = DW * silu_e
+    dsilu = sig_e * (1.0 + e * (1.0 - sig_e))
+    de = DW * g * dsilu
+    d_upA = s_up * ((df @ B_up).t() @ X)
+    d_upB = s_up * (df.t() @ X @ A_up.t())
+    d_gateA = s_gate * ((de @ B_gate).t() @ X)
+    d_gateB = s_gate * (de.t() @ X @ A_gate.t())
+    dX = df @ W_up + s_up * ((df @ B_up) @ A_up) + de @ W_gate + s_gate * ((de @ B_gate) @ A_gate)
+    return dX, d_gateA, d_gateB, d_upA, d_upB, d_downA, d_downB
+
+
+def run_forward(X, params, save_eg=True):
+    """Dispatch on dtype: float64 -> the reference's PyTorch path, bf16 ->
+    the HIP kernels.  Returns (out with X's leading shape, e, g)."""
+    if X.dtype == torch.float64:
+        Xf = X.reshape(-1, X.shape[-1])
+        out, e, g = torch_forward(Xf, *params)
+    else:
+        if X.dtype != torch.bfloat16:
+            raise TypeError(f"LoRA-MLP kernels run in bf16 (or float64 via PyTorch), got {X.dtype}")
+        out, e, g = mlp_forward(X.reshape(-1, X.shape[-1]), *params, save_eg=save_eg)
+    if X.dim() == 3:
+        out = out.reshape(X.shape[0], X.shape[1], -1)
+        if e is not None:
+            e = e.reshape(X.shape[0], X.shape[1], -1)
+            g = g.reshape(X.shape[0], X.shape[1], -1)
+    return out, e, g
+
+
+def run_backward(dY, X, e, g, params):
+    dY2 = dY.reshape(-1, dY.shape[-1])
+    X2 = X.reshape(-1, X.shape[-1])
+    e2 = e.reshape(-1, e.shape[-1])
+    g2 = g.reshape(-1, g.shape[-1])
+    if X.dtype == torch.float64:
+        return torch_backward(dY2, X2, e2, g2, *params)
+    return mlp_backward(dY2, X2, e2, g2, *params)
+
+
+def stack_lora_a(A_gate: torch.Tensor, A_up: torch.Tensor) -> torch.Tensor:
+    """cat([A_gate, A_up]) [2r, H] (v6 :262-276; kept for API parity — the
+    HIP path reads the two A matrices directly)."""
+    return torch.cat([A_gate, A_up], dim=0).contiguous()
+
+
+def stack_gate_lora_a(W_gate, A_gate, A_up):
+    """cat([W_gate, A_gate, A_up]) [I+2r, H] (v6 :279-294; API parity)."""
+    return torch.cat([W_gate, A_gate, A_up], dim=0).contiguous()
+
+
+def stack_down_lora_a(W_down, A_down):
+    """cat([W_down, A_down]) [H+r, I] (v6 :297-309; API parity)."""
+    return torch.cat([W_down, A_down], dim=0).contiguous()
+
+
+def fused_lora_a_stacked(X: torch.Tensor, A_stack: torch.Tensor, r: int) -> Tuple[torch.Tensor, torch.Tensor]:
+    """X @ A_stack^T -> (xa_gate, xa_up) views of one [M, 2r] buffer (v6 :312-330)."""
+    X2 = as_operand(X.reshape(-1, X.shape[-1]))
+    out = lora_a(X2, [A_stack[:r], A_stack[r:2 * r]], [1.0, 1.0])
+    return out[:, :r], out[:, r:2 * r]
+
+
+def fused_lora_swiglu(e_base, g_base, xa_gate, xa_up, B_gate, B_up, s_gate=1.0, s_up=1.0, save_eg=False,
+                      inplace=False):
+    """h = silu(e_base + sg xa_g Bg^T) * (g_base + su xa_u Bu^T)
+    (v3 `fused_lora_swiglu` :141-200; v6 in-place variant :81-151 with
+    inplace=True writes e_full/g_full over e_base/g_base).
+    The rank-r update is one K-segment GEMM with beta=1 over the base tensor;
+    the SwiGLU is the HIP SwiGLU kernel."""
+    from kernels.swiglu import swiglu_forward
+
+    M, N = e_base.shape
+    if xa_gate is not None:
+        e_full = e_base if inplace else e_base.clone()
+        g_full = g_base if inplace else g_base.clone()
+        r = xa_gate.shape[1]
+        xg, xu = as_operand(xa_gate), as_operand(xa_up)
+        Bg, Bu = _w(B_gate), _w(B_up)
+        gemm(M, N, [(xg, ld(xg), Bg, ld(Bg), r)], ROW, COL, out=e_full, alpha=s_gate, beta=1.0)
+        gemm(M, N, [(xu, ld(xu), Bu, ld(Bu), r)], ROW, COL, out=g_full, alpha=s_up, beta=1.0)
+    else:
+        e_full, g_full = e_base, g_base
+    h = swiglu_forward(e_full, g_full)[0]
+    if save_eg:
+        return h, e_full, g_full
+    return h, None, None

@@ -1,0 +1,153 @@
+"""LoRA-QKV (GQA-asymmetric widths) on MI355X, optionally fused with RoPE.
+
+Forward (reference `lora_qkv_v2_3`,
+kernels/lora_qkv/experiments/v2/lora_qkv_kernel_v2_3.py:177-267):
+  1. xa = [sq X Aq^T | sk X Ak^T | sv X Av^T]            forge_lora_a [M, 3r]
+  2. out = [Q | K | V] = X [Wq; Wk; Wv]^T + LoRA-B terms, one MFMA GEMM
+     (per-projection K segments, no packed weight copy); with RoPE the
+     epilogue rotates the Q and K heads in registers  forge_lora_qkv_rope
+  Q, K, V are returned as column views of `out` (row pitch Hq + 2 Hkv), the
+  reference's "strided views of one packed buffer" contract.
+Backward (reference `LoRAQKVv4Function.backward`,
+kernels/lora_qkv/experiments/v4/lora_qkv_kernel_v4.py:221-336):
+  t  = [sq dQ Bq | sk dK Bk | sv dV Bv]                   forge_gemm x3 [M, 3r]
+  dA = t^T X (rows split per projection)                 split-K forge_gemm
+  dB_p = s_p dY_p^T (X A_p^T)                            split-K forge_gemm
+  dX = dQ Wq + dK Wk + dV Wv + sum_p t_p A_p             forge_gemm (6 K segments,
+                                                          no cat of dQ/dK/dV)
+With fused RoPE the incoming dQ/dK are first rotated back by -theta
+(forge_rope backward) — the chain rule through the rotation.
+"""
+from __future__ import annotations
+
+from typing import Optional
+
+import torch
+
+from forge_hip import _lib as L
+from kernels._lora_ops import COL, ROW, as_operand, gemm, grad_at_b, ld, lora_a
+
+
+def _w(t):
+    return None if t is None else as_operand(t)
+
+
+def qkv_forward(X2, W_q, W_k, W_v, A_q, B_q, s_q, A_k, B_k, s_k, A_v, B_v, s_v,
+                rope: Optional[dict] = None):
+    """Returns out [M, Hq + 2 Hkv] bf16.  rope = {cos, sin, positions, head_dim}
+    (bf16 tables [P, D]; int64 positions [M]) applies RoPE to Q and K."""
+    L.require_gpu(X2, W_q, W_k, W_v)
+    X2 = as_operand(X2)
+    Wq, Wk, Wv = _w(W_q), _w(W_k), _w(W_v)
+    M, K = X2.shape
+    Hq, Hkv = Wq.shape[0], Wk.shape[0]
+    has_lora = A_q is not None and B_q is not None
+    r = A_q.shape[0] if has_lora else 0
+    out = torch.empty(M, Hq + 2 * Hkv, dtype=torch.bfloat16, device=X2.device)
+    xa = None
+    Bq = Bk = Bv = None
+    if has_lora:
+        xa = lora_a(X2, [A_q, A_k, A_v], [s_q, s_k, s_v])
+        Bq, Bk, Bv = _w(B_q), _w(B_k), _w(B_v)
+    if rope is not None:
+        cos, sin = rope["cos"], rope["sin"]
+        pos = rope.get("positions")
+        hd = rope["head_dim"]
+        cos_p, sin_p, cs_ld = cos.data_ptr(), sin.data_ptr(), cos.stride(0)
+        pos_p = None if pos is None else pos.data_ptr()
+        apply = 1
+    else:
+        cos_p = sin_p = pos_p = None
+        cs_ld, hd, apply = 0, 128, 0
+    L.check(
+        L.forge_lora_qkv_rope(
+            M, K, Hq, Hkv, r, X2.data_ptr(), ld(X2), Wq.data_ptr(), Wk.data_ptr(), Wv.data_ptr(), ld(Wq),
+            L.ptr(xa), 3 * r, L.ptr(Bq), L.ptr(Bk), L.ptr(Bv), r, out.data_ptr(), ld(out),
+            cos_p, sin_p, cs_ld, pos_p, hd, apply, L.stream_of(X2)),
+        "forge_lora_qkv_rope",
+    )
+    return out
+
+
+def qkv_backward(dQ, dK, dV, X2, W_q, W_k, W_v, A_q, B_q, s_q, A_k, B_k, s_k, A_v, B_v, s_v):
+    """Returns (dX, dA_q, dB_q, dA_k, dB_k, dA_v, dB_v)."""
+    X2 = as_operand(X2)
+    dQ, dK, dV = as_operand(dQ), as_operand(dK), as_operand(dV)
+    Wq, Wk, Wv = _w(W_q), _w(W_k), _w(W_v)
+    M, K = X2.shape
+    Hq, Hkv = Wq.shape[0], Wk.shape[0]
+    r = A_q.shape[0]
+    dev = X2.device
+    Aq, Bq, Ak, Bk, Av, Bv = (_w(t) for t in (A_q, B_q, A_k, B_k, A_v, B_v))
+    t = torch.empty(M, 3 * r, dtype=torch.bfloat16, device=dev)
+    gemm(M, r, [(dQ, ld(dQ), Bq, ld(Bq), Hq)], ROW, ROW, out=t[:, :r], alpha=s_q)
+    gemm(M, r, [(dK, ld(dK), Bk, ld(Bk), Hkv)], ROW, ROW, out=t[:, r:2 * r], alpha=s_k)
+    gemm(M, r, [(dV, ld(dV), Bv, ld(Bv), Hkv)], ROW, ROW, out=t[:, 2 * r:], alpha=s_v)
+    dA = grad_at_b(t, 3 * r, X2, ld(X2), 3 * r, K, M)  # [3r, K] (scales included via t)
+    xa = lora_a(X2, [Aq, Ak, Av], [1.0, 1.0, 1.0])     # unscaled X A_p^T
+    dBq = grad_at_b(dQ, ld(dQ), xa[:, :r], 3 * r, Hq, r, M, alpha=s_q)
+    dBk = grad_at_b(dK, ld(dK), xa[:, r:2 * r], 3 * r, Hkv, r, M, alpha=s_k)
+    dBv = grad_at_b(dV, ld(dV), xa[:, 2 * r:], 3 * r, Hkv, r, M, alpha=s_v)
+    dX = gemm(M, K, [(dQ, ld(dQ), Wq, ld(Wq), Hq), (dK, ld(dK), Wk, ld(Wk), Hkv), (dV, ld(dV), Wv, ld(Wv), Hkv),
+                     (t[:, :r], 3 * r, Aq, ld(Aq), r), (t[:, r:2 * r], 3 * r, Ak, ld(Ak), r),
+                     (t[:, 2 * r:], 3 * r, Av, ld(Av), r)], ROW, ROW)
+    dt = A_q.dtype
+    return (dX, dA[:r].to(dt), dBq.to(dt), dA[r:2 * r].to(dt), dBk.to(dt), dA[2 * r:].to(dt), dBv.to(dt))
+
+
+def torch_qkv_forward(X, W_q, W_k, W_v, A_q, B_q, s_q, A_k, B_k, s_k, A_v, B_v, s_v):
+    """The reference's plain-PyTorch forward for float64 / no-LoRA inputs
+    (kernels/lora_qkv/reference/lora_qkv_pytorch.py:34-121)."""
+    def proj(W, A, B, s):
+        out = X @ W.t()
+        if A is not None and B is not None:
+            out = out + s * ((X @ A.t()) @ B.t())
+        return out
+    return proj(W_q, A_q, B_q, s_q), proj(W_k, A_k, B_k, s_k), proj(W_v, A_v, B_v, s_v)
+
+
+def torch_qkv_backward(dQ, dK, dV, X, W_q, W_k, W_v, A_q, B_q, s_q, A_k, B_k, s_k, A_v, B_v, s_v):
+    """The reference's float64 backward (lora_qkv_pytorch.py:170-214)."""
+    dX = dQ @ W_q + dK @ W_k + dV @ W_v
+    grads = []
+    for dY, A, B, s in ((dQ, A_q, B_q, s_q), (dK, A_k, B_k, s_k), (dV, A_v, B_v, s_v)):
+        dYB = dY @ B
+        dX = dX + s * (dYB @ A)
+        grads += [s * (dYB.t() @ X), s * (dY.t() @ (X @ A.t()))]
+    return (dX, *grads)
+
+
+def pack_weights_all(W_q, A_q, W_k, A_k, W_v, A_v):
+    """[W_q; A_q; W_k; A_k; W_v; A_v] (v2_3 :47-76; API parity — the HIP
+    forward reads the six matrices directly)."""
+    parts = [W_q]
+    if A_q is not None:
+        parts.append(A_q)
+    parts.append(W_k)
+    if A_k is not None:
+        parts.append(A_k)
+    parts.append(W_v)
+    if A_v is not None:
+        parts.append(A_v)
+    return torch.cat(parts, dim=0).contiguous()
+
+
+def pack_weights_backward(W_q, W_k, W_v):
+    """[W_q; W_k; W_v] (v4 :55-63)."""
+    return torch.cat([W_q, W_k, W_v], dim=0).contiguous()
+
+
+def pack_lora_a(A_q, A_k, A_v):
+    """[A_q; A_k; A_v] (v4 :66-72)."""
+    return torch.cat([A_q, A_k, A_v], dim=0).contiguous()
+
+
+def split_views(out, Hq, Hkv, orig_shape):
+    Q = out[:, :Hq]
+    K_ = out[:, Hq:Hq + Hkv]
+    V = out[:, Hq + Hkv:Hq + 2 * Hkv]
+    if len(orig_shape) == 3:
+        Q = Q.view(orig_shape[0], orig_shape[1], Hq)
+        K_ = K_.view(orig_shape[0], orig_shape[1], Hkv)
+        V = V.view(orig_shape[0], orig_shape[1], Hkv)
+    return Q, K_, V

@@ -1,0 +1,152 @@
+"""LoRA-QKV v4 API on MI355X (training), plus the fused QKV + RoPE variant.
+
+Drop-in for kernels/lora_qkv/experiments/v4/lora_qkv_kernel_v4.py of
+Forge-researchlab/kernel-POCs: `LoRAQKVv4Function` (16 forward arguments,
+saves (X, A_q, B_q, A_k, B_k, A_v, B_v, W_dX_packed, A_packed),
+ctx.scalings / ctx.dims, 16-tuple backward), `lora_qkv_v4`,
+`pack_weights_backward`, `pack_lora_a`.  The packed weights are accepted and
+saved when given; they are not built when absent (the backward reads
+W_q/W_k/W_v as separate K segments, so no [Hq+2Hkv, K] copy is made).
+
+`LoRAQKVRoPEFunction` / `lora_qkv_rope` add the fusion of the caller's RoPE
+(forge/forge/patching/kernels/lora.py:250-264 for models without q/k norm):
+the Q and K heads are rotated in the GEMM epilogue with per-token positions
+(packed variable-length batches), and the backward rotates dQ/dK back before
+the v4 backward.  Outputs equal lora_qkv_v4 followed by apply_rope.
+"""
+from __future__ import annotations
+
+import torch
+
+from forge_hip import _lib as L
+from kernels.lora_qkv._impl import (  # noqa: F401
+    pack_lora_a,
+    pack_weights_backward,
+    qkv_backward,
+    qkv_forward,
+    split_views,
+    torch_qkv_backward,
+    torch_qkv_forward,
+)
+
+
+def _flat(t):
+    return t.reshape(-1, t.shape[-1])
+
+
+class LoRAQKVv4Function(torch.autograd.Function):
+    """v4 :170-336."""
+
+    @staticmethod
+    def forward(ctx, X, W_q, W_k, W_v, A_q, B_q, s_q, A_k, B_k, s_k, A_v, B_v, s_v,
+                W_all=None, W_dX_packed=None, A_packed=None):
+        use_hip = X.dtype != torch.float64
+        orig_shape = X.shape
+        X2 = _flat(X)
+        if use_hip:
+            out = qkv_forward(X2, W_q, W_k, W_v, A_q, B_q, s_q, A_k, B_k, s_k, A_v, B_v, s_v)
+            Q, K, V = split_views(out, W_q.shape[0], W_k.shape[0], orig_shape)
+        else:
+            Q, K, V = torch_qkv_forward(X2, W_q, W_k, W_v, A_q, B_q, s_q, A_k, B_k, s_k, A_v, B_v, s_v)
+            if len(orig_shape) == 3:
+                Q, K, V = (t.view(orig_shape[0], orig_shape[1], -1) for t in (Q, K, V))
+        ctx.save_for_backward(X, A_q, B_q, A_k, B_k, A_v, B_v, W_dX_packed, A_packed)
+        ctx.scalings = (s_q, s_k, s_v)
+        ctx.dims = (W_q.shape[0], W_k.shape[0], A_q.shape[0])
+        ctx.use_triton = use_hip  # name kept from the reference (:217)
+        ctx.base_weights = (W_q, W_k, W_v)
+        return Q, K, V
+
+    @staticmethod
+    def backward(ctx, dQ, dK, dV):
+        X, A_q, B_q, A_k, B_k, A_v, B_v, _, _ = ctx.saved_tensors
+        s_q, s_k, s_v = ctx.scalings
+        W_q, W_k, W_v = ctx.base_weights
+        X2 = _flat(X)
+        fn = qkv_backward if ctx.use_triton else torch_qkv_backward
+        dX, dAq, dBq, dAk, dBk, dAv, dBv = fn(_flat(dQ), _flat(dK), _flat(dV), X2, W_q, W_k, W_v,
+                                              A_q, B_q, s_q, A_k, B_k, s_k, A_v, B_v, s_v)
+        if X.dim() == 3:
+            dX = dX.reshape(X.shape)
+        return (dX, None, None, None, dAq, dBq, None, dAk, dBk, None, dAv, dBv, None, None, None, None)
+
+
+def lora_qkv_v4(X, W_q, A_q, B_q, s_q, W_k, A_k, B_k, s_k, W_v, A_v, B_v, s_v,
+                W_all=None, W_dX_packed=None, A_packed=None):
+    """v4 :343-379."""
+    return LoRAQKVv4Function.apply(X, W_q, W_k, W_v, A_q, B_q, s_q, A_k, B_k, s_k, A_v, B_v, s_v,
+                                   W_all, W_dX_packed, A_packed)
+
+
+def _rope_rows_backward(d, n_heads, head_dim, cos, sin, positions):
+    """Rotates a [M, n_heads*head_dim] gradient (any row pitch) by -theta per
+    token with forge_rope; returns a new contiguous tensor."""
+    M = d.shape[0]
+    out = torch.empty(M, n_heads * head_dim, dtype=d.dtype, device=d.device)
+    st = L.stream_of(d)
+    ldd = d.stride(0)
+    L.check(
+        L.forge_rope(L.dtype_code(d.dtype),
+                     d.data_ptr(), 0, head_dim, ldd,
+                     d.data_ptr(), 0, head_dim, ldd,
+                     out.data_ptr(), 0, head_dim, n_heads * head_dim,
+                     out.data_ptr(), 0, head_dim, n_heads * head_dim,
+                     cos.data_ptr(), 0, cos.stride(0), sin.data_ptr(), 0, sin.stride(0),
+                     positions.data_ptr() if positions is not None else None,
+                     1, n_heads, 0, M, head_dim, 1, st),
+        "forge_rope(backward)",
+    )
+    return out
+
+
+class LoRAQKVRoPEFunction(torch.autograd.Function):
+    """LoRA-QKV with RoPE fused into the GEMM epilogue.
+
+    forward(ctx, X, W_q, W_k, W_v, A_q, B_q, s_q, A_k, B_k, s_k, A_v, B_v, s_v,
+            cos, sin, positions, head_dim) -> (Q_rot, K_rot, V)
+    cos/sin: bf16 tables [P, head_dim] (rows = positions); positions: int64
+    [M] (token -> table row; restarts per sequence for packed varlen)."""
+
+    @staticmethod
+    def forward(ctx, X, W_q, W_k, W_v, A_q, B_q, s_q, A_k, B_k, s_k, A_v, B_v, s_v, cos, sin, positions,
+                head_dim=128):
+        orig_shape = X.shape
+        X2 = _flat(X)
+        cos2 = cos.reshape(-1, cos.shape[-1]).to(torch.bfloat16).contiguous()
+        sin2 = sin.reshape(-1, sin.shape[-1]).to(torch.bfloat16).contiguous()
+        pos = positions.reshape(-1).to(device=X.device, dtype=torch.int64).contiguous() if positions is not None else None
+        out = qkv_forward(X2, W_q, W_k, W_v, A_q, B_q, s_q, A_k, B_k, s_k, A_v, B_v, s_v,
+                          rope={"cos": cos2, "sin": sin2, "positions": pos, "head_dim": int(head_dim)})
+        ctx.save_for_backward(X, A_q, B_q, A_k, B_k, A_v, B_v, cos2, sin2, pos)
+        ctx.scalings = (s_q, s_k, s_v)
+        ctx.base_weights = (W_q, W_k, W_v)
+        ctx.head_dim = int(head_dim)
+        return split_views(out, W_q.shape[0], W_k.shape[0], orig_shape)
+
+    @staticmethod
+    def backward(ctx, dQ, dK, dV):
+        X, A_q, B_q, A_k, B_k, A_v, B_v, cos2, sin2, pos = ctx.saved_tensors
+        s_q, s_k, s_v = ctx.scalings
+        W_q, W_k, W_v = ctx.base_weights
+        D = ctx.head_dim
+        dQ2, dK2 = _flat(dQ), _flat(dK)
+        dQ2 = dQ2 if dQ2.stride(-1) == 1 else dQ2.contiguous()
+        dK2 = dK2 if dK2.stride(-1) == 1 else dK2.contiguous()
+        dQu = _rope_rows_backward(dQ2, dQ2.shape[1] // D, D, cos2, sin2, pos)
+        dKu = _rope_rows_backward(dK2, dK2.shape[1] // D, D, cos2, sin2, pos)
+        dX, dAq, dBq, dAk, dBk, dAv, dBv = qkv_backward(dQu, dKu, _flat(dV), _flat(X), W_q, W_k, W_v,
+                                                        A_q, B_q, s_q, A_k, B_k, s_k, A_v, B_v, s_v)
+        if X.dim() == 3:
+            dX = dX.reshape(X.shape)
+        return (dX, None, None, None, dAq, dBq, None, dAk, dBk, None, dAv, dBv, None, None, None, None, None)
+
+
+def lora_qkv_rope(X, W_q, A_q, B_q, s_q, W_k, A_k, B_k, s_k, W_v, A_v, B_v, s_v, cos, sin, positions=None,
+                  head_dim=128):
+    """LoRA-QKV followed by RoPE on Q and K, fused (see LoRAQKVRoPEFunction)."""
+    return LoRAQKVRoPEFunction.apply(X, W_q, W_k, W_v, A_q, B_q, s_q, A_k, B_k, s_k, A_v, B_v, s_v,
+                                     cos, sin, positions, head_dim)
+
+
+__all__ = ["LoRAQKVv4Function", "lora_qkv_v4", "pack_weights_backward", "pack_lora_a",
+           "LoRAQKVRoPEFunction", "lora_qkv_rope"]

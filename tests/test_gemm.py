@@ -76,11 +76,11 @@ def test_gemm_segments_beta_alpha():
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("split", [1, 4, 7])
-def test_gemm_split_k_atomic(split):
-    """LoRA-A-gradient shape: [r, H] = T^T @ X with K = tokens."""
+@pytest.mark.parametrize("split,T", [(1, 2048), (4, 2048), (7, 2048), (3, 1001)])
+def test_gemm_split_k_atomic(split, T):
+    """LoRA-A-gradient shape: [r, H] = T^T @ X with K = tokens (any count)."""
     gen = torch.Generator().manual_seed(split)
-    r, H, T = 16, 512, 2048
+    r, H = 16, 512
     t, Tm = _operand(r, T, 1, gen)  # A = T^T stored as [T][r]
     x_stored = torch.randn(T, H, generator=gen).to(torch.bfloat16)
     c = torch.zeros(r, H, dtype=torch.float32, device="cuda")
@@ -92,7 +92,7 @@ def test_gemm_split_k_atomic(split):
 def test_gemm_rejects_bad_segments_without_gpu():
     """Argument validation happens on the host before any launch."""
     seg = (L.GemmSegment * 1)()
-    seg[0] = L.GemmSegment(16, 8, 16, 8, 12)  # K not a multiple of 8
+    seg[0] = L.GemmSegment(16, 8, 16, 8, 12)  # K not a multiple of 8 with a K-contiguous A
     rc = L.forge_gemm(8, 8, seg, 1, 0, 1, 16, 8, L.DTYPE_BF16, 1.0, 0.0, L.EPI_STORE, 1, None)
     assert rc == 1 and b"multiple of 8" in L.forge_last_error()
     rc = L.forge_gemm(8, 8, seg, 0, 0, 1, 16, 8, L.DTYPE_BF16, 1.0, 0.0, L.EPI_STORE, 1, None)

@@ -1,0 +1,126 @@
+"""LoRA-MLP parity: the fused MFMA pipeline (LoRAMLPv6 / LoRAMLPv3 through
+libforge_hip.so) vs the CPU oracle (kernels/lora_mlp/reference/lora_mlp_pytorch.py
+restated, fp32 on the same bf16 values).
+
+Tolerance (bf16): |a - b| <= 2e-2 * max(1, rms(b)) + 2e-2 |b| elementwise, and
+cosine similarity > 0.9999 (the reference's forge/tests/test_lora_mlp.py:56-66
+acceptance).  The BASELINE config (M=8192, H=4096, I=14336, r=16) is checked
+on token rows against the oracle and for additivity of the LoRA gradients
+over token chunks.
+"""
+import pytest
+import torch
+
+from kernels.lora_mlp.experiments.v3.lora_mlp_kernel_v3 import LoRAMLPv3, lora_mlp_v3
+from kernels.lora_mlp.experiments.v6.lora_mlp_kernel_v6 import LoRAMLPv6, LoRAMLPv6Module, lora_mlp_v6
+from oracle import lora_mlp as orc
+from _parity import close_bf16 as _close_bf16
+
+NAMES = ["dX", "dA_gate", "dB_gate", "dA_up", "dB_up", "dA_down", "dB_down"]
+
+
+
+
+def _params_cuda(params):
+    out = []
+    for t in params:
+        out.append(t.cuda().requires_grad_(t.shape[0] <= 64 or t.shape[1] <= 64) if isinstance(t, torch.Tensor) else t)
+    return out
+
+
+def _run(fn, X, dY, params):
+    p = _params_cuda(params)
+    x = X.cuda().requires_grad_(True)
+    out = fn(x, *p)
+    out.backward(dY.cuda())
+    lora = [p[1], p[2], p[5], p[6], p[9], p[10]]
+    return out, [x.grad] + [t.grad for t in lora]
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("B,S,H,I,r,alpha", [(2, 128, 512, 1024, 16, 32), (1, 200, 256, 768, 8, 16),
+                                              (2, 256, 1024, 2816, 64, 128)])
+@pytest.mark.parametrize("version", ["v6", "v3"])
+def test_lora_mlp_matches_oracle(B, S, H, I, r, alpha, version):
+    gen = torch.Generator().manual_seed(B * S + H + r)
+    params = orc.make_params(H, I, r, alpha, gen)
+    X = torch.randn(B, S, H, generator=gen).to(torch.bfloat16)
+    dY = torch.randn(B, S, H, generator=gen).to(torch.bfloat16)
+    ref_out, ref_grads = orc.fwd_bwd(X, dY, params)
+    fn = (lambda x, *p: LoRAMLPv6.apply(x, *p)) if version == "v6" else (lambda x, *p: LoRAMLPv3.apply(x, *p))
+    out, grads = _run(fn, X, dY, params)
+    assert out.shape == (B, S, H) and out.dtype == torch.bfloat16
+    _close_bf16(out.reshape(-1, H), ref_out, "out")
+    for n, a, b in zip(NAMES, grads, ref_grads):
+        _close_bf16(a.reshape(b.shape), b, n)
+
+
+@pytest.mark.gpu
+def test_lora_mlp_saved_tensors_contract():
+    """save_for_backward = (A_gate, B_gate, A_up, B_up, A_down, B_down, X, e, g)
+    with e/g = pre-activations WITH LoRA added (v6 :586)."""
+    gen = torch.Generator().manual_seed(3)
+    H, I, r = 256, 512, 16
+    params = orc.make_params(H, I, r, 32, gen)
+    X = torch.randn(1, 64, H, generator=gen).to(torch.bfloat16)
+    p = _params_cuda(params)
+    x = X.cuda().requires_grad_(True)
+    out = LoRAMLPv6.apply(x, *p)
+    saved = out.grad_fn.saved_tensors
+    assert len(saved) == 9 and saved[6].data_ptr() == x.data_ptr()
+    _, e_ref, g_ref = orc.forward(X.float().reshape(-1, H), *[t.float() if isinstance(t, torch.Tensor) else t for t in params])
+    _close_bf16(saved[7].reshape(-1, I), e_ref, "e")
+    _close_bf16(saved[8].reshape(-1, I), g_ref, "g")
+
+
+@pytest.mark.gpu
+def test_lora_mlp_no_grad_api_and_module():
+    gen = torch.Generator().manual_seed(4)
+    H, I, r = 256, 512, 16
+    params = orc.make_params(H, I, r, 32, gen)
+    X = torch.randn(2, 32, H, generator=gen).to(torch.bfloat16)
+    ref_out, _, _ = orc.forward(X.float().reshape(-1, H), *[t.float() if isinstance(t, torch.Tensor) else t for t in params])
+    p = [t.cuda() if isinstance(t, torch.Tensor) else t for t in params]
+    _close_bf16(lora_mlp_v6(X.cuda(), *p).reshape(-1, H), ref_out, "lora_mlp_v6")
+    _close_bf16(lora_mlp_v3(X.cuda(), *p).reshape(-1, H), ref_out, "lora_mlp_v3")
+    m = LoRAMLPv6Module(H, I, r, dtype=torch.bfloat16, device="cuda")
+    y = m(torch.randn(2, 16, H, device="cuda", dtype=torch.bfloat16))
+    y.float().sum().backward()
+    assert m.A_gate.grad is not None and m.W_gate.grad is None
+
+
+@pytest.mark.gpu
+def test_lora_mlp_fp64_gradcheck_uses_reference_torch_path():
+    """v6 :552-557 / tests :1560: float64 goes through the PyTorch formulas."""
+    gen = torch.Generator().manual_seed(5)
+    H, I, r = 8, 12, 2
+    params = [t.double().cuda() if isinstance(t, torch.Tensor) else t for t in orc.make_params(H, I, r, 4, gen)]
+    for i in (1, 2, 5, 6, 9, 10):
+        params[i].requires_grad_(True)
+    X = torch.randn(1, 3, H, dtype=torch.float64, device="cuda", requires_grad=True)
+    assert torch.autograd.gradcheck(lambda x, *lp: LoRAMLPv6.apply(
+        x, params[0], lp[0], lp[1], params[3], params[4], lp[2], lp[3], params[7], params[8], lp[4], lp[5], params[11]),
+        (X, params[1], params[2], params[5], params[6], params[9], params[10]))
+
+
+@pytest.mark.gpu
+def test_lora_mlp_baseline_config():
+    """X [8192, 4096] ~ N(0,1), W ~ N(0, 0.02^2),
+    r=16, alpha=32, A Kaiming-uniform, B ~ N(0, 0.01^2)."""
+    gen = torch.Generator().manual_seed(31)
+    M, H, I, r = 8192, 4096, 14336, 16
+    params = orc.make_params(H, I, r, 32, gen)
+    X = torch.randn(1, M, H, generator=gen).to(torch.bfloat16)
+    dY = torch.randn(1, M, H, generator=gen).to(torch.bfloat16)
+    out, grads = _run(lambda x, *p: LoRAMLPv6.apply(x, *p), X, dY, params)
+    # rows 0..255 of out and dX depend only on the same rows of X / dY
+    n = 256
+    ref_out, ref_grads = orc.fwd_bwd(X[:, :n], dY[:, :n], params)
+    _close_bf16(out.reshape(-1, H)[:n], ref_out, "out[:256]")
+    _close_bf16(grads[0].reshape(-1, H)[:n], ref_grads[0], "dX[:256]")
+    # LoRA gradients are sums over tokens: full == first half + second half
+    h = M // 2
+    _, g1 = _run(lambda x, *p: LoRAMLPv6.apply(x, *p), X[:, :h], dY[:, :h], params)
+    _, g2 = _run(lambda x, *p: LoRAMLPv6.apply(x, *p), X[:, h:], dY[:, h:], params)
+    for name, a, b1, b2 in zip(NAMES[1:], grads[1:], g1[1:], g2[1:]):
+        _close_bf16(a, b1.float() + b2.float(), name + " additivity")

@@ -1,0 +1,116 @@
+"""LoRA-QKV parity: v2_3 / v3 / v4 APIs and the fused QKV+RoPE entry point
+(through libforge_hip.so) vs the CPU oracle
+(kernels/lora_qkv/reference/lora_qkv_pytorch.py restated + the caller's RoPE).
+Tolerance as in tests/test_lora_mlp.py (bf16 2e-2 scaled, cosine > 0.9999)."""
+import pytest
+import torch
+
+from kernels.lora_qkv.experiments.v2.lora_qkv_kernel_v2_3 import lora_qkv_v2_3
+from kernels.lora_qkv.experiments.v3.lora_qkv_kernel_v3 import LoRAQKVFunction
+from kernels.lora_qkv.experiments.v4.lora_qkv_kernel_v4 import (
+    LoRAQKVv4Function,
+    lora_qkv_rope,
+    pack_lora_a,
+    pack_weights_backward,
+)
+from oracle import lora_qkv as orc
+from oracle.rope import cos_sin
+from _parity import close_bf16 as _close_bf16
+
+NAMES = ["dX", "dA_q", "dB_q", "dA_k", "dB_k", "dA_v", "dB_v"]
+
+
+def _cuda(params):
+    out = []
+    for i, t in enumerate(params):
+        if isinstance(t, torch.Tensor):
+            out.append(t.cuda().requires_grad_(i in (3, 4, 6, 7, 9, 10)))
+        else:
+            out.append(t)
+    return out
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("T,K,Hq,Hkv,r", [(256, 512, 512, 128, 16), (300, 256, 512, 256, 64), (128, 1024, 1024, 256, 8)])
+@pytest.mark.parametrize("api", ["v4", "v3"])
+def test_lora_qkv_matches_oracle(T, K, Hq, Hkv, r, api):
+    gen = torch.Generator().manual_seed(T + K + r)
+    params = orc.make_params(K, Hq, Hkv, r, 2 * r, gen)
+    X = torch.randn(T, K, generator=gen).to(torch.bfloat16)
+    dQ = torch.randn(T, Hq, generator=gen).to(torch.bfloat16)
+    dK = torch.randn(T, Hkv, generator=gen).to(torch.bfloat16)
+    dV = torch.randn(T, Hkv, generator=gen).to(torch.bfloat16)
+    f = lambda t: t.float() if isinstance(t, torch.Tensor) else t  # noqa: E731
+    pf = [f(t) for t in params]
+    Qr, Kr, Vr = orc.forward(X.float(), *pf)
+    ref_grads = orc.backward(dQ.float(), dK.float(), dV.float(), X.float(), *pf)
+    p = _cuda(params)
+    x = X.cuda().requires_grad_(True)
+    Fn = LoRAQKVv4Function if api == "v4" else LoRAQKVFunction
+    Q, K_, V = Fn.apply(x, *p)
+    # outputs are column views of one packed buffer
+    assert Q.stride(0) == Hq + 2 * Hkv and K_.data_ptr() == Q.data_ptr() + 2 * Hq
+    for a, b, n in ((Q, Qr, "Q"), (K_, Kr, "K"), (V, Vr, "V")):
+        _close_bf16(a, b, n)
+    torch.autograd.backward((Q, K_, V), (dQ.cuda(), dK.cuda(), dV.cuda()))
+    got = [x.grad, p[3].grad, p[4].grad, p[6].grad, p[7].grad, p[9].grad, p[10].grad]
+    for n, a, b in zip(NAMES, got, ref_grads):
+        _close_bf16(a, b, n)
+
+
+@pytest.mark.gpu
+def test_lora_qkv_v2_3_and_packed_helpers():
+    gen = torch.Generator().manual_seed(8)
+    T, K, Hq, Hkv, r = 64, 256, 256, 64, 16
+    params = orc.make_params(K, Hq, Hkv, r, 32, gen)
+    X = torch.randn(2, T // 2, K, generator=gen).to(torch.bfloat16)
+    pf = [t.float() if isinstance(t, torch.Tensor) else t for t in params]
+    Qr, Kr, Vr = orc.forward(X.float().reshape(-1, K), *pf)
+    Wq, Wk, Wv, Aq, Bq, sq, Ak, Bk, sk, Av, Bv, sv = [t.cuda() if isinstance(t, torch.Tensor) else t for t in params]
+    Q, K_, V = lora_qkv_v2_3(X.cuda(), Wq, Aq, Bq, sq, Wk, Ak, Bk, sk, Wv, Av, Bv, sv)
+    assert Q.shape == (2, T // 2, Hq)
+    for a, b, n in ((Q, Qr, "Q"), (K_, Kr, "K"), (V, Vr, "V")):
+        _close_bf16(a.reshape(-1, a.shape[-1]), b, n)
+    assert torch.equal(pack_weights_backward(Wq, Wk, Wv), torch.cat([Wq, Wk, Wv]))
+    assert torch.equal(pack_lora_a(Aq, Ak, Av), torch.cat([Aq, Ak, Av]))
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("head_dim", [128, 64])
+def test_lora_qkv_rope_fused_matches_composition(head_dim):
+    """Fused QKV+RoPE == LoRA-QKV then RoPE with per-token (varlen) positions."""
+    gen = torch.Generator().manual_seed(head_dim)
+    lens = [37, 120, 99]
+    pos = orc.positions_for(lens)
+    T, K, Hq, Hkv, r = int(pos.numel()), 512, 512, 256, 16
+    params = orc.make_params(K, Hq, Hkv, r, 32, gen)
+    X = torch.randn(T, K, generator=gen).to(torch.bfloat16)
+    dQ = torch.randn(T, Hq, generator=gen).to(torch.bfloat16)
+    dK = torch.randn(T, Hkv, generator=gen).to(torch.bfloat16)
+    dV = torch.randn(T, Hkv, generator=gen).to(torch.bfloat16)
+    c, s = cos_sin(torch.arange(256), head_dim, 500000.0, torch.bfloat16)
+    (Qr, Kr, Vr), ref_grads = orc.qkv_rope_fwd_bwd(X, dQ, dK, dV, params, c[pos], s[pos], head_dim)
+    p = _cuda(params)
+    x = X.cuda().requires_grad_(True)
+    Q, K_, V = lora_qkv_rope(x, p[0], p[3], p[4], p[5], p[1], p[6], p[7], p[8], p[2], p[9], p[10], p[11],
+                             c.cuda(), s.cuda(), pos.cuda(), head_dim)
+    for a, b, n in ((Q, Qr, "Q"), (K_, Kr, "K"), (V, Vr, "V")):
+        _close_bf16(a, b, n)
+    torch.autograd.backward((Q, K_, V), (dQ.cuda(), dK.cuda(), dV.cuda()))
+    got = [x.grad, p[3].grad, p[4].grad, p[6].grad, p[7].grad, p[9].grad, p[10].grad]
+    for n, a, b in zip(NAMES, got, ref_grads):
+        _close_bf16(a, b, n)
+
+
+@pytest.mark.gpu
+def test_lora_qkv_fp64_gradcheck_uses_reference_torch_path():
+    gen = torch.Generator().manual_seed(9)
+    K, Hq, Hkv, r = 8, 8, 4, 2
+    params = [t.double().cuda() if isinstance(t, torch.Tensor) else t for t in orc.make_params(K, Hq, Hkv, r, 4, gen)]
+    X = torch.randn(5, K, dtype=torch.float64, device="cuda", requires_grad=True)
+    lora = [params[i].requires_grad_(True) for i in (3, 4, 6, 7, 9, 10)]
+
+    def f(x, aq, bq, ak, bk, av, bv):
+        return LoRAQKVv4Function.apply(x, params[0], params[1], params[2], aq, bq, params[5], ak, bk, params[8],
+                                       av, bv, params[11])
+    assert torch.autograd.gradcheck(f, (X, *lora))
