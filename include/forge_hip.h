@@ -227,13 +227,22 @@ int forge_lora_qkv_rope(int64_t M, int64_t K, int64_t hq, int64_t hkv, int64_t r
 /* Rank-r LoRA-A projections of one input, one GEMM:
  *   out[:, p*r:(p+1)*r] = scales[p] * X @ A_p^T     for p < n_proj (<= 4)
  * X [M, K] (row pitch ldx), A_p [r, K] (pitch lda), out [M, n_proj*r] bf16.
- * scales is a host array.  Replaces the LoRA-A GEMMs X @ A^T of the
+ * scales is a host array.  split_k > 1 spreads K over split_k workgroups
+ * per output tile, reducing in `work` (fp32 [M, n_proj*r], caller-owned, no
+ * initialisation needed) before the bf16 cast.  Replaces the LoRA-A GEMMs X @ A^T of the
  * reference (the stacked [W; A_g; A_u] cuBLAS call,
  * kernels/lora_mlp/experiments/v6/lora_mlp_kernel_v6.py:373-381, and
  * `XA_all = X @ A_packed^T`, kernels/lora_qkv/experiments/v4/lora_qkv_kernel_v4.py:260). */
 int forge_lora_a(int64_t M, int64_t K, int64_t r, int n_proj, const void* x, int64_t ldx,
                  const void* const* a_mats, int64_t lda, const float* scales, void* out,
-                 int64_t ld_out, void* stream);
+                 int64_t ld_out, float* work, int split_k, void* stream);
+
+/* Utilities for split-K reductions (no counterpart in the reference, which
+ * delegates these to cuBLAS): zero an fp32 workspace with a fill kernel, and
+ * cast a reduced fp32 [rows, cols] block to bf16. */
+int forge_zero(void* ptr, int64_t bytes, void* stream);
+int forge_cast_f32_bf16(const float* src, int64_t ld_src, void* dst, int64_t ld_dst, int64_t rows,
+                        int64_t cols, void* stream);
 
 #ifdef __cplusplus
 }

@@ -120,19 +120,63 @@ __device__ __forceinline__ void transpose8x8(const uint4 (&in)[8], uint4 (&out)[
 }
 
 // Tile loader: fetches a BROWS x BK operand tile from global memory into
-// registers, then writes it k-contiguous into LDS.
+// registers with raw buffer loads, then writes it k-contiguous into LDS.
 //   KCONTIG: element (row, k) at base[row * ld + k]   (A ROW, B COL)
 //   !KCONTIG: element (row, k) at base[k * ld + row]  (A COL, B ROW)
-template <int BROWS, int NT, bool KCONTIG>
-struct TileLoader {
-  static constexpr int VPT = KCONTIG ? (BROWS * BK / 8 + NT - 1) / NT        // 16-byte vectors
-                                     : 8 * ((BROWS / 8) * (BK / 8) + NT - 1) / NT;  // 8 per 8x8 block
-  uint4 regs[VPT > 0 ? VPT : 1];
+// Per segment, setup() precomputes each thread's byte offsets inside the
+// tile's panel; rows outside the matrix / the segment's column range get an
+// offset past the buffer's num_records, which the hardware returns as zeros,
+// so the K loop has no branches.  Per K tile, load() rebases the buffer
+// resource on k0 (scalar work) and masks k beyond the segment's end.
+// DUAL (B only): vector i of a thread lies in 32-row group i % 4 of a 128-row
+// wave slab; even groups read pointer 0 (gate), odd groups pointer 1 (up).
+constexpr uint32_t OOB = 0x80000000u;       // offset >= num_records -> reads 0
+constexpr int NUM_RECORDS = 0x7fffffff;
 
-  // Row source: base pointer for LDS row q (nullptr = zeros) and the number
-  // of valid k in this tile (k < kvalid).
-  template <class RowPtr>
-  __device__ __forceinline__ void load(RowPtr rowptr, int64_t ld, int64_t k0, int64_t kvalid) {
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+
+// The base is wave-uniform by construction; readfirstlane makes that
+// visible to the compiler so the descriptor lives in SGPRs (a descriptor it
+// cannot prove uniform turns every buffer load into a waterfall loop).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base) {
+  const uint64_t b = reinterpret_cast<uint64_t>(base);
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)b);
+  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(b >> 32));
+  void* ub = reinterpret_cast<void*>(((uint64_t)hi << 32) | lo);
+  return __builtin_amdgcn_make_buffer_rsrc(ub, (short)0, NUM_RECORDS, 0x00020000);
+}
+
+__device__ __forceinline__ uint4 buf_load16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  i32x4 v = __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 0);
+  return make_uint4((uint32_t)v.x, (uint32_t)v.y, (uint32_t)v.z, (uint32_t)v.w);
+}
+
+template <int BROWS, int NT, bool KCONTIG, bool DUAL>
+struct TileLoader {
+  static constexpr int NVEC = BROWS * BK / 8;                  // 16-byte vectors per tile
+  static constexpr int NBLK = (BROWS / 8) * (BK / 8);          // 8x8 blocks per tile
+  static constexpr int VPT = KCONTIG ? (NVEC + NT - 1) / NT : 8 * ((NBLK + NT - 1) / NT);
+  static constexpr int BPT = VPT / 8;                          // 8x8 blocks per thread (!KCONTIG)
+  static_assert(!DUAL || (KCONTIG && NT == 256 && BROWS == 256), "dual loader: 256x64 K-contiguous tile");
+
+  struct Stage {  // one K tile in flight (registers)
+    uint4 v[VPT];
+  };
+  uint32_t voff[KCONTIG ? VPT : BPT];  // byte offsets of the rows (OOB = zero-fill)
+  const char* base[2];
+  int64_t ld_bytes;
+
+  // Panel p0/p1 + panel_off rows (KCONTIG) or columns (!KCONTIG);
+  // row_src(q, sel) -> index of tile row q relative to that panel start
+  // (-1 = no data: zero-fill).  Relative offsets keep every byte offset
+  // inside one tile panel, far below 2^31.
+  template <class RowSrc>
+  __device__ __forceinline__ void setup(const void* p0, const void* p1, int64_t ld, int64_t panel_off,
+                                        RowSrc row_src) {
+    ld_bytes = ld * 2;
+    const int64_t pan = KCONTIG ? panel_off * ld_bytes : panel_off * 2;
+    base[0] = p0 ? (const char*)p0 + pan : nullptr;
+    base[1] = DUAL ? (p1 ? (const char*)p1 + pan : nullptr) : base[0];
     const int tid = threadIdx.x;
     if constexpr (KCONTIG) {
 #pragma unroll
@@ -140,67 +184,86 @@ struct TileLoader {
         const int v = tid + i * NT;
         const int q = v / (BK / 8);
         const int kc = (v % (BK / 8)) * 8;
-        uint4 val = make_uint4(0, 0, 0, 0);
-        if (v < BROWS * BK / 8 && kc < kvalid) {
-          const __bf16* p = rowptr(q);
-          if (p) val = *reinterpret_cast<const uint4*>(p + (k0 + kc));
-        }
-        regs[i] = val;
+        const int sel = DUAL ? (i % 2) : 0;
+        const int64_t row = (v < NVEC && base[sel]) ? row_src(q, sel) : -1;
+        voff[i] = row < 0 ? OOB : (uint32_t)(row * ld_bytes + kc * 2);
       }
-      (void)ld;
     } else {
-      constexpr int NBLK = (BROWS / 8) * (BK / 8);
 #pragma unroll
-      for (int bi = 0; bi < VPT / 8; ++bi) {
+      for (int bi = 0; bi < BPT; ++bi) {
         const int blk = tid + bi * NT;
-        const int qb = (blk % (BROWS / 8)) * 8;  // rows qb..qb+7 (contiguous in memory)
-        const int kb = (blk / (BROWS / 8)) * 8;  // k rows kb..kb+7
-        uint4 in[8];
-        const __bf16* p = (blk < NBLK) ? rowptr(qb) : nullptr;
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-          in[i] = make_uint4(0, 0, 0, 0);
-          if (p && kb + i < kvalid) in[i] = *reinterpret_cast<const uint4*>(p + (k0 + kb + i) * ld);
-        }
-        uint4 out[8];
-        transpose8x8(in, out);
-#pragma unroll
-        for (int i = 0; i < 8; ++i) regs[bi * 8 + i] = out[i];
+        const int kb = (blk % (BK / 8)) * 8;   // k-block fastest: the 8 lanes of a row
+        const int qb = (blk / (BK / 8)) * 8;   // group write one 128-byte LDS row span
+        const int64_t col = (blk < NBLK && base[0]) ? row_src(qb, 0) : -1;  // first of 8 contiguous rows
+        voff[bi] = col < 0 ? OOB : (uint32_t)(kb * ld_bytes + col * 2);
       }
     }
   }
 
-  __device__ __forceinline__ void store(__bf16* lds) {
+  __device__ __forceinline__ void load(int64_t k0, int64_t kvalid, Stage& st) {
+    uint4* regs = st.v;
+    const int tid = threadIdx.x;
+    if constexpr (KCONTIG) {
+      const __amdgpu_buffer_rsrc_t r0 = make_rsrc(base[0] + k0 * 2);
+      const __amdgpu_buffer_rsrc_t r1 = make_rsrc(base[1] + k0 * 2);
+      const int kc = (tid % (BK / 8)) * 8;  // same for every i (NT is a multiple of 8)
+      const bool kin = kc < kvalid;
+#pragma unroll
+      for (int i = 0; i < VPT; ++i) {
+        const uint32_t off = kin ? voff[i] : OOB;
+        regs[i] = buf_load16((DUAL && (i % 2)) ? r1 : r0, off);
+      }
+    } else {
+      const __amdgpu_buffer_rsrc_t r0 = make_rsrc(base[0] + k0 * ld_bytes);
+#pragma unroll
+      for (int bi = 0; bi < BPT; ++bi) {
+        const int blk = tid + bi * NT;
+        const int kb = (blk % (BK / 8)) * 8;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          const bool ok = voff[bi] != OOB && kb + i < kvalid;
+          regs[bi * 8 + i] = buf_load16(r0, ok ? voff[bi] + (uint32_t)(i * ld_bytes) : OOB);
+        }
+      }
+    }
+  }
+
+  __device__ __forceinline__ void store(const Stage& st, __bf16* lds) {
+    const uint4* regs = st.v;
     const int tid = threadIdx.x;
     if constexpr (KCONTIG) {
 #pragma unroll
       for (int i = 0; i < VPT; ++i) {
         const int v = tid + i * NT;
-        if (v < BROWS * BK / 8) {
+        if (NVEC % NT == 0 || v < NVEC) {
           const int q = v / (BK / 8);
           const int kc = (v % (BK / 8)) * 8;
           *reinterpret_cast<uint4*>(lds + q * LDS_PITCH + kc) = regs[i];
         }
       }
     } else {
-      constexpr int NBLK = (BROWS / 8) * (BK / 8);
 #pragma unroll
-      for (int bi = 0; bi < VPT / 8; ++bi) {
+      for (int bi = 0; bi < BPT; ++bi) {
         const int blk = tid + bi * NT;
-        if (blk < NBLK) {
-          const int qb = (blk % (BROWS / 8)) * 8;
-          const int kb = (blk / (BROWS / 8)) * 8;
+        if (NBLK % NT == 0 || blk < NBLK) {
+          const int kb = (blk % (BK / 8)) * 8;
+          const int qb = (blk / (BK / 8)) * 8;
+          // transpose here, not in load(): the loads stay in flight during the MFMAs
+          uint4 in[8], out[8];
+#pragma unroll
+          for (int i = 0; i < 8; ++i) in[i] = regs[bi * 8 + i];
+          transpose8x8(in, out);
 #pragma unroll
           for (int i = 0; i < 8; ++i)
-            *reinterpret_cast<uint4*>(lds + (qb + i) * LDS_PITCH + kb) = regs[bi * 8 + i];
+            *reinterpret_cast<uint4*>(lds + (qb + i) * LDS_PITCH + kb) = out[i];
         }
       }
     }
   }
 };
 
-__device__ __forceinline__ float silu_f(float x) { return x / (1.0f + __expf(-x)); }
-__device__ __forceinline__ float sigmoid_f(float x) { return 1.0f / (1.0f + __expf(-x)); }
+__device__ __forceinline__ float sigmoid_f(float x) { return __builtin_amdgcn_rcpf(1.0f + __expf(-x)); }
+__device__ __forceinline__ float silu_f(float x) { return x * sigmoid_f(x); }
 __device__ __forceinline__ float bf16r(float x) { return (float)(__bf16)x; }
 
 // XCD-aware tile order: consecutive workgroup ids land on different XCDs
@@ -225,8 +288,13 @@ __device__ __forceinline__ void tile_coords(int64_t tiles_m, int64_t tiles_n, in
   tn = (int)(in / gm);
 }
 
+// Scheduling-group masks of __builtin_amdgcn_sched_group_barrier.
+constexpr int SG_MFMA = 0x008;
+constexpr int SG_DS_READ = 0x100;
+
 template <int BM, int BN, int WAVES_M, int WAVES_N, int A_LAYOUT, int B_LAYOUT, int BMODE, int EPI>
-__global__ __launch_bounds__(WAVES_M * WAVES_N * 64) void gemm_kernel(GemmArgs args) {
+__global__ __launch_bounds__(WAVES_M * WAVES_N * 64) __attribute__((amdgpu_waves_per_eu(1, 1)))
+void gemm_kernel(GemmArgs args) {
   constexpr int NT = WAVES_M * WAVES_N * 64;
   constexpr int TM = BM / WAVES_M, TN = BN / WAVES_N;  // wave sub-tile
   constexpr int FM = TM / 32, FN = TN / 32;            // 32x32 MFMA tiles per wave
@@ -274,71 +342,115 @@ __global__ __launch_bounds__(WAVES_M * WAVES_N * 64) void gemm_kernel(GemmArgs a
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
 
-  TileLoader<BM, NT, A_LAYOUT == ROW> la;
-  TileLoader<BN, NT, B_LAYOUT == COL> lb;
+  TileLoader<BM, NT, A_LAYOUT == ROW, false> la;
+  TileLoader<BN, NT, B_LAYOUT == COL, BMODE == B_DUAL> lb;
 
-  // Resolves flat tile index t -> (segment, k0) and loads it into registers.
-  auto load_tile = [&](int t) {
-    int s = 0, base = 0;
-    while (s < args.n_segs && t >= base + seg_tiles[s]) { base += seg_tiles[s]; ++s; }
+  // Points the loaders at segment s (this tile's panels of A and B).
+  auto setup_seg = [&](int s) {
     const Seg& sg = args.segs[s];
-    const int64_t k0 = (int64_t)(t - base) * BK;
-    const int64_t kvalid = sg.k - k0;
-    const __bf16* abase = sg.a;
-    const int64_t lda = sg.lda;
-    la.load(
-        [&](int q) -> const __bf16* {
-          const int64_t m = m0 + q;
-          if (m >= M) return nullptr;
-          return A_LAYOUT == ROW ? abase + m * lda : abase + m;
-        },
-        lda, k0, kvalid);
-    lb.load(
-        [&](int q) -> const __bf16* {
-          int64_t n;
-          const __bf16* bp;
-          if constexpr (BMODE == B_DUAL) {
-            const int t4 = (q % 128) / 32;
-            n = n0 + (q / 128) * 64 + (t4 / 2) * 32 + q % 32;
-            bp = (t4 % 2 == 0) ? sg.b : sg.b2;
-          } else {
-            n = n0 + q;
-            bp = sg.b;
-          }
-          if (!bp || n >= args.N || n < sg.n_lo || n >= sg.n_hi) return nullptr;
-          const int64_t nr = n - sg.n_lo;
-          return B_LAYOUT == COL ? bp + nr * sg.ldb : bp + nr;
-        },
-        sg.ldb, k0, kvalid);
+    la.setup(sg.a, sg.a, sg.lda, m0, [&](int q, int) -> int64_t { return m0 + q < M ? q : -1; });
+    if constexpr (BMODE == B_DUAL) {
+      lb.setup(sg.b, sg.b2, sg.ldb, n0, [&](int q, int) -> int64_t {
+        const int t4 = (q % 128) / 32;
+        const int rel = (q / 128) * 64 + (t4 / 2) * 32 + q % 32;
+        return n0 + rel < args.N ? rel : -1;
+      });
+    } else {
+      const int64_t off = n0 - sg.n_lo;
+      lb.setup(sg.b, sg.b, sg.ldb, off, [&](int q, int) -> int64_t {
+        const int64_t n = n0 + q;
+        return (n < args.N && n >= sg.n_lo && n < sg.n_hi) ? q : -1;
+      });
+    }
   };
 
-  if (t_begin < t_end) {
-    load_tile(t_begin);
-    la.store(As(0));
-    lb.store(Bs(0));
+  // cursor over (segment, k0) for the flat tile range [t_begin, t_end)
+  int cur_s = 0, cur_t = t_begin;
+  {
+    int acc_t = 0;
+    while (cur_s < args.n_segs && cur_t >= acc_t + seg_tiles[cur_s]) { acc_t += seg_tiles[cur_s]; ++cur_s; }
+    cur_t -= acc_t;  // tile index inside segment cur_s
+  }
+
+  // Advances the (segment, tile) cursor to the next K tile of this workgroup;
+  // a segment switch re-points the loaders (rare: once per segment).
+  int64_t seg_k = 0;
+  int cur_n = 0;
+  auto next_tile = [&](bool first) {
+    if (!first) {
+      ++cur_t;
+      if (cur_t >= cur_n) {
+        do { ++cur_s; } while (seg_tiles[cur_s] == 0);
+        cur_t = 0;
+        cur_n = seg_tiles[cur_s];
+        setup_seg(cur_s);
+        seg_k = args.segs[cur_s].k;
+      }
+    } else {
+      cur_n = seg_tiles[cur_s];
+      setup_seg(cur_s);
+      seg_k = args.segs[cur_s].k;
+    }
+  };
+  typename decltype(la)::Stage sa[1];
+  typename decltype(lb)::Stage sb[1];
+  auto issue = [&](int set) {  // global loads of the cursor's tile into staging set `set`
+    const int64_t k0 = (int64_t)cur_t * BK;
+    la.load(k0, seg_k - k0, sa[set]);
+    lb.load(k0, seg_k - k0, sb[set]);
+  };
+
+  // MFMAs of one K tile held in LDS stage `buf`.
+  auto compute = [&](int buf) {
+    const __bf16* a_s = As(buf) + (wm * TM + lane % 32) * LDS_PITCH + (lane / 32) * 8;
+    const __bf16* b_s = Bs(buf) + (wn * TN + lane % 32) * LDS_PITCH + (lane / 32) * 8;
+    // Two-slot fragment ring: the reads of k-steps 0 and 1 are issued first;
+    // after the MFMAs of k-step ks consume slot ks&1, the reads of k-step
+    // ks+2 refill it, so each k-step's operands arrive while the previous
+    // k-step's MFMAs run.  (The sched_group_barriers pin this order.)
+    bf16x8 af[2][FM], bfr[2][FN];
+    auto read_frags = [&](int ks, int slot) {
+#pragma unroll
+      for (int i = 0; i < FM; ++i) af[slot][i] = *reinterpret_cast<const bf16x8*>(a_s + i * 32 * LDS_PITCH + ks * 16);
+#pragma unroll
+      for (int j = 0; j < FN; ++j) bfr[slot][j] = *reinterpret_cast<const bf16x8*>(b_s + j * 32 * LDS_PITCH + ks * 16);
+    };
+    read_frags(0, 0);
+    read_frags(1, 1);
+    __builtin_amdgcn_sched_group_barrier(SG_DS_READ, 2 * (FM + FN), 0);
+#pragma unroll
+    for (int ks = 0; ks < BK / 16; ++ks) {
+      const int slot = ks & 1;
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[slot][i], bfr[slot][j], acc[i][j], 0, 0, 0);
+      __builtin_amdgcn_sched_group_barrier(SG_MFMA, FM * FN, 0);
+      if (ks + 2 < BK / 16) {
+        read_frags(ks + 2, slot);
+        __builtin_amdgcn_sched_group_barrier(SG_DS_READ, FM + FN, 0);
+      }
+    }
+  };
+
+  // Pipeline: global loads run one K tile ahead of the MFMAs (one register
+  // staging set), LDS is double-buffered; one barrier per K tile.
+  const int n_t = t_end - t_begin;
+  if (n_t > 0) {
+    next_tile(true);
+    issue(0);
+    la.store(sa[0], As(0));
+    lb.store(sb[0], Bs(0));
     __syncthreads();
     int buf = 0;
-    for (int t = t_begin; t < t_end; ++t) {
-      const bool more = t + 1 < t_end;
-      if (more) load_tile(t + 1);
-      const __bf16* a_s = As(buf) + (wm * TM + lane % 32) * LDS_PITCH + (lane / 32) * 8;
-      const __bf16* b_s = Bs(buf) + (wn * TN + lane % 32) * LDS_PITCH + (lane / 32) * 8;
-#pragma unroll
-      for (int ks = 0; ks < BK / 16; ++ks) {
-        bf16x8 af[FM], bfr[FN];
-#pragma unroll
-        for (int i = 0; i < FM; ++i) af[i] = *reinterpret_cast<const bf16x8*>(a_s + i * 32 * LDS_PITCH + ks * 16);
-#pragma unroll
-        for (int j = 0; j < FN; ++j) bfr[j] = *reinterpret_cast<const bf16x8*>(b_s + j * 32 * LDS_PITCH + ks * 16);
-#pragma unroll
-        for (int i = 0; i < FM; ++i)
-#pragma unroll
-          for (int j = 0; j < FN; ++j)
-            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[i], bfr[j], acc[i][j], 0, 0, 0);
-      }
+    for (int t = 0; t < n_t; ++t) {
+      const bool more = t + 1 < n_t;
+      if (more) { next_tile(false); issue(0); }
+      compute(buf);
       if (more) {
-        la.store(As(buf ^ 1));
-        lb.store(Bs(buf ^ 1));
+        la.store(sa[0], As(buf ^ 1));
+        lb.store(sb[0], Bs(buf ^ 1));
       }
       __syncthreads();
       buf ^= 1;

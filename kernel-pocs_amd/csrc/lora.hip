@@ -121,22 +121,34 @@ extern "C" int forge_lora_qkv_rope(int64_t M, int64_t K, int64_t hq, int64_t hkv
 
 extern "C" int forge_lora_a(int64_t M, int64_t K, int64_t r, int n_proj, const void* x, int64_t ldx,
                             const void* const* a_mats, int64_t lda, const float* scales, void* out,
-                            int64_t ld_out, void* stream) {
+                            int64_t ld_out, float* work, int split_k, void* stream) {
   if (M < 0 || K < 0 || r <= 0 || n_proj < 1 || n_proj > 4)
     return forge_set_error(FORGE_ERR_INVALID, "lora_a: shape (r > 0, 1 <= n_proj <= 4)");
+  if (split_k > 1 && !work) return forge_set_error(FORGE_ERR_INVALID, "lora_a: split_k > 1 needs a workspace");
+  const int64_t N = r * n_proj;
+  hipStream_t s = (hipStream_t)stream;
   GemmArgs a = {};
   a.M = M;
-  a.N = r * n_proj;
-  a.split_k = 1;
+  a.N = N;
+  a.split_k = split_k > 1 ? split_k : 1;
   a.n_segs = n_proj;
   for (int p = 0; p < n_proj; ++p)
     a.segs[p] = Seg{(const __bf16*)x, ldx, (const __bf16*)a_mats[p], nullptr, lda, K, p * r, (p + 1) * r};
-  a.ep.c = out;
-  a.ep.ldc = ld_out;
   a.ep.alpha = 1.f;
   a.ep.alpha_group = r;
   for (int p = 0; p < 4; ++p) a.ep.alphas[p] = p < n_proj ? scales[p] : 1.f;
   // 256 x 32 tiles: every tile covers at most two projections' columns and
-  // no MFMA work is spent on columns outside [0, n_proj * r)
-  return run(1 /* CFG_SKINNY_N */, ROW, COL, EPI_STORE_BF16, a, (hipStream_t)stream);
+  // no MFMA work is spent on columns outside [0, n_proj * r).  With split_k
+  // the K range is spread over split_k workgroups per tile (the skinny output
+  // alone gives only M/256 tiles) and reduced with fp32 atomics in `work`.
+  if (split_k <= 1) {
+    a.ep.c = out;
+    a.ep.ldc = ld_out;
+    return run(1 /* CFG_SKINNY_N */, ROW, COL, EPI_STORE_BF16, a, s);
+  }
+  if (int e = forge_zero(work, M * N * (int64_t)sizeof(float), stream)) return e;
+  a.ep.c = work;
+  a.ep.ldc = N;
+  if (int e = run(1 /* CFG_SKINNY_N */, ROW, COL, EPI_ATOMIC_F32, a, s)) return e;
+  return forge_cast_f32_bf16(work, N, out, ld_out, M, N, stream);
 }

@@ -117,8 +117,12 @@ forge_lora_qkv_rope = _decl(
 
 forge_lora_a = _decl(
     "forge_lora_a",
-    [c_i64, c_i64, c_i64, c_int, c_vp, c_i64, ctypes.POINTER(c_vp), c_i64, ctypes.POINTER(c_f32), c_vp, c_i64, c_vp],
+    [c_i64, c_i64, c_i64, c_int, c_vp, c_i64, ctypes.POINTER(c_vp), c_i64, ctypes.POINTER(c_f32), c_vp, c_i64,
+     c_vp, c_int, c_vp],
 )
+
+forge_zero = _decl("forge_zero", [c_vp, c_i64, c_vp])
+forge_cast_f32_bf16 = _decl("forge_cast_f32_bf16", [c_vp, c_i64, c_vp, c_i64, c_i64, c_i64, c_vp])
 
 # Every symbol include/forge_hip.h declares (checked by the CPU test suite).
 EXPORTED = [
@@ -126,7 +130,7 @@ EXPORTED = [
     "forge_swiglu_fwd", "forge_swiglu_bwd", "forge_rope",
     "forge_ce_fwd", "forge_ce_scale", "forge_sum_f32",
     "forge_gemm", "forge_lora_mlp_gate_up", "forge_lora_mlp_down_bwd", "forge_lora_qkv_rope",
-    "forge_lora_a",
+    "forge_lora_a", "forge_zero", "forge_cast_f32_bf16",
 ]
 
 # Number of successful library calls (tests use it to prove the HIP path ran).

@@ -32,16 +32,38 @@ def ld(t: torch.Tensor) -> int:
     return t.stride(0) if t.dim() == 2 and t.shape[0] > 1 else t.shape[-1]
 
 
+def skinny_split(M: int, N: int, K: int) -> int:
+    """Split-K factor for a skinny output (N <= 64): the 256 x 32 tiles alone
+    give only M/256 workgroups, too few to keep HBM busy; aim for ~512."""
+    tiles = max(1, (M + 255) // 256) * max(1, (N + 31) // 32)
+    k_tiles = max(1, (K + 63) // 64)
+    return max(1, min(16, 512 // tiles, k_tiles // 4))
+
+
 def gemm(M: int, N: int, segs: Sequence[Tuple[torch.Tensor, int, torch.Tensor, int, int]], a_layout: int,
          b_layout: int, out: Optional[torch.Tensor] = None, alpha: float = 1.0, beta: float = 0.0,
          out_dtype=torch.bfloat16, atomic: bool = False, split_k: int = 1, device=None) -> torch.Tensor:
     """C[M, N] = alpha * sum_s A_s @ B_s (+ beta C).  segs: (A, lda, B, ldb, K).
     atomic=True accumulates into a zero-initialised fp32 C over split_k
-    K partitions."""
+    K partitions.  A skinny bf16 output (N <= 64, beta = 0) is computed the
+    same way (split-K into an fp32 workspace, then cast)."""
     dev = device if device is not None else segs[0][0].device
+    K = sum(int(k) for (_, _, _, _, k) in segs)
+    if not atomic and beta == 0.0 and N <= 64 and M >= 1024 and (out is None or out.dtype == torch.bfloat16):
+        split = skinny_split(M, N, K)
+        if split > 1:
+            if out is None:
+                out = torch.empty(M, N, dtype=torch.bfloat16, device=dev)
+            work = torch.empty(M, N, dtype=torch.float32, device=dev)
+            L.check(L.forge_zero(work.data_ptr(), work.numel() * 4, L.stream_of(work)), "forge_zero")
+            gemm(M, N, segs, a_layout, b_layout, out=work, alpha=alpha, atomic=True, split_k=split, device=dev)
+            L.check(L.forge_cast_f32_bf16(work.data_ptr(), N, out.data_ptr(), ld(out), M, N, L.stream_of(work)),
+                    "forge_cast_f32_bf16")
+            return out
     if out is None:
         if atomic:
-            out = torch.zeros(M, N, dtype=torch.float32, device=dev)
+            out = torch.empty(M, N, dtype=torch.float32, device=dev)
+            L.check(L.forge_zero(out.data_ptr(), out.numel() * 4, L.stream_of(out)), "forge_zero")
         else:
             out = torch.empty(M, N, dtype=out_dtype, device=dev)
     arr = (L.GemmSegment * len(segs))()
@@ -67,9 +89,11 @@ def lora_a(x: torch.Tensor, mats: Sequence[torch.Tensor], scales: Sequence[float
     mats = [as_operand(a) for a in mats]
     ptrs = (ctypes.c_void_p * n)(*[a.data_ptr() for a in mats])
     sc = (ctypes.c_float * n)(*[float(s) for s in scales])
+    split = skinny_split(M, n * r, K) if M >= 1024 else 1
+    work = torch.empty(M, n * r, dtype=torch.float32, device=x.device) if split > 1 else None
     L.check(
         L.forge_lora_a(M, K, r, n, x.data_ptr(), ld(x), ptrs, ld(mats[0]), sc, out.data_ptr(), ld(out),
-                       L.stream_of(x)),
+                       L.ptr(work), split, L.stream_of(x)),
         "forge_lora_a",
     )
     return out
