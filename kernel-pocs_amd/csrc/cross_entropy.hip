@@ -287,115 +287,209 @@ __global__ __launch_bounds__(kStreamBlock) void ce_stream_kernel(CeArgs a) {
 }
 
 // ---------------------------------------------------------------------------
-// Register-resident engine (plain CE with optional smoothing / z-loss)
+// Resident engine (plain CE with optional label smoothing / z-loss)
+//
+// One 640-thread workgroup per row, two workgroups per CU.  The row is read
+// from HBM once and written once: thread t owns the 16-byte vectors
+// t + 640 i; vectors i < NL live in LDS (filled by LDS-DMA loads, no
+// registers involved), vectors NL <= i < NL + NR in registers.  With two rows
+// per CU, one row's exp / reduction work overlaps the other row's memory
+// traffic (the VALU work per element is comparable to its HBM time on this
+// part, so a single row per CU would serialise the two).
+//   pass A: row max via packed 16-bit integer max on the raw bf16/fp16 bits
+//           (order-preserving for non-negative values; a row whose max is
+//           negative takes a float max pass instead)
+//   pass B: p = exp(x - m) in fp32, row sum, p kept as fp16 in place of x
+//   pass C: dlogits = p * scale - shift (target column corrected), stored
 // ---------------------------------------------------------------------------
-constexpr int kResBlock = 1024;
+constexpr int kResBlock = 640;
 constexpr int kResWaves = kResBlock / 64;
+constexpr int kResNL = 7;     // vectors per thread in LDS (70 KB per workgroup)
+constexpr int kResNRMax = 19; // vectors per thread in registers (76 VGPRs)
 
 typedef __fp16 half2_t __attribute__((ext_vector_type(2)));
+typedef short short2_t __attribute__((ext_vector_type(2)));
+typedef int i32x4_t __attribute__((ext_vector_type(4)));
 
-template <class T, int NV>
-__global__ __launch_bounds__(kResBlock) void ce_resident_kernel(CeArgs a) {
+#define LDS_AS __attribute__((address_space(3)))
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t row_rsrc(const void* base, uint32_t bytes) {
+  const uint64_t b = reinterpret_cast<uint64_t>(base);
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)b);
+  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(b >> 32));
+  return __builtin_amdgcn_make_buffer_rsrc(reinterpret_cast<void*>(((uint64_t)hi << 32) | lo), (short)0,
+                                           (int)bytes, 0x00020000);
+}
+
+__device__ __forceinline__ short2_t as_s2(uint32_t w) { return __builtin_bit_cast(short2_t, w); }
+
+template <class T, int NR>
+__global__ __launch_bounds__(kResBlock) __attribute__((amdgpu_waves_per_eu(5, 5)))
+void ce_resident_kernel(CeArgs a) {
   constexpr int VEC = 16 / sizeof(T);
+  constexpr int NL = kResNL;
+  constexpr int VSTRIDE = kResBlock * 16;  // bytes between a thread's vectors i and i+1
+  __shared__ __attribute__((aligned(16))) uint4 lds_row[NL * kResBlock];
   __shared__ float redf[2 * kResWaves];
   const int64_t row = blockIdx.x;
   const int64_t y = a.target[row * a.target_stride];
   T* xr = (T*)a.x + row * a.ld;
   const int64_t V = a.n_cols;
+  const int tid = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
 
   if (y == a.ignore_index) {
     zero_row<T>(xr, V, true);
-    if (threadIdx.x == 0) write_ignored_outputs(a, row);
+    if (tid == 0) write_ignored_outputs(a, row);
     return;
   }
   const float xy = to_f32(xr[y]);
   const float ls = a.label_smoothing;
+  // vector i of this thread is valid iff tid < lim(i) (lim is wave-uniform)
+  const int nvec = (int)(V / VEC);
+  auto valid = [&](int i) { return tid < nvec - i * kResBlock; };
+  const uint32_t voff = (uint32_t)tid * 16u;
 
-  // Column of vector i of this thread: (i * kResBlock + tid) * VEC.
-  Vec16<T> buf[NV];
+  // ---- loads: LDS part by DMA (1 KB per wave instruction, lane-ordered),
+  //      register part by buffer loads ----
+  const __amdgpu_buffer_rsrc_t rs = row_rsrc(xr, (uint32_t)(V * sizeof(T)));
 #pragma unroll
-  for (int i = 0; i < NV; ++i) {
-    const int64_t c0 = ((int64_t)i * kResBlock + threadIdx.x) * VEC;
-    if (c0 < V) buf[i] = load16_nt(xr + c0);
-  }
-
-  // pass A: exact max (and the smoothing sum)
-  float m = -INFINITY, sx = 0.f;
-#pragma unroll
-  for (int i = 0; i < NV; ++i) {
-    const int64_t c0 = ((int64_t)i * kResBlock + threadIdx.x) * VEC;
-    if (c0 < V) {
-#pragma unroll
-      for (int j = 0; j < VEC; ++j) {
-        float v = to_f32(buf[i].v[j]);
-        m = fmaxf(m, v);
-        if (ls > 0.f) sx += v;
-      }
+  for (int i = 0; i < NL; ++i) {
+    if (valid(i)) {
+      LDS_AS void* dst = (LDS_AS void*)((LDS_AS char*)lds_row + (i * kResWaves + wave) * 1024);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, dst, 16, voff, i * VSTRIDE, 0, 0);
     }
   }
-  m = block_max<kResWaves>(m, redf);
-  const float ml2 = m * kLog2e;
-
-  // pass B: sum of exp(x - m); keep p = exp(x - m) as fp16 in the buffer
-  float d = 0.f;
+  uint4 reg[NR];
 #pragma unroll
-  for (int i = 0; i < NV; ++i) {
-    const int64_t c0 = ((int64_t)i * kResBlock + threadIdx.x) * VEC;
-    if (c0 < V) {
-      Vec16<T> pv;
-      half2_t* ph = reinterpret_cast<half2_t*>(&pv.raw);
-#pragma unroll
-      for (int j = 0; j < VEC; j += 2) {
-        float p0 = fast_exp2(fmaf(to_f32(buf[i].v[j]), kLog2e, -ml2));
-        float p1 = fast_exp2(fmaf(to_f32(buf[i].v[j + 1]), kLog2e, -ml2));
-        d += p0 + p1;
-        if constexpr (sizeof(T) == 2) ph[j / 2] = __builtin_amdgcn_cvt_pkrtz(p0, p1);
-        else { buf[i].v[j] = from_f32<T>(p0); buf[i].v[j + 1] = from_f32<T>(p1); }
-      }
-      if constexpr (sizeof(T) == 2) buf[i].raw = pv.raw;
+  for (int i = 0; i < NR; ++i) {
+    reg[i] = make_uint4(0, 0, 0, 0);
+    if (valid(NL + i)) {
+      i32x4_t v = __builtin_amdgcn_raw_buffer_load_b128(rs, (int)voff, (NL + i) * VSTRIDE, 0);
+      reg[i] = make_uint4((uint32_t)v.x, (uint32_t)v.y, (uint32_t)v.z, (uint32_t)v.w);
     }
   }
+  __builtin_amdgcn_s_waitcnt(0);  // our DMA writes have landed
+  __syncthreads();                // ... and everyone else's
+  uint4* my_lds = lds_row + tid;  // slot of vector i: my_lds[i * kResBlock]
+
+  // ---- pass A: row max ----
+  short2_t mi = {(short)0x8000, (short)0x8000};
+  auto max_vec = [&](const uint4& v) {
+    mi = __builtin_elementwise_max(mi, as_s2(v.x));
+    mi = __builtin_elementwise_max(mi, as_s2(v.y));
+    mi = __builtin_elementwise_max(mi, as_s2(v.z));
+    mi = __builtin_elementwise_max(mi, as_s2(v.w));
+  };
+#pragma unroll 1
+  for (int i = 0; i < NL; ++i)
+    if (valid(i)) max_vec(my_lds[i * kResBlock]);
+#pragma unroll
+  for (int i = 0; i < NR; ++i)
+    if (valid(NL + i)) max_vec(reg[i]);
+  auto bits_to_f = [](short h) -> float {
+    return __is_same(T, bf16_t) ? __uint_as_float(((uint32_t)(uint16_t)h) << 16)
+                                : (float)__builtin_bit_cast(fp16_t, h);
+  };
+  const short hmax = mi.x > mi.y ? mi.x : mi.y;
+  // int16 order matches float order for non-negative values (both types)
+  float m = block_max<kResWaves>(hmax >= 0 ? bits_to_f(hmax) : -INFINITY, redf);
+  if (m == -INFINITY) {  // every value negative (or -inf): float max pass
+    float fm = -INFINITY;
+    auto fmax_vec = [&](const uint4& v) {
+      Vec16<T> t;
+      t.raw = v;
+#pragma unroll
+      for (int j = 0; j < VEC; ++j) fm = fmaxf(fm, to_f32(t.v[j]));
+    };
+#pragma unroll 1
+    for (int i = 0; i < NL; ++i)
+      if (valid(i)) fmax_vec(my_lds[i * kResBlock]);
+#pragma unroll
+    for (int i = 0; i < NR; ++i)
+      if (valid(NL + i)) fmax_vec(reg[i]);
+    m = block_max<kResWaves>(fm, redf);
+  }
+  // p is kept as fp16 scaled by 2^kPShift (max 2^15 < 65504), which moves
+  // fp16's flush-to-zero point from ~6e-8 down to ~2e-12 of the row max;
+  // d carries the same factor, so p / d is unchanged
+  constexpr float kPShift = 15.f;
+  const float ml2 = m * kLog2e - kPShift;
+
+  // ---- pass B: p = exp(x - m) * 2^kPShift, sum; p overwrites x as fp16 pairs ----
+  float d = 0.f, sx = 0.f;
+  auto exp_vec = [&](uint4& v) {
+    Vec16<T> t;
+    t.raw = v;
+    uint32_t w[4];
+#pragma unroll
+    for (int j = 0; j < VEC; j += 2) {
+      const float x0 = to_f32(t.v[j]), x1 = to_f32(t.v[j + 1]);
+      if (ls > 0.f) sx += x0 + x1;
+      const float p0 = fast_exp2(fmaf(x0, kLog2e, -ml2));
+      const float p1 = fast_exp2(fmaf(x1, kLog2e, -ml2));
+      d += p0 + p1;
+      w[j / 2] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(p0, p1));
+    }
+    v = make_uint4(w[0], w[1], w[2], w[3]);
+  };
+#pragma unroll 1
+  for (int i = 0; i < NL; ++i)
+    if (valid(i)) {
+      uint4 v = my_lds[i * kResBlock];
+      exp_vec(v);
+      my_lds[i * kResBlock] = v;
+    }
+#pragma unroll
+  for (int i = 0; i < NR; ++i)
+    if (valid(NL + i)) exp_vec(reg[i]);
   d = block_sum<kResWaves>(d, redf);
   float sx_tot = 0.f;
   if (ls > 0.f) sx_tot = block_sum<kResWaves>(sx, redf);
-  const float lse = m + __logf(d);
+  const float lse = m + __logf(d) - kPShift * kLn2;
 
+  // ---- pass C: gradient ----
   if (a.flags & FORGE_CE_HAS_GRADIENTS) {
     const bool mean = a.flags & FORGE_CE_REDUCTION_MEAN;
     const float eps = ls / (float)V;
-    // g = p * scale - shift   (+ the target adjustment below)
     float scale = (1.f + 2.f * a.lse_square_scale * lse) / d;
     float shift = eps;
-    float ydelta = (1.f - ls);
+    float ydelta = 1.f - ls;
     if (mean) {
       scale /= a.n_non_ignore;
       shift /= a.n_non_ignore;
       ydelta /= a.n_non_ignore;
     }
+    const int yv = (int)(y / VEC);            // vector holding the target column
+    const int yi = yv / kResBlock, yt = yv % kResBlock;  // (i, thread) of that vector
+    auto grad_store = [&](const uint4& v, int i) {
+      const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+      Vec16<T> o;
 #pragma unroll
-    for (int i = 0; i < NV; ++i) {
-      const int64_t c0 = ((int64_t)i * kResBlock + threadIdx.x) * VEC;
-      if (c0 < V) {
-        Vec16<T> o;
-        const half2_t* ph = reinterpret_cast<const half2_t*>(&buf[i].raw);
-#pragma unroll
-        for (int j = 0; j < VEC; j += 2) {
-          float p0, p1;
-          if constexpr (sizeof(T) == 2) { p0 = (float)ph[j / 2].x; p1 = (float)ph[j / 2].y; }
-          else { p0 = to_f32(buf[i].v[j]); p1 = to_f32(buf[i].v[j + 1]); }
-          o.v[j] = from_f32<T>(fmaf(p0, scale, -shift));
-          o.v[j + 1] = from_f32<T>(fmaf(p1, scale, -shift));
-        }
-        if (y >= c0 && y < c0 + VEC) {
-          // exact value for the target column (recomputed from x_y in fp32)
-          const float py = fast_exp2(fmaf(xy, kLog2e, -ml2));
-          o.v[y - c0] = from_f32<T>(fmaf(py, scale, -shift) - ydelta);
-        }
-        store16_nt(xr + c0, o);
+      for (int j = 0; j < VEC; j += 2) {
+        const half2_t ph = __builtin_bit_cast(half2_t, w[j / 2]);
+        o.v[j] = from_f32<T>(fmaf((float)ph.x, scale, -shift));
+        o.v[j + 1] = from_f32<T>(fmaf((float)ph.y, scale, -shift));
       }
-    }
+      if (i == yi && tid == yt) {
+        const float py = fast_exp2(fmaf(xy, kLog2e, -ml2));
+        const T gy = from_f32<T>(fmaf(py, scale, -shift) - ydelta);
+        const int yj = (int)(y % VEC);
+#pragma unroll
+        for (int j = 0; j < VEC; ++j)
+          if (j == yj) o.v[j] = gy;  // static indices: no scratch array
+      }
+      const i32x4_t ov = {(int)o.raw.x, (int)o.raw.y, (int)o.raw.z, (int)o.raw.w};
+      __builtin_amdgcn_raw_buffer_store_b128(ov, rs, (int)voff, i * VSTRIDE, 0);
+    };
+#pragma unroll 1
+    for (int i = 0; i < NL; ++i)
+      if (valid(i)) grad_store(my_lds[i * kResBlock], i);
+#pragma unroll
+    for (int i = 0; i < NR; ++i)
+      if (valid(NL + i)) grad_store(reg[i], NL + i);
   }
-  if (threadIdx.x == 0) {
+  if (tid == 0) {
     const float sxs = -(ls / (float)V) * sx_tot;
     write_row_outputs(a, row, y, lse, xy, 1.f, sxs, 0);
   }
@@ -407,15 +501,17 @@ int launch_ce(CeArgs a, hipStream_t s) {
   const bool vec = aligned16(a.x) && (a.ld % V == 0) && (a.n_cols % V == 0);
   const bool plain = !(a.flags & (FORGE_CE_HAS_WEIGHT | FORGE_CE_HAS_SOFTCAP |
                                   FORGE_CE_RETURN_ACCURACY | FORGE_CE_RETURN_PREDICTED));
-  const int64_t nvec = (a.n_cols + (int64_t)kResBlock * V - 1) / ((int64_t)kResBlock * V);
+  // vectors per thread of the resident engine
+  const int64_t nvec = (a.n_cols / V + kResBlock - 1) / kResBlock;
   dim3 grid((unsigned)a.n_rows);
-  if (vec && plain && sizeof(T) == 2 && nvec <= 16) {
-    if (nvec <= 4)
-      ce_resident_kernel<T, 4><<<grid, kResBlock, 0, s>>>(a);
-    else if (nvec <= 8)
-      ce_resident_kernel<T, 8><<<grid, kResBlock, 0, s>>>(a);
+  if (vec && plain && sizeof(T) == 2 && nvec <= kResNL + kResNRMax && a.n_cols * (int64_t)sizeof(T) < 0x7fffffff) {
+    const int64_t nr = nvec > kResNL ? nvec - kResNL : 0;
+    if (nr <= 7)
+      ce_resident_kernel<T, 7><<<grid, kResBlock, 0, s>>>(a);
+    else if (nr <= 13)
+      ce_resident_kernel<T, 13><<<grid, kResBlock, 0, s>>>(a);
     else
-      ce_resident_kernel<T, 16><<<grid, kResBlock, 0, s>>>(a);
+      ce_resident_kernel<T, kResNRMax><<<grid, kResBlock, 0, s>>>(a);
   } else if (vec) {
     ce_stream_kernel<T, V><<<grid, kStreamBlock, 0, s>>>(a);
   } else {

@@ -11,15 +11,22 @@
 // Work decomposition: one work item = (token t, 16-byte column chunk c of the
 // lo half, group of HPT heads).  The item loads its cos/sin chunk once and
 // rotates that chunk in HPT heads (Q heads first, then K heads), so every
-// thread keeps 2*HPT independent 16-byte loads in flight.  Any element strides
-// for (batch, head, seq) are accepted, so the HF `transpose(1, 2)` view of a
-// [B, S, H, D] projection is rotated in place of memory order, with no copy.
+// thread keeps 2*HPT independent 16-byte loads in flight; the lanes that
+// share (t, head group) cover a head's half rows, so for head_dim 128 every
+// load and store instruction consumes whole 128-byte lines.  Any element
+// strides for (batch, head, seq) are accepted, so the HF `transpose(1, 2)`
+// view of a [B, S, H, D] projection is rotated in place of memory order, with
+// no copy.  Index math runs in 32 bits whenever every offset fits (the usual
+// case); x is touched once, so its 16-byte loads and stores are nontemporal.
+// The grid is capped at 8 workgroups per CU and strides over the items: on
+// MI355X that measured faster than one item per thread.
 #include "common.h"
 
 namespace {
 
 constexpr int kBlock = 256;
-constexpr int kHPT = 8;  // heads per work item
+constexpr int kHPT = 4;           // heads per work item
+constexpr int kMaxBlocks = 2048;  // 8 workgroups per CU
 
 struct RopeArgs {
   const void* q; int64_t q_sb, q_sh, q_ss;
@@ -33,24 +40,31 @@ struct RopeArgs {
   float sign;  // +1 forward, -1 backward
 };
 
-template <class T, int VEC>
+// I: index type of the item / x offset math (int32_t when every offset fits).
+template <class T, int VEC, class I>
 __global__ __launch_bounds__(kBlock) void rope_kernel(RopeArgs a) {
-  const int64_t stride = (int64_t)gridDim.x * kBlock;
-  for (int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x; i < a.n_items; i += stride) {
-    const int64_t c = i % a.chunks;
-    const int64_t rest = i / a.chunks;
-    const int64_t hg = rest % a.n_hgroups;
-    const int64_t t = rest / a.n_hgroups;
-    const int64_t b = t / a.seq_len;
-    const int64_t s = t - b * a.seq_len;
-    const int64_t pos = a.positions ? a.positions[t] : s;
-    const int64_t col = c * VEC;
+  constexpr bool kVec16 = VEC * sizeof(T) == 16;
+  const I stride = (I)gridDim.x * kBlock;
+  const I n_items = (I)a.n_items, chunks = (I)a.chunks, n_hgroups = (I)a.n_hgroups;
+  const I seq_len = (I)a.seq_len, n_q = (I)a.n_q, n_heads = (I)a.n_heads, half = (I)a.half;
+  for (I i = (I)blockIdx.x * kBlock + threadIdx.x; i < n_items; i += stride) {
+    const I c = i % chunks;
+    const I rest = i / chunks;
+    const I hg = rest % n_hgroups;
+    const I t = rest / n_hgroups;
+    const I b = t / seq_len;
+    const I s = t - b * seq_len;
+    const I col = c * VEC;
+    // table offsets stay 64-bit: positions are caller data
+    const int64_t pos = a.positions ? a.positions[t] : (int64_t)s;
+    const int64_t cso = (int64_t)b * a.cos_sb + pos * a.cos_ss + col;
+    const int64_t sno = (int64_t)b * a.sin_sb + pos * a.sin_ss + col;
 
     float cs[VEC], sn[VEC];
     {
-      const T* cp = (const T*)a.cos + b * a.cos_sb + pos * a.cos_ss + col;
-      const T* sp = (const T*)a.sin + b * a.sin_sb + pos * a.sin_ss + col;
-      if constexpr (VEC * sizeof(T) == 16) {
+      const T* cp = (const T*)a.cos + cso;
+      const T* sp = (const T*)a.sin + sno;
+      if constexpr (kVec16) {
         Vec16<T> cv = load16(cp), sv = load16(sp);
 #pragma unroll
         for (int j = 0; j < VEC; ++j) { cs[j] = to_f32(cv.v[j]); sn[j] = a.sign * to_f32(sv.v[j]); }
@@ -60,32 +74,31 @@ __global__ __launch_bounds__(kBlock) void rope_kernel(RopeArgs a) {
       }
     }
 
-    const int64_t h0 = hg * kHPT;
+    const I h0 = hg * kHPT;
     T lo[kHPT][VEC], hi[kHPT][VEC];
 #pragma unroll
     for (int u = 0; u < kHPT; ++u) {
-      const int64_t h = h0 + u;
-      if (h < a.n_heads) {
-        const T* src = h < a.n_q
-                           ? (const T*)a.q + b * a.q_sb + h * a.q_sh + s * a.q_ss + col
-                           : (const T*)a.k + b * a.k_sb + (h - a.n_q) * a.k_sh + s * a.k_ss + col;
-        if constexpr (VEC * sizeof(T) == 16) {
-          Vec16<T> l = load16(src), r = load16(src + a.half);
+      const I h = h0 + u;
+      if (h < n_heads) {
+        const T* src = h < n_q ? (const T*)a.q + (b * (I)a.q_sb + h * (I)a.q_sh + s * (I)a.q_ss + col)
+                               : (const T*)a.k + (b * (I)a.k_sb + (h - n_q) * (I)a.k_sh + s * (I)a.k_ss + col);
+        if constexpr (kVec16) {
+          Vec16<T> l = load16_nt(src), r = load16_nt(src + half);
 #pragma unroll
           for (int j = 0; j < VEC; ++j) { lo[u][j] = l.v[j]; hi[u][j] = r.v[j]; }
         } else {
 #pragma unroll
-          for (int j = 0; j < VEC; ++j) { lo[u][j] = src[j]; hi[u][j] = src[a.half + j]; }
+          for (int j = 0; j < VEC; ++j) { lo[u][j] = src[j]; hi[u][j] = src[half + j]; }
         }
       }
     }
 #pragma unroll
     for (int u = 0; u < kHPT; ++u) {
-      const int64_t h = h0 + u;
-      if (h < a.n_heads) {
-        T* dst = h < a.n_q ? (T*)a.qo + b * a.qo_sb + h * a.qo_sh + s * a.qo_ss + col
-                           : (T*)a.ko + b * a.ko_sb + (h - a.n_q) * a.ko_sh + s * a.ko_ss + col;
-        if constexpr (VEC * sizeof(T) == 16) {
+      const I h = h0 + u;
+      if (h < n_heads) {
+        T* dst = h < n_q ? (T*)a.qo + (b * (I)a.qo_sb + h * (I)a.qo_sh + s * (I)a.qo_ss + col)
+                         : (T*)a.ko + (b * (I)a.ko_sb + (h - n_q) * (I)a.ko_sh + s * (I)a.ko_ss + col);
+        if constexpr (kVec16) {
           Vec16<T> ol, oh;
 #pragma unroll
           for (int j = 0; j < VEC; ++j) {
@@ -93,14 +106,14 @@ __global__ __launch_bounds__(kBlock) void rope_kernel(RopeArgs a) {
             ol.v[j] = from_f32<T>(x0 * cs[j] - x1 * sn[j]);
             oh.v[j] = from_f32<T>(x1 * cs[j] + x0 * sn[j]);
           }
-          store16(dst, ol);
-          store16(dst + a.half, oh);
+          store16_nt(dst, ol);
+          store16_nt(dst + half, oh);
         } else {
 #pragma unroll
           for (int j = 0; j < VEC; ++j) {
             float x0 = to_f32(lo[u][j]), x1 = to_f32(hi[u][j]);
             dst[j] = from_f32<T>(x0 * cs[j] - x1 * sn[j]);
-            dst[a.half + j] = from_f32<T>(x1 * cs[j] + x0 * sn[j]);
+            dst[half + j] = from_f32<T>(x1 * cs[j] + x0 * sn[j]);
           }
         }
       }
@@ -108,21 +121,33 @@ __global__ __launch_bounds__(kBlock) void rope_kernel(RopeArgs a) {
   }
 }
 
+// Largest |element offset| any (b, h, s, d < D) address of a tensor reaches.
+int64_t max_offset(int64_t sb, int64_t sh, int64_t ss, int64_t nb, int64_t nh, int64_t ns, int64_t d) {
+  auto ext = [](int64_t st, int64_t n) { return n > 0 ? (st < 0 ? -st : st) * (n - 1) : 0; };
+  return ext(sb, nb) + ext(sh, nh) + ext(ss, ns) + d;
+}
+
 template <class T>
-int launch(RopeArgs a, int64_t head_dim, bool all_aligned, hipStream_t s) {
+int launch(RopeArgs a, bool all_aligned, bool offsets_fit32, hipStream_t s) {
   constexpr int V = 16 / sizeof(T);
   const bool vec = all_aligned && (a.half % V == 0);
   const int vw = vec ? V : 1;
   a.chunks = a.half / vw;
   a.n_hgroups = (a.n_heads + kHPT - 1) / kHPT;
   a.n_items = a.n_items * a.chunks * a.n_hgroups;  // n_items held the token count
-  int grid = grid_for(a.n_items, kBlock);
-  if (vec)
-    rope_kernel<T, V><<<grid, kBlock, 0, s>>>(a);
-  else
-    rope_kernel<T, 1><<<grid, kBlock, 0, s>>>(a);
+  int64_t blocks = (a.n_items + kBlock - 1) / kBlock;
+  if (blocks > kMaxBlocks) blocks = kMaxBlocks;
+  // the loop index runs up to n_items + one grid stride
+  const bool i32 = offsets_fit32 && a.n_items + (int64_t)kMaxBlocks * kBlock < 0x7fffffffLL;
+  const dim3 grid((unsigned)blocks);
+  if (vec) {
+    if (i32) rope_kernel<T, V, int32_t><<<grid, kBlock, 0, s>>>(a);
+    else rope_kernel<T, V, int64_t><<<grid, kBlock, 0, s>>>(a);
+  } else {
+    if (i32) rope_kernel<T, 1, int32_t><<<grid, kBlock, 0, s>>>(a);
+    else rope_kernel<T, 1, int64_t><<<grid, kBlock, 0, s>>>(a);
+  }
   FORGE_CHECK_LAUNCH();
-  (void)head_dim;
   return FORGE_OK;
 }
 
@@ -166,12 +191,20 @@ extern "C" int forge_rope(int dtype, const void* q, int64_t q_sb, int64_t q_sh, 
                      cos_sb, cos_ss, sin_sb, sin_ss})
     al = al && (st % V == 0);
 
+  // 32-bit x offsets when every Q / K / output address fits
+  const int64_t lim = 0x7fffffffLL;
+  const bool fit32 = max_offset(q_sb, q_sh, q_ss, batch, n_q, seq_len, head_dim) < lim &&
+                     max_offset(qo_sb, qo_sh, qo_ss, batch, n_q, seq_len, head_dim) < lim &&
+                     max_offset(k_sb, k_sh, k_ss, batch, n_kv, seq_len, head_dim) < lim &&
+                     max_offset(ko_sb, ko_sh, ko_ss, batch, n_kv, seq_len, head_dim) < lim &&
+                     batch * seq_len < lim;
+
   hipStream_t s = (hipStream_t)stream;
   switch (dtype) {
-    case FORGE_DTYPE_F32: return launch<float>(a, head_dim, al, s);
-    case FORGE_DTYPE_BF16: return launch<bf16_t>(a, head_dim, al, s);
-    case FORGE_DTYPE_F16: return launch<fp16_t>(a, head_dim, al, s);
-    case FORGE_DTYPE_F64: return launch<double>(a, head_dim, al, s);
+    case FORGE_DTYPE_F32: return launch<float>(a, al, fit32, s);
+    case FORGE_DTYPE_BF16: return launch<bf16_t>(a, al, fit32, s);
+    case FORGE_DTYPE_F16: return launch<fp16_t>(a, al, fit32, s);
+    case FORGE_DTYPE_F64: return launch<double>(a, al, fit32, s);
     default: return forge_set_error(FORGE_ERR_UNSUPPORTED, "rope: dtype %d", dtype);
   }
 }

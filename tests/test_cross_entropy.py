@@ -278,3 +278,35 @@ def test_baseline_config_bf16():
     gy = gv.gather(1, tv.unsqueeze(1)).squeeze(1)
     assert (gy < 0).all()
     del rows
+
+
+# Resident-row engine (2-byte logits, 16-byte aligned rows, no weight /
+# softcap / accuracy / predictions): a row is held on chip as up to 7 vectors
+# per thread in LDS plus NR in registers (NR buckets 7 / 13 / 19, 640 threads,
+# 8 values a vector), so V <= 26 * 640 * 8 = 133120.  These vocab sizes hit
+# each bucket, the exact maximum, and the first size past it (streaming
+# engine); the target sits in the first and last columns of some rows.
+RESIDENT_V = [4096, 35840, 50000, 80000, 102400, 128256, 133120, 133128]
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("vocab", RESIDENT_V)
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_resident_engine_buckets(vocab, dtype):
+    logits, target = _case(6, vocab, dtype, scalar=2.0, seed=vocab)
+    target[0], target[1], target[2] = 0, vocab - 1, -100
+    _check(logits, target, reduction="sum", ignore_index=-100)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_resident_engine_negative_rows_and_features(dtype):
+    """Rows whose every logit is negative take the float max pass (the packed
+    int16 max only orders non-negative values); label smoothing and z-loss
+    run in the resident engine too; a dominant logit leaves most p tiny."""
+    logits, target = _case(5, 50000, dtype, seed=7)
+    logits[0] = -logits[0].abs() - 1.0
+    logits[1] = -torch.rand(50000) * 0.01 - 30.0
+    logits[2, 123] = 60.0
+    target[2] = 123
+    _check(logits, target, reduction="mean", label_smoothing=0.1, lse_square_scale=1e-4, return_z_loss=True)
