@@ -45,8 +45,10 @@ def ce_reference(logits, target, weight=None, ignore_index=-100, lse_square_scal
     z_row = lse_square_scale * lse * lse
     n = valid.sum().to(compute_dtype)
     if reduction == "mean":
-        loss_row = loss_row / denom
-        z_row = z_row / n
+        # no valid row: every row is masked below; a unit divisor keeps the
+        # masked branch finite so the gradient is 0, not NaN (v2 semantics)
+        loss_row = loss_row / (denom if n > 0 else torch.ones_like(denom))
+        z_row = z_row / n.clamp_min(1)
     loss_row = torch.where(valid, loss_row + z_row, torch.zeros_like(loss_row))
     z_row = torch.where(valid, z_row, torch.zeros_like(z_row))
     if reduction == "none":
