@@ -98,6 +98,22 @@ def time_launches(launch_fn, n, warmup=3):
     return statistics.mean(a.elapsed_time(b) for a, b in evs)
 
 
+def run_steps(args, step_fn, prepare=None):
+    """time_steps unless --only-launches (then the step loop is skipped)."""
+    if args.only_launches:
+        return None, None
+    return time_steps(step_fn, args.steps, args.warmup, prepare)
+
+
+def rate(amount, ms, scale):
+    """amount per second / scale, or None when the step loop was skipped."""
+    return None if ms is None else round(amount / (ms * 1e-3) / scale, 1)
+
+
+def rnd(x, n):
+    return None if x is None else round(x, n)
+
+
 def cpu_time(fn, reps):
     fn()
     ts = []
@@ -143,9 +159,9 @@ def bench_swiglu(args):
         out = swiglu(gi, ui)
         out.backward(dout)
 
-    ms, wall = time_steps(step, args.steps, args.warmup)
+    ms, wall = run_steps(args, step)
     bytes_step = 8 * n * 4  # fwd 3 tensors + bwd 5 tensors, fp32
-    gbs = bytes_step / (ms * 1e-3) / 1e9
+    gbs = rate(bytes_step, ms, 1e9)
     # dominant kernel: backward (5 tensor passes)
     gf, uf, out = gate0.clone(), up0.clone(), torch.empty_like(gate0)
     st = L.stream_of(gf)
@@ -158,13 +174,13 @@ def bench_swiglu(args):
     res = {
         "config": {"workload": "swiglu_fwd_bwd", "dtype": "fp32", "shape": [R, C], "gate_multiplier": 1.0,
                    "down_multiplier": 1.0, "preserve_inputs": False},
-        "value": round(gbs, 1), "unit": "GB/s", "ms_per_step": round(ms, 5), "wall_ms_per_step": round(wall, 5),
-        "frac_of_hbm_peak": round(gbs / HBM_PEAK_GBS, 4), "algorithmic_bytes_per_step": bytes_step,
+        "value": gbs, "unit": "GB/s", "ms_per_step": rnd(ms, 5), "wall_ms_per_step": rnd(wall, 5),
+        "frac_of_hbm_peak": rnd(gbs and gbs / HBM_PEAK_GBS, 4), "algorithmic_bytes_per_step": bytes_step,
         "launches_ms": {"forge_swiglu_fwd": round(fwd_ms, 5), "forge_swiglu_bwd": round(bwd_ms, 5)},
         "roofline": _roof("hbm", bwd_bytes / (bwd_ms * 1e-3) / 1e9, HBM_PEAK_GBS, "GB/s", _traffic("swiglu_bwd")),
         "dtype": "f32",
     }
-    if not args.no_cpu_baseline:
+    if not (args.no_cpu_baseline or args.only_launches):
         from oracle.swiglu import swiglu_fwd_bwd
 
         rows = 512
@@ -210,24 +226,24 @@ def bench_rope(args):
         oq, ok = apply_rope(qi, ki, c, s)
         torch.autograd.backward((oq, ok), (dqv, dkv))
 
-    ms, wall = time_steps(step, args.steps, args.warmup)
+    ms, wall = run_steps(args, step)
     elems = q.numel() + k.numel()
     bytes_dir = 2 * elems * 2 + 2 * S * D * 2  # read+write Q,K + cos/sin (the reference's formula)
     bytes_step = 2 * bytes_dir
-    gbs = bytes_step / (ms * 1e-3) / 1e9
+    gbs = rate(bytes_step, ms, 1e9)
     oq, ok = torch.empty_like(qv), torch.empty_like(kv)
     launch_ms = time_launches(lambda i: _rope_launch(qv, kv, oq, ok, tabs[i % 2][0], tabs[i % 2][1], bool(i % 2)),
                               max(2 * args.steps, 20))
     res = {
         "config": {"workload": "rope_fwd_bwd", "dtype": "bf16", "q": [B, NQ, S, D], "k": [B, NKV, S, D],
                    "layout": "BSHD memory, HF transpose(1,2) view", "bases": [10000, 500000]},
-        "value": round(gbs, 1), "unit": "GB/s", "ms_per_step": round(ms, 5), "wall_ms_per_step": round(wall, 5),
-        "frac_of_hbm_peak": round(gbs / HBM_PEAK_GBS, 4), "algorithmic_bytes_per_step": bytes_step,
+        "value": gbs, "unit": "GB/s", "ms_per_step": rnd(ms, 5), "wall_ms_per_step": rnd(wall, 5),
+        "frac_of_hbm_peak": rnd(gbs and gbs / HBM_PEAK_GBS, 4), "algorithmic_bytes_per_step": bytes_step,
         "launches_ms": {"forge_rope": round(launch_ms, 5)},
         "roofline": _roof("hbm", bytes_dir / (launch_ms * 1e-3) / 1e9, HBM_PEAK_GBS, "GB/s", _traffic("rope")),
         "dtype": "bf16",
     }
-    if not args.no_cpu_baseline:
+    if not (args.no_cpu_baseline or args.only_launches):
         from oracle.rope import rope_fwd_bwd
 
         sb = 1024  # tokens of batch 0
@@ -269,27 +285,27 @@ def bench_ce(args):
         loss.backward()
         bufs[i] = None
 
-    ms, wall = time_steps(step, args.steps, args.warmup, prepare)
+    ms, wall = run_steps(args, step, prepare)
     bytes_step = V * 2 * (2 * n_valid + n_ign) + 8 * BT
-    gbs = bytes_step / (ms * 1e-3) / 1e9
+    gbs = rate(bytes_step, ms, 1e9)
     xb = logits0.clone()
     loss1d = torch.empty(BT, device="cuda")
     st = L.stream_of(xb)
     flags = L.CE_HAS_GRADIENTS | L.CE_REDUCTION_MEAN
     launch_ms = time_launches(
         lambda i: L.forge_ce_fwd(2, xb.data_ptr(), V, BT, V, target.data_ptr(), 1, None, loss1d.data_ptr(), None,
-                                 None, None, -100, float(n_valid), float(n_valid), 0.0, 0.0, 0.0, 0.0, flags, st),
+                                 None, None, -100, float(n_valid), float(n_valid), 0.0, 0.0, 0.0, 0.0, flags, None, st),
         max(args.steps, 10))
     res = {
         "config": {"workload": "cross_entropy_fwd_bwd", "dtype": "bf16", "logits": [BT, V], "ignored_rows": n_ign,
                    "reduction": "mean", "grad_output": 1.0},
-        "value": round(gbs, 1), "unit": "GB/s", "ms_per_step": round(ms, 5), "wall_ms_per_step": round(wall, 5),
-        "frac_of_hbm_peak": round(gbs / HBM_PEAK_GBS, 4), "algorithmic_bytes_per_step": bytes_step,
+        "value": gbs, "unit": "GB/s", "ms_per_step": rnd(ms, 5), "wall_ms_per_step": rnd(wall, 5),
+        "frac_of_hbm_peak": rnd(gbs and gbs / HBM_PEAK_GBS, 4), "algorithmic_bytes_per_step": bytes_step,
         "launches_ms": {"forge_ce_fwd": round(launch_ms, 5)},
         "roofline": _roof("hbm", bytes_step / (launch_ms * 1e-3) / 1e9, HBM_PEAK_GBS, "GB/s", _traffic("ce_fwd")),
         "dtype": "bf16",
     }
-    if not args.no_cpu_baseline:
+    if not (args.no_cpu_baseline or args.only_launches):
         import torch.nn.functional as F
 
         rows = 256
@@ -346,9 +362,9 @@ def bench_lora_mlp(args):
         out = LoRAMLPv6.apply(X, *params)
         out.backward(dY)
 
-    ms, wall = time_steps(step, args.steps, args.warmup)
+    ms, wall = run_steps(args, step)
     fl = flops(M, H, I, r)
-    tf = fl / (ms * 1e-3) / 1e12
+    tf = rate(fl, ms, 1e12)
     # dominant kernel: the fused gate/up GEMM + SwiGLU epilogue
     X2 = X.detach().reshape(M, H)
     Wg, Ag, Bg, sg, Wu, Au, Bu, su = [t.detach() if isinstance(t, torch.Tensor) else t for t in params[:8]]
@@ -363,14 +379,14 @@ def bench_lora_mlp(args):
     res = {
         "config": {"workload": "lora_mlp_fwd_bwd", "dtype": "bf16", "M": M, "H": H, "I": I, "rank": r, "alpha": 32,
                    "api": "LoRAMLPv6"},
-        "value": round(tf, 1), "unit": "TFLOP/s", "ms_per_step": round(ms, 4), "wall_ms_per_step": round(wall, 4),
-        "frac_of_mfma_peak": round(tf / BF16_PEAK_TFLOPS, 4), "algorithmic_flops_per_step": fl,
+        "value": tf, "unit": "TFLOP/s", "ms_per_step": rnd(ms, 4), "wall_ms_per_step": rnd(wall, 4),
+        "frac_of_mfma_peak": rnd(tf and tf / BF16_PEAK_TFLOPS, 4), "algorithmic_flops_per_step": fl,
         "launches_ms": {"forge_lora_mlp_gate_up": round(launch_ms, 4)},
         "roofline": _roof("mfma", gu_flops / (launch_ms * 1e-3) / 1e12, BF16_PEAK_TFLOPS, "TFLOP/s",
                           _traffic("lora_mlp_gate_up")),
         "dtype": "bf16",
     }
-    if not args.no_cpu_baseline:
+    if not (args.no_cpu_baseline or args.only_launches):
         from oracle.lora_mlp import fwd_bwd
 
         ms_ = 64
@@ -419,18 +435,31 @@ def bench_lora_qkv(args):
         Q, K_, V = lora_qkv_rope(X, Wq, Aq, Bq, s, Wk, Ak, Bk, s, Wv, Av, Bv, s, c, sn, pos, D)
         torch.autograd.backward((Q, K_, V), (dQ, dK, dV))
 
-    ms, wall = time_steps(step, args.steps, args.warmup)
+    ms, wall = run_steps(args, step)
     fl = T * flops_per_token(K, Hq, Hkv, r)
-    tf = fl / (ms * 1e-3) / 1e12
+    tf = rate(fl, ms, 1e12)
+    # dominant kernel: the forward GEMM (X [Wq;Wk;Wv]^T + LoRA-B segment, RoPE epilogue)
+    from forge_hip import _lib as L
+    from kernels.lora_qkv._impl import qkv_forward
+
+    Xd = X.detach()
+    rope = {"cos": c, "sin": sn, "positions": pos, "head_dim": D}
+    launch_ms = time_launches(lambda i: qkv_forward(Xd, Wq, Wk, Wv, Aq.detach(), Bq.detach(), s, Ak.detach(),
+                                                    Bk.detach(), s, Av.detach(), Bv.detach(), s, rope=rope),
+                              max(args.steps, 10))
+    fwd_flops = 2 * T * K * (Hq + 2 * Hkv) + 2 * T * 3 * r * K + 2 * T * r * (Hq + 2 * Hkv)
     res = {
         "config": {"workload": "lora_qkv_rope_fwd_bwd", "dtype": "bf16", "tokens": T, "seq_lens": lens,
                    "hidden": K, "q_heads": 32, "kv_heads": 8, "head_dim": D, "rank": r, "alpha": 128,
                    "rope_base": 500000},
-        "value": round(tf, 1), "unit": "TFLOP/s", "ms_per_step": round(ms, 4), "wall_ms_per_step": round(wall, 4),
-        "frac_of_mfma_peak": round(tf / BF16_PEAK_TFLOPS, 4), "algorithmic_flops_per_step": fl,
+        "value": tf, "unit": "TFLOP/s", "ms_per_step": rnd(ms, 4), "wall_ms_per_step": rnd(wall, 4),
+        "frac_of_mfma_peak": rnd(tf and tf / BF16_PEAK_TFLOPS, 4), "algorithmic_flops_per_step": fl,
+        "launches_ms": {"lora_qkv_forward (forge_lora_a + forge_lora_qkv_rope)": round(launch_ms, 4)},
+        "roofline": _roof("mfma", fwd_flops / (launch_ms * 1e-3) / 1e12, BF16_PEAK_TFLOPS, "TFLOP/s",
+                          _traffic("lora_qkv_fwd")),
         "dtype": "bf16",
     }
-    if not args.no_cpu_baseline:
+    if not (args.no_cpu_baseline or args.only_launches):
         from oracle.lora_qkv import qkv_rope_fwd_bwd
 
         n = 64
@@ -456,7 +485,28 @@ def _cpu(value, unit, sample):
             "sample": sample, "cpu_count": os.cpu_count()}
 
 
-BENCHES = {"swiglu": bench_swiglu, "rope": bench_rope, "ce": bench_ce, "lora_mlp": bench_lora_mlp,
+def bench_copy(args):
+    """Calibration workload for the rocprofv3 byte counters: forge_cast_f32_bf16
+    over 2^28 fp32 values reads exactly 1 GiB and writes exactly 512 MiB, so
+    FETCH_SIZE / WRITE_SIZE of its dispatches give the counters' scale."""
+    import torch
+    from forge_hip import _lib as L
+
+    n = 1 << 28
+    src = torch.randn(n, device="cuda")
+    dst = torch.empty(n, device="cuda", dtype=torch.bfloat16)
+    st = L.stream_of(src)
+    ms = time_launches(lambda i: L.forge_cast_f32_bf16(src.data_ptr(), n, dst.data_ptr(), n, 1, n, st),
+                       max(args.steps, 10))
+    moved = n * 4 + n * 2
+    gbs = moved / (ms * 1e-3) / 1e9
+    return {"config": {"workload": "copy_calibration", "read_bytes": n * 4, "write_bytes": n * 2},
+            "value": round(gbs, 1), "unit": "GB/s", "ms_per_step": round(ms, 5), "launches_ms":
+            {"forge_cast_f32_bf16": round(ms, 5)}, "roofline": _roof("hbm", gbs, HBM_PEAK_GBS, "GB/s", None),
+            "dtype": "f32"}
+
+
+BENCHES = {"copy": bench_copy, "swiglu": bench_swiglu, "rope": bench_rope, "ce": bench_ce, "lora_mlp": bench_lora_mlp,
            "lora_qkv": bench_lora_qkv}
 
 

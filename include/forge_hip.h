@@ -113,6 +113,11 @@ enum {
  * and — with FORGE_CE_HAS_GRADIENTS — dloss/dlogits written over the logits
  * (ignored rows are zero-filled).  weight (fp32 [n_cols]) is read only with
  * FORGE_CE_HAS_WEIGHT.  Scalars follow the reference kernel's arguments.
+ * stats (optional, device int64[4] from forge_ce_target_stats on the same
+ * stream): when given, n_non_ignore (and sum_non_ignore_weight without
+ * weights) are taken from stats[0] on the device, and nothing is written if
+ * stats[3] == 0 (targets out of range).  A row whose target is neither
+ * ignore_index nor in [0, n_cols) is always left untouched.
  * Replaces `forge_cross_entropy_kernel`
  * (kernels/cross_entropy/experiments/v2/cross_entropy_kernel_v2.py:65-338)
  * launched by `cross_entropy_forward` (same file :346-458). */
@@ -123,18 +128,32 @@ int forge_ce_fwd(int dtype, void* logits, int64_t ld, int64_t n_rows, int64_t n_
                  int64_t* predicted_tokens,
                  int64_t ignore_index, float n_non_ignore, float sum_non_ignore_weight,
                  float weight_sum, float lse_square_scale, float label_smoothing,
-                 float softcap, int flags, void* stream);
+                 float softcap, int flags, const int64_t* stats, void* stream);
 
-/* x[r, :] *= *grad_output (device fp32 scalar), in place.
+/* stats[0] = number of targets != ignore_index; stats[1], stats[2] = min and
+ * max of target * (target != ignore_index); stats[3] = 1 if that range lies in
+ * [0, n_cols), else 0.  Device int64[4], written on `stream`.  Replaces the
+ * host-side `.item()` reads and bounds asserts of `cross_entropy_forward`
+ * (kernels/cross_entropy/experiments/v2/cross_entropy_kernel_v2.py:374-387),
+ * whose values the host still reads (for the same AssertionError) after the
+ * main kernel is queued. */
+int forge_ce_target_stats(const int64_t* target, int64_t target_stride, int64_t n_rows,
+                          int64_t ignore_index, int64_t n_cols, int64_t* stats, void* stream);
+
+/* x[r, :] *= *grad_output (device scalar of grad_dtype: fp32, bf16 or fp16),
+ * in place; a no-op when *grad_output == 1 (the reference's torch.equal
+ * skip, :465-467, decided on the device so the host does not wait).
  * Replaces `_element_mul_kernel`
  * (kernels/cross_entropy/experiments/v2/cross_entropy_kernel_v2.py:49-62). */
 int forge_ce_scale(int dtype, void* x, int64_t ld, int64_t n_rows, int64_t n_cols,
-                   const float* grad_output, void* stream);
+                   const void* grad_output, int grad_dtype, void* stream);
 
-/* Sum of an fp32 vector into out[0] (fp32), deterministic two-level tree.
- * Used for the loss reduction in place of `torch.sum(loss_1d)`
+/* Sum of an fp32 vector into out[0] (fp32), deterministic two-level tree;
+ * when out_cast is given the sum is also stored there rounded to cast_dtype
+ * (fp32, bf16 or fp16: the loss in the logits' dtype).  Used for the loss
+ * reduction in place of `torch.sum(loss_1d)` and the cast that follows
  * (kernels/cross_entropy/experiments/v2/cross_entropy_kernel_v2.py:451). */
-int forge_sum_f32(const float* x, int64_t n, float* out, void* stream);
+int forge_sum_f32(const float* x, int64_t n, float* out, void* out_cast, int cast_dtype, void* stream);
 
 /* ------------------------------------------------------------------------
  * bf16 MFMA GEMM core (fp32 accumulation) with fused LoRA epilogues

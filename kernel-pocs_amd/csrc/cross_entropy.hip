@@ -11,12 +11,12 @@
 //     reduction scaling of :298-330.
 //
 // Two row engines:
-//   * ce_resident_kernel: the whole row is held in registers (one 1024-thread
-//     workgroup per row), so the logits are read from HBM once and written once.
-//     Pass A finds the exact row max, pass B sums exp(x - m) and keeps
-//     p = exp(x - m) as fp16 in place of the input, pass C writes p/d.
-//     Used for the common case (no class weights / softcap / argmax) when the
-//     row fits in 1024 * 8 * NV elements.
+//   * ce_resident_kernel: the whole row is held on chip (LDS + registers of
+//     one 512-thread workgroup, two rows per CU), so the logits are read from
+//     HBM once and written once.  Pass A finds the exact row max, pass B sums
+//     exp(x - m) and keeps p = exp(x - m) as fp16 in place of the input, pass
+//     C writes p/d.  Used for the common case (2-byte logits, no class
+//     weights / softcap / argmax) when the row fits in 512 * 32 * 8 elements.
 //   * ce_stream_kernel: any row length and every feature; the row is streamed
 //     twice (online max/sum, then gradient), the second read largely served by
 //     the L2 / Infinity Cache.
@@ -42,7 +42,24 @@ struct CeArgs {
   int64_t ignore_index;
   float n_non_ignore, sum_non_ignore_weight, weight_sum, lse_square_scale, label_smoothing, softcap;
   int flags;
+  const int64_t* stats;  // optional device [n_valid, min, max, in_range] from forge_ce_target_stats
 };
+
+// Row preamble shared by both engines.  With device-side target stats the
+// non-ignored count comes from them (no host round trip), and a launch whose
+// targets failed the range check touches nothing: the host raises the
+// reference's AssertionError once it reads the same stats.  A row whose own
+// target is out of range is left untouched too (a direct C-ABI caller that
+// skipped the check must not make the kernel read outside the row).
+// Returns false when the row must be skipped.
+__device__ __forceinline__ bool ce_prologue(CeArgs& a, int64_t y) {
+  if (a.stats) {
+    if (a.stats[3] == 0) return false;
+    a.n_non_ignore = (float)a.stats[0];
+    if (!(a.flags & FORGE_CE_HAS_WEIGHT)) a.sum_non_ignore_weight = a.n_non_ignore;
+  }
+  return y == a.ignore_index || (y >= 0 && y < a.n_cols);
+}
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
@@ -175,6 +192,7 @@ __global__ __launch_bounds__(kStreamBlock) void ce_stream_kernel(CeArgs a) {
   __shared__ int64_t redi[kStreamWaves];
   const int64_t row = blockIdx.x;
   const int64_t y = a.target[row * a.target_stride];
+  if (!ce_prologue(a, y)) return;
   T* xr = (T*)a.x + row * a.ld;
   const int64_t V = a.n_cols;
   const bool vec = VEC > 1;
@@ -289,23 +307,26 @@ __global__ __launch_bounds__(kStreamBlock) void ce_stream_kernel(CeArgs a) {
 // ---------------------------------------------------------------------------
 // Resident engine (plain CE with optional label smoothing / z-loss)
 //
-// One 640-thread workgroup per row, two workgroups per CU.  The row is read
+// One 512-thread workgroup per row, two workgroups per CU.  The row is read
 // from HBM once and written once: thread t owns the 16-byte vectors
-// t + 640 i; vectors i < NL live in LDS (filled by LDS-DMA loads, no
-// registers involved), vectors NL <= i < NL + NR in registers.  With two rows
-// per CU, one row's exp / reduction work overlaps the other row's memory
-// traffic (the VALU work per element is comparable to its HBM time on this
-// part, so a single row per CU would serialise the two).
+// t + 512 i; vectors i < NL live in LDS (filled by LDS-DMA loads, no
+// registers involved), vectors NL <= i < NL + NR in registers (up to 8 + 24
+// vectors = 131072 bf16 values per row, within the 128-VGPR budget of 4
+// waves per SIMD, with no spills).  With two rows per CU, one row's exp /
+// reduction work overlaps the other row's memory traffic.  Every global
+// access carries the nontemporal policy (the row is touched once): measured
+// on MI355X at [8192, 128256] bf16, 811 -> 765 us.
 //   pass A: row max via packed 16-bit integer max on the raw bf16/fp16 bits
 //           (order-preserving for non-negative values; a row whose max is
 //           negative takes a float max pass instead)
 //   pass B: p = exp(x - m) in fp32, row sum, p kept as fp16 in place of x
 //   pass C: dlogits = p * scale - shift (target column corrected), stored
 // ---------------------------------------------------------------------------
-constexpr int kResBlock = 640;
+constexpr int kResBlock = 512;
 constexpr int kResWaves = kResBlock / 64;
-constexpr int kResNL = 7;     // vectors per thread in LDS (70 KB per workgroup)
-constexpr int kResNRMax = 19; // vectors per thread in registers (76 VGPRs)
+constexpr int kResNL = 8;      // vectors per thread in LDS (64 KB per workgroup)
+constexpr int kResNRMax = 24;  // vectors per thread in registers (96 VGPRs)
+constexpr int kNT = 2;         // buffer-instruction cache policy: nontemporal
 
 typedef __fp16 half2_t __attribute__((ext_vector_type(2)));
 typedef short short2_t __attribute__((ext_vector_type(2)));
@@ -324,7 +345,7 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t row_rsrc(const void* base, uin
 __device__ __forceinline__ short2_t as_s2(uint32_t w) { return __builtin_bit_cast(short2_t, w); }
 
 template <class T, int NR>
-__global__ __launch_bounds__(kResBlock) __attribute__((amdgpu_waves_per_eu(5, 5)))
+__global__ __launch_bounds__(kResBlock) __attribute__((amdgpu_waves_per_eu(4, 4)))
 void ce_resident_kernel(CeArgs a) {
   constexpr int VEC = 16 / sizeof(T);
   constexpr int NL = kResNL;
@@ -333,6 +354,7 @@ void ce_resident_kernel(CeArgs a) {
   __shared__ float redf[2 * kResWaves];
   const int64_t row = blockIdx.x;
   const int64_t y = a.target[row * a.target_stride];
+  if (!ce_prologue(a, y)) return;
   T* xr = (T*)a.x + row * a.ld;
   const int64_t V = a.n_cols;
   const int tid = threadIdx.x;
@@ -357,7 +379,7 @@ void ce_resident_kernel(CeArgs a) {
   for (int i = 0; i < NL; ++i) {
     if (valid(i)) {
       LDS_AS void* dst = (LDS_AS void*)((LDS_AS char*)lds_row + (i * kResWaves + wave) * 1024);
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, dst, 16, voff, i * VSTRIDE, 0, 0);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, dst, 16, voff, i * VSTRIDE, 0, kNT);
     }
   }
   uint4 reg[NR];
@@ -365,7 +387,7 @@ void ce_resident_kernel(CeArgs a) {
   for (int i = 0; i < NR; ++i) {
     reg[i] = make_uint4(0, 0, 0, 0);
     if (valid(NL + i)) {
-      i32x4_t v = __builtin_amdgcn_raw_buffer_load_b128(rs, (int)voff, (NL + i) * VSTRIDE, 0);
+      i32x4_t v = __builtin_amdgcn_raw_buffer_load_b128(rs, (int)voff, (NL + i) * VSTRIDE, kNT);
       reg[i] = make_uint4((uint32_t)v.x, (uint32_t)v.y, (uint32_t)v.z, (uint32_t)v.w);
     }
   }
@@ -480,7 +502,7 @@ void ce_resident_kernel(CeArgs a) {
           if (j == yj) o.v[j] = gy;  // static indices: no scratch array
       }
       const i32x4_t ov = {(int)o.raw.x, (int)o.raw.y, (int)o.raw.z, (int)o.raw.w};
-      __builtin_amdgcn_raw_buffer_store_b128(ov, rs, (int)voff, i * VSTRIDE, 0);
+      __builtin_amdgcn_raw_buffer_store_b128(ov, rs, (int)voff, i * VSTRIDE, kNT);
     };
 #pragma unroll 1
     for (int i = 0; i < NL; ++i)
@@ -506,10 +528,10 @@ int launch_ce(CeArgs a, hipStream_t s) {
   dim3 grid((unsigned)a.n_rows);
   if (vec && plain && sizeof(T) == 2 && nvec <= kResNL + kResNRMax && a.n_cols * (int64_t)sizeof(T) < 0x7fffffff) {
     const int64_t nr = nvec > kResNL ? nvec - kResNL : 0;
-    if (nr <= 7)
-      ce_resident_kernel<T, 7><<<grid, kResBlock, 0, s>>>(a);
-    else if (nr <= 13)
-      ce_resident_kernel<T, 13><<<grid, kResBlock, 0, s>>>(a);
+    if (nr <= 8)
+      ce_resident_kernel<T, 8><<<grid, kResBlock, 0, s>>>(a);
+    else if (nr <= 16)
+      ce_resident_kernel<T, 16><<<grid, kResBlock, 0, s>>>(a);
     else
       ce_resident_kernel<T, kResNRMax><<<grid, kResBlock, 0, s>>>(a);
   } else if (vec) {
@@ -526,8 +548,11 @@ int launch_ce(CeArgs a, hipStream_t s) {
 // ---------------------------------------------------------------------------
 template <class T, int VEC>
 __global__ __launch_bounds__(256) void ce_scale_kernel(T* x, int64_t ld, int64_t rows, int64_t cols,
-                                                       const float* g) {
-  const float s = *g;
+                                                       const void* g, int g_dtype) {
+  const float s = g_dtype == FORGE_DTYPE_BF16 ? (float)*(const bf16_t*)g
+                  : g_dtype == FORGE_DTYPE_F16 ? (float)*(const fp16_t*)g
+                                               : *(const float*)g;
+  if (s == 1.0f) return;  // the reference skips grad_output == 1 (torch.equal), here without a host sync
   const int64_t cpr = cols / VEC;
   const int64_t n = rows * cpr;
   for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) {
@@ -545,27 +570,75 @@ __global__ __launch_bounds__(256) void ce_scale_kernel(T* x, int64_t ld, int64_t
 }
 
 template <class T>
-int launch_scale(void* x, int64_t ld, int64_t rows, int64_t cols, const float* g, hipStream_t s) {
+int launch_scale(void* x, int64_t ld, int64_t rows, int64_t cols, const void* g, int g_dtype, hipStream_t s) {
   constexpr int V = 16 / sizeof(T);
   const bool vec = aligned16(x) && ld % V == 0 && cols % V == 0;
+  // 8 workgroups per CU, grid-stride: full bandwidth when scaling, and a
+  // cheap launch when grad_output == 1 makes every workgroup exit at once
   if (vec) {
-    int grid = grid_for(rows * cols / V, 256);
-    ce_scale_kernel<T, V><<<grid, 256, 0, s>>>((T*)x, ld, rows, cols, g);
+    int grid = grid_for(rows * cols / V, 256, 2048);
+    ce_scale_kernel<T, V><<<grid, 256, 0, s>>>((T*)x, ld, rows, cols, g, g_dtype);
   } else {
-    int grid = grid_for(rows * cols, 256);
-    ce_scale_kernel<T, 1><<<grid, 256, 0, s>>>((T*)x, ld, rows, cols, g);
+    int grid = grid_for(rows * cols, 256, 2048);
+    ce_scale_kernel<T, 1><<<grid, 256, 0, s>>>((T*)x, ld, rows, cols, g, g_dtype);
   }
   FORGE_CHECK_LAUNCH();
   return FORGE_OK;
 }
 
 // Single-workgroup deterministic sum (the vector is one value per row).
-__global__ __launch_bounds__(1024) void sum_f32_kernel(const float* x, int64_t n, float* out) {
+// n_valid, min / max of target * (target != ignore) (ignored rows count as 0,
+// as the reference's masked max / min do), and whether that range is inside
+// [0, n_cols).  One workgroup; labels are a few thousand to a few million.
+__global__ __launch_bounds__(1024) void ce_target_stats_kernel(const int64_t* t, int64_t stride, int64_t n,
+                                                               int64_t ignore, int64_t n_cols, int64_t* out) {
+  __shared__ int64_t red[3][16];
+  int64_t cnt = 0, mn = INT64_MAX, mx = INT64_MIN;
+  for (int64_t i = threadIdx.x; i < n; i += 1024) {
+    const int64_t v = t[i * stride];
+    const bool valid = v != ignore;
+    const int64_t m = valid ? v : 0;
+    cnt += valid;
+    mn = m < mn ? m : mn;
+    mx = m > mx ? m : mx;
+  }
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) {
+    cnt += __shfl_xor(cnt, off, 64);
+    const int64_t a = __shfl_xor(mn, off, 64), b = __shfl_xor(mx, off, 64);
+    mn = a < mn ? a : mn;
+    mx = b > mx ? b : mx;
+  }
+  const int w = threadIdx.x >> 6;
+  if ((threadIdx.x & 63) == 0) { red[0][w] = cnt; red[1][w] = mn; red[2][w] = mx; }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    for (int i = 1; i < 16; ++i) {
+      cnt += red[0][i];
+      mn = red[1][i] < mn ? red[1][i] : mn;
+      mx = red[2][i] > mx ? red[2][i] : mx;
+    }
+    out[0] = cnt;
+    out[1] = mn;
+    out[2] = mx;
+    out[3] = (mn >= 0 && mx < n_cols) ? 1 : 0;
+  }
+}
+
+__global__ __launch_bounds__(1024) void sum_f32_kernel(const float* x, int64_t n, float* out, void* out_cast,
+                                                       int cast_dtype) {
   __shared__ float red[16];
   float acc = 0.f;
   for (int64_t i = threadIdx.x; i < n; i += 1024) acc += x[i];
   acc = block_sum<16>(acc, red);
-  if (threadIdx.x == 0) out[0] = acc;
+  if (threadIdx.x == 0) {
+    out[0] = acc;
+    if (out_cast) {
+      if (cast_dtype == FORGE_DTYPE_BF16) *(bf16_t*)out_cast = (bf16_t)acc;
+      else if (cast_dtype == FORGE_DTYPE_F16) *(fp16_t*)out_cast = (fp16_t)acc;
+      else *(float*)out_cast = acc;
+    }
+  }
 }
 
 }  // namespace
@@ -575,7 +648,8 @@ extern "C" int forge_ce_fwd(int dtype, void* logits, int64_t ld, int64_t n_rows,
                             float* loss, float* z_loss, float* token_accuracy,
                             int64_t* predicted_tokens, int64_t ignore_index, float n_non_ignore,
                             float sum_non_ignore_weight, float weight_sum, float lse_square_scale,
-                            float label_smoothing, float softcap, int flags, void* stream) {
+                            float label_smoothing, float softcap, int flags, const int64_t* stats,
+                            void* stream) {
   if (n_rows < 0 || n_cols < 0) return forge_set_error(FORGE_ERR_INVALID, "ce_fwd: negative shape");
   if (n_rows == 0) return FORGE_OK;
   if (n_rows > 0x7fffffff) return forge_set_error(FORGE_ERR_INVALID, "ce_fwd: too many rows");
@@ -597,6 +671,7 @@ extern "C" int forge_ce_fwd(int dtype, void* logits, int64_t ld, int64_t n_rows,
   a.sum_non_ignore_weight = sum_non_ignore_weight; a.weight_sum = weight_sum;
   a.lse_square_scale = lse_square_scale; a.label_smoothing = label_smoothing; a.softcap = softcap;
   a.flags = flags;
+  a.stats = stats;
   hipStream_t s = (hipStream_t)stream;
   switch (dtype) {
     case FORGE_DTYPE_F32: return launch_ce<float>(a, s);
@@ -607,20 +682,34 @@ extern "C" int forge_ce_fwd(int dtype, void* logits, int64_t ld, int64_t n_rows,
 }
 
 extern "C" int forge_ce_scale(int dtype, void* x, int64_t ld, int64_t n_rows, int64_t n_cols,
-                              const float* grad_output, void* stream) {
+                              const void* grad_output, int grad_dtype, void* stream) {
   if (n_rows <= 0 || n_cols <= 0) return FORGE_OK;
+  if (grad_dtype != FORGE_DTYPE_F32 && grad_dtype != FORGE_DTYPE_BF16 && grad_dtype != FORGE_DTYPE_F16)
+    return forge_set_error(FORGE_ERR_UNSUPPORTED, "ce_scale: grad_output dtype %d", grad_dtype);
   hipStream_t s = (hipStream_t)stream;
   switch (dtype) {
-    case FORGE_DTYPE_F32: return launch_scale<float>(x, ld, n_rows, n_cols, grad_output, s);
-    case FORGE_DTYPE_BF16: return launch_scale<bf16_t>(x, ld, n_rows, n_cols, grad_output, s);
-    case FORGE_DTYPE_F16: return launch_scale<fp16_t>(x, ld, n_rows, n_cols, grad_output, s);
+    case FORGE_DTYPE_F32: return launch_scale<float>(x, ld, n_rows, n_cols, grad_output, grad_dtype, s);
+    case FORGE_DTYPE_BF16: return launch_scale<bf16_t>(x, ld, n_rows, n_cols, grad_output, grad_dtype, s);
+    case FORGE_DTYPE_F16: return launch_scale<fp16_t>(x, ld, n_rows, n_cols, grad_output, grad_dtype, s);
     default: return forge_set_error(FORGE_ERR_UNSUPPORTED, "ce_scale: dtype %d", dtype);
   }
 }
 
-extern "C" int forge_sum_f32(const float* x, int64_t n, float* out, void* stream) {
+extern "C" int forge_ce_target_stats(const int64_t* target, int64_t target_stride, int64_t n_rows,
+                                     int64_t ignore_index, int64_t n_cols, int64_t* stats, void* stream) {
+  if (n_rows <= 0) return forge_set_error(FORGE_ERR_INVALID, "ce_target_stats: n_rows must be positive");
+  if (!target || !stats) return forge_set_error(FORGE_ERR_INVALID, "ce_target_stats: null pointer");
+  ce_target_stats_kernel<<<1, 1024, 0, (hipStream_t)stream>>>(target, target_stride, n_rows, ignore_index, n_cols,
+                                                              stats);
+  FORGE_CHECK_LAUNCH();
+  return FORGE_OK;
+}
+
+extern "C" int forge_sum_f32(const float* x, int64_t n, float* out, void* out_cast, int cast_dtype, void* stream) {
   if (n < 0) return forge_set_error(FORGE_ERR_INVALID, "sum_f32: negative length");
-  sum_f32_kernel<<<1, 1024, 0, (hipStream_t)stream>>>(x, n, out);
+  if (out_cast && cast_dtype != FORGE_DTYPE_F32 && cast_dtype != FORGE_DTYPE_BF16 && cast_dtype != FORGE_DTYPE_F16)
+    return forge_set_error(FORGE_ERR_UNSUPPORTED, "sum_f32: cast dtype %d", cast_dtype);
+  sum_f32_kernel<<<1, 1024, 0, (hipStream_t)stream>>>(x, n, out, out_cast, cast_dtype);
   FORGE_CHECK_LAUNCH();
   return FORGE_OK;
 }

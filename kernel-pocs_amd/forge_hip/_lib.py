@@ -92,10 +92,11 @@ forge_ce_fwd = _decl(
     "forge_ce_fwd",
     [c_int, c_vp, c_i64, c_i64, c_i64, c_vp, c_i64, c_vp, c_vp, c_vp, c_vp, c_vp, c_i64]
     + [c_f32] * 6
-    + [c_int, c_vp],
+    + [c_int, c_vp, c_vp],
 )
-forge_ce_scale = _decl("forge_ce_scale", [c_int, c_vp, c_i64, c_i64, c_i64, c_vp, c_vp])
-forge_sum_f32 = _decl("forge_sum_f32", [c_vp, c_i64, c_vp, c_vp])
+forge_ce_target_stats = _decl("forge_ce_target_stats", [c_vp, c_i64, c_i64, c_i64, c_i64, c_vp, c_vp])
+forge_ce_scale = _decl("forge_ce_scale", [c_int, c_vp, c_i64, c_i64, c_i64, c_vp, c_int, c_vp])
+forge_sum_f32 = _decl("forge_sum_f32", [c_vp, c_i64, c_vp, c_vp, c_int, c_vp])
 forge_gemm = _decl(
     "forge_gemm",
     [c_i64, c_i64, ctypes.POINTER(GemmSegment), c_int, c_int, c_int, c_vp, c_i64, c_int, c_f32, c_f32, c_int, c_int, c_vp],
@@ -128,7 +129,7 @@ forge_cast_f32_bf16 = _decl("forge_cast_f32_bf16", [c_vp, c_i64, c_vp, c_i64, c_
 EXPORTED = [
     "forge_version", "forge_last_error", "forge_arch_ok",
     "forge_swiglu_fwd", "forge_swiglu_bwd", "forge_rope",
-    "forge_ce_fwd", "forge_ce_scale", "forge_sum_f32",
+    "forge_ce_fwd", "forge_ce_target_stats", "forge_ce_scale", "forge_sum_f32",
     "forge_gemm", "forge_lora_mlp_gate_up", "forge_lora_mlp_down_bwd", "forge_lora_qkv_rope",
     "forge_lora_a", "forge_zero", "forge_cast_f32_bf16",
 ]

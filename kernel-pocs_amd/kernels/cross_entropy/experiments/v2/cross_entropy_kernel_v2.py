@@ -37,13 +37,53 @@ class CrossEntropyOutput:
     predicted_tokens: Optional[torch.Tensor] = None
 
 
-def _target_stats(target: torch.Tensor, ignore_index: int):
-    """n_non_ignore and the masked target range in one host sync (the
-    reference takes them with .item() and two asserts, :382-387)."""
-    mask = target != ignore_index
-    masked = target * mask
-    n, tmax, tmin = torch.stack([mask.sum(), masked.max(), masked.min()]).tolist()
-    return mask, int(n), int(tmax), int(tmin)
+def _target_stats_async(target: torch.Tensor, ignore_index: int, n_cols: int):
+    """Queues forge_ce_target_stats and a copy of its 4 values to pinned host
+    memory; returns (device stats, host stats, event).  The reference reads
+    the same values with `.item()` (:374-387) before launching; here the main
+    kernel is queued first and the host waits only for this copy."""
+    stats = torch.empty(4, dtype=torch.int64, device=target.device)
+    L.check(
+        L.forge_ce_target_stats(target.data_ptr(), target.stride(-1), target.numel(), int(ignore_index), int(n_cols),
+                                stats.data_ptr(), L.stream_of(target)),
+        "forge_ce_target_stats",
+    )
+    # the copy runs on a side stream so the main stream goes straight on to
+    # the CE kernel (no copy packet between the two)
+    main = torch.cuda.current_stream(target.device)
+    ready = torch.cuda.Event()
+    ready.record(main)
+    side = _side_stream(target.device)
+    side.wait_event(ready)
+    host = torch.empty(4, dtype=torch.int64, pin_memory=True)
+    with torch.cuda.stream(side):
+        host.copy_(stats, non_blocking=True)
+        done = torch.cuda.Event()
+        done.record(side)
+    stats.record_stream(side)
+    return stats, host, done
+
+
+_SIDE_STREAMS = {}
+
+
+def _side_stream(device) -> "torch.cuda.Stream":
+    """One default-priority side stream per device for the stats copy."""
+    key = torch.device(device).index
+    s = _SIDE_STREAMS.get(key)
+    if s is None:
+        s = _SIDE_STREAMS[key] = torch.cuda.Stream(device=device)
+    return s
+
+
+def _check_targets(host: torch.Tensor, ev, n_cols: int) -> int:
+    """The reference's bounds asserts (:382-387) on the masked target range;
+    returns n_non_ignore."""
+    ev.synchronize()
+    n, tmin, tmax, _ = host.tolist()
+    assert tmax < n_cols, f"Target {tmax} is out of bounds. Expected < {n_cols}"
+    assert tmin >= 0, f"Target {tmin} is out of bounds. Expected >= 0"
+    return int(n)
 
 
 def _cross_entropy_forward_impl(
@@ -58,9 +98,11 @@ def _cross_entropy_forward_impl(
     return_z_loss,
     return_token_accuracy=False,
     return_predicted_tokens=False,
+    out_dtype=None,
 ):
-    """Returns (loss_fp32, z_loss_fp32, token_accuracy, predicted_tokens, _input)
-    before the final cast of loss / z_loss to the logits dtype."""
+    """Returns (loss, z_loss, token_accuracy, predicted_tokens, _input); loss
+    and z_loss are fp32 unless out_dtype is given (then already cast to it,
+    the cast of a reduced loss fused into the sum kernel)."""
     assert isinstance(return_z_loss, bool), f"return_z_loss must be True or False. Got: {return_z_loss}"
     assert isinstance(return_token_accuracy, bool), (
         f"return_token_accuracy must be True or False. Got: {return_token_accuracy}"
@@ -77,27 +119,31 @@ def _cross_entropy_forward_impl(
     token_accuracy_1d = torch.empty(BT, dtype=torch.float32, device=dev) if return_token_accuracy else None
     predicted_tokens_1d = torch.empty(BT, dtype=torch.int64, device=dev) if return_predicted_tokens else None
 
+    if target.dtype != torch.int64:
+        target = target.to(torch.int64)
+    if target.stride(-1) != 1:
+        target = target.contiguous()
+    if _input.stride(-1) != 1:
+        _input = _input.contiguous()
+
+    stats = None
+    n_non_ignore = 0
     if BT > 0:
-        target_mask, n_non_ignore, tmax, tmin = _target_stats(target, ignore_index)
-        assert tmax < V, f"Target {tmax} is out of bounds. Expected < {V}"
-        assert tmin >= 0, f"Target {tmin} is out of bounds. Expected >= 0"
-    else:
-        target_mask, n_non_ignore = target != ignore_index, 0
-    sum_non_ignore_weight = float(n_non_ignore)
+        stats, stats_host, stats_ev = _target_stats_async(target, ignore_index, V)
+    sum_non_ignore_weight = 0.0
     weight_sum = 0.0
     if weight is not None:
+        # the weighted sums need validated targets: check first, as the reference does
+        if BT > 0:
+            n_non_ignore = _check_targets(stats_host, stats_ev, V)
         assert weight.shape[0] == V, f"If given, weight has to be a Tensor of size V. Got: {weight.shape}"
         assert torch.is_floating_point(weight), (
             f"If given, weight has to be a Tensor of floating point dtype. Got: {weight.dtype}"
         )
+        target_mask = target != ignore_index
         sum_non_ignore_weight = torch.gather(weight, dim=0, index=target.masked_select(target_mask)).sum().item()
         weight_sum = weight.sum().item()
         weight = weight.to(torch.float32).contiguous()
-
-    if _input.stride(-1) != 1:
-        _input = _input.contiguous()
-    if target.stride(-1) != 1:
-        target = target.contiguous()
 
     flags = 0
     if _input.requires_grad:
@@ -116,6 +162,7 @@ def _cross_entropy_forward_impl(
         flags |= L.CE_REDUCTION_MEAN
 
     if BT > 0:
+        # n_non_ignore (unweighted) is read by the kernel from `stats`
         L.check(
             L.forge_ce_fwd(
                 L.dtype_code(_input.dtype), _input.data_ptr(), _input.stride(-2), BT, V,
@@ -123,27 +170,35 @@ def _cross_entropy_forward_impl(
                 loss_1d.data_ptr(), L.ptr(z_loss_1d), L.ptr(token_accuracy_1d), L.ptr(predicted_tokens_1d),
                 int(ignore_index), float(n_non_ignore), float(sum_non_ignore_weight), float(weight_sum),
                 float(lse_square_scale), float(label_smoothing), float(softcap or 0.0), flags,
-                L.stream_of(_input),
+                stats.data_ptr(), L.stream_of(_input),
             ),
             "forge_ce_fwd",
         )
+        if weight is None:
+            # the kernel is already queued (and writes nothing if this fails)
+            n_non_ignore = _check_targets(stats_host, stats_ev, V)
 
     if reduction == "none":
         loss = loss_1d
         z_loss = z_loss_1d if return_z_loss else None
         token_accuracy = token_accuracy_1d if return_token_accuracy else None
     else:
-        loss = _sum_f32(loss_1d)
-        z_loss = _sum_f32(z_loss_1d) if return_z_loss else None
+        loss = _sum_f32(loss_1d, out_dtype)
+        z_loss = _sum_f32(z_loss_1d, out_dtype) if return_z_loss else None
         token_accuracy = torch.sum(token_accuracy_1d) / n_non_ignore if return_token_accuracy else None
     predicted_tokens = predicted_tokens_1d if return_predicted_tokens else None
     return loss, z_loss, token_accuracy, predicted_tokens, _input
 
 
-def _sum_f32(x: torch.Tensor) -> torch.Tensor:
+def _sum_f32(x: torch.Tensor, out_dtype=None) -> torch.Tensor:
+    """fp32 sum of x (one deterministic workgroup); with out_dtype, the sum
+    rounded to that dtype, from the same kernel."""
     out = torch.empty((), dtype=torch.float32, device=x.device)
-    L.check(L.forge_sum_f32(x.data_ptr(), x.numel(), out.data_ptr(), L.stream_of(x)), "forge_sum_f32")
-    return out
+    cast = None if out_dtype in (None, torch.float32) else torch.empty((), dtype=out_dtype, device=x.device)
+    L.check(L.forge_sum_f32(x.data_ptr(), x.numel(), out.data_ptr(), L.ptr(cast),
+                            L.dtype_code(out_dtype) if cast is not None else L.DTYPE_F32, L.stream_of(x)),
+            "forge_sum_f32")
+    return out if cast is None else cast
 
 
 def cross_entropy_forward(
@@ -164,9 +219,9 @@ def cross_entropy_forward(
     dloss/dlogits."""
     loss, z_loss, acc, pred, _input = _cross_entropy_forward_impl(
         _input, target, weight, ignore_index, lse_square_scale, label_smoothing, reduction, softcap,
-        return_z_loss, return_token_accuracy, return_predicted_tokens,
+        return_z_loss, return_token_accuracy, return_predicted_tokens, out_dtype=_input.dtype,
     )
-    loss = loss.to(_input.dtype)
+    loss = loss.to(_input.dtype)  # reduced losses already are (no-op); 'none' rows are cast here
     if z_loss is not None:
         z_loss = z_loss.to(_input.dtype)
     return loss, z_loss, acc, pred, _input
@@ -175,16 +230,19 @@ def cross_entropy_forward(
 def cross_entropy_backward(_input, grad_output):
     """cross_entropy_kernel_v2.py:461-485."""
     # If cross entropy is the last layer, grad_output is 1.0: nothing to do.
-    if torch.equal(grad_output, torch.tensor(1.0, device=grad_output.device)):
-        pass
-    elif grad_output.ndim > 0:
+    # For a scalar grad_output forge_ce_scale makes that test on the device
+    # (a no-op kernel when it is 1.0), so the host does not wait on the GPU.
+    if grad_output.ndim > 0:
         _input = _input * grad_output.unsqueeze(dim=1)
     else:
         BT, V = _input.shape
-        g = grad_output.detach().to(torch.float32).reshape(1).contiguous()
+        g = grad_output.detach()
+        if g.dtype not in (torch.float32, torch.bfloat16, torch.float16):
+            g = g.to(torch.float32)
+        g = g.reshape(1).contiguous()
         L.check(
             L.forge_ce_scale(L.dtype_code(_input.dtype), _input.data_ptr(), _input.stride(-2), BT, V,
-                             g.data_ptr(), L.stream_of(_input)),
+                             g.data_ptr(), L.dtype_code(g.dtype), L.stream_of(_input)),
             "forge_ce_scale",
         )
     return _input

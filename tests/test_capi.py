@@ -42,7 +42,7 @@ def test_status_codes_and_messages():
     assert rc == 1
     rc = L.forge_rope(2, *([16, 0, 0, 0] * 4), *([16, 0, 0] * 2), None, 1, 4, 3, 8, 128, 0, None)
     assert rc == 1 and b"n_q" in L.forge_last_error()
-    rc = L.forge_ce_fwd(2, 16, 4, 2, 8, 16, 1, None, None, None, None, None, -100, *([0.0] * 6), 0, None)
+    rc = L.forge_ce_fwd(2, 16, 4, 2, 8, 16, 1, None, None, None, None, None, -100, *([0.0] * 6), 0, None, None)
     assert rc == 1 and b"ld" in L.forge_last_error()
     rc = L.forge_lora_qkv_rope(16, 64, 100, 256, 0, *([16] * 20)[:14], 16, 16, 8, None, 96, 1, None)
     assert rc == 2
@@ -50,4 +50,4 @@ def test_status_codes_and_messages():
 
 def test_zero_size_calls_are_noops():
     assert L.forge_swiglu_fwd(0, None, None, 0, None, 0, 0, 0, 1.0, 1.0, None) == 0
-    assert L.forge_ce_fwd(2, None, 0, 0, 0, None, 1, None, None, None, None, None, -100, *([0.0] * 6), 0, None) == 0
+    assert L.forge_ce_fwd(2, None, 0, 0, 0, None, 1, None, None, None, None, None, -100, *([0.0] * 6), 0, None, None) == 0

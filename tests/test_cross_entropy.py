@@ -145,12 +145,41 @@ def test_all_ignored_mean_is_zero_not_nan():
 
 @pytest.mark.gpu
 @pytest.mark.parametrize("bad_target", [-1, 128])
-def test_out_of_bounds_target_raises(bad_target):
-    logits = torch.randn(8, 128, device="cuda", requires_grad=True)
-    target = torch.randint(0, 128, (8,), device="cuda")
-    target[2] = bad_target
+@pytest.mark.parametrize("vocab,dtype", [(128, torch.float32), (4096, torch.bfloat16)])
+def test_out_of_bounds_target_raises(bad_target, vocab, dtype):
+    """The reference asserts the masked target range before launching
+    (cross_entropy_kernel_v2.py:382-387).  Here the kernel is queued before
+    the host reads the range, so it must leave the logits untouched when the
+    range check fails (both engines: fp32 -> streaming, bf16 -> resident)."""
+    logits = torch.randn(8, vocab, device="cuda").to(dtype)
+    before = logits.clone()
+    target = torch.randint(0, vocab, (8,), device="cuda")
+    target[2] = vocab if bad_target == 128 else bad_target
+    x = logits.requires_grad_(True)
     with pytest.raises((AssertionError, IndexError), match="out of bounds"):
-        forge_cross_entropy(logits, target)
+        forge_cross_entropy(x, target)
+    torch.cuda.synchronize()
+    assert torch.equal(logits.detach(), before)
+
+
+@pytest.mark.gpu
+def test_c_abi_skips_rows_with_out_of_range_targets():
+    """Called directly (no stats), forge_ce_fwd leaves a row whose target is
+    outside [0, V) untouched and processes the others."""
+    BT, V = 4, 256
+    x = torch.randn(BT, V, device="cuda")
+    ref_x = x.clone()
+    t = torch.tensor([3, V + 5, -7, 10], device="cuda")
+    loss = torch.full((BT,), -1.0, device="cuda")
+    rc = L.forge_ce_fwd(0, x.data_ptr(), V, BT, V, t.data_ptr(), 1, None, loss.data_ptr(), None, None, None, -100,
+                        2.0, 2.0, 0.0, 0.0, 0.0, 0.0, L.CE_HAS_GRADIENTS, None, L.stream_of(x))
+    assert rc == 0
+    torch.cuda.synchronize()
+    assert torch.equal(x[1], ref_x[1]) and torch.equal(x[2], ref_x[2])
+    assert loss[1].item() == -1.0 and loss[2].item() == -1.0
+    _, _, rows, _, _, g = ce_reference(ref_x[[0, 3]].cpu(), t[[0, 3]].cpu(), reduction="none")
+    torch.testing.assert_close(loss[[0, 3]].cpu(), rows, rtol=1e-5, atol=1e-6)
+    torch.testing.assert_close(x[[0, 3]].cpu(), g, rtol=1e-5, atol=1e-6)
 
 
 @pytest.mark.gpu
@@ -281,12 +310,13 @@ def test_baseline_config_bf16():
 
 
 # Resident-row engine (2-byte logits, 16-byte aligned rows, no weight /
-# softcap / accuracy / predictions): a row is held on chip as up to 7 vectors
-# per thread in LDS plus NR in registers (NR buckets 7 / 13 / 19, 640 threads,
-# 8 values a vector), so V <= 26 * 640 * 8 = 133120.  These vocab sizes hit
-# each bucket, the exact maximum, and the first size past it (streaming
-# engine); the target sits in the first and last columns of some rows.
-RESIDENT_V = [4096, 35840, 50000, 80000, 102400, 128256, 133120, 133128]
+# softcap / accuracy / predictions): a row is held on chip as up to 8 vectors
+# per thread in LDS plus NR in registers (NR buckets 8 / 16 / 24, 512
+# threads, 8 values a vector), so V <= 32 * 512 * 8 = 131072.  These vocab
+# sizes hit each bucket and its edges, the exact maximum, and the first size
+# past it (streaming engine); the target sits in the first and last columns
+# of some rows.
+RESIDENT_V = [4096, 32768, 50000, 65536, 65544, 98304, 128256, 131072, 131080]
 
 
 @pytest.mark.gpu
