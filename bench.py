@@ -16,7 +16,8 @@ events on the stream the kernel is launched on.  roofline.traffic comes from
 profiles/traffic.json (rocprofv3 FETCH_SIZE + WRITE_SIZE per dispatch, scaled
 by the copy-kernel calibration) when present, else null.
 cpu_baseline: the oracle (the reference's PyTorch path restated, oracle/) on
-the host cores on a bounded sample of the same workload, scaled to the metric.
+the host cores on a bounded sample of the same workload (about 10 s of CPU
+work per kernel, median per call), scaled to the metric.
 """
 from __future__ import annotations
 
@@ -40,8 +41,8 @@ METRIC = "fwd+bwd GB/s (% of HBM peak) for SwiGLU/RoPE/CE; LoRA-MLP MFMA TFLOPS"
 def _parse():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--kernels", default="swiglu,rope,ce,lora_mlp,lora_qkv")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--only-launches", action="store_true",
@@ -114,14 +115,21 @@ def rnd(x, n):
     return None if x is None else round(x, n)
 
 
-def cpu_time(fn, reps):
+CPU_BUDGET_S = 10.0
+
+
+def cpu_time(fn, budget_s=CPU_BUDGET_S, min_reps=3):
+    """Median seconds per call of fn on the host: one untimed call, then
+    repeated calls until about budget_s of CPU work (at least min_reps).
+    Returns (median, reps)."""
     fn()
     ts = []
-    for _ in range(reps):
+    t_start = time.perf_counter()
+    while len(ts) < min_reps or time.perf_counter() - t_start < budget_s:
         t0 = time.perf_counter()
         fn()
         ts.append(time.perf_counter() - t0)
-    return statistics.median(ts)
+    return statistics.median(ts), len(ts)
 
 
 def _traffic(name):
@@ -183,10 +191,11 @@ def bench_swiglu(args):
     if not (args.no_cpu_baseline or args.only_launches):
         from oracle.swiglu import swiglu_fwd_bwd
 
-        rows = 512
+        rows = R  # the whole workload
         gc, uc, dc = gate0[:rows].cpu(), up0[:rows].cpu(), dout[:rows].cpu()
-        t = cpu_time(lambda: swiglu_fwd_bwd(gc, uc, dc), 5)
-        res["cpu_baseline"] = _cpu(8 * rows * C * 4 / t / 1e9, "GB/s", f"{rows} of {R} rows, fp32 fwd+bwd, median of 5")
+        t, reps = cpu_time(lambda: swiglu_fwd_bwd(gc, uc, dc))
+        res["cpu_baseline"] = _cpu(8 * rows * C * 4 / t / 1e9, "GB/s",
+                                   f"all {R} rows, reference torch path in fp32 + autograd, fwd+bwd, median of {reps}")
     return res
 
 
@@ -246,15 +255,16 @@ def bench_rope(args):
     if not (args.no_cpu_baseline or args.only_launches):
         from oracle.rope import rope_fwd_bwd
 
-        sb = 1024  # tokens of batch 0
+        sb = S  # all of batch 0: a quarter of the workload
         qc = q[:1, :sb].transpose(1, 2).cpu()
         kc = k[:1, :sb].transpose(1, 2).cpu()
         dqc, dkc = dq[:1, :sb].transpose(1, 2).cpu(), dk[:1, :sb].transpose(1, 2).cpu()
         c, s = tabs[0][0][:, :sb].cpu(), tabs[0][1][:, :sb].cpu()
-        t = cpu_time(lambda: rope_fwd_bwd(qc, kc, c, s, dqc, dkc), 5)
+        t, reps = cpu_time(lambda: rope_fwd_bwd(qc, kc, c, s, dqc, dkc))
         frac = sb / (B * S)
         res["cpu_baseline"] = _cpu(bytes_step * frac / t / 1e9, "GB/s",
-                                   f"{sb} of {B * S} tokens, HF formula in fp32, fwd+bwd, median of 5")
+                                   f"{sb} of {B * S} tokens (batch 0), HF formula in fp32 + autograd, fwd+bwd, "
+                                   f"median of {reps}")
     return res
 
 
@@ -308,7 +318,7 @@ def bench_ce(args):
     if not (args.no_cpu_baseline or args.only_launches):
         import torch.nn.functional as F
 
-        rows = 256
+        rows = 1024
         xc = logits0[:rows].cpu()
         tc = target[:rows].cpu()
 
@@ -316,10 +326,11 @@ def bench_ce(args):
             x = xc.clone().requires_grad_(True)
             F.cross_entropy(x, tc, ignore_index=-100).backward()
 
-        t = cpu_time(cpu_step, 3)
+        t, reps = cpu_time(cpu_step)
         nv = int((tc != -100).sum())
         res["cpu_baseline"] = _cpu((V * 2 * (2 * nv + (rows - nv)) + 8 * rows) / t / 1e9, "GB/s",
-                                   f"{rows} of {BT} rows, F.cross_entropy bf16 fwd+bwd, median of 3")
+                                   f"{rows} of {BT} rows, F.cross_entropy (the reference's CPU path) bf16 fwd+bwd, "
+                                   f"median of {reps}")
     return res
 
 
@@ -389,12 +400,12 @@ def bench_lora_mlp(args):
     if not (args.no_cpu_baseline or args.only_launches):
         from oracle.lora_mlp import fwd_bwd
 
-        ms_ = 64
+        ms_ = 512
         cpu_params = [t.detach().cpu() if isinstance(t, torch.Tensor) else t for t in params]
         Xc, dYc = X.detach()[:, :ms_].cpu(), dY[:, :ms_].cpu()
-        t = cpu_time(lambda: fwd_bwd(Xc, dYc, cpu_params, compute_dtype=torch.bfloat16), 3)
+        t, reps = cpu_time(lambda: fwd_bwd(Xc, dYc, cpu_params, compute_dtype=torch.bfloat16))
         res["cpu_baseline"] = _cpu(flops(ms_, H, I, r) / t / 1e12, "TFLOP/s",
-                                   f"{ms_} of {M} tokens, reference LoRAMLP formulas in bf16, fwd+bwd, median of 3")
+                                   f"{ms_} of {M} tokens, reference LoRAMLP formulas in bf16, fwd+bwd, median of {reps}")
     return res
 
 
@@ -462,14 +473,14 @@ def bench_lora_qkv(args):
     if not (args.no_cpu_baseline or args.only_launches):
         from oracle.lora_qkv import qkv_rope_fwd_bwd
 
-        n = 64
+        n = 1024
         cpu_p = [t.detach().cpu() if isinstance(t, torch.Tensor) else t
                  for t in (Wq, Wk, Wv, Aq, Bq, s, Ak, Bk, s, Av, Bv, s)]
         pc = pos[:n].cpu()
         args_ = (X.detach()[:n].cpu(), dQ[:n].cpu(), dK[:n].cpu(), dV[:n].cpu(), cpu_p, c.cpu()[pc], sn.cpu()[pc], D)
-        t = cpu_time(lambda: qkv_rope_fwd_bwd(*args_, compute_dtype=torch.bfloat16), 3)
+        t, reps = cpu_time(lambda: qkv_rope_fwd_bwd(*args_, compute_dtype=torch.bfloat16))
         res["cpu_baseline"] = _cpu(n * flops_per_token(K, Hq, Hkv, r) / t / 1e12, "TFLOP/s",
-                                   f"{n} of {T} tokens, reference LoRAQKV + HF RoPE in bf16, fwd+bwd, median of 3")
+                                   f"{n} of {T} tokens, reference LoRAQKV + HF RoPE in bf16, fwd+bwd, median of {reps}")
     return res
 
 
@@ -521,7 +532,8 @@ def main():
     if not torch.cuda.is_available():
         print(json.dumps({"error": "no ROCm GPU visible"}))
         return 1
-    torch.set_num_threads(os.cpu_count() or 1)
+    # the host share this process may use (OMP_NUM_THREADS on the GPU box), else every core
+    torch.set_num_threads(int(os.environ.get("OMP_NUM_THREADS", 0)) or os.cpu_count() or 1)
     names = [n for n in args.kernels.split(",") if n]
     results = {}
     for n in names:

@@ -13,6 +13,11 @@
 // (gate_up = [.., 2H]) is the same kernel with up = gate + H and ld = 2H.
 // One thread owns one 16-byte vector of each operand; UNROLL vectors are in
 // flight per thread so each CU keeps enough bytes outstanding to saturate HBM.
+// Loads are ordinary (the backward re-reads gate/up right after the forward,
+// largely from the Infinity Cache); stores are nontemporal, so the outputs do
+// not displace those lines and the next kernel does not pay their write-back
+// (measured on MI355X in a fwd+bwd loop at [2048, 11008] fp32: 142 -> 135 us
+// per step).
 #include "common.h"
 
 namespace {
@@ -93,7 +98,7 @@ __global__ __launch_bounds__(kBlock) void swiglu_fwd_kernel(
 #pragma unroll
           for (int j = 0; j < VEC; ++j)
             o.v[j] = from_f32<T>(swiglu_fwd_elem<T>(to_f32(gv[u][j]), to_f32(uv[u][j]), gm, dm));
-          store16(op, o);
+          store16_nt(op, o);
         } else {
 #pragma unroll
           for (int j = 0; j < VEC; ++j)
@@ -148,8 +153,8 @@ __global__ __launch_bounds__(kBlock) void swiglu_bwd_kernel(
             og.v[j] = from_f32<T>(a);
             ou.v[j] = from_f32<T>(b);
           }
-          store16(dgp, og);
-          store16(dup_, ou);
+          store16_nt(dgp, og);
+          store16_nt(dup_, ou);
         } else {
 #pragma unroll
           for (int j = 0; j < VEC; ++j) {

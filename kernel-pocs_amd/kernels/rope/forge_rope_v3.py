@@ -25,7 +25,7 @@ from forge_hip import _lib as L
 
 # launch geometry of csrc/rope.hip (fixed; there is no autotuning)
 _BLOCK = 256
-_HEADS_PER_ITEM = 8
+_HEADS_PER_ITEM = 4
 
 
 def _rope_launch(q_in, k_in, q_out, k_out, cos, sin, backward_pass: bool, positions=None):
