@@ -19,7 +19,20 @@ static int launch_cfg(const GemmArgs& a, hipStream_t s) {
   const int64_t tn = (a.N + OUT_BN - 1) / OUT_BN;
   if (tm * tn > 0x7fffffffLL) return forge_set_error(FORGE_ERR_INVALID, "gemm: too many tiles");
   dim3 grid((unsigned)(tm * tn), 1, (unsigned)a.split_k);
-  gemm_kernel<BM, BN, WM, WN, AL, BL, BMODE, EPI><<<grid, WM * WN * 64, 0, s>>>(a);
+  constexpr bool CAN_STAGE = staged_ok(BM, BN, WM, WN, EPI);
+  const bool staged = CAN_STAGE && a.ep.vec_ok;
+  if constexpr (BM == 256 && BN == 256 && AL == ROW && BL == COL) {
+    // both operands K-contiguous: the LDS-DMA engine (64-deep tiles, 2 stages)
+    if (staged)
+      gemm_dma_kernel<BM, BN, WM, WN, BMODE, EPI, 64, 2, CAN_STAGE><<<grid, WM * WN * 64, 0, s>>>(a);
+    else
+      gemm_dma_kernel<BM, BN, WM, WN, BMODE, EPI, 64, 2, false><<<grid, WM * WN * 64, 0, s>>>(a);
+  } else {
+    if (staged)
+      gemm_kernel<BM, BN, WM, WN, AL, BL, BMODE, EPI, CAN_STAGE><<<grid, WM * WN * 64, 0, s>>>(a);
+    else
+      gemm_kernel<BM, BN, WM, WN, AL, BL, BMODE, EPI, false><<<grid, WM * WN * 64, 0, s>>>(a);
+  }
   FORGE_CHECK_LAUNCH();
   return FORGE_OK;
 }
@@ -73,8 +86,18 @@ static int check_segs(const GemmArgs& a, int al, int bl) {
   return FORGE_OK;
 }
 
-int run(int cfg, int al, int bl, int epi, const GemmArgs& a, hipStream_t s) {
-  if (int e = check_segs(a, al, bl)) return e;
+int run(int cfg, int al, int bl, int epi, const GemmArgs& args, hipStream_t s) {
+  if (int e = check_segs(args, al, bl)) return e;
+  // 16-byte vector epilogue when every buffer it touches allows it
+  GemmArgs a = args;
+  {
+    const EpiArgs& ep = a.ep;
+    bool ok = aligned16(ep.c) && ep.ldc % 8 == 0;
+    if (ep.e || ep.g) ok = ok && aligned16(ep.e) && aligned16(ep.g) && ep.ld_eg % 8 == 0;
+    if (ep.cos || ep.sin)
+      ok = ok && aligned16(ep.cos) && aligned16(ep.sin) && ep.cs_ld % 8 == 0 && ep.head_dim % 16 == 0;
+    a.ep.vec_ok = ok ? 1 : 0;
+  }
   // transposed-operand tiles are fetched as 8-row blocks of 16-byte vectors
   if (al == COL && a.M % 8 != 0)
     return forge_set_error(FORGE_ERR_INVALID, "gemm: A^T layout needs M %% 8 == 0 (M=%lld)", (long long)a.M);

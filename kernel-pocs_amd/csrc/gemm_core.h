@@ -8,13 +8,21 @@
 //
 // Tiling: BM x BN x 64 block tile, WAVES_M x WAVES_N waves, each wave owns a
 // (BM/WAVES_M) x (BN/WAVES_N) sub-tile computed with v_mfma_f32_32x32x16_bf16.
-// LDS holds both operands k-contiguous ([rows][64 + 8 pad] bf16, 144-byte row
-// pitch so the 16-byte fragment reads of 8 consecutive lanes hit distinct
-// banks), double-buffered: the global loads of tile k+1 are in flight while
-// the MFMAs of tile k run, one barrier per K tile.
-// Operands whose K dimension is not contiguous in memory (A^T, or a [K][N]
-// B) are loaded as 8x8 blocks of 16-byte vectors and transposed in registers
-// (v_perm_b32) before the LDS store, so both layouts feed the same LDS image.
+// Two main loops feed the same MFMA core:
+//   * gemm_dma_kernel (256 x 256 tiles, both operands K-contiguous: X W^T and
+//     its LoRA segments, the SwiGLU-dual and RoPE GEMMs): global -> LDS by
+//     LDS-DMA (buffer_load ... lds, no VGPR staging, no ds_write), XOR-swizzled
+//     unpadded LDS rows, a 2-stage ring (measured on MI355X: 918 -> 1018
+//     TFLOP/s on the 8192 x 28672 x 4096 gate/up GEMM; a 4-stage ring of
+//     32-deep tiles and an interleaved DMA issue were no faster);
+//   * gemm_kernel (every layout): loads through registers into padded LDS
+//     rows ([rows][64 + 8 pad] bf16, 144-byte pitch, conflict-free fragment
+//     reads), double-buffered.  Operands whose K dimension is not contiguous
+//     in memory (A^T, or a [K][N] B) are loaded as 8x8 blocks of 16-byte
+//     vectors and transposed in registers (v_perm_b32) before the LDS store.
+// Epilogues with bf16 outputs on 256 x 256 tiles are "staged": the fp32 tile
+// goes through LDS so that side inputs and outputs move as 16-byte vectors
+// (measured: the SwiGLU-backward GEMM of LoRA-MLP 1.93 -> ~1.2 ms).
 //
 // MFMA lane layouts (v_mfma_f32_32x32x16_bf16, 64 lanes):
 //   A operand: lane l holds A[row = l % 32][k = 8 * (l / 32) + 0..7]
@@ -80,6 +88,7 @@ struct EpiArgs {
   const int64_t* positions;  // per output row (token); nullptr = row index
   int64_t rope_cols;         // columns [0, rope_cols) are rotated
   int head_dim;              // 64 or 128
+  int vec_ok;                // every output / side buffer 16-byte aligned with pitches % 8 == 0
 };
 
 struct GemmArgs {
@@ -292,7 +301,327 @@ __device__ __forceinline__ void tile_coords(int64_t tiles_m, int64_t tiles_n, in
 constexpr int SG_MFMA = 0x008;
 constexpr int SG_DS_READ = 0x100;
 
-template <int BM, int BN, int WAVES_M, int WAVES_N, int A_LAYOUT, int B_LAYOUT, int BMODE, int EPI>
+// ---------------------------------------------------------------------------
+// Staged epilogue (256 x 256 tiles, bf16 outputs): the accumulators go through
+// LDS, half a tile (128 rows) at a time in fp32, so that every thread then
+// owns contiguous 8-column chunks: side inputs (C for beta, e / g, cos / sin)
+// are read and every output is written with 16-byte vector accesses instead
+// of one 2-byte access per lane and element.  Values are rounded exactly as
+// in the per-element epilogue (single rounding of the fp32 result).
+// ---------------------------------------------------------------------------
+constexpr int STAGED_PITCH = 256 + 4;                   // floats per LDS row (bank-shifted)
+constexpr int STAGED_BYTES = 128 * STAGED_PITCH * 4;    // one 128-row half tile
+
+__device__ __forceinline__ uint4 ld16(const void* p) { return *reinterpret_cast<const uint4*>(p); }
+__device__ __forceinline__ void st16(void* p, uint4 v) { *reinterpret_cast<uint4*>(p) = v; }
+__device__ __forceinline__ void unpack8(uint4 v, float (&f)[8]) {
+  const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    f[2 * i] = __uint_as_float(w[i] << 16);
+    f[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
+  }
+}
+__device__ __forceinline__ uint4 pack8(const float (&f)[8]) {
+  uint32_t w[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const __bf16 lo = (__bf16)f[2 * i], hi = (__bf16)f[2 * i + 1];
+    w[i] = (uint32_t)__builtin_bit_cast(uint16_t, lo) | ((uint32_t)__builtin_bit_cast(uint16_t, hi) << 16);
+  }
+  return make_uint4(w[0], w[1], w[2], w[3]);
+}
+
+// Tiles and epilogues the staged epilogue serves.
+constexpr bool staged_ok(int bm, int bn, int wm, int wn, int epi) {
+  return bm == 256 && bn == 256 && wm == 2 && wn == 2 &&
+         (epi == EPI_STORE_BF16 || epi == EPI_SWIGLU_FWD || epi == EPI_SWIGLU_BWD || epi == EPI_ROPE);
+}
+
+template <int BMODE, int EPI>
+__device__ __forceinline__ void epilogue_staged(const GemmArgs& args, f32x16 (&acc)[4][4], int64_t m0, int64_t n0,
+                                                int lane, int wm, int wn, float* lds) {
+  constexpr int P = STAGED_PITCH;
+  constexpr int NT = 256;
+  const EpiArgs& ep = args.ep;
+  const int64_t M = args.M, N = args.N;
+  const int tid = threadIdx.x;
+  __syncthreads();  // the main loop's LDS reads are done
+#pragma unroll 1
+  for (int pass = 0; pass < 2; ++pass) {
+    if (pass) __syncthreads();  // pass 0's readers are done with the buffer
+    if (wm == pass) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+          for (int r = 0; r < 16; ++r)
+            lds[(i * 32 + 8 * (r / 4) + 4 * (lane / 32) + r % 4) * P + wn * 128 + j * 32 + lane % 32] = acc[i][j][r];
+    }
+    __syncthreads();
+    const int64_t mrow0 = m0 + pass * 128;
+    if constexpr (BMODE == B_DUAL) {
+      // LDS column layout per wave wn: 32-col groups (gate jp=0, up jp=0, gate jp=1, up jp=1);
+      // output column c (0..127) -> wave c/64, pair (c%64)/32
+#pragma unroll 2
+      for (int it = 0; it < 128 * 16 / NT; ++it) {
+        const int id = it * NT + tid;
+        const int rr = id / 16, c = (id % 16) * 8;
+        const int64_t m = mrow0 + rr, n = n0 + c;
+        if (m >= M || n >= N) continue;
+        const int lc = (c / 64) * 128 + ((c % 64) / 32) * 64 + c % 32;
+        const float* pg = lds + rr * P + lc;
+        float e[8], g[8], h[8];
+#pragma unroll
+        for (int q = 0; q < 8; ++q) { e[q] = pg[q]; g[q] = pg[32 + q]; h[q] = silu_f(e[q]) * g[q]; }
+        const int64_t off = m * ep.ld_eg + n;
+        if (n + 8 <= N) {
+          st16(ep.e + off, pack8(e));
+          st16(ep.g + off, pack8(g));
+          st16((__bf16*)ep.c + m * ep.ldc + n, pack8(h));
+        } else {
+          for (int q = 0; q < 8 && n + q < N; ++q) {
+            ep.e[off + q] = (__bf16)e[q];
+            ep.g[off + q] = (__bf16)g[q];
+            ((__bf16*)ep.c)[m * ep.ldc + n + q] = (__bf16)h[q];
+          }
+        }
+      }
+    } else {
+#pragma unroll 2
+      for (int it = 0; it < 128 * 32 / NT; ++it) {
+        const int id = it * NT + tid;
+        const int rr = id / 32, c = (id % 32) * 8;
+        const int64_t m = mrow0 + rr, n = n0 + c;
+        if (m >= M || n >= N) continue;
+        const float* pv = lds + rr * P + c;
+        float v[8];
+#pragma unroll
+        for (int q = 0; q < 8; ++q) v[q] = pv[q];
+        const bool full = n + 8 <= N;
+        if constexpr (EPI == EPI_STORE_BF16) {
+#pragma unroll
+          for (int q = 0; q < 8; ++q) {
+            float a = ep.alpha;
+            if (ep.alpha_group > 0) {
+              const int64_t grp = (n + q) / ep.alpha_group;
+              a = ep.alphas[grp < 4 ? grp : 3];
+            }
+            v[q] *= a;
+          }
+          __bf16* cp = (__bf16*)ep.c + m * ep.ldc + n;
+          if (full) {
+            if (ep.beta != 0.f) {
+              float cv[8];
+              unpack8(ld16(cp), cv);
+#pragma unroll
+              for (int q = 0; q < 8; ++q) v[q] += ep.beta * cv[q];
+            }
+            st16(cp, pack8(v));
+          } else {
+            for (int q = 0; q < 8 && n + q < N; ++q) {
+              float o = v[q];
+              if (ep.beta != 0.f) o += ep.beta * (float)cp[q];
+              cp[q] = (__bf16)o;
+            }
+          }
+        } else if constexpr (EPI == EPI_SWIGLU_BWD) {
+          const int64_t off = m * ep.ld_eg + n;
+          float ev[8], gv[8], hv[8], dfv[8], dev[8];
+          if (full) {
+            unpack8(ld16(ep.e + off), ev);
+            unpack8(ld16(ep.g + off), gv);
+          } else {
+            for (int q = 0; q < 8; ++q) {
+              ev[q] = n + q < N ? (float)ep.e[off + q] : 0.f;
+              gv[q] = n + q < N ? (float)ep.g[off + q] : 0.f;
+            }
+          }
+#pragma unroll
+          for (int q = 0; q < 8; ++q) {
+            const float dw = bf16r(v[q]);
+            const float e = ev[q], g = gv[q];
+            const float se = sigmoid_f(e);
+            const float f = bf16r(se * e);
+            hv[q] = f * g;
+            dfv[q] = dw * f;
+            const float dg = bf16r(dw * g);
+            dev[q] = dg * se * (1.0f + e * (1.0f - se));
+          }
+          if (full) {
+            st16((__bf16*)ep.c + m * ep.ldc + n, pack8(hv));
+            st16(ep.e + off, pack8(dfv));
+            st16(ep.g + off, pack8(dev));
+          } else {
+            for (int q = 0; q < 8 && n + q < N; ++q) {
+              ((__bf16*)ep.c)[m * ep.ldc + n + q] = (__bf16)hv[q];
+              ep.e[off + q] = (__bf16)dfv[q];
+              ep.g[off + q] = (__bf16)dev[q];
+            }
+          }
+        } else if constexpr (EPI == EPI_ROPE) {
+          if (n < ep.rope_cols) {
+            // the 128-column wave tile holds whole heads: partner half in LDS
+            const int half = ep.head_dim / 2;
+            const int in_head = (int)(n % ep.head_dim);
+            const bool lo = in_head < half;
+            const float* pp = lds + rr * P + (lo ? c + half : c - half);
+            const int d = in_head % half;
+            const int64_t pos = ep.positions ? ep.positions[m] : m;
+            float cs[8], sn[8];
+            unpack8(ld16(ep.cos + pos * ep.cs_ld + d), cs);
+            unpack8(ld16(ep.sin + pos * ep.cs_ld + d), sn);
+#pragma unroll
+            for (int q = 0; q < 8; ++q) {
+              const float x = bf16r(v[q]), xp = bf16r(pp[q]);
+              v[q] = lo ? x * cs[q] - xp * sn[q] : x * cs[q] + xp * sn[q];
+            }
+          }
+          __bf16* cp = (__bf16*)ep.c + m * ep.ldc + n;
+          if (full) st16(cp, pack8(v));
+          else
+            for (int q = 0; q < 8 && n + q < N; ++q) cp[q] = (__bf16)v[q];
+        }
+      }
+    }
+  }
+}
+
+template <int BM, int BN, int WAVES_M, int WAVES_N, int BMODE, int EPI>
+__device__ __forceinline__ void epilogue(const GemmArgs& args, f32x16 (&acc)[BM / WAVES_M / 32][BN / WAVES_N / 32],
+                                         int64_t m0, int64_t n0, int lane, int wm, int wn) {
+  constexpr int TM = BM / WAVES_M, TN = BN / WAVES_N;
+  constexpr int FM = TM / 32, FN = TN / 32;
+  const int64_t M = args.M;
+  const EpiArgs& ep = args.ep;
+  const int64_t row_base = m0 + wm * TM + 4 * (lane / 32);
+  const int col_in = lane % 32;
+
+  if constexpr (EPI == EPI_STORE_BF16 || EPI == EPI_STORE_F32 || EPI == EPI_ATOMIC_F32) {
+#pragma unroll
+    for (int j = 0; j < FN; ++j) {
+      const int64_t n = n0 + wn * TN + j * 32 + col_in;
+      if (n >= args.N) continue;
+      float col_alpha = ep.alpha;
+      if (ep.alpha_group > 0) {
+        const int64_t grp = n / ep.alpha_group;
+        col_alpha = ep.alphas[grp < 4 ? grp : 3];
+      }
+#pragma unroll
+      for (int i = 0; i < FM; ++i) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int64_t m = row_base + i * 32 + 8 * (r / 4) + (r % 4);
+          if (m >= M) continue;
+          const float v = col_alpha * acc[i][j][r];
+          if constexpr (EPI == EPI_STORE_BF16) {
+            __bf16* cp = (__bf16*)ep.c + m * ep.ldc + n;
+            float o = v;
+            if (ep.beta != 0.f) o += ep.beta * (float)(*cp);
+            *cp = (__bf16)o;
+          } else if constexpr (EPI == EPI_STORE_F32) {
+            float* cp = (float*)ep.c + m * ep.ldc + n;
+            float o = v;
+            if (ep.beta != 0.f) o += ep.beta * (*cp);
+            *cp = o;
+          } else {
+            atomicAdd((float*)ep.c + m * ep.ldc + n, v);
+          }
+        }
+      }
+    }
+  } else if constexpr (EPI == EPI_SWIGLU_FWD) {
+    // wave tiles (0,1) and (2,3) are (gate, up) pairs for 32 output columns each
+#pragma unroll
+    for (int jp = 0; jp < FN / 2; ++jp) {
+      const int64_t n = n0 + wn * 64 + jp * 32 + col_in;
+      if (n >= args.N) continue;
+#pragma unroll
+      for (int i = 0; i < FM; ++i) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int64_t m = row_base + i * 32 + 8 * (r / 4) + (r % 4);
+          if (m >= M) continue;
+          const float e = acc[i][2 * jp][r];
+          const float g = acc[i][2 * jp + 1][r];
+          const int64_t off = m * ep.ld_eg + n;
+          ep.e[off] = (__bf16)e;
+          ep.g[off] = (__bf16)g;
+          ((__bf16*)ep.c)[m * ep.ldc + n] = (__bf16)(silu_f(e) * g);
+        }
+      }
+    }
+  } else if constexpr (EPI == EPI_SWIGLU_BWD) {
+    // Unsloth-style in-place SwiGLU backward on the DW = dY @ W_down tile:
+    //   f = silu(e) -> bf16, h = f*g, df = DW*f, de = (DW*g) * sig*(1 + e*(1-sig))
+#pragma unroll
+    for (int j = 0; j < FN; ++j) {
+      const int64_t n = n0 + wn * TN + j * 32 + col_in;
+      if (n >= args.N) continue;
+#pragma unroll
+      for (int i = 0; i < FM; ++i) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int64_t m = row_base + i * 32 + 8 * (r / 4) + (r % 4);
+          if (m >= M) continue;
+          const int64_t off = m * ep.ld_eg + n;
+          const float dw = bf16r(acc[i][j][r]);
+          const float e = (float)ep.e[off];
+          const float g = (float)ep.g[off];
+          const float se = sigmoid_f(e);
+          const float f = bf16r(se * e);
+          const float h = f * g;
+          const float df = dw * f;
+          const float dg = bf16r(dw * g);
+          const float de = dg * se * (1.0f + e * (1.0f - se));
+          ((__bf16*)ep.c)[m * ep.ldc + n] = (__bf16)h;
+          ep.e[off] = (__bf16)df;
+          ep.g[off] = (__bf16)de;
+        }
+      }
+    }
+  } else if constexpr (EPI == EPI_ROPE) {
+    // Each wave covers TN = 128 output columns aligned to a head boundary
+    // (head_dim 128: tiles 0,1 = lo half, 2,3 = hi half; head_dim 64: two
+    // heads, tiles (0,1) and (2,3)).
+    const int half_tiles = ep.head_dim / 64;  // partner distance in 32-col tiles
+#pragma unroll
+    for (int i = 0; i < FM; ++i) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int64_t m = row_base + i * 32 + 8 * (r / 4) + (r % 4);
+        if (m >= M) continue;
+        const int64_t pos = ep.positions ? ep.positions[m] : m;
+#pragma unroll
+        for (int j = 0; j < FN; ++j) {
+          const int64_t n = n0 + wn * TN + j * 32 + col_in;
+          if (n >= args.N) continue;
+          float v = acc[i][j][r];
+          if (n < ep.rope_cols) {
+            const int jj = j % (2 * half_tiles);
+            const bool lo = jj < half_tiles;
+            const int partner = lo ? j + half_tiles : j - half_tiles;
+            float pv = 0.f;
+#pragma unroll
+            for (int q = 0; q < FN; ++q)
+              if (q == partner) pv = acc[i][q][r];
+            const int d = (int)(n % ep.head_dim) % (ep.head_dim / 2);
+            const float c = (float)ep.cos[pos * ep.cs_ld + d];
+            const float s = (float)ep.sin[pos * ep.cs_ld + d];
+            // round the projection to bf16 first: RoPE is applied to the
+            // materialised Q/K in the unfused reference path
+            const float x = bf16r(v), xp = bf16r(pv);
+            v = lo ? x * c - xp * s : x * c + xp * s;
+          }
+          ((__bf16*)ep.c)[m * ep.ldc + n] = (__bf16)v;
+        }
+      }
+    }
+  }
+}
+
+template <int BM, int BN, int WAVES_M, int WAVES_N, int A_LAYOUT, int B_LAYOUT, int BMODE, int EPI, bool STAGED>
 __global__ __launch_bounds__(WAVES_M * WAVES_N * 64) __attribute__((amdgpu_waves_per_eu(1, 1)))
 void gemm_kernel(GemmArgs args) {
   constexpr int NT = WAVES_M * WAVES_N * 64;
@@ -457,131 +786,259 @@ void gemm_kernel(GemmArgs args) {
     }
   }
 
-  // ---------------- epilogue ----------------
-  const EpiArgs& ep = args.ep;
-  const int64_t row_base = m0 + wm * TM + 4 * (lane / 32);
-  const int col_in = lane % 32;
+  if constexpr (STAGED) {
+    static_assert(staged_ok(BM, BN, WAVES_M, WAVES_N, EPI), "staged epilogue: 256 x 256, 2 x 2 waves, bf16 out");
+    epilogue_staged<BMODE, EPI>(args, acc, m0, n0, lane, wm, wn, reinterpret_cast<float*>(smem));
+  } else {
+    epilogue<BM, BN, WAVES_M, WAVES_N, BMODE, EPI>(args, acc, m0, n0, lane, wm, wn);
+  }
+}
 
-  if constexpr (EPI == EPI_STORE_BF16 || EPI == EPI_STORE_F32 || EPI == EPI_ATOMIC_F32) {
+// ===========================================================================
+// LDS-DMA engine (both operands K-contiguous: A ROW, B COL).
+//
+// Global -> LDS without registers: each wave instruction (buffer_load ... lds)
+// moves 64 lanes x 16 bytes into 1 KB of LDS at the wave-uniform M0 base, lane
+// L at +16 L.  A tile stage is BROWS rows of BKT bf16 (RB = 2 BKT bytes per
+// row, no padding); the lane -> (row, chunk) map applies an XOR swizzle to
+// the 16-byte chunk positions, chunk' = chunk ^ swz(row), so that the MFMA
+// fragment reads (32 rows, one chunk each) hit distinct banks.  NSTAGE stages
+// form a ring: iteration t waits for its own tile, one barrier, issues the
+// tile NSTAGE-1 ahead into the slot freed by iteration t-1, computes.
+// ===========================================================================
+template <int BKT>
+__device__ __forceinline__ int swz(int row) {
+  if constexpr (BKT == 64) return (row >> 1) & 7;  // 2 rows per 256 bytes
+  else return (row >> 2) & 3;                      // BKT == 32: 4 rows per 256 bytes
+}
+
+template <int BROWS, int BKT, int NT, bool DUAL>
+struct DmaLoader {
+  static constexpr int RB = BKT * 2;          // LDS bytes per row
+  static constexpr int CPR = RB / 16;         // 16-byte chunks per row
+  static constexpr int RPI = 64 / CPR;        // rows per wave instruction
+  static constexpr int NINST = BROWS / RPI;   // wave instructions per tile
+  static constexpr int NW = NT / 64;
+  static constexpr int IPW = NINST / NW;      // instructions per wave per tile
+  static_assert(NINST % NW == 0 && IPW * RPI == BROWS / NW, "tile / wave split");
+  static_assert(!DUAL || (BROWS / NW) % 64 == 0, "dual: 32-row groups inside a wave's rows");
+  uint32_t voff[IPW];   // byte offset of this lane's chunk in the panel (OOB = zero-fill)
+  const char* base[2];
+  int64_t ld_bytes;
+
+  template <class RowSrc>
+  __device__ __forceinline__ void setup(const void* p0, const void* p1, int64_t ld, int64_t panel_off,
+                                        RowSrc row_src) {
+    ld_bytes = ld * 2;
+    const int64_t pan = panel_off * ld_bytes;
+    base[0] = p0 ? (const char*)p0 + pan : nullptr;
+    base[1] = DUAL ? (p1 ? (const char*)p1 + pan : nullptr) : base[0];
+    const int lane = threadIdx.x % 64, wave = threadIdx.x / 64;
 #pragma unroll
-    for (int j = 0; j < FN; ++j) {
-      const int64_t n = n0 + wn * TN + j * 32 + col_in;
-      if (n >= args.N) continue;
-      float col_alpha = ep.alpha;
-      if (ep.alpha_group > 0) {
-        const int64_t grp = n / ep.alpha_group;
-        col_alpha = ep.alphas[grp < 4 ? grp : 3];
+    for (int j = 0; j < IPW; ++j) {
+      const int q = (wave * IPW + j) * RPI + lane / CPR;   // tile row
+      const int chunk = (lane % CPR) ^ swz<BKT>(q);        // source chunk of LDS slot lane % CPR
+      const int sel = DUAL ? ((j * RPI) / 32) % 2 : 0;     // 32-row groups alternate gate / up
+      const int64_t row = base[sel] ? row_src(q, sel) : -1;
+      voff[j] = row < 0 ? OOB : (uint32_t)(row * ld_bytes + chunk * 16);
+    }
+  }
+
+  // DMA of the K tile at k0 (kvalid valid k) into the LDS stage `dst`.
+  __device__ __forceinline__ void load(int64_t k0, int64_t kvalid, char* dst) {
+    const int lane = threadIdx.x % 64, wave = threadIdx.x / 64;
+    const __amdgpu_buffer_rsrc_t r0 = make_rsrc(base[0] + k0 * 2);
+    const __amdgpu_buffer_rsrc_t r1 = make_rsrc(base[1] + k0 * 2);
+#pragma unroll
+    for (int j = 0; j < IPW; ++j) {
+      uint32_t off = voff[j];
+      if (kvalid < BKT) {  // segment tail: chunks past kvalid read zeros
+        const int q = (wave * IPW + j) * RPI + lane / CPR;
+        const int chunk = (lane % CPR) ^ swz<BKT>(q);
+        if (chunk * 8 >= kvalid) off = OOB;
       }
+      const int sel = DUAL ? ((j * RPI) / 32) % 2 : 0;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(sel ? r1 : r0,
+                                               (__attribute__((address_space(3))) void*)(dst + (wave * IPW + j) * 1024),
+                                               16, off, 0, 0, 0);
+    }
+  }
+};
+
+// s_waitcnt with only vmcnt constrained (gfx9 encoding: vmcnt [3:0] + [15:14],
+// expcnt [6:4] = 7 and lgkmcnt [11:8] = 15 mean "don't wait").
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+template <int BM, int BN, int WAVES_M, int WAVES_N, int BMODE, int EPI, int BKT, int NSTAGE, bool STAGED>
+__global__ __launch_bounds__(WAVES_M * WAVES_N * 64) __attribute__((amdgpu_waves_per_eu(1, 1)))
+void gemm_dma_kernel(GemmArgs args) {
+  constexpr int NT = WAVES_M * WAVES_N * 64;
+  constexpr int TM = BM / WAVES_M, TN = BN / WAVES_N;
+  constexpr int FM = TM / 32, FN = TN / 32;
+  constexpr int RB = BKT * 2;
+  constexpr int A_BYTES = BM * RB, B_BYTES = BN * RB, STAGE = A_BYTES + B_BYTES;
+  static_assert(BMODE == B_SINGLE || TN == 128, "dual mode expects 128-row wave tiles");
+  constexpr int SMEM = NSTAGE * STAGE > STAGED_BYTES ? NSTAGE * STAGE : STAGED_BYTES;
+  __shared__ __attribute__((aligned(1024))) char smem[SMEM];
+
+  const int64_t M = args.M;
+  constexpr int OUT_BN = (BMODE == B_DUAL) ? BN / 2 : BN;
+  const int64_t tiles_m = (M + BM - 1) / BM;
+  const int64_t tiles_n = (args.N + OUT_BN - 1) / OUT_BN;
+  int tmi, tni;
+  tile_coords(tiles_m, tiles_n, tmi, tni);
+  const int64_t m0 = (int64_t)tmi * BM;
+  const int64_t n0 = (int64_t)tni * OUT_BN;
+  const int lane = threadIdx.x % 64;
+  const int wave = threadIdx.x / 64;
+  const int wm = wave % WAVES_M;
+  const int wn = wave / WAVES_M;
+
+  int seg_tiles[MAX_SEGS];
+  int total_tiles = 0;
+  for (int s = 0; s < args.n_segs; ++s) {
+    const Seg& sg = args.segs[s];
+    const bool active = sg.n_hi > n0 && sg.n_lo < n0 + OUT_BN;
+    seg_tiles[s] = active ? (int)((sg.k + BKT - 1) / BKT) : 0;
+    total_tiles += seg_tiles[s];
+  }
+  const int per = (total_tiles + args.split_k - 1) / args.split_k;
+  const int t_begin = blockIdx.z * per;
+  const int t_end = min(total_tiles, t_begin + per);
+
+  f32x16 acc[FM][FN];
 #pragma unroll
-      for (int i = 0; i < FM; ++i) {
+  for (int i = 0; i < FM; ++i)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int64_t m = row_base + i * 32 + 8 * (r / 4) + (r % 4);
-          if (m >= M) continue;
-          const float v = col_alpha * acc[i][j][r];
-          if constexpr (EPI == EPI_STORE_BF16) {
-            __bf16* cp = (__bf16*)ep.c + m * ep.ldc + n;
-            float o = v;
-            if (ep.beta != 0.f) o += ep.beta * (float)(*cp);
-            *cp = (__bf16)o;
-          } else if constexpr (EPI == EPI_STORE_F32) {
-            float* cp = (float*)ep.c + m * ep.ldc + n;
-            float o = v;
-            if (ep.beta != 0.f) o += ep.beta * (*cp);
-            *cp = o;
-          } else {
-            atomicAdd((float*)ep.c + m * ep.ldc + n, v);
-          }
-        }
+    for (int j = 0; j < FN; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+
+  DmaLoader<BM, BKT, NT, false> la;
+  DmaLoader<BN, BKT, NT, BMODE == B_DUAL> lb;
+  auto setup_seg = [&](int s) {
+    const Seg& sg = args.segs[s];
+    la.setup(sg.a, sg.a, sg.lda, m0, [&](int q, int) -> int64_t { return m0 + q < M ? q : -1; });
+    if constexpr (BMODE == B_DUAL) {
+      lb.setup(sg.b, sg.b2, sg.ldb, n0, [&](int q, int) -> int64_t {
+        const int t4 = (q % 128) / 32;
+        const int rel = (q / 128) * 64 + (t4 / 2) * 32 + q % 32;
+        return n0 + rel < args.N ? rel : -1;
+      });
+    } else {
+      const int64_t off = n0 - sg.n_lo;
+      lb.setup(sg.b, sg.b, sg.ldb, off, [&](int q, int) -> int64_t {
+        const int64_t n = n0 + q;
+        return (n < args.N && n >= sg.n_lo && n < sg.n_hi) ? q : -1;
+      });
+    }
+  };
+  int cur_s = 0, cur_t = t_begin;
+  {
+    int acc_t = 0;
+    while (cur_s < args.n_segs && cur_t >= acc_t + seg_tiles[cur_s]) { acc_t += seg_tiles[cur_s]; ++cur_s; }
+    cur_t -= acc_t;
+  }
+  int64_t seg_k = 0;
+  int cur_n = 0;
+  auto next_tile = [&](bool first) {
+    if (!first) {
+      ++cur_t;
+      if (cur_t >= cur_n) {
+        do { ++cur_s; } while (seg_tiles[cur_s] == 0);
+        cur_t = 0;
+        cur_n = seg_tiles[cur_s];
+        setup_seg(cur_s);
+        seg_k = args.segs[cur_s].k;
+      }
+    } else {
+      cur_n = seg_tiles[cur_s];
+      setup_seg(cur_s);
+      seg_k = args.segs[cur_s].k;
+    }
+  };
+  auto issue = [&](int slot) {
+    const int64_t k0 = (int64_t)cur_t * BKT;
+    char* st = smem + slot * STAGE;
+    la.load(k0, seg_k - k0, st);
+    lb.load(k0, seg_k - k0, st + A_BYTES);
+  };
+
+  // per-lane fragment offsets: row (wave tile + lane % 32), chunk 2 ks + lane / 32, swizzled
+  const int hi = lane / 32;
+  const int g = swz<BKT>(lane % 32) ^ hi;          // chunk ^ swz = 2 ks ^ g
+  const int a_row = (wm * TM + lane % 32) * RB;
+  const int b_row = A_BYTES + (wn * TN + lane % 32) * RB;
+  auto compute = [&](int slot) {
+    const char* st = smem + slot * STAGE;
+    constexpr int KS = BKT / 16;
+    bf16x8 af[2][FM], bfr[2][FN];
+    auto read_frags = [&](int ks, int sl) {
+      const int ko = ((2 * ks) ^ g) << 4;
+#pragma unroll
+      for (int i = 0; i < FM; ++i) af[sl][i] = *reinterpret_cast<const bf16x8*>(st + a_row + i * 32 * RB + ko);
+#pragma unroll
+      for (int j = 0; j < FN; ++j) bfr[sl][j] = *reinterpret_cast<const bf16x8*>(st + b_row + j * 32 * RB + ko);
+    };
+    read_frags(0, 0);
+    if (KS > 1) read_frags(1, 1);
+    __builtin_amdgcn_sched_group_barrier(SG_DS_READ, (KS > 1 ? 2 : 1) * (FM + FN), 0);
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      const int sl = ks & 1;
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[sl][i], bfr[sl][j], acc[i][j], 0, 0, 0);
+      __builtin_amdgcn_sched_group_barrier(SG_MFMA, FM * FN, 0);
+      if (ks + 2 < KS) {
+        read_frags(ks + 2, sl);
+        __builtin_amdgcn_sched_group_barrier(SG_DS_READ, FM + FN, 0);
       }
     }
-  } else if constexpr (EPI == EPI_SWIGLU_FWD) {
-    // wave tiles (0,1) and (2,3) are (gate, up) pairs for 32 output columns each
+  };
+
+  constexpr int PER_TILE = DmaLoader<BM, BKT, NT, false>::IPW + DmaLoader<BN, BKT, NT, BMODE == B_DUAL>::IPW;
+  const int n_t = t_end - t_begin;
+  if (n_t > 0) {
+    // prologue: tiles 0 .. NSTAGE-2 in flight
 #pragma unroll
-    for (int jp = 0; jp < FN / 2; ++jp) {
-      const int64_t n = n0 + wn * 64 + jp * 32 + col_in;
-      if (n >= args.N) continue;
-#pragma unroll
-      for (int i = 0; i < FM; ++i) {
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int64_t m = row_base + i * 32 + 8 * (r / 4) + (r % 4);
-          if (m >= M) continue;
-          const float e = acc[i][2 * jp][r];
-          const float g = acc[i][2 * jp + 1][r];
-          const int64_t off = m * ep.ld_eg + n;
-          ep.e[off] = (__bf16)e;
-          ep.g[off] = (__bf16)g;
-          ((__bf16*)ep.c)[m * ep.ldc + n] = (__bf16)(silu_f(e) * g);
-        }
+    for (int p = 0; p < NSTAGE - 1; ++p) {
+      if (p < n_t) {
+        next_tile(p == 0);
+        issue(p);
       }
     }
-  } else if constexpr (EPI == EPI_SWIGLU_BWD) {
-    // Unsloth-style in-place SwiGLU backward on the DW = dY @ W_down tile:
-    //   f = silu(e) -> bf16, h = f*g, df = DW*f, de = (DW*g) * sig*(1 + e*(1-sig))
-#pragma unroll
-    for (int j = 0; j < FN; ++j) {
-      const int64_t n = n0 + wn * TN + j * 32 + col_in;
-      if (n >= args.N) continue;
-#pragma unroll
-      for (int i = 0; i < FM; ++i) {
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int64_t m = row_base + i * 32 + 8 * (r / 4) + (r % 4);
-          if (m >= M) continue;
-          const int64_t off = m * ep.ld_eg + n;
-          const float dw = bf16r(acc[i][j][r]);
-          const float e = (float)ep.e[off];
-          const float g = (float)ep.g[off];
-          const float se = sigmoid_f(e);
-          const float f = bf16r(se * e);
-          const float h = f * g;
-          const float df = dw * f;
-          const float dg = bf16r(dw * g);
-          const float de = dg * se * (1.0f + e * (1.0f - se));
-          ((__bf16*)ep.c)[m * ep.ldc + n] = (__bf16)h;
-          ep.e[off] = (__bf16)df;
-          ep.g[off] = (__bf16)de;
-        }
+    for (int t = 0; t < n_t; ++t) {
+      // tile t landed when at most min(NSTAGE-2, n_t-1-t) later tiles are outstanding
+      if (n_t - 1 - t >= NSTAGE - 2) wait_vmcnt<(NSTAGE - 2) * PER_TILE>();
+      else wait_vmcnt<0>();
+      // every wave has waited for its own part of tile t (vmcnt above), so
+      // after the barrier the whole tile is in LDS and slot (t-1) % NSTAGE is
+      // free.  A bare s_barrier: __syncthreads()'s release fence would make
+      // the compiler drain every outstanding LDS-DMA (vmcnt(0)) here and
+      // collapse the ring to one tile in flight.  The empty asm keeps LDS
+      // accesses from moving across the barrier at compile time.
+      asm volatile("" ::: "memory");
+      __builtin_amdgcn_s_barrier();
+      asm volatile("" ::: "memory");
+      if (t + NSTAGE - 1 < n_t) {
+        next_tile(false);
+        issue((t + NSTAGE - 1) % NSTAGE);
       }
+      compute(t % NSTAGE);
     }
-  } else if constexpr (EPI == EPI_ROPE) {
-    // Each wave covers TN = 128 output columns aligned to a head boundary
-    // (head_dim 128: tiles 0,1 = lo half, 2,3 = hi half; head_dim 64: two
-    // heads, tiles (0,1) and (2,3)).
-    const int half_tiles = ep.head_dim / 64;  // partner distance in 32-col tiles
-#pragma unroll
-    for (int i = 0; i < FM; ++i) {
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int64_t m = row_base + i * 32 + 8 * (r / 4) + (r % 4);
-        if (m >= M) continue;
-        const int64_t pos = ep.positions ? ep.positions[m] : m;
-#pragma unroll
-        for (int j = 0; j < FN; ++j) {
-          const int64_t n = n0 + wn * TN + j * 32 + col_in;
-          if (n >= args.N) continue;
-          float v = acc[i][j][r];
-          if (n < ep.rope_cols) {
-            const int jj = j % (2 * half_tiles);
-            const bool lo = jj < half_tiles;
-            const int partner = lo ? j + half_tiles : j - half_tiles;
-            float pv = 0.f;
-#pragma unroll
-            for (int q = 0; q < FN; ++q)
-              if (q == partner) pv = acc[i][q][r];
-            const int d = (int)(n % ep.head_dim) % (ep.head_dim / 2);
-            const float c = (float)ep.cos[pos * ep.cs_ld + d];
-            const float s = (float)ep.sin[pos * ep.cs_ld + d];
-            // round the projection to bf16 first: RoPE is applied to the
-            // materialised Q/K in the unfused reference path
-            const float x = bf16r(v), xp = bf16r(pv);
-            v = lo ? x * c - xp * s : x * c + xp * s;
-          }
-          ((__bf16*)ep.c)[m * ep.ldc + n] = (__bf16)v;
-        }
-      }
-    }
+  }
+  if constexpr (STAGED) {
+    static_assert(staged_ok(BM, BN, WAVES_M, WAVES_N, EPI), "staged epilogue: 256 x 256, 2 x 2 waves, bf16 out");
+    epilogue_staged<BMODE, EPI>(args, acc, m0, n0, lane, wm, wn, reinterpret_cast<float*>(smem));
+  } else {
+    epilogue<BM, BN, WAVES_M, WAVES_N, BMODE, EPI>(args, acc, m0, n0, lane, wm, wn);
   }
 }
 

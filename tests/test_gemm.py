@@ -89,6 +89,31 @@ def test_gemm_split_k_atomic(split, T):
     torch.testing.assert_close(c.cpu(), ref, atol=1e-3 * ref.abs().max().item(), rtol=1e-3)
 
 
+@pytest.mark.gpu
+@pytest.mark.parametrize("N,ldc", [(300, 304), (300, 301), (512, 520)])
+@pytest.mark.parametrize("b_layout", [0, 1])
+def test_gemm_bf16_epilogue_paths(N, ldc, b_layout):
+    """bf16 output through the staged (LDS, 16-byte vector) epilogue and the
+    per-element one: an N tail that is not a multiple of 8 (scalar tail of the
+    staged path), an output pitch that is not a multiple of 8 (per-element
+    path), alpha and beta (C read back) on both, untouched padding columns."""
+    if b_layout == 0 and N % 8:
+        pytest.skip("[K][N] B needs N % 8 == 0")
+    gen = torch.Generator().manual_seed(N + ldc)
+    M, K = 520, 192
+    a, A = _operand(M, K, 0, gen)
+    b, B = _b_operand(N, K, b_layout, gen)
+    ldb = K if b_layout == 1 else N
+    c0 = torch.randn(M, ldc, generator=gen).to(torch.bfloat16)
+    buf = c0.cuda()
+    c = buf[:, :N]
+    _gemm(M, N, [(a, K, b, ldb, K)], 0, b_layout, c, L.DTYPE_BF16, alpha=0.75, beta=0.5)
+    ref = 0.75 * (A @ B) + 0.5 * c0[:, :N].float()
+    scale = ref.abs().max()
+    torch.testing.assert_close(c.float().cpu() / scale, ref / scale, atol=2e-2, rtol=0)
+    assert torch.equal(buf[:, N:].cpu(), c0[:, N:])
+
+
 def test_gemm_rejects_bad_segments_without_gpu():
     """Argument validation happens on the host before any launch."""
     seg = (L.GemmSegment * 1)()

@@ -103,6 +103,29 @@ def test_lora_qkv_rope_fused_matches_composition(head_dim):
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("head_dim", [128, 64])
+def test_qkv_rope_epilogue_paths_agree(head_dim):
+    """The fused RoPE epilogue has a 16-byte staged path and a per-element
+    path (taken when the cos/sin rows are not 8-element aligned); both must
+    give bit-identical Q/K/V."""
+    from kernels.lora_qkv._impl import qkv_forward
+
+    gen = torch.Generator().manual_seed(100 + head_dim)
+    T, K, Hq, Hkv, r = 300, 512, 512, 256, 16
+    p = _cuda(orc.make_params(K, Hq, Hkv, r, 32, gen))
+    X = torch.randn(T, K, generator=gen).to(torch.bfloat16).cuda()
+    pos = torch.randint(0, 200, (T,), generator=gen).cuda()
+    c, s = (t.cuda() for t in cos_sin(torch.arange(200), head_dim, 10000.0, torch.bfloat16))
+    c_odd = torch.zeros(200, head_dim + 2, dtype=torch.bfloat16, device="cuda")[:, :head_dim].copy_(c)
+    s_odd = torch.zeros(200, head_dim + 2, dtype=torch.bfloat16, device="cuda")[:, :head_dim].copy_(s)
+    args = (X, p[0], p[1], p[2], p[3].detach(), p[4].detach(), p[5], p[6].detach(), p[7].detach(), p[8],
+            p[9].detach(), p[10].detach(), p[11])
+    vec = qkv_forward(*args, rope={"cos": c, "sin": s, "positions": pos, "head_dim": head_dim})
+    per_elem = qkv_forward(*args, rope={"cos": c_odd, "sin": s_odd, "positions": pos, "head_dim": head_dim})
+    assert torch.equal(vec, per_elem)
+
+
+@pytest.mark.gpu
 def test_lora_qkv_fp64_gradcheck_uses_reference_torch_path():
     gen = torch.Generator().manual_seed(9)
     K, Hq, Hkv, r = 8, 8, 4, 2
