@@ -212,6 +212,9 @@ int forge_lora_mlp_gate_up(int64_t M, int64_t H, int64_t I, int64_t r,
  *   DW = dY Wd + t Ad   (dY [M, H], Wd [H, I], t = sd dY Bd [M, r], Ad [r, I])
  *   then in place: h_out = silu(e) g,  e <- df = DW silu(e),
  *                  g <- de = DW g sig(e) (1 + e (1 - sig(e)))
+ * w_layout FORGE_LAYOUT_ROW: w_down = Wd [H, I], a_down = Ad [r, I];
+ * FORGE_LAYOUT_COL: w_down = Wd^T [I, H], a_down = Ad^T [I, r] (K-contiguous,
+ * the faster engine; callers with frozen weights keep the transpose).
  * Replaces `matmul_lora(dY, W_down^T, ...)` + `_DWf_DW_dfg_kernel`
  * (kernels/lora_mlp/experiments/v6/lora_mlp_kernel_v6.py:632-634;
  * kernels/lora_mlp/reference/unsloth_baseline.py:34-55, 118-168). */
@@ -219,7 +222,7 @@ int forge_lora_mlp_down_bwd(int64_t M, int64_t H, int64_t I, int64_t r,
                             const void* dy, int64_t lddy,
                             const void* w_down, int64_t ldwd,
                             const void* t_d, int64_t ld_t,
-                            const void* a_down, int64_t ld_ad,
+                            const void* a_down, int64_t ld_ad, int w_layout,
                             void* h_out, void* e_df, void* g_de, int64_t ld, void* stream);
 
 /* LoRA-QKV forward with GQA-asymmetric widths and optional fused RoPE:

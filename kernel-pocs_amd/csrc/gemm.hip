@@ -111,6 +111,7 @@ int run(int cfg, int al, int bl, int epi, const GemmArgs& args, hipStream_t s) {
     case EPI_ATOMIC_F32: return launch_epi<EPI_ATOMIC_F32>(cfg, al, bl, a, s);
     case EPI_SWIGLU_BWD:
       if (al == ROW && bl == ROW) return launch_layout<ROW, ROW, B_SINGLE, EPI_SWIGLU_BWD>(CFG_BIG, a, s);
+      if (al == ROW && bl == COL) return launch_layout<ROW, COL, B_SINGLE, EPI_SWIGLU_BWD>(CFG_BIG, a, s);
       break;
     case EPI_SWIGLU_FWD:
       if (al == ROW && bl == COL) return launch_layout<ROW, COL, B_DUAL, EPI_SWIGLU_FWD>(CFG_BIG, a, s);

@@ -52,15 +52,18 @@ extern "C" int forge_lora_mlp_down_bwd(int64_t M, int64_t H, int64_t I, int64_t 
                                        const void* dy, int64_t lddy,
                                        const void* w_down, int64_t ldwd,
                                        const void* t_d, int64_t ld_t,
-                                       const void* a_down, int64_t ld_ad,
+                                       const void* a_down, int64_t ld_ad, int w_layout,
                                        void* h_out, void* e_df, void* g_de, int64_t ld, void* stream) {
   if (M < 0 || H < 0 || I < 0 || r < 0) return forge_set_error(FORGE_ERR_INVALID, "lora_mlp_down_bwd: shape");
+  if (w_layout != ROW && w_layout != COL) return forge_set_error(FORGE_ERR_INVALID, "lora_mlp_down_bwd: w_layout");
   GemmArgs a = {};
   a.M = M;
   a.N = I;
   a.split_k = 1;
   int ns = 0;
-  // DW[m, i] = sum_h dY[m, h] Wd[h, i]  (+ sum_j T[m, j] Ad[j, i]); B is [K][N]
+  // DW[m, i] = sum_h dY[m, h] Wd[h, i]  (+ sum_j T[m, j] Ad[j, i]).
+  // ROW: w_down = Wd [H][I], a_down = Ad [r][I] (B as [K][N]);
+  // COL: w_down = Wd^T [I][H], a_down = Ad^T [I][r] (B K-contiguous: the LDS-DMA engine)
   a.segs[ns++] = Seg{(const __bf16*)dy, lddy, (const __bf16*)w_down, nullptr, ldwd, H, 0, I};
   if (r > 0 && t_d) a.segs[ns++] = Seg{(const __bf16*)t_d, ld_t, (const __bf16*)a_down, nullptr, ld_ad, r, 0, I};
   a.n_segs = ns;
@@ -70,7 +73,7 @@ extern "C" int forge_lora_mlp_down_bwd(int64_t M, int64_t H, int64_t I, int64_t 
   a.ep.e = (__bf16*)e_df;
   a.ep.g = (__bf16*)g_de;
   a.ep.ld_eg = ld;
-  return run(-1, ROW, ROW, EPI_SWIGLU_BWD, a, (hipStream_t)stream);
+  return run(-1, ROW, w_layout, EPI_SWIGLU_BWD, a, (hipStream_t)stream);
 }
 
 extern "C" int forge_lora_qkv_rope(int64_t M, int64_t K, int64_t hq, int64_t hkv, int64_t r,

@@ -107,7 +107,7 @@ forge_lora_mlp_gate_up = _decl(
 )
 forge_lora_mlp_down_bwd = _decl(
     "forge_lora_mlp_down_bwd",
-    [c_i64] * 4 + [c_vp, c_i64, c_vp, c_i64, c_vp, c_i64, c_vp, c_i64, c_vp, c_vp, c_vp, c_i64, c_vp],
+    [c_i64] * 4 + [c_vp, c_i64, c_vp, c_i64, c_vp, c_i64, c_vp, c_i64, c_int, c_vp, c_vp, c_vp, c_i64, c_vp],
 )
 forge_lora_qkv_rope = _decl(
     "forge_lora_qkv_rope",

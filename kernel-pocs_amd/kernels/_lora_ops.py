@@ -8,6 +8,7 @@ the library on torch's current stream.
 from __future__ import annotations
 
 import ctypes
+import weakref
 from typing import Optional, Sequence, Tuple
 
 import torch
@@ -97,6 +98,38 @@ def lora_a(x: torch.Tensor, mats: Sequence[torch.Tensor], scales: Sequence[float
         "forge_lora_a",
     )
     return out
+
+
+_T_CACHE = {}
+
+
+def frozen_t(w: torch.Tensor) -> torch.Tensor:
+    """Contiguous W^T of a frozen base weight, kept for the weight's lifetime.
+
+    The backward GEMMs contract over the weight's output dimension, which is
+    not contiguous in the nn.Linear layout; with W^T they become K-contiguous
+    and run on the LDS-DMA engine.  The copy is made once per weight (LoRA
+    freezes the base weights) and dropped when the weight is freed, changed
+    in place (tensor._version) or given new storage (data_ptr).
+    """
+    key = id(w)
+    ent = _T_CACHE.get(key)
+    if ent is not None:
+        ref, ver, ptr, wt = ent
+        if ref() is w and ver == w._version and ptr == w.data_ptr():
+            return wt
+    wt = w.detach().t().contiguous()
+
+    def _drop(_ref, key=key):
+        _T_CACHE.pop(key, None)
+
+    _T_CACHE[key] = (weakref.ref(w, _drop), w._version, w.data_ptr(), wt)
+    return wt
+
+
+def small_t(a: torch.Tensor) -> torch.Tensor:
+    """A^T contiguous for a rank-r LoRA matrix (r x features: a few hundred KB)."""
+    return a.detach().t().contiguous()
 
 
 def split_k_for(k: int, tiles: int, target_wgs: int = 512, min_tiles_per_split: int = 4) -> int:

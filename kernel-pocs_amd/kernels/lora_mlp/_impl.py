@@ -29,7 +29,7 @@ import torch
 import torch.nn.functional as F
 
 from forge_hip import _lib as L
-from kernels._lora_ops import COL, ROW, as_operand, gemm, grad_at_b, ld, lora_a
+from kernels._lora_ops import COL, ROW, as_operand, frozen_t, gemm, grad_at_b, ld, lora_a, small_t
 
 
 def _w(t):
@@ -89,9 +89,14 @@ def mlp_backward(dY2, X2, e, g, W_gate, A_gate, B_gate, s_gate, W_up, A_up, B_up
     # 1-2: DW = dY Wd + sd (dY Bd) Ad with the SwiGLU backward fused in place
     td = gemm(M, r, [(dY2, ld(dY2), Bd, ld(Bd), H)], ROW, ROW, alpha=s_down)
     h = torch.empty(M, I, dtype=torch.bfloat16, device=dev)
+    # K-contiguous weights (cached W^T, small A^T) put the three big GEMMs of
+    # the backward on the LDS-DMA engine; a rank that is not a multiple of 8
+    # keeps the [K][N] layout
+    kt = r % 8 == 0
+    WdB, AdB, wl = (frozen_t(W_down), small_t(Ad), COL) if kt else (Wd, Ad, ROW)
     L.check(
-        L.forge_lora_mlp_down_bwd(M, H, I, r, dY2.data_ptr(), ld(dY2), Wd.data_ptr(), ld(Wd), td.data_ptr(), r,
-                                  Ad.data_ptr(), ld(Ad), h.data_ptr(), e.data_ptr(), g.data_ptr(), I,
+        L.forge_lora_mlp_down_bwd(M, H, I, r, dY2.data_ptr(), ld(dY2), WdB.data_ptr(), ld(WdB), td.data_ptr(), r,
+                                  AdB.data_ptr(), ld(AdB), wl, h.data_ptr(), e.data_ptr(), g.data_ptr(), I,
                                   L.stream_of(X2)),
         "forge_lora_mlp_down_bwd",
     )
@@ -112,8 +117,13 @@ def mlp_backward(dY2, X2, e, g, W_gate, A_gate, B_gate, s_gate, W_up, A_up, B_up
     dBg = grad_at_b(de, I, xa_ug[:, r:], 2 * r, I, r, M, alpha=s_gate)
 
     # 5: dX
-    dX = gemm(M, H, [(df, I, Wu, ld(Wu), I), (de, I, Wg, ld(Wg), I),
-                     (v[:, :r], 2 * r, Au, ld(Au), r), (v[:, r:], 2 * r, Ag, ld(Ag), r)], ROW, ROW)
+    if kt:
+        WuT, WgT, AuT, AgT = frozen_t(W_up), frozen_t(W_gate), small_t(Au), small_t(Ag)
+        dX = gemm(M, H, [(df, I, WuT, I, I), (de, I, WgT, I, I),
+                         (v[:, :r], 2 * r, AuT, r, r), (v[:, r:], 2 * r, AgT, r, r)], ROW, COL)
+    else:
+        dX = gemm(M, H, [(df, I, Wu, ld(Wu), I), (de, I, Wg, ld(Wg), I),
+                         (v[:, :r], 2 * r, Au, ld(Au), r), (v[:, r:], 2 * r, Ag, ld(Ag), r)], ROW, ROW)
     dt = A_gate.dtype
     return (dX, dA_ug[r:].to(dt), dBg.to(dt), dA_ug[:r].to(dt), dBu.to(dt), dAd.to(dt), dBd.to(dt))
 

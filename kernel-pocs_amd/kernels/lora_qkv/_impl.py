@@ -25,7 +25,7 @@ from typing import Optional
 import torch
 
 from forge_hip import _lib as L
-from kernels._lora_ops import COL, ROW, as_operand, gemm, grad_at_b, ld, lora_a
+from kernels._lora_ops import COL, ROW, as_operand, frozen_t, gemm, grad_at_b, ld, lora_a, small_t
 
 
 def _w(t):
@@ -88,9 +88,15 @@ def qkv_backward(dQ, dK, dV, X2, W_q, W_k, W_v, A_q, B_q, s_q, A_k, B_k, s_k, A_
     dBq = grad_at_b(dQ, ld(dQ), xa[:, :r], 3 * r, Hq, r, M, alpha=s_q)
     dBk = grad_at_b(dK, ld(dK), xa[:, r:2 * r], 3 * r, Hkv, r, M, alpha=s_k)
     dBv = grad_at_b(dV, ld(dV), xa[:, 2 * r:], 3 * r, Hkv, r, M, alpha=s_v)
-    dX = gemm(M, K, [(dQ, ld(dQ), Wq, ld(Wq), Hq), (dK, ld(dK), Wk, ld(Wk), Hkv), (dV, ld(dV), Wv, ld(Wv), Hkv),
-                     (t[:, :r], 3 * r, Aq, ld(Aq), r), (t[:, r:2 * r], 3 * r, Ak, ld(Ak), r),
-                     (t[:, 2 * r:], 3 * r, Av, ld(Av), r)], ROW, ROW)
+    if r % 8 == 0:  # K-contiguous weights: the LDS-DMA engine (cached W^T, small A^T)
+        dX = gemm(M, K, [(dQ, ld(dQ), frozen_t(W_q), Hq, Hq), (dK, ld(dK), frozen_t(W_k), Hkv, Hkv),
+                         (dV, ld(dV), frozen_t(W_v), Hkv, Hkv), (t[:, :r], 3 * r, small_t(Aq), r, r),
+                         (t[:, r:2 * r], 3 * r, small_t(Ak), r, r), (t[:, 2 * r:], 3 * r, small_t(Av), r, r)],
+                  ROW, COL)
+    else:
+        dX = gemm(M, K, [(dQ, ld(dQ), Wq, ld(Wq), Hq), (dK, ld(dK), Wk, ld(Wk), Hkv),
+                         (dV, ld(dV), Wv, ld(Wv), Hkv), (t[:, :r], 3 * r, Aq, ld(Aq), r),
+                         (t[:, r:2 * r], 3 * r, Ak, ld(Ak), r), (t[:, 2 * r:], 3 * r, Av, ld(Av), r)], ROW, ROW)
     dt = A_q.dtype
     return (dX, dA[:r].to(dt), dBq.to(dt), dA[r:2 * r].to(dt), dBk.to(dt), dA[2 * r:].to(dt), dBv.to(dt))
 
