@@ -180,7 +180,10 @@ enum {
 
 /* C[M, N] = alpha * sum_s A_s @ B_s + beta * C.  A and B layouts are shared by
  * all segments.  c_dtype is FORGE_DTYPE_BF16 or FORGE_DTYPE_F32.  split_k > 1
- * (only with FORGE_EPI_ATOMIC_F32) partitions the K range across workgroups.
+ * partitions the K range across workgroups: with FORGE_EPI_ATOMIC_F32 they
+ * accumulate into C; with FORGE_EPI_STORE and an fp32 C (beta = 0) split z
+ * writes its partial sums to C + z*M*ldc (C holds split_k slices of [M, ldc]),
+ * to be summed by forge_splitk_reduce (deterministic order).
  * Replaces the cuBLAS calls (`torch.matmul` / `addmm_`) of the LoRA paths:
  * kernels/lora_mlp/experiments/v6/lora_mlp_kernel_v6.py:373-443, 623-653;
  * kernels/lora_qkv/experiments/v4/lora_qkv_kernel_v4.py:248-287. */
@@ -250,8 +253,9 @@ int forge_lora_qkv_rope(int64_t M, int64_t K, int64_t hq, int64_t hkv, int64_t r
  *   out[:, p*r:(p+1)*r] = scales[p] * X @ A_p^T     for p < n_proj (<= 4)
  * X [M, K] (row pitch ldx), A_p [r, K] (pitch lda), out [M, n_proj*r] bf16.
  * scales is a host array.  split_k > 1 spreads K over split_k workgroups
- * per output tile, reducing in `work` (fp32 [M, n_proj*r], caller-owned, no
- * initialisation needed) before the bf16 cast.  Replaces the LoRA-A GEMMs X @ A^T of the
+ * per output tile, each writing fp32 partial sums to its slice of `work`
+ * (fp32 [split_k][M][n_proj*r], caller-owned, no initialisation needed),
+ * summed in a fixed order and rounded to bf16.  Replaces the LoRA-A GEMMs X @ A^T of the
  * reference (the stacked [W; A_g; A_u] cuBLAS call,
  * kernels/lora_mlp/experiments/v6/lora_mlp_kernel_v6.py:373-381, and
  * `XA_all = X @ A_packed^T`, kernels/lora_qkv/experiments/v4/lora_qkv_kernel_v4.py:260). */
@@ -263,6 +267,13 @@ int forge_lora_a(int64_t M, int64_t K, int64_t r, int n_proj, const void* x, int
  * delegates these to cuBLAS): zero an fp32 workspace with a fill kernel, and
  * cast a reduced fp32 [rows, cols] block to bf16. */
 int forge_zero(void* ptr, int64_t bytes, void* stream);
+
+/* out[m, n] = alpha * sum_{z < n_split} parts[z*split_stride + m*ld_parts + n],
+ * summed in z order (deterministic), rounded once to out_dtype (fp32, bf16 or
+ * fp16).  The reduction of forge_gemm / forge_lora_a split-K partials; no
+ * reference counterpart (the reference's cuBLAS GEMMs do not split K). */
+int forge_splitk_reduce(const float* parts, int64_t split_stride, int n_split, int64_t rows, int64_t cols,
+                        int64_t ld_parts, void* out, int64_t ld_out, int out_dtype, float alpha, void* stream);
 int forge_cast_f32_bf16(const float* src, int64_t ld_src, void* dst, int64_t ld_dst, int64_t rows,
                         int64_t cols, void* stream);
 

@@ -159,10 +159,19 @@ extern "C" int forge_gemm(int64_t M, int64_t N, const forge_gemm_segment* segs, 
       return forge_set_error(FORGE_ERR_INVALID, "gemm: atomic epilogue needs an fp32 C");
     epi = EPI_ATOMIC_F32;
   } else if (epilogue == FORGE_EPI_STORE) {
-    if (split_k != 1) return forge_set_error(FORGE_ERR_INVALID, "gemm: split_k needs the atomic epilogue");
-    if (c_dtype == FORGE_DTYPE_BF16) epi = EPI_STORE_BF16;
-    else if (c_dtype == FORGE_DTYPE_F32) epi = EPI_STORE_F32;
-    else return forge_set_error(FORGE_ERR_UNSUPPORTED, "gemm: C dtype %d", c_dtype);
+    if (c_dtype == FORGE_DTYPE_BF16) {
+      if (split_k != 1)
+        return forge_set_error(FORGE_ERR_INVALID, "gemm: split_k needs an fp32 C (partials) or the atomic epilogue");
+      epi = EPI_STORE_BF16;
+    } else if (c_dtype == FORGE_DTYPE_F32) {
+      epi = EPI_STORE_F32;
+      if (split_k > 1) {  // partial sums: split z owns C[z] = c + z * M * ldc
+        if (beta != 0.f) return forge_set_error(FORGE_ERR_INVALID, "gemm: split-K partials need beta == 0");
+        a.ep.split_stride = M * ldc;
+      }
+    } else {
+      return forge_set_error(FORGE_ERR_UNSUPPORTED, "gemm: C dtype %d", c_dtype);
+    }
   } else {
     return forge_set_error(FORGE_ERR_INVALID, "gemm: epilogue %d", epilogue);
   }

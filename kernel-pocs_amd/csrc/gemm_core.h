@@ -64,7 +64,7 @@ constexpr int MAX_SEGS = 6;
 
 enum Epi {
   EPI_STORE_BF16 = 0,   // C = alpha*acc + beta*C
-  EPI_STORE_F32 = 1,
+  EPI_STORE_F32 = 1,     // C = alpha*acc + beta*C; with split-K, one partial slice per split
   EPI_ATOMIC_F32 = 2,   // C += alpha*acc
   EPI_SWIGLU_FWD = 3,   // dual: e, g, h = silu(e) * g
   EPI_SWIGLU_BWD = 4,   // DW: (DW, e, g) -> (h, df, de) in place
@@ -89,6 +89,7 @@ struct EpiArgs {
   int64_t rope_cols;         // columns [0, rope_cols) are rotated
   int head_dim;              // 64 or 128
   int vec_ok;                // every output / side buffer 16-byte aligned with pitches % 8 == 0
+  int64_t split_stride;      // STORE_F32 with split-K: split z writes its partial sums at c + z * split_stride
 };
 
 struct GemmArgs {
@@ -521,7 +522,7 @@ __device__ __forceinline__ void epilogue(const GemmArgs& args, f32x16 (&acc)[BM 
             if (ep.beta != 0.f) o += ep.beta * (float)(*cp);
             *cp = (__bf16)o;
           } else if constexpr (EPI == EPI_STORE_F32) {
-            float* cp = (float*)ep.c + m * ep.ldc + n;
+            float* cp = (float*)ep.c + (int64_t)blockIdx.z * ep.split_stride + m * ep.ldc + n;
             float o = v;
             if (ep.beta != 0.f) o += ep.beta * (*cp);
             *cp = o;

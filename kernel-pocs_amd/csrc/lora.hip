@@ -143,15 +143,17 @@ extern "C" int forge_lora_a(int64_t M, int64_t K, int64_t r, int n_proj, const v
   // 256 x 32 tiles: every tile covers at most two projections' columns and
   // no MFMA work is spent on columns outside [0, n_proj * r).  With split_k
   // the K range is spread over split_k workgroups per tile (the skinny output
-  // alone gives only M/256 tiles) and reduced with fp32 atomics in `work`.
+  // alone gives only M/256 tiles): split z writes fp32 partial sums to
+  // work[z] ([split_k][M][N]), which one reduction pass sums in a fixed order
+  // (deterministic) and rounds to bf16.
   if (split_k <= 1) {
     a.ep.c = out;
     a.ep.ldc = ld_out;
     return run(1 /* CFG_SKINNY_N */, ROW, COL, EPI_STORE_BF16, a, s);
   }
-  if (int e = forge_zero(work, M * N * (int64_t)sizeof(float), stream)) return e;
   a.ep.c = work;
   a.ep.ldc = N;
-  if (int e = run(1 /* CFG_SKINNY_N */, ROW, COL, EPI_ATOMIC_F32, a, s)) return e;
-  return forge_cast_f32_bf16(work, N, out, ld_out, M, N, stream);
+  a.ep.split_stride = M * N;
+  if (int e = run(1 /* CFG_SKINNY_N */, ROW, COL, EPI_STORE_F32, a, s)) return e;
+  return forge_splitk_reduce(work, M * N, split_k, M, N, N, out, ld_out, FORGE_DTYPE_BF16, 1.0f, stream);
 }

@@ -1,6 +1,7 @@
-// Small utility kernels used by the split-K paths: zero fill of an fp32
-// workspace (a kernel, not hipMemsetAsync, so the sequence stays valid under
-// stream capture) and the fp32 -> bf16 cast of the reduced result.
+// Small utility kernels used by the split-K paths: the deterministic
+// reduction of per-split fp32 partial sums, zero fill of an fp32 workspace (a
+// kernel, not hipMemsetAsync, so the sequence stays valid under stream
+// capture) and the fp32 -> bf16 cast.
 #include "common.h"
 
 namespace {
@@ -21,7 +22,62 @@ __global__ __launch_bounds__(256) void cast_f32_bf16_kernel(const float* src, in
   }
 }
 
+// out[m, n] = alpha * sum_z parts[z * stride + m * ldp + n], z = 0 .. n_split-1
+// in that order (deterministic), rounded once to the output type.
+template <class T, int VEC>
+__global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* parts, int64_t stride, int n_split,
+                                                            int64_t rows, int64_t cols, int64_t ldp, T* out,
+                                                            int64_t ldo, float alpha) {
+  const int64_t cpr = cols / VEC;
+  const int64_t n = rows * cpr;
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) {
+    const int64_t r = i / cpr, c = (i - r * cpr) * VEC;
+    float acc[VEC];
+#pragma unroll
+    for (int q = 0; q < VEC; ++q) acc[q] = 0.f;
+    const float* p = parts + r * ldp + c;
+    for (int z = 0; z < n_split; ++z, p += stride) {
+      if constexpr (VEC == 4) {
+        const float4 v = *reinterpret_cast<const float4*>(p);
+        acc[0] += v.x; acc[1] += v.y; acc[2] += v.z; acc[3] += v.w;
+      } else {
+        acc[0] += p[0];
+      }
+    }
+#pragma unroll
+    for (int q = 0; q < VEC; ++q) out[r * ldo + c + q] = from_f32<T>(alpha * acc[q]);
+  }
+}
+
+template <class T>
+int launch_reduce(const float* parts, int64_t stride, int n_split, int64_t rows, int64_t cols, int64_t ldp, void* out,
+                  int64_t ldo, float alpha, hipStream_t s) {
+  const bool vec = cols % 4 == 0 && ldp % 4 == 0 && stride % 4 == 0 && ((uintptr_t)parts % 16) == 0;
+  if (vec)
+    splitk_reduce_kernel<T, 4><<<grid_for(rows * cols / 4, 256, 4096), 256, 0, s>>>(parts, stride, n_split, rows, cols,
+                                                                                   ldp, (T*)out, ldo, alpha);
+  else
+    splitk_reduce_kernel<T, 1><<<grid_for(rows * cols, 256, 4096), 256, 0, s>>>(parts, stride, n_split, rows, cols, ldp,
+                                                                               (T*)out, ldo, alpha);
+  FORGE_CHECK_LAUNCH();
+  return FORGE_OK;
+}
+
 }  // namespace
+
+extern "C" int forge_splitk_reduce(const float* parts, int64_t split_stride, int n_split, int64_t rows, int64_t cols,
+                                   int64_t ld_parts, void* out, int64_t ld_out, int out_dtype, float alpha,
+                                   void* stream) {
+  if (rows < 0 || cols < 0 || n_split < 1) return forge_set_error(FORGE_ERR_INVALID, "splitk_reduce: shape");
+  if (rows == 0 || cols == 0) return FORGE_OK;
+  hipStream_t s = (hipStream_t)stream;
+  switch (out_dtype) {
+    case FORGE_DTYPE_F32: return launch_reduce<float>(parts, split_stride, n_split, rows, cols, ld_parts, out, ld_out, alpha, s);
+    case FORGE_DTYPE_BF16: return launch_reduce<bf16_t>(parts, split_stride, n_split, rows, cols, ld_parts, out, ld_out, alpha, s);
+    case FORGE_DTYPE_F16: return launch_reduce<fp16_t>(parts, split_stride, n_split, rows, cols, ld_parts, out, ld_out, alpha, s);
+    default: return forge_set_error(FORGE_ERR_UNSUPPORTED, "splitk_reduce: dtype %d", out_dtype);
+  }
+}
 
 extern "C" int forge_zero(void* ptr, int64_t bytes, void* stream) {
   if (bytes <= 0) return FORGE_OK;

@@ -95,6 +95,7 @@ forge_ce_fwd = _decl(
     + [c_int, c_vp, c_vp],
 )
 forge_ce_target_stats = _decl("forge_ce_target_stats", [c_vp, c_i64, c_i64, c_i64, c_i64, c_vp, c_vp])
+forge_splitk_reduce = _decl("forge_splitk_reduce", [c_vp, c_i64, c_int, c_i64, c_i64, c_i64, c_vp, c_i64, c_int, c_f32, c_vp])
 forge_ce_scale = _decl("forge_ce_scale", [c_int, c_vp, c_i64, c_i64, c_i64, c_vp, c_int, c_vp])
 forge_sum_f32 = _decl("forge_sum_f32", [c_vp, c_i64, c_vp, c_vp, c_int, c_vp])
 forge_gemm = _decl(
@@ -131,7 +132,7 @@ EXPORTED = [
     "forge_swiglu_fwd", "forge_swiglu_bwd", "forge_rope",
     "forge_ce_fwd", "forge_ce_target_stats", "forge_ce_scale", "forge_sum_f32",
     "forge_gemm", "forge_lora_mlp_gate_up", "forge_lora_mlp_down_bwd", "forge_lora_qkv_rope",
-    "forge_lora_a", "forge_zero", "forge_cast_f32_bf16",
+    "forge_lora_a", "forge_zero", "forge_cast_f32_bf16", "forge_splitk_reduce",
 ]
 
 # Number of successful library calls (tests use it to prove the HIP path ran).

@@ -46,8 +46,8 @@ def gemm(M: int, N: int, segs: Sequence[Tuple[torch.Tensor, int, torch.Tensor, i
          out_dtype=torch.bfloat16, atomic: bool = False, split_k: int = 1, device=None) -> torch.Tensor:
     """C[M, N] = alpha * sum_s A_s @ B_s (+ beta C).  segs: (A, lda, B, ldb, K).
     atomic=True accumulates into a zero-initialised fp32 C over split_k
-    K partitions.  A skinny bf16 output (N <= 64, beta = 0) is computed the
-    same way (split-K into an fp32 workspace, then cast)."""
+    K partitions.  A skinny bf16 output (N <= 64, beta = 0) is split over K
+    into fp32 partial slices, then summed in a fixed order and rounded."""
     dev = device if device is not None else segs[0][0].device
     K = sum(int(k) for (_, _, _, _, k) in segs)
     if not atomic and beta == 0.0 and N <= 64 and M >= 1024 and (out is None or out.dtype == torch.bfloat16):
@@ -55,12 +55,7 @@ def gemm(M: int, N: int, segs: Sequence[Tuple[torch.Tensor, int, torch.Tensor, i
         if split > 1:
             if out is None:
                 out = torch.empty(M, N, dtype=torch.bfloat16, device=dev)
-            work = torch.empty(M, N, dtype=torch.float32, device=dev)
-            L.check(L.forge_zero(work.data_ptr(), work.numel() * 4, L.stream_of(work)), "forge_zero")
-            gemm(M, N, segs, a_layout, b_layout, out=work, alpha=alpha, atomic=True, split_k=split, device=dev)
-            L.check(L.forge_cast_f32_bf16(work.data_ptr(), N, out.data_ptr(), ld(out), M, N, L.stream_of(work)),
-                    "forge_cast_f32_bf16")
-            return out
+            return split_gemm(M, N, segs, a_layout, b_layout, split, out, alpha, dev)
     if out is None:
         if atomic:
             out = torch.empty(M, N, dtype=torch.float32, device=dev)
@@ -79,6 +74,25 @@ def gemm(M: int, N: int, segs: Sequence[Tuple[torch.Tensor, int, torch.Tensor, i
     return out
 
 
+def split_gemm(M: int, N: int, segs, a_layout: int, b_layout: int, split: int, out: torch.Tensor,
+               alpha: float = 1.0, device=None) -> torch.Tensor:
+    """out = alpha * sum_s A_s @ B_s with K split `split` ways: each split
+    writes fp32 partials to its slice of a [split, M, N] workspace and
+    forge_splitk_reduce sums them in a fixed order (deterministic) and rounds
+    once to out's dtype."""
+    dev = device if device is not None else out.device
+    parts = torch.empty(split, M, N, dtype=torch.float32, device=dev)
+    arr = (L.GemmSegment * len(segs))()
+    for i, (a, lda, b, ldb, k) in enumerate(segs):
+        arr[i] = L.GemmSegment(a.data_ptr(), int(lda), b.data_ptr(), int(ldb), int(k))
+    st = L.stream_of(parts)
+    L.check(L.forge_gemm(M, N, arr, len(segs), a_layout, b_layout, parts.data_ptr(), N, L.DTYPE_F32, float(alpha),
+                         0.0, L.EPI_STORE, int(split), st), "forge_gemm")
+    L.check(L.forge_splitk_reduce(parts.data_ptr(), M * N, int(split), M, N, N, out.data_ptr(), ld(out),
+                                  L.dtype_code(out.dtype), 1.0, st), "forge_splitk_reduce")
+    return out
+
+
 def lora_a(x: torch.Tensor, mats: Sequence[torch.Tensor], scales: Sequence[float],
            out: Optional[torch.Tensor] = None) -> torch.Tensor:
     """[s_p * x @ A_p^T for p] concatenated along columns -> [M, n*r] bf16."""
@@ -91,7 +105,7 @@ def lora_a(x: torch.Tensor, mats: Sequence[torch.Tensor], scales: Sequence[float
     ptrs = (ctypes.c_void_p * n)(*[a.data_ptr() for a in mats])
     sc = (ctypes.c_float * n)(*[float(s) for s in scales])
     split = skinny_split(M, n * r, K) if M >= 1024 else 1
-    work = torch.empty(M, n * r, dtype=torch.float32, device=x.device) if split > 1 else None
+    work = torch.empty(split, M, n * r, dtype=torch.float32, device=x.device) if split > 1 else None
     L.check(
         L.forge_lora_a(M, K, r, n, x.data_ptr(), ld(x), ptrs, ld(mats[0]), sc, out.data_ptr(), ld(out),
                        L.ptr(work), split, L.stream_of(x)),
@@ -141,12 +155,14 @@ def split_k_for(k: int, tiles: int, target_wgs: int = 512, min_tiles_per_split: 
 
 
 def grad_at_b(a_t: torch.Tensor, lda: int, b: torch.Tensor, ldb: int, rows: int, cols: int, k: int,
-              alpha: float = 1.0) -> torch.Tensor:
+              alpha: float = 1.0, out_dtype=torch.float32) -> torch.Tensor:
     """alpha * A^T @ B where A is stored [k][rows] and B [k][cols] (both
     row-major over the reduction dim k): the LoRA weight-gradient shape
-    (rank x features or features x rank, reduced over tokens).  fp32
-    split-K accumulation, returned as fp32 [rows, cols]."""
+    (rank x features or features x rank, reduced over tokens).  Split over k
+    into fp32 partials, reduced in a fixed order, returned as [rows, cols] in
+    out_dtype (rounded once)."""
     tiles_m = max(1, (rows + 255) // 256) if rows > 64 else 1
     tiles_n = max(1, (cols + 255) // 256) if cols > 64 else 1
     split = split_k_for(k, tiles_m * tiles_n)
-    return gemm(rows, cols, [(a_t, lda, b, ldb, k)], COL, ROW, alpha=alpha, atomic=True, split_k=split)
+    out = torch.empty(rows, cols, dtype=out_dtype, device=a_t.device)
+    return split_gemm(rows, cols, [(a_t, lda, b, ldb, k)], COL, ROW, split, out, alpha)

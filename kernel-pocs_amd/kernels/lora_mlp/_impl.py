@@ -37,8 +37,10 @@ def _w(t):
 
 
 def mlp_forward(X2, W_gate, A_gate, B_gate, s_gate, W_up, A_up, B_up, s_up,
-                W_down, A_down, B_down, s_down, save_eg: bool = True):
-    """Returns (out [M, H], e [M, I], g [M, I]) (e, g None unless save_eg)."""
+                W_down, A_down, B_down, s_down, save_eg: bool = True, aux: Optional[dict] = None):
+    """Returns (out [M, H], e [M, I], g [M, I]) (e, g None unless save_eg).
+    aux (a dict, optional) receives the LoRA-A products the backward reuses:
+    xa = [sg X Ag^T | su X Au^T] [M, 2r] and xd = sd h Ad^T [M, r]."""
     L.require_gpu(X2, W_gate, W_up, W_down)
     X2 = as_operand(X2)
     Wg, Wu, Wd = _w(W_gate), _w(W_up), _w(W_down)
@@ -67,6 +69,8 @@ def mlp_forward(X2, W_gate, A_gate, B_gate, s_gate, W_up, A_up, B_up, s_up,
         xd = lora_a(h, [A_down], [s_down])
         Bd = _w(B_down)
         segs.append((xd, r, Bd, ld(Bd), r))
+        if aux is not None:
+            aux["xa"], aux["xd"] = xa, xd
     out = gemm(M, Wd.shape[0], segs, ROW, COL)
     if not save_eg:
         e = g = None
@@ -74,9 +78,13 @@ def mlp_forward(X2, W_gate, A_gate, B_gate, s_gate, W_up, A_up, B_up, s_up,
 
 
 def mlp_backward(dY2, X2, e, g, W_gate, A_gate, B_gate, s_gate, W_up, A_up, B_up, s_up,
-                 W_down, A_down, B_down, s_down):
+                 W_down, A_down, B_down, s_down, aux: Optional[dict] = None):
     """Returns (dX [M, H], dAg, dBg, dAu, dBu, dAd, dBd).  e and g are
-    overwritten with df and de."""
+    overwritten with df and de.  With the forward's aux (xa, xd) the
+    weight gradients of B reuse those products instead of re-reading X and h;
+    xd then comes from the forward's h (fp32 e, g), which differs from the
+    backward's recomputed h (bf16-rounded, lora_mlp_pytorch.py:165) only by
+    rounding."""
     dY2 = as_operand(dY2)
     X2 = as_operand(X2)
     Wg, Wu, Wd = _w(W_gate), _w(W_up), _w(W_down)
@@ -103,18 +111,27 @@ def mlp_backward(dY2, X2, e, g, W_gate, A_gate, B_gate, s_gate, W_up, A_up, B_up
     df, de = e, g
 
     # 3: down-projection LoRA grads
-    dAd = grad_at_b(td, r, h, I, r, I, M)                        # [r, I] = (sd dY Bd)^T h
-    u = lora_a(h, [Ad], [1.0])                                    # h Ad^T [M, r]
-    dBd = grad_at_b(dY2, ld(dY2), u, r, H, r, M, alpha=s_down)   # [H, r]
+    dt = A_gate.dtype
+    dAd = grad_at_b(td, r, h, I, r, I, M, out_dtype=dt)          # [r, I] = (sd dY Bd)^T h
+    if aux is not None and "xd" in aux:
+        dBd = grad_at_b(dY2, ld(dY2), aux["xd"], r, H, r, M, out_dtype=dt)  # [H, r] = dY^T (sd h Ad^T)
+    else:
+        u = lora_a(h, [Ad], [1.0])                                # h Ad^T [M, r]
+        dBd = grad_at_b(dY2, ld(dY2), u, r, H, r, M, alpha=s_down, out_dtype=dt)
 
     # 4: up / gate LoRA grads
     v = torch.empty(M, 2 * r, dtype=torch.bfloat16, device=dev)  # [su df Bu | sg de Bg]
     gemm(M, r, [(df, I, Bu, ld(Bu), I)], ROW, ROW, out=v[:, :r], alpha=s_up)
     gemm(M, r, [(de, I, Bg, ld(Bg), I)], ROW, ROW, out=v[:, r:], alpha=s_gate)
-    dA_ug = grad_at_b(v, 2 * r, X2, ld(X2), 2 * r, H, M)         # [2r, H]: rows [dAu; dAg]
-    xa_ug = lora_a(X2, [Au, Ag], [1.0, 1.0])                     # [X Au^T | X Ag^T]
-    dBu = grad_at_b(df, I, xa_ug[:, :r], 2 * r, I, r, M, alpha=s_up)
-    dBg = grad_at_b(de, I, xa_ug[:, r:], 2 * r, I, r, M, alpha=s_gate)
+    dA_ug = grad_at_b(v, 2 * r, X2, ld(X2), 2 * r, H, M, out_dtype=dt)  # [2r, H]: rows [dAu; dAg]
+    if aux is not None and "xa" in aux:
+        xa = aux["xa"]                                            # [sg X Ag^T | su X Au^T]
+        dBu = grad_at_b(df, I, xa[:, r:], 2 * r, I, r, M, out_dtype=dt)
+        dBg = grad_at_b(de, I, xa[:, :r], 2 * r, I, r, M, out_dtype=dt)
+    else:
+        xa_ug = lora_a(X2, [Au, Ag], [1.0, 1.0])                 # [X Au^T | X Ag^T]
+        dBu = grad_at_b(df, I, xa_ug[:, :r], 2 * r, I, r, M, alpha=s_up, out_dtype=dt)
+        dBg = grad_at_b(de, I, xa_ug[:, r:], 2 * r, I, r, M, alpha=s_gate, out_dtype=dt)
 
     # 5: dX
     if kt:
@@ -124,8 +141,7 @@ def mlp_backward(dY2, X2, e, g, W_gate, A_gate, B_gate, s_gate, W_up, A_up, B_up
     else:
         dX = gemm(M, H, [(df, I, Wu, ld(Wu), I), (de, I, Wg, ld(Wg), I),
                          (v[:, :r], 2 * r, Au, ld(Au), r), (v[:, r:], 2 * r, Ag, ld(Ag), r)], ROW, ROW)
-    dt = A_gate.dtype
-    return (dX, dA_ug[r:].to(dt), dBg.to(dt), dA_ug[:r].to(dt), dBu.to(dt), dAd.to(dt), dBd.to(dt))
+    return (dX, dA_ug[r:], dBg, dA_ug[:r], dBu, dAd, dBd)
 
 
 def torch_forward(X, W_gate, A_gate, B_gate, s_gate, W_up, A_up, B_up, s_up, W_down, A_down, B_down, s_down):
@@ -159,16 +175,17 @@ def torch_backward(dY, X, e, g, W_gate, A_gate, B_gate, s_gate, W_up, A_up, B_up
     return dX, d_gateA, d_gateB, d_upA, d_upB, d_downA, d_downB
 
 
-def run_forward(X, params, save_eg=True):
+def run_forward(X, params, save_eg=True, aux=None):
     """Dispatch on dtype: float64 -> the reference's PyTorch path, bf16 ->
-    the HIP kernels.  Returns (out with X's leading shape, e, g)."""
+    the HIP kernels.  Returns (out with X's leading shape, e, g); aux (a dict)
+    collects the LoRA-A products for run_backward."""
     if X.dtype == torch.float64:
         Xf = X.reshape(-1, X.shape[-1])
         out, e, g = torch_forward(Xf, *params)
     else:
         if X.dtype != torch.bfloat16:
             raise TypeError(f"LoRA-MLP kernels run in bf16 (or float64 via PyTorch), got {X.dtype}")
-        out, e, g = mlp_forward(X.reshape(-1, X.shape[-1]), *params, save_eg=save_eg)
+        out, e, g = mlp_forward(X.reshape(-1, X.shape[-1]), *params, save_eg=save_eg, aux=aux)
     if X.dim() == 3:
         out = out.reshape(X.shape[0], X.shape[1], -1)
         if e is not None:
@@ -177,14 +194,14 @@ def run_forward(X, params, save_eg=True):
     return out, e, g
 
 
-def run_backward(dY, X, e, g, params):
+def run_backward(dY, X, e, g, params, aux=None):
     dY2 = dY.reshape(-1, dY.shape[-1])
     X2 = X.reshape(-1, X.shape[-1])
     e2 = e.reshape(-1, e.shape[-1])
     g2 = g.reshape(-1, g.shape[-1])
     if X.dtype == torch.float64:
         return torch_backward(dY2, X2, e2, g2, *params)
-    return mlp_backward(dY2, X2, e2, g2, *params)
+    return mlp_backward(dY2, X2, e2, g2, *params, aux=aux)
 
 
 def stack_lora_a(A_gate: torch.Tensor, A_up: torch.Tensor) -> torch.Tensor:

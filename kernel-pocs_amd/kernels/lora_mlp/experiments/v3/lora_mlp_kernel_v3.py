@@ -24,7 +24,9 @@ class LoRAMLPv3(torch.autograd.Function):
     @staticmethod
     def forward(ctx, X, W_gate, A_gate, B_gate, s_gate, W_up, A_up, B_up, s_up, W_down, A_down, B_down, s_down):
         params = (W_gate, A_gate, B_gate, s_gate, W_up, A_up, B_up, s_up, W_down, A_down, B_down, s_down)
-        out, e, g = run_forward(X, params, save_eg=True)
+        aux = {}  # LoRA-A products reused by the backward (kept on ctx, outside saved_tensors)
+        out, e, g = run_forward(X, params, save_eg=True, aux=aux)
+        ctx.lora_aux = aux
         ctx.save_for_backward(A_gate, B_gate, A_up, B_up, A_down, B_down, X, e, g)
         ctx.scales = (s_gate, s_up, s_down)
         ctx.base_weights = (W_gate, W_up, W_down)
@@ -37,7 +39,7 @@ class LoRAMLPv3(torch.autograd.Function):
         W_gate, W_up, W_down = ctx.base_weights
         batch, seq_len, hd = X.shape
         params = (W_gate, A_gate, B_gate, s_gate, W_up, A_up, B_up, s_up, W_down, A_down, B_down, s_down)
-        dX, dAg, dBg, dAu, dBu, dAd, dBd = run_backward(dY, X, e, g, params)
+        dX, dAg, dBg, dAu, dBu, dAd, dBd = run_backward(dY, X, e, g, params, aux=ctx.lora_aux)
         return (
             dX.view(batch, seq_len, hd),
             None, dAg, dBg, None,

@@ -50,7 +50,9 @@ class LoRAMLPv6(torch.autograd.Function):
                 A_stack=None, W_gate_stack=None, W_down_stack=None, enable_streams: bool = True,
                 side_stream: Optional[torch.cuda.Stream] = None):
         params = (W_gate, A_gate, B_gate, s_gate, W_up, A_up, B_up, s_up, W_down, A_down, B_down, s_down)
-        out, e, g = run_forward(X, params, save_eg=True)
+        aux = {}  # LoRA-A products reused by the backward (kept on ctx, outside saved_tensors)
+        out, e, g = run_forward(X, params, save_eg=True, aux=aux)
+        ctx.lora_aux = aux
         ctx.save_for_backward(A_gate, B_gate, A_up, B_up, A_down, B_down, X, e, g)
         ctx.scales = (s_gate, s_up, s_down)
         ctx.base_weights = (W_gate, W_up, W_down)
@@ -63,7 +65,7 @@ class LoRAMLPv6(torch.autograd.Function):
         W_gate, W_up, W_down = ctx.base_weights
         batch, seq_len, hd = X.shape
         params = (W_gate, A_gate, B_gate, s_gate, W_up, A_up, B_up, s_up, W_down, A_down, B_down, s_down)
-        dX, dAg, dBg, dAu, dBu, dAd, dBd = run_backward(dY, X, e, g, params)
+        dX, dAg, dBg, dAu, dBu, dAd, dBd = run_backward(dY, X, e, g, params, aux=ctx.lora_aux)
         return (
             dX.view(batch, seq_len, hd),
             None, dAg, dBg, None,

@@ -33,9 +33,11 @@ def _w(t):
 
 
 def qkv_forward(X2, W_q, W_k, W_v, A_q, B_q, s_q, A_k, B_k, s_k, A_v, B_v, s_v,
-                rope: Optional[dict] = None):
+                rope: Optional[dict] = None, aux: Optional[dict] = None):
     """Returns out [M, Hq + 2 Hkv] bf16.  rope = {cos, sin, positions, head_dim}
-    (bf16 tables [P, D]; int64 positions [M]) applies RoPE to Q and K."""
+    (bf16 tables [P, D]; int64 positions [M]) applies RoPE to Q and K.
+    aux (a dict, optional) receives xa = [sq X Aq^T | sk X Ak^T | sv X Av^T]
+    for the backward's B gradients."""
     L.require_gpu(X2, W_q, W_k, W_v)
     X2 = as_operand(X2)
     Wq, Wk, Wv = _w(W_q), _w(W_k), _w(W_v)
@@ -49,6 +51,8 @@ def qkv_forward(X2, W_q, W_k, W_v, A_q, B_q, s_q, A_k, B_k, s_k, A_v, B_v, s_v,
     if has_lora:
         xa = lora_a(X2, [A_q, A_k, A_v], [s_q, s_k, s_v])
         Bq, Bk, Bv = _w(B_q), _w(B_k), _w(B_v)
+        if aux is not None:
+            aux["xa"] = xa
     if rope is not None:
         cos, sin = rope["cos"], rope["sin"]
         pos = rope.get("positions")
@@ -69,8 +73,10 @@ def qkv_forward(X2, W_q, W_k, W_v, A_q, B_q, s_q, A_k, B_k, s_k, A_v, B_v, s_v,
     return out
 
 
-def qkv_backward(dQ, dK, dV, X2, W_q, W_k, W_v, A_q, B_q, s_q, A_k, B_k, s_k, A_v, B_v, s_v):
-    """Returns (dX, dA_q, dB_q, dA_k, dB_k, dA_v, dB_v)."""
+def qkv_backward(dQ, dK, dV, X2, W_q, W_k, W_v, A_q, B_q, s_q, A_k, B_k, s_k, A_v, B_v, s_v,
+                 aux: Optional[dict] = None):
+    """Returns (dX, dA_q, dB_q, dA_k, dB_k, dA_v, dB_v).  With the forward's
+    aux the B gradients reuse its scaled xa instead of re-reading X."""
     X2 = as_operand(X2)
     dQ, dK, dV = as_operand(dQ), as_operand(dK), as_operand(dV)
     Wq, Wk, Wv = _w(W_q), _w(W_k), _w(W_v)
@@ -83,11 +89,15 @@ def qkv_backward(dQ, dK, dV, X2, W_q, W_k, W_v, A_q, B_q, s_q, A_k, B_k, s_k, A_
     gemm(M, r, [(dQ, ld(dQ), Bq, ld(Bq), Hq)], ROW, ROW, out=t[:, :r], alpha=s_q)
     gemm(M, r, [(dK, ld(dK), Bk, ld(Bk), Hkv)], ROW, ROW, out=t[:, r:2 * r], alpha=s_k)
     gemm(M, r, [(dV, ld(dV), Bv, ld(Bv), Hkv)], ROW, ROW, out=t[:, 2 * r:], alpha=s_v)
-    dA = grad_at_b(t, 3 * r, X2, ld(X2), 3 * r, K, M)  # [3r, K] (scales included via t)
-    xa = lora_a(X2, [Aq, Ak, Av], [1.0, 1.0, 1.0])     # unscaled X A_p^T
-    dBq = grad_at_b(dQ, ld(dQ), xa[:, :r], 3 * r, Hq, r, M, alpha=s_q)
-    dBk = grad_at_b(dK, ld(dK), xa[:, r:2 * r], 3 * r, Hkv, r, M, alpha=s_k)
-    dBv = grad_at_b(dV, ld(dV), xa[:, 2 * r:], 3 * r, Hkv, r, M, alpha=s_v)
+    dt = A_q.dtype
+    dA = grad_at_b(t, 3 * r, X2, ld(X2), 3 * r, K, M, out_dtype=dt)  # [3r, K] (scales included via t)
+    if aux is not None and "xa" in aux:
+        xa, sc = aux["xa"], (1.0, 1.0, 1.0)            # scaled s_p X A_p^T from the forward
+    else:
+        xa, sc = lora_a(X2, [Aq, Ak, Av], [1.0, 1.0, 1.0]), (s_q, s_k, s_v)
+    dBq = grad_at_b(dQ, ld(dQ), xa[:, :r], 3 * r, Hq, r, M, alpha=sc[0], out_dtype=dt)
+    dBk = grad_at_b(dK, ld(dK), xa[:, r:2 * r], 3 * r, Hkv, r, M, alpha=sc[1], out_dtype=dt)
+    dBv = grad_at_b(dV, ld(dV), xa[:, 2 * r:], 3 * r, Hkv, r, M, alpha=sc[2], out_dtype=dt)
     if r % 8 == 0:  # K-contiguous weights: the LDS-DMA engine (cached W^T, small A^T)
         dX = gemm(M, K, [(dQ, ld(dQ), frozen_t(W_q), Hq, Hq), (dK, ld(dK), frozen_t(W_k), Hkv, Hkv),
                          (dV, ld(dV), frozen_t(W_v), Hkv, Hkv), (t[:, :r], 3 * r, small_t(Aq), r, r),
@@ -97,8 +107,7 @@ def qkv_backward(dQ, dK, dV, X2, W_q, W_k, W_v, A_q, B_q, s_q, A_k, B_k, s_k, A_
         dX = gemm(M, K, [(dQ, ld(dQ), Wq, ld(Wq), Hq), (dK, ld(dK), Wk, ld(Wk), Hkv),
                          (dV, ld(dV), Wv, ld(Wv), Hkv), (t[:, :r], 3 * r, Aq, ld(Aq), r),
                          (t[:, r:2 * r], 3 * r, Ak, ld(Ak), r), (t[:, 2 * r:], 3 * r, Av, ld(Av), r)], ROW, ROW)
-    dt = A_q.dtype
-    return (dX, dA[:r].to(dt), dBq.to(dt), dA[r:2 * r].to(dt), dBk.to(dt), dA[2 * r:].to(dt), dBv.to(dt))
+    return (dX, dA[:r], dBq, dA[r:2 * r], dBk, dA[2 * r:], dBv)
 
 
 def torch_qkv_forward(X, W_q, W_k, W_v, A_q, B_q, s_q, A_k, B_k, s_k, A_v, B_v, s_v):

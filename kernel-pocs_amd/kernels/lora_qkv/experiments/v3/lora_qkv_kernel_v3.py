@@ -20,8 +20,9 @@ class LoRAQKVFunction(torch.autograd.Function):
         orig_shape = X.shape
         X2 = X.reshape(-1, X.shape[-1])
         ctx.use_hip = X.dtype != torch.float64
+        ctx.lora_aux = {}  # forward products reused by the backward (outside saved_tensors)
         if ctx.use_hip:
-            out = qkv_forward(X2, W_q, W_k, W_v, A_q, B_q, s_q, A_k, B_k, s_k, A_v, B_v, s_v)
+            out = qkv_forward(X2, W_q, W_k, W_v, A_q, B_q, s_q, A_k, B_k, s_k, A_v, B_v, s_v, aux=ctx.lora_aux)
             Q, K, V = split_views(out, W_q.shape[0], W_k.shape[0], orig_shape)
         else:
             Q, K, V = torch_qkv_forward(X2, W_q, W_k, W_v, A_q, B_q, s_q, A_k, B_k, s_k, A_v, B_v, s_v)
@@ -35,10 +36,12 @@ class LoRAQKVFunction(torch.autograd.Function):
     def backward(ctx, dQ, dK, dV):
         X, W_q, W_k, W_v, A_q, B_q, A_k, B_k, A_v, B_v = ctx.saved_tensors
         s_q, s_k, s_v = ctx.scalings
-        fn = qkv_backward if ctx.use_hip else torch_qkv_backward
         f = lambda t: t.reshape(-1, t.shape[-1])  # noqa: E731
-        dX, dAq, dBq, dAk, dBk, dAv, dBv = fn(f(dQ), f(dK), f(dV), f(X), W_q, W_k, W_v,
-                                              A_q, B_q, s_q, A_k, B_k, s_k, A_v, B_v, s_v)
+        args = (f(dQ), f(dK), f(dV), f(X), W_q, W_k, W_v, A_q, B_q, s_q, A_k, B_k, s_k, A_v, B_v, s_v)
+        if ctx.use_hip:
+            dX, dAq, dBq, dAk, dBk, dAv, dBv = qkv_backward(*args, aux=ctx.lora_aux)
+        else:
+            dX, dAq, dBq, dAk, dBk, dAv, dBv = torch_qkv_backward(*args)
         if X.dim() == 3:
             dX = dX.reshape(X.shape)
         return (dX, None, None, None, dAq, dBq, None, dAk, dBk, None, dAv, dBv, None, None)

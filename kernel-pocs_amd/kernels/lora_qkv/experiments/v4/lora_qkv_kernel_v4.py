@@ -43,8 +43,9 @@ class LoRAQKVv4Function(torch.autograd.Function):
         use_hip = X.dtype != torch.float64
         orig_shape = X.shape
         X2 = _flat(X)
+        ctx.lora_aux = {}  # forward products reused by the backward (outside saved_tensors)
         if use_hip:
-            out = qkv_forward(X2, W_q, W_k, W_v, A_q, B_q, s_q, A_k, B_k, s_k, A_v, B_v, s_v)
+            out = qkv_forward(X2, W_q, W_k, W_v, A_q, B_q, s_q, A_k, B_k, s_k, A_v, B_v, s_v, aux=ctx.lora_aux)
             Q, K, V = split_views(out, W_q.shape[0], W_k.shape[0], orig_shape)
         else:
             Q, K, V = torch_qkv_forward(X2, W_q, W_k, W_v, A_q, B_q, s_q, A_k, B_k, s_k, A_v, B_v, s_v)
@@ -63,9 +64,11 @@ class LoRAQKVv4Function(torch.autograd.Function):
         s_q, s_k, s_v = ctx.scalings
         W_q, W_k, W_v = ctx.base_weights
         X2 = _flat(X)
-        fn = qkv_backward if ctx.use_triton else torch_qkv_backward
-        dX, dAq, dBq, dAk, dBk, dAv, dBv = fn(_flat(dQ), _flat(dK), _flat(dV), X2, W_q, W_k, W_v,
-                                              A_q, B_q, s_q, A_k, B_k, s_k, A_v, B_v, s_v)
+        args = (_flat(dQ), _flat(dK), _flat(dV), X2, W_q, W_k, W_v, A_q, B_q, s_q, A_k, B_k, s_k, A_v, B_v, s_v)
+        if ctx.use_triton:
+            dX, dAq, dBq, dAk, dBk, dAv, dBv = qkv_backward(*args, aux=ctx.lora_aux)
+        else:
+            dX, dAq, dBq, dAk, dBk, dAv, dBv = torch_qkv_backward(*args)
         if X.dim() == 3:
             dX = dX.reshape(X.shape)
         return (dX, None, None, None, dAq, dBq, None, dAk, dBk, None, dAv, dBv, None, None, None, None)
@@ -115,8 +118,10 @@ class LoRAQKVRoPEFunction(torch.autograd.Function):
         cos2 = cos.reshape(-1, cos.shape[-1]).to(torch.bfloat16).contiguous()
         sin2 = sin.reshape(-1, sin.shape[-1]).to(torch.bfloat16).contiguous()
         pos = positions.reshape(-1).to(device=X.device, dtype=torch.int64).contiguous() if positions is not None else None
+        ctx.lora_aux = {}  # forward products reused by the backward (outside saved_tensors)
         out = qkv_forward(X2, W_q, W_k, W_v, A_q, B_q, s_q, A_k, B_k, s_k, A_v, B_v, s_v,
-                          rope={"cos": cos2, "sin": sin2, "positions": pos, "head_dim": int(head_dim)})
+                          rope={"cos": cos2, "sin": sin2, "positions": pos, "head_dim": int(head_dim)},
+                          aux=ctx.lora_aux)
         ctx.save_for_backward(X, A_q, B_q, A_k, B_k, A_v, B_v, cos2, sin2, pos)
         ctx.scalings = (s_q, s_k, s_v)
         ctx.base_weights = (W_q, W_k, W_v)
@@ -135,7 +140,8 @@ class LoRAQKVRoPEFunction(torch.autograd.Function):
         dQu = _rope_rows_backward(dQ2, dQ2.shape[1] // D, D, cos2, sin2, pos)
         dKu = _rope_rows_backward(dK2, dK2.shape[1] // D, D, cos2, sin2, pos)
         dX, dAq, dBq, dAk, dBk, dAv, dBv = qkv_backward(dQu, dKu, _flat(dV), _flat(X), W_q, W_k, W_v,
-                                                        A_q, B_q, s_q, A_k, B_k, s_k, A_v, B_v, s_v)
+                                                        A_q, B_q, s_q, A_k, B_k, s_k, A_v, B_v, s_v,
+                                                        aux=ctx.lora_aux)
         if X.dim() == 3:
             dX = dX.reshape(X.shape)
         return (dX, None, None, None, dAq, dBq, None, dAk, dBk, None, dAv, dBv, None, None, None, None, None)

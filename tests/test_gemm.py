@@ -122,3 +122,36 @@ def test_gemm_rejects_bad_segments_without_gpu():
     assert rc == 1 and b"multiple of 8" in L.forge_last_error()
     rc = L.forge_gemm(8, 8, seg, 0, 0, 1, 16, 8, L.DTYPE_BF16, 1.0, 0.0, L.EPI_STORE, 1, None)
     assert rc == 1
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("dtype,code", [(torch.float32, 0), (torch.bfloat16, 2)])
+@pytest.mark.parametrize("rows,cols,n_split", [(37, 52, 5), (16, 14336, 9), (3, 7, 1)])
+def test_splitk_reduce_sums_partials_in_order(dtype, code, rows, cols, n_split):
+    """forge_splitk_reduce: alpha * sum over split slices, fixed order,
+    rounded once; both the 4-wide and the scalar paths (cols % 4)."""
+    gen = torch.Generator().manual_seed(rows * cols + n_split)
+    parts = torch.randn(n_split, rows, cols, generator=gen)
+    out = torch.empty(rows, cols, dtype=dtype, device="cuda")
+    p = parts.cuda()
+    L.check(L.forge_splitk_reduce(p.data_ptr(), rows * cols, n_split, rows, cols, cols, out.data_ptr(), cols, code,
+                                  0.5, L.stream_of(p)), "forge_splitk_reduce")
+    acc = torch.zeros(rows, cols)
+    for z in range(n_split):
+        acc = acc + parts[z]
+    ref = (0.5 * acc).to(dtype)
+    assert torch.equal(out.cpu(), ref)
+
+
+@pytest.mark.gpu
+def test_gemm_split_k_partials_match_single_pass():
+    """EPI_STORE with an fp32 C and split_k > 1 writes one partial slice per
+    split; their sum equals the unsplit product."""
+    gen = torch.Generator().manual_seed(11)
+    M, N, K, split = 1024, 32, 2048, 6
+    a, A = _operand(M, K, 0, gen)
+    b, B = _b_operand(N, K, 1, gen)
+    parts = torch.empty(split, M, N, dtype=torch.float32, device="cuda")
+    _gemm(M, N, [(a, K, b, K, K)], 0, 1, parts.view(split * M, N), L.DTYPE_F32, split_k=split)
+    ref = A @ B
+    torch.testing.assert_close(parts.sum(0).cpu(), ref, atol=1e-3 * ref.abs().max().item(), rtol=1e-3)

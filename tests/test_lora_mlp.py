@@ -104,6 +104,22 @@ def test_lora_mlp_fp64_gradcheck_uses_reference_torch_path():
 
 
 @pytest.mark.gpu
+def test_lora_mlp_gradients_are_deterministic():
+    """Split-K products are reduced in a fixed order (no atomics), so two
+    identical fwd+bwd passes give bit-identical outputs and gradients."""
+    gen = torch.Generator().manual_seed(77)
+    H, I, r = 512, 1536, 16
+    params = orc.make_params(H, I, r, 32, gen)
+    X = torch.randn(1, 2048, H, generator=gen).to(torch.bfloat16)
+    dY = torch.randn(1, 2048, H, generator=gen).to(torch.bfloat16)
+    out1, g1 = _run(LoRAMLPv6.apply, X, dY, params)
+    out2, g2 = _run(LoRAMLPv6.apply, X, dY, params)
+    assert torch.equal(out1, out2)
+    for a, b in zip(g1, g2):
+        assert torch.equal(a, b)
+
+
+@pytest.mark.gpu
 def test_lora_mlp_baseline_config():
     """X [8192, 4096] ~ N(0,1), W ~ N(0, 0.02^2),
     r=16, alpha=32, A Kaiming-uniform, B ~ N(0, 0.01^2)."""
