@@ -7,7 +7,7 @@ namespace fgemm {
 
 // Tile configurations.
 enum Cfg {
-  CFG_BIG = 0,       // 256 x 256, 2 x 2 waves (128 x 128 per wave)
+  CFG_BIG = 0,       // 256 x 256: 2 x 2 waves (128 x 128 per wave); 4 x 2 on the LDS-DMA path
   CFG_SKINNY_N = 1,  // 256 x 32, 4 x 1 waves: N <= 32-ish (rank-r outputs)
   CFG_SKINNY_M = 2,  // 32 x 256, 1 x 4 waves: M <= 32-ish (LoRA A gradients)
 };
@@ -22,11 +22,14 @@ static int launch_cfg(const GemmArgs& a, hipStream_t s) {
   constexpr bool CAN_STAGE = staged_ok(BM, BN, WM, WN, EPI);
   const bool staged = CAN_STAGE && a.ep.vec_ok;
   if constexpr (BM == 256 && BN == 256 && AL == ROW && BL == COL) {
-    // both operands K-contiguous: the LDS-DMA engine (64-deep tiles, 2 stages)
-    if (staged)
-      gemm_dma_kernel<BM, BN, WM, WN, BMODE, EPI, 64, 2, CAN_STAGE><<<grid, WM * WN * 64, 0, s>>>(a);
+    // both operands K-contiguous: the LDS-DMA engine (64-deep tiles, 2 stages),
+    // 8 waves so that two share each SIMD
+    constexpr int DWM = 4, DWN = 2;
+    constexpr bool DMA_STAGE = staged_ok(BM, BN, DWM, DWN, EPI);
+    if (DMA_STAGE && a.ep.vec_ok)
+      gemm_dma_kernel<BM, BN, DWM, DWN, BMODE, EPI, 64, 2, DMA_STAGE><<<grid, DWM * DWN * 64, 0, s>>>(a);
     else
-      gemm_dma_kernel<BM, BN, WM, WN, BMODE, EPI, 64, 2, false><<<grid, WM * WN * 64, 0, s>>>(a);
+      gemm_dma_kernel<BM, BN, DWM, DWN, BMODE, EPI, 64, 2, false><<<grid, DWM * DWN * 64, 0, s>>>(a);
   } else {
     if (staged)
       gemm_kernel<BM, BN, WM, WN, AL, BL, BMODE, EPI, CAN_STAGE><<<grid, WM * WN * 64, 0, s>>>(a);

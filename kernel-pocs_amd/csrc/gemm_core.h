@@ -14,7 +14,10 @@
 //     LDS-DMA (buffer_load ... lds, no VGPR staging, no ds_write), XOR-swizzled
 //     unpadded LDS rows, a 2-stage ring (measured on MI355X: 918 -> 1018
 //     TFLOP/s on the 8192 x 28672 x 4096 gate/up GEMM; a 4-stage ring of
-//     32-deep tiles and an interleaved DMA issue were no faster);
+//     32-deep tiles and an interleaved DMA issue were no faster).  It runs
+//     8 waves (4 x 2, 64 x 128 per wave) so that each SIMD holds two waves
+//     whose MFMA chains cover each other's LDS reads and barriers (measured:
+//     the 8192 x 4096 x 14336 down-projection 1075 -> 1213 TFLOP/s);
 //   * gemm_kernel (every layout): loads through registers into padded LDS
 //     rows ([rows][64 + 8 pad] bf16, 144-byte pitch, conflict-free fragment
 //     reads), double-buffered.  Operands whose K dimension is not contiguous
@@ -335,15 +338,18 @@ __device__ __forceinline__ uint4 pack8(const float (&f)[8]) {
 
 // Tiles and epilogues the staged epilogue serves.
 constexpr bool staged_ok(int bm, int bn, int wm, int wn, int epi) {
-  return bm == 256 && bn == 256 && wm == 2 && wn == 2 &&
+  return bm == 256 && bn == 256 && (256 / wm) % 32 == 0 && (256 / wn) % 32 == 0 && 256 / wm <= 128 &&
          (epi == EPI_STORE_BF16 || epi == EPI_SWIGLU_FWD || epi == EPI_SWIGLU_BWD || epi == EPI_ROPE);
 }
 
-template <int BMODE, int EPI>
-__device__ __forceinline__ void epilogue_staged(const GemmArgs& args, f32x16 (&acc)[4][4], int64_t m0, int64_t n0,
-                                                int lane, int wm, int wn, float* lds) {
+template <int WAVES_M, int WAVES_N, int BMODE, int EPI>
+__device__ __forceinline__ void epilogue_staged(const GemmArgs& args,
+                                                f32x16 (&acc)[256 / WAVES_M / 32][256 / WAVES_N / 32], int64_t m0,
+                                                int64_t n0, int lane, int wm, int wn, float* lds) {
   constexpr int P = STAGED_PITCH;
-  constexpr int NT = 256;
+  constexpr int NT = WAVES_M * WAVES_N * 64;
+  constexpr int TM = 256 / WAVES_M, TN = 256 / WAVES_N;
+  constexpr int FM = TM / 32, FN = TN / 32;
   const EpiArgs& ep = args.ep;
   const int64_t M = args.M, N = args.N;
   const int tid = threadIdx.x;
@@ -351,14 +357,16 @@ __device__ __forceinline__ void epilogue_staged(const GemmArgs& args, f32x16 (&a
 #pragma unroll 1
   for (int pass = 0; pass < 2; ++pass) {
     if (pass) __syncthreads();  // pass 0's readers are done with the buffer
-    if (wm == pass) {
+    if ((wm * TM) / 128 == pass) {  // this wave's rows lie in the half being staged
+      const int row0 = wm * TM - pass * 128;
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
+      for (int i = 0; i < FM; ++i)
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
+        for (int j = 0; j < FN; ++j)
 #pragma unroll
           for (int r = 0; r < 16; ++r)
-            lds[(i * 32 + 8 * (r / 4) + 4 * (lane / 32) + r % 4) * P + wn * 128 + j * 32 + lane % 32] = acc[i][j][r];
+            lds[(row0 + i * 32 + 8 * (r / 4) + 4 * (lane / 32) + r % 4) * P + wn * TN + j * 32 + lane % 32] =
+                acc[i][j][r];
     }
     __syncthreads();
     const int64_t mrow0 = m0 + pass * 128;
@@ -788,8 +796,8 @@ void gemm_kernel(GemmArgs args) {
   }
 
   if constexpr (STAGED) {
-    static_assert(staged_ok(BM, BN, WAVES_M, WAVES_N, EPI), "staged epilogue: 256 x 256, 2 x 2 waves, bf16 out");
-    epilogue_staged<BMODE, EPI>(args, acc, m0, n0, lane, wm, wn, reinterpret_cast<float*>(smem));
+    static_assert(staged_ok(BM, BN, WAVES_M, WAVES_N, EPI), "staged epilogue: 256 x 256 tile, wave tiles of <= 128 rows");
+    epilogue_staged<WAVES_M, WAVES_N, BMODE, EPI>(args, acc, m0, n0, lane, wm, wn, reinterpret_cast<float*>(smem));
   } else {
     epilogue<BM, BN, WAVES_M, WAVES_N, BMODE, EPI>(args, acc, m0, n0, lane, wm, wn);
   }
@@ -822,7 +830,7 @@ struct DmaLoader {
   static constexpr int NW = NT / 64;
   static constexpr int IPW = NINST / NW;      // instructions per wave per tile
   static_assert(NINST % NW == 0 && IPW * RPI == BROWS / NW, "tile / wave split");
-  static_assert(!DUAL || (BROWS / NW) % 64 == 0, "dual: 32-row groups inside a wave's rows");
+  static_assert(!DUAL || RPI <= 32, "dual: an instruction's rows inside one 32-row group");
   uint32_t voff[IPW];   // byte offset of this lane's chunk in the panel (OOB = zero-fill)
   const char* base[2];
   int64_t ld_bytes;
@@ -839,7 +847,7 @@ struct DmaLoader {
     for (int j = 0; j < IPW; ++j) {
       const int q = (wave * IPW + j) * RPI + lane / CPR;   // tile row
       const int chunk = (lane % CPR) ^ swz<BKT>(q);        // source chunk of LDS slot lane % CPR
-      const int sel = DUAL ? ((j * RPI) / 32) % 2 : 0;     // 32-row groups alternate gate / up
+      const int sel = DUAL ? (((wave * IPW + j) * RPI) / 32) % 2 : 0;  // 32-row groups alternate gate / up
       const int64_t row = base[sel] ? row_src(q, sel) : -1;
       voff[j] = row < 0 ? OOB : (uint32_t)(row * ld_bytes + chunk * 16);
     }
@@ -847,7 +855,8 @@ struct DmaLoader {
 
   // DMA of the K tile at k0 (kvalid valid k) into the LDS stage `dst`.
   __device__ __forceinline__ void load(int64_t k0, int64_t kvalid, char* dst) {
-    const int lane = threadIdx.x % 64, wave = threadIdx.x / 64;
+    const int lane = threadIdx.x % 64;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / 64);
     const __amdgpu_buffer_rsrc_t r0 = make_rsrc(base[0] + k0 * 2);
     const __amdgpu_buffer_rsrc_t r1 = make_rsrc(base[1] + k0 * 2);
 #pragma unroll
@@ -858,7 +867,7 @@ struct DmaLoader {
         const int chunk = (lane % CPR) ^ swz<BKT>(q);
         if (chunk * 8 >= kvalid) off = OOB;
       }
-      const int sel = DUAL ? ((j * RPI) / 32) % 2 : 0;
+      const int sel = DUAL ? (((wave * IPW + j) * RPI) / 32) % 2 : 0;
       __builtin_amdgcn_raw_ptr_buffer_load_lds(sel ? r1 : r0,
                                                (__attribute__((address_space(3))) void*)(dst + (wave * IPW + j) * 1024),
                                                16, off, 0, 0, 0);
@@ -874,8 +883,12 @@ __device__ __forceinline__ void wait_vmcnt() {
   __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
 }
 
+// One workgroup per CU (the ring plus the staged epilogue take ~130 KB of LDS),
+// so the register budget is set by the waves per SIMD that one workgroup puts
+// there: 4 waves -> 1 per SIMD (512 VGPRs), 8 waves -> 2 per SIMD (256 each).
 template <int BM, int BN, int WAVES_M, int WAVES_N, int BMODE, int EPI, int BKT, int NSTAGE, bool STAGED>
-__global__ __launch_bounds__(WAVES_M * WAVES_N * 64) __attribute__((amdgpu_waves_per_eu(1, 1)))
+__global__ __launch_bounds__(WAVES_M * WAVES_N * 64)
+__attribute__((amdgpu_waves_per_eu(WAVES_M * WAVES_N / 4, WAVES_M * WAVES_N / 4)))
 void gemm_dma_kernel(GemmArgs args) {
   constexpr int NT = WAVES_M * WAVES_N * 64;
   constexpr int TM = BM / WAVES_M, TN = BN / WAVES_N;
@@ -1036,8 +1049,8 @@ void gemm_dma_kernel(GemmArgs args) {
     }
   }
   if constexpr (STAGED) {
-    static_assert(staged_ok(BM, BN, WAVES_M, WAVES_N, EPI), "staged epilogue: 256 x 256, 2 x 2 waves, bf16 out");
-    epilogue_staged<BMODE, EPI>(args, acc, m0, n0, lane, wm, wn, reinterpret_cast<float*>(smem));
+    static_assert(staged_ok(BM, BN, WAVES_M, WAVES_N, EPI), "staged epilogue: 256 x 256 tile, wave tiles of <= 128 rows");
+    epilogue_staged<WAVES_M, WAVES_N, BMODE, EPI>(args, acc, m0, n0, lane, wm, wn, reinterpret_cast<float*>(smem));
   } else {
     epilogue<BM, BN, WAVES_M, WAVES_N, BMODE, EPI>(args, acc, m0, n0, lane, wm, wn);
   }
