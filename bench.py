@@ -369,7 +369,11 @@ def bench_lora_mlp(args):
     X = torch.randn(1, M, H, device="cuda", generator=g).to(torch.bfloat16).requires_grad_(True)
     dY = torch.randn(1, M, H, device="cuda", generator=g).to(torch.bfloat16)
 
+    leaves = [X] + [t for t in params if isinstance(t, torch.Tensor) and t.requires_grad]
+
     def step(i):
+        for t in leaves:  # a training step after zero_grad(set_to_none=True)
+            t.grad = None
         out = LoRAMLPv6.apply(X, *params)
         out.backward(dY)
 
@@ -442,7 +446,11 @@ def bench_lora_qkv(args):
     dV = torch.randn(T, Hkv, device="cuda", generator=g).to(bf)
     c, sn = rope_cos_sin(torch.arange(max(lens), device="cuda"), D, 500000.0, bf)
 
+    leaves = (X, Aq, Bq, Ak, Bk, Av, Bv)
+
     def step(i):
+        for t in leaves:  # a training step after zero_grad(set_to_none=True)
+            t.grad = None
         Q, K_, V = lora_qkv_rope(X, Wq, Aq, Bq, s, Wk, Ak, Bk, s, Wv, Av, Bv, s, c, sn, pos, D)
         torch.autograd.backward((Q, K_, V), (dQ, dK, dV))
 

@@ -10,7 +10,15 @@ enum Cfg {
   CFG_BIG = 0,       // 256 x 256: 2 x 2 waves (128 x 128 per wave); 4 x 2 on the LDS-DMA path
   CFG_SKINNY_N = 1,  // 256 x 32, 4 x 1 waves: N <= 32-ish (rank-r outputs)
   CFG_SKINNY_M = 2,  // 32 x 256, 1 x 4 waves: M <= 32-ish (LoRA A gradients)
+  CFG_SKINNY_N64 = 3,  // 256 x 64, 4 x 1 waves (K-contiguous operands; else 256 x 32): 32 < N <= 64
 };
+
+#ifndef SKINNY_NSTAGE
+#define SKINNY_NSTAGE 2
+#endif
+#ifndef SKINNY_WPE
+#define SKINNY_WPE 2
+#endif
 
 template <int BM, int BN, int WM, int WN, int AL, int BL, int BMODE, int EPI>
 static int launch_cfg(const GemmArgs& a, hipStream_t s) {
@@ -27,9 +35,14 @@ static int launch_cfg(const GemmArgs& a, hipStream_t s) {
     constexpr int DWM = 4, DWN = 2;
     constexpr bool DMA_STAGE = staged_ok(BM, BN, DWM, DWN, EPI);
     if (DMA_STAGE && a.ep.vec_ok)
-      gemm_dma_kernel<BM, BN, DWM, DWN, BMODE, EPI, 64, 2, DMA_STAGE><<<grid, DWM * DWN * 64, 0, s>>>(a);
+      gemm_dma_kernel<BM, BN, DWM, DWN, BMODE, EPI, 64, 2, DMA_STAGE, 2><<<grid, DWM * DWN * 64, 0, s>>>(a);
     else
-      gemm_dma_kernel<BM, BN, DWM, DWN, BMODE, EPI, 64, 2, false><<<grid, DWM * DWN * 64, 0, s>>>(a);
+      gemm_dma_kernel<BM, BN, DWM, DWN, BMODE, EPI, 64, 2, false, 2><<<grid, DWM * DWN * 64, 0, s>>>(a);
+  } else if constexpr (BM == 256 && BN <= 64 && AL == ROW && BL == COL && BMODE == B_SINGLE) {
+    // skinny output, K-contiguous operands (X A^T, dY B with B^T given): the
+    // big operand streams through the LDS-DMA ring; ~72-80 KB of LDS lets two
+    // workgroups share a CU, so two K tiles per CU are in flight
+    gemm_dma_kernel<BM, BN, WM, WN, BMODE, EPI, 64, SKINNY_NSTAGE, false, SKINNY_WPE><<<grid, WM * WN * 64, 0, s>>>(a);
   } else {
     if (staged)
       gemm_kernel<BM, BN, WM, WN, AL, BL, BMODE, EPI, CAN_STAGE><<<grid, WM * WN * 64, 0, s>>>(a);
@@ -50,6 +63,12 @@ static int launch_layout(int cfg, const GemmArgs& a, hipStream_t s) {
     case CFG_SKINNY_M:
       if constexpr (BMODE == B_SINGLE) return launch_cfg<32, 256, 1, 4, AL, BL, BMODE, EPI>(a, s);
       break;
+    case CFG_SKINNY_N64:
+      if constexpr (BMODE == B_SINGLE) {
+        if constexpr (AL == ROW && BL == COL) return launch_cfg<256, 64, 4, 1, AL, BL, BMODE, EPI>(a, s);
+        return launch_cfg<256, 32, 4, 1, AL, BL, BMODE, EPI>(a, s);
+      }
+      break;
   }
   return forge_set_error(FORGE_ERR_UNSUPPORTED, "gemm: tile config %d", cfg);
 }
@@ -65,7 +84,8 @@ static int launch_epi(int cfg, int al, int bl, const GemmArgs& a, hipStream_t s)
 
 // Picks a tile shape from the output shape.
 static int pick_cfg(int64_t M, int64_t N) {
-  if (N <= 64 && M > N) return CFG_SKINNY_N;
+  if (N <= 32 && M > N) return CFG_SKINNY_N;
+  if (N <= 64 && M > N) return CFG_SKINNY_N64;
   if (M <= 64 && N > M) return CFG_SKINNY_M;
   return CFG_BIG;
 }

@@ -134,26 +134,39 @@ extern "C" int forge_lora_a(int64_t M, int64_t K, int64_t r, int n_proj, const v
   a.M = M;
   a.N = N;
   a.split_k = split_k > 1 ? split_k : 1;
-  a.n_segs = n_proj;
-  for (int p = 0; p < n_proj; ++p)
-    a.segs[p] = Seg{(const __bf16*)x, ldx, (const __bf16*)a_mats[p], nullptr, lda, K, p * r, (p + 1) * r};
+  // Matrices that are consecutive rows of one [n_proj * r][K] buffer (a
+  // stacked A) form a single K segment: X streams once per column tile.
+  // Otherwise each projection is a segment of its own, applied to its r
+  // output columns.
+  bool stacked = true;
+  for (int p = 1; p < n_proj; ++p)
+    stacked = stacked && (const char*)a_mats[p] == (const char*)a_mats[0] + (int64_t)p * r * lda * 2;
+  if (stacked) {
+    a.n_segs = 1;
+    a.segs[0] = Seg{(const __bf16*)x, ldx, (const __bf16*)a_mats[0], nullptr, lda, K, 0, N};
+  } else {
+    a.n_segs = n_proj;
+    for (int p = 0; p < n_proj; ++p)
+      a.segs[p] = Seg{(const __bf16*)x, ldx, (const __bf16*)a_mats[p], nullptr, lda, K, p * r, (p + 1) * r};
+  }
   a.ep.alpha = 1.f;
   a.ep.alpha_group = r;
   for (int p = 0; p < 4; ++p) a.ep.alphas[p] = p < n_proj ? scales[p] : 1.f;
-  // 256 x 32 tiles: every tile covers at most two projections' columns and
-  // no MFMA work is spent on columns outside [0, n_proj * r).  With split_k
-  // the K range is spread over split_k workgroups per tile (the skinny output
-  // alone gives only M/256 tiles): split z writes fp32 partial sums to
-  // work[z] ([split_k][M][N]), which one reduction pass sums in a fixed order
-  // (deterministic) and rounds to bf16.
+  // 256 x 32 tiles for N <= 32, else 256 x 64 (X A^T is K-contiguous: both
+  // run on the LDS-DMA ring).  With split_k the K range is spread over
+  // split_k workgroups per tile (the skinny output alone gives only M/256
+  // tiles): split z writes fp32 partial sums to work[z] ([split_k][M][N]),
+  // which one reduction pass sums in a fixed order (deterministic) and rounds
+  // to bf16.
+  const int cfg = N <= 32 ? 1 /* CFG_SKINNY_N */ : 3 /* CFG_SKINNY_N64 */;
   if (split_k <= 1) {
     a.ep.c = out;
     a.ep.ldc = ld_out;
-    return run(1 /* CFG_SKINNY_N */, ROW, COL, EPI_STORE_BF16, a, s);
+    return run(cfg, ROW, COL, EPI_STORE_BF16, a, s);
   }
   a.ep.c = work;
   a.ep.ldc = N;
   a.ep.split_stride = M * N;
-  if (int e = run(1 /* CFG_SKINNY_N */, ROW, COL, EPI_STORE_F32, a, s)) return e;
+  if (int e = run(cfg, ROW, COL, EPI_STORE_F32, a, s)) return e;
   return forge_splitk_reduce(work, M * N, split_k, M, N, N, out, ld_out, FORGE_DTYPE_BF16, 1.0f, stream);
 }

@@ -34,11 +34,13 @@ def ld(t: torch.Tensor) -> int:
 
 
 def skinny_split(M: int, N: int, K: int) -> int:
-    """Split-K factor for a skinny output (N <= 64): the 256 x 32 tiles alone
-    give only M/256 workgroups, too few to keep HBM busy; aim for ~512."""
-    tiles = max(1, (M + 255) // 256) * max(1, (N + 31) // 32)
+    """Split-K factor for a skinny output: the 256 x 32 (N <= 32) or 256 x 64
+    tiles alone give only M/256 workgroups per column tile, too few to keep
+    HBM busy; aim for ~512 (two workgroups on each of the 256 CUs)."""
+    tile_n = 32 if N <= 32 else 64
+    tiles = max(1, (M + 255) // 256) * max(1, (N + tile_n - 1) // tile_n)
     k_tiles = max(1, (K + 63) // 64)
-    return max(1, min(16, 512 // tiles, k_tiles // 4))
+    return max(1, min(16, -(-512 // tiles), k_tiles // 4))
 
 
 def gemm(M: int, N: int, segs: Sequence[Tuple[torch.Tensor, int, torch.Tensor, int, int]], a_layout: int,
@@ -93,6 +95,13 @@ def split_gemm(M: int, N: int, segs, a_layout: int, b_layout: int, split: int, o
     return out
 
 
+def _row_stacked(mats: Sequence[torch.Tensor]) -> bool:
+    """True when mats are consecutive row blocks of one buffer (same pitch)."""
+    r, pitch, base = mats[0].shape[0], ld(mats[0]), mats[0].data_ptr()
+    return all(ld(a) == pitch and a.data_ptr() == base + p * r * pitch * a.element_size()
+               for p, a in enumerate(mats))
+
+
 def lora_a(x: torch.Tensor, mats: Sequence[torch.Tensor], scales: Sequence[float],
            out: Optional[torch.Tensor] = None) -> torch.Tensor:
     """[s_p * x @ A_p^T for p] concatenated along columns -> [M, n*r] bf16."""
@@ -102,6 +111,10 @@ def lora_a(x: torch.Tensor, mats: Sequence[torch.Tensor], scales: Sequence[float
     if out is None:
         out = torch.empty(M, n * r, dtype=torch.bfloat16, device=x.device)
     mats = [as_operand(a) for a in mats]
+    if n > 1 and not _row_stacked(mats):
+        # one [n r, K] buffer: the kernel then streams x once per column tile
+        stack = torch.cat([a.detach() for a in mats], 0)
+        mats = [stack[p * r:(p + 1) * r] for p in range(n)]
     ptrs = (ctypes.c_void_p * n)(*[a.data_ptr() for a in mats])
     sc = (ctypes.c_float * n)(*[float(s) for s in scales])
     split = skinny_split(M, n * r, K) if M >= 1024 else 1
