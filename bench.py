@@ -459,23 +459,26 @@ def bench_lora_qkv(args):
     tf = rate(fl, ms, 1e12)
     # dominant kernel: the forward GEMM (X [Wq;Wk;Wv]^T + LoRA-B segment, RoPE epilogue)
     from forge_hip import _lib as L
-    from kernels.lora_qkv._impl import qkv_forward
+    from kernels._lora_ops import lora_a
 
     Xd = X.detach()
-    rope = {"cos": c, "sin": sn, "positions": pos, "head_dim": D}
-    launch_ms = time_launches(lambda i: qkv_forward(Xd, Wq, Wk, Wv, Aq.detach(), Bq.detach(), s, Ak.detach(),
-                                                    Bk.detach(), s, Av.detach(), Bv.detach(), s, rope=rope),
-                              max(args.steps, 10))
-    fwd_flops = 2 * T * K * (Hq + 2 * Hkv) + 2 * T * 3 * r * K + 2 * T * r * (Hq + 2 * Hkv)
+    xa = lora_a(Xd, [Aq.detach(), Ak.detach(), Av.detach()], [s, s, s])  # the forward's LoRA-A product
+    out = torch.empty(T, Hq + 2 * Hkv, device="cuda", dtype=bf)
+    st = L.stream_of(Xd)
+    launch_ms = time_launches(lambda i: L.forge_lora_qkv_rope(
+        T, K, Hq, Hkv, r, Xd.data_ptr(), K, Wq.data_ptr(), Wk.data_ptr(), Wv.data_ptr(), K, xa.data_ptr(), 3 * r,
+        Bq.data_ptr(), Bk.data_ptr(), Bv.data_ptr(), r, out.data_ptr(), Hq + 2 * Hkv, c.data_ptr(), sn.data_ptr(),
+        c.stride(0), pos.data_ptr(), D, 1, st), max(args.steps, 10))
+    fwd_flops = 2 * T * K * (Hq + 2 * Hkv) + 2 * T * r * (Hq + 2 * Hkv)
     res = {
         "config": {"workload": "lora_qkv_rope_fwd_bwd", "dtype": "bf16", "tokens": T, "seq_lens": lens,
                    "hidden": K, "q_heads": 32, "kv_heads": 8, "head_dim": D, "rank": r, "alpha": 128,
                    "rope_base": 500000},
         "value": tf, "unit": "TFLOP/s", "ms_per_step": rnd(ms, 4), "wall_ms_per_step": rnd(wall, 4),
         "frac_of_mfma_peak": rnd(tf and tf / BF16_PEAK_TFLOPS, 4), "algorithmic_flops_per_step": fl,
-        "launches_ms": {"lora_qkv_forward (forge_lora_a + forge_lora_qkv_rope)": round(launch_ms, 4)},
+        "launches_ms": {"forge_lora_qkv_rope": round(launch_ms, 4)},
         "roofline": _roof("mfma", fwd_flops / (launch_ms * 1e-3) / 1e12, BF16_PEAK_TFLOPS, "TFLOP/s",
-                          _traffic("lora_qkv_fwd")),
+                          _traffic("lora_qkv_fwd_gemm")),
         "dtype": "bf16",
     }
     if not (args.no_cpu_baseline or args.only_launches):
