@@ -155,6 +155,41 @@ int forge_ce_scale(int dtype, void* x, int64_t ld, int64_t n_rows, int64_t n_col
  * (kernels/cross_entropy/experiments/v2/cross_entropy_kernel_v2.py:451). */
 int forge_sum_f32(const float* x, int64_t n, float* out, void* out_cast, int cast_dtype, void* stream);
 
+/* Token scaling of the fused linear + cross-entropy path: prob[r] = the
+ * softmax probability of row r's target class after the optional softcap
+ * (softcap <= 0: none), rounded to the logits dtype; 0 for ignored rows.
+ * Replaces the `use_token_scaling` block of `fused_linear_cross_entropy_forward`
+ * (kernels/cross_entropy/experiments/v2/fused_linear_cross_entropy.py:148-160). */
+int forge_ce_target_prob(int dtype, const void* logits, int64_t ld, int64_t n_rows, int64_t n_cols,
+                         const int64_t* target, int64_t target_stride, int64_t ignore_index, float softcap,
+                         float* prob, void* stream);
+
+/* x[r, :n_cols] *= scale[r] (fp32 scales), in place, rounded to x's dtype
+ * (fp32, bf16 or fp16).  Replaces the loss and dlogits multiplications by the
+ * token scaling factors (fused_linear_cross_entropy.py:196-205). */
+int forge_row_scale(int dtype, void* x, int64_t ld, int64_t n_rows, int64_t n_cols, const float* scale,
+                    void* stream);
+
+/* ------------------------------------------------------------------------
+ * Generic GEMM (any strides, fp32 / fp16 / bf16 operands, fp32 accumulation)
+ * ------------------------------------------------------------------------ */
+
+/* C[m, n] = alpha * sum_k A[m*a_sm + k*a_sk] * B[k*b_sk + n*b_sn]
+ *           + beta * C[m, n] + bias[n]   (bias of the operand dtype, optional)
+ * with one fp32 fmaf per k in increasing k order (deterministic).  Operands
+ * of `dtype` (fp32, fp16 or bf16); C of c_dtype = fp32 or dtype, row stride
+ * ldc.  Any shape and stride: the path for fp32 / fp16 models and for K or
+ * pitches that are not multiples of 8, which the bf16 MFMA core does not take.
+ * Replaces the cuBLAS products of the fused linear + cross-entropy path
+ * (kernels/cross_entropy/experiments/v2/fused_linear_cross_entropy.py:142-144,
+ * 207-219: logits = X W^T + b, dX = dlogits W, dW += dlogits^T X,
+ * db += colsum(dlogits)). */
+int forge_gemm_generic(int64_t M, int64_t N, int64_t K, int dtype,
+                       const void* a, int64_t a_sm, int64_t a_sk,
+                       const void* b, int64_t b_sk, int64_t b_sn,
+                       void* c, int64_t ldc, int c_dtype, float alpha, float beta,
+                       const void* bias, void* stream);
+
 /* ------------------------------------------------------------------------
  * bf16 MFMA GEMM core (fp32 accumulation) with fused LoRA epilogues
  * ------------------------------------------------------------------------ */

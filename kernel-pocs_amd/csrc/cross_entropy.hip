@@ -641,6 +641,48 @@ __global__ __launch_bounds__(1024) void sum_f32_kernel(const float* x, int64_t n
   }
 }
 
+// Token scaling of the fused linear + cross-entropy path: the probability of
+// the target class under softmax(softcap(x)) of each row, detached from the
+// graph.  The softcapped logits are rounded to the logits dtype and p is
+// rounded to it too, as the reference builds both as tensors of that dtype;
+// ignored rows get 0.  One 256-thread workgroup per row.
+template <class T>
+__global__ __launch_bounds__(256) void ce_target_prob_kernel(const T* x, int64_t ld, int64_t V, const int64_t* target,
+                                                             int64_t tstride, int64_t ignore_index, float softcap,
+                                                             float* prob) {
+  __shared__ float red[8];
+  const int64_t row = blockIdx.x;
+  const int64_t y = target[row * tstride];
+  if (y == ignore_index || y < 0 || y >= V) {
+    if (threadIdx.x == 0) prob[row] = 0.f;
+    return;
+  }
+  const T* xr = x + row * ld;
+  auto capped = [&](float v) { return softcap > 0.f ? round_to<T>(softcap * tanhf(v / softcap)) : v; };
+  float m = -INFINITY, d = 0.f;
+  for (int64_t c = threadIdx.x; c < V; c += 256) {
+    const float v = capped(to_f32(xr[c])) * kLog2e;
+    if (v > m) {
+      d = (m == -INFINITY) ? 0.f : d * fast_exp2(m - v);
+      m = v;
+    }
+    d += fast_exp2(v - m);
+  }
+  block_lse<4>(m, d, red);
+  if (threadIdx.x == 0) prob[row] = round_to<T>(fast_exp2(capped(to_f32(xr[y])) * kLog2e - m) / d);
+}
+
+// x[r, c] *= s[r], rounded to x's dtype (the per-row token scale).
+template <class T>
+__global__ __launch_bounds__(256) void row_scale_kernel(T* x, int64_t ld, int64_t rows, int64_t cols, const float* s) {
+  const int64_t n = rows * cols;
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) {
+    const int64_t r = i / cols, c = i - r * cols;
+    T* p = x + r * ld + c;
+    *p = from_f32<T>(to_f32(*p) * s[r]);
+  }
+}
+
 }  // namespace
 
 extern "C" int forge_ce_fwd(int dtype, void* logits, int64_t ld, int64_t n_rows, int64_t n_cols,
@@ -710,6 +752,51 @@ extern "C" int forge_sum_f32(const float* x, int64_t n, float* out, void* out_ca
   if (out_cast && cast_dtype != FORGE_DTYPE_F32 && cast_dtype != FORGE_DTYPE_BF16 && cast_dtype != FORGE_DTYPE_F16)
     return forge_set_error(FORGE_ERR_UNSUPPORTED, "sum_f32: cast dtype %d", cast_dtype);
   sum_f32_kernel<<<1, 1024, 0, (hipStream_t)stream>>>(x, n, out, out_cast, cast_dtype);
+  FORGE_CHECK_LAUNCH();
+  return FORGE_OK;
+}
+
+extern "C" int forge_ce_target_prob(int dtype, const void* logits, int64_t ld, int64_t n_rows, int64_t n_cols,
+                                    const int64_t* target, int64_t target_stride, int64_t ignore_index, float softcap,
+                                    float* prob, void* stream) {
+  if (n_rows < 0 || n_cols <= 0) return forge_set_error(FORGE_ERR_INVALID, "ce_target_prob: shape");
+  if (n_rows == 0) return FORGE_OK;
+  if (n_rows > 0x7fffffff) return forge_set_error(FORGE_ERR_INVALID, "ce_target_prob: too many rows");
+  if (!logits || !target || !prob) return forge_set_error(FORGE_ERR_INVALID, "ce_target_prob: null pointer");
+  hipStream_t s = (hipStream_t)stream;
+  const dim3 grid((unsigned)n_rows);
+  switch (dtype) {
+    case FORGE_DTYPE_F32:
+      ce_target_prob_kernel<float><<<grid, 256, 0, s>>>((const float*)logits, ld, n_cols, target, target_stride,
+                                                        ignore_index, softcap, prob);
+      break;
+    case FORGE_DTYPE_BF16:
+      ce_target_prob_kernel<bf16_t><<<grid, 256, 0, s>>>((const bf16_t*)logits, ld, n_cols, target, target_stride,
+                                                         ignore_index, softcap, prob);
+      break;
+    case FORGE_DTYPE_F16:
+      ce_target_prob_kernel<fp16_t><<<grid, 256, 0, s>>>((const fp16_t*)logits, ld, n_cols, target, target_stride,
+                                                         ignore_index, softcap, prob);
+      break;
+    default: return forge_set_error(FORGE_ERR_UNSUPPORTED, "ce_target_prob: dtype %d", dtype);
+  }
+  FORGE_CHECK_LAUNCH();
+  return FORGE_OK;
+}
+
+extern "C" int forge_row_scale(int dtype, void* x, int64_t ld, int64_t n_rows, int64_t n_cols, const float* scale,
+                               void* stream) {
+  if (n_rows < 0 || n_cols < 0) return forge_set_error(FORGE_ERR_INVALID, "row_scale: shape");
+  if (n_rows == 0 || n_cols == 0) return FORGE_OK;
+  if (!x || !scale) return forge_set_error(FORGE_ERR_INVALID, "row_scale: null pointer");
+  hipStream_t s = (hipStream_t)stream;
+  const int grid = grid_for(n_rows * n_cols, 256, 4096);
+  switch (dtype) {
+    case FORGE_DTYPE_F32: row_scale_kernel<float><<<grid, 256, 0, s>>>((float*)x, ld, n_rows, n_cols, scale); break;
+    case FORGE_DTYPE_BF16: row_scale_kernel<bf16_t><<<grid, 256, 0, s>>>((bf16_t*)x, ld, n_rows, n_cols, scale); break;
+    case FORGE_DTYPE_F16: row_scale_kernel<fp16_t><<<grid, 256, 0, s>>>((fp16_t*)x, ld, n_rows, n_cols, scale); break;
+    default: return forge_set_error(FORGE_ERR_UNSUPPORTED, "row_scale: dtype %d", dtype);
+  }
   FORGE_CHECK_LAUNCH();
   return FORGE_OK;
 }

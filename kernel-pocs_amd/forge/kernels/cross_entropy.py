@@ -3,12 +3,22 @@ from kernels.cross_entropy.experiments.v2 import (
     CrossEntropyOutput,
     ForgeCrossEntropyFunction,
     ForgeCrossEntropyLoss,
+    ForgeFusedLinearCrossEntropyFunction,
+    ForgeFusedLinearCrossEntropyLoss,
     forge_cross_entropy,
+    forge_fused_linear_cross_entropy,
+    fused_linear_cross_entropy_backward,
+    fused_linear_cross_entropy_forward,
 )
 
 __all__ = [
     "CrossEntropyOutput",
     "ForgeCrossEntropyFunction",
     "ForgeCrossEntropyLoss",
+    "ForgeFusedLinearCrossEntropyFunction",
+    "ForgeFusedLinearCrossEntropyLoss",
     "forge_cross_entropy",
+    "forge_fused_linear_cross_entropy",
+    "fused_linear_cross_entropy_backward",
+    "fused_linear_cross_entropy_forward",
 ]

@@ -123,6 +123,15 @@ forge_lora_a = _decl(
      c_vp, c_int, c_vp],
 )
 
+forge_ce_target_prob = _decl(
+    "forge_ce_target_prob", [c_int, c_vp, c_i64, c_i64, c_i64, c_vp, c_i64, c_i64, c_f32, c_vp, c_vp]
+)
+forge_row_scale = _decl("forge_row_scale", [c_int, c_vp, c_i64, c_i64, c_i64, c_vp, c_vp])
+forge_gemm_generic = _decl(
+    "forge_gemm_generic",
+    [c_i64, c_i64, c_i64, c_int, c_vp, c_i64, c_i64, c_vp, c_i64, c_i64, c_vp, c_i64, c_int, c_f32, c_f32, c_vp, c_vp],
+)
+
 forge_zero = _decl("forge_zero", [c_vp, c_i64, c_vp])
 forge_cast_f32_bf16 = _decl("forge_cast_f32_bf16", [c_vp, c_i64, c_vp, c_i64, c_i64, c_i64, c_vp])
 
@@ -133,6 +142,7 @@ EXPORTED = [
     "forge_ce_fwd", "forge_ce_target_stats", "forge_ce_scale", "forge_sum_f32",
     "forge_gemm", "forge_lora_mlp_gate_up", "forge_lora_mlp_down_bwd", "forge_lora_qkv_rope",
     "forge_lora_a", "forge_zero", "forge_cast_f32_bf16", "forge_splitk_reduce",
+    "forge_ce_target_prob", "forge_row_scale", "forge_gemm_generic",
 ]
 
 # Number of successful library calls (tests use it to prove the HIP path ran).

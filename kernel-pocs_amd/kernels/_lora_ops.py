@@ -130,7 +130,7 @@ def lora_a(x: torch.Tensor, mats: Sequence[torch.Tensor], scales: Sequence[float
 _T_CACHE = {}
 
 
-def frozen_t(w: torch.Tensor) -> torch.Tensor:
+def frozen_t(w: torch.Tensor, pitch_multiple: int = 1) -> torch.Tensor:
     """Contiguous W^T of a frozen base weight, kept for the weight's lifetime.
 
     The backward GEMMs contract over the weight's output dimension, which is
@@ -138,14 +138,22 @@ def frozen_t(w: torch.Tensor) -> torch.Tensor:
     and run on the LDS-DMA engine.  The copy is made once per weight (LoRA
     freezes the base weights) and dropped when the weight is freed, changed
     in place (tensor._version) or given new storage (data_ptr).
+    pitch_multiple > 1 returns [in, out_pad] with out_pad the next multiple
+    (columns past `out` are zero), for GEMMs that read K in 8-element chunks.
     """
-    key = id(w)
+    key = (id(w), pitch_multiple)
     ent = _T_CACHE.get(key)
     if ent is not None:
         ref, ver, ptr, wt = ent
         if ref() is w and ver == w._version and ptr == w.data_ptr():
             return wt
-    wt = w.detach().t().contiguous()
+    n_out = w.shape[0]
+    pad = -(-n_out // pitch_multiple) * pitch_multiple
+    if pad == n_out:
+        wt = w.detach().t().contiguous()
+    else:
+        wt = torch.zeros(w.shape[1], pad, dtype=w.dtype, device=w.device)
+        wt[:, :n_out].copy_(w.detach().t())
 
     def _drop(_ref, key=key):
         _T_CACHE.pop(key, None)

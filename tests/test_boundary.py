@@ -18,7 +18,10 @@ REEXPORTS = {
         "torch_swiglu_reference"]),
     "forge.kernels.rope": ("kernels.rope.forge_rope_v3", ["apply_rope", "ForgeRoPEv3", "ForgeRoPEv3Function"]),
     "forge.kernels.cross_entropy": ("kernels.cross_entropy.experiments.v2", [
-        "CrossEntropyOutput", "ForgeCrossEntropyFunction", "ForgeCrossEntropyLoss", "forge_cross_entropy"]),
+        "CrossEntropyOutput", "ForgeCrossEntropyFunction", "ForgeCrossEntropyLoss", "forge_cross_entropy",
+        "ForgeFusedLinearCrossEntropyFunction", "ForgeFusedLinearCrossEntropyLoss",
+        "forge_fused_linear_cross_entropy", "fused_linear_cross_entropy_backward",
+        "fused_linear_cross_entropy_forward"]),
     "forge.kernels.lora_mlp": ("kernels.lora_mlp.experiments.v6.lora_mlp_kernel_v6", [
         "LoRAMLPv6", "LoRAMLPv6Module", "lora_mlp_v6", "stack_lora_a"]),
     "forge.kernels.lora_qkv": ("kernels.lora_qkv.experiments.v4.lora_qkv_kernel_v4", [
@@ -81,6 +84,38 @@ def test_cross_entropy_loss_module_assertions():
     with pytest.raises(AssertionError, match="reduction"):
         ForgeCrossEntropyLoss(reduction="avg")
     ForgeCrossEntropyLoss(label_smoothing=0.0, reduction="none")
+
+
+def test_fused_linear_ce_argument_checks():
+    """fused_linear_cross_entropy.py:59-84 and :441-447: the shape checks
+    raise ValueError, the flag and Module checks AssertionError, all before
+    any device work (so they hold on the CPU too)."""
+    from kernels.cross_entropy.experiments.v2 import (
+        ForgeFusedLinearCrossEntropyLoss,
+        fused_linear_cross_entropy_forward as fwd,
+    )
+
+    x, W, t = torch.zeros(4, 8), torch.zeros(5, 8), torch.zeros(4, dtype=torch.int64)
+    with pytest.raises(AssertionError, match="return_z_loss must be True or False"):
+        fwd(x, W, t, return_z_loss=1)
+    with pytest.raises(ValueError, match=r"_input must be 2D \(B\*T, H\)"):
+        fwd(x.view(2, 2, 8), W, t)
+    with pytest.raises(ValueError, match=r"weight must be 2D \(V, H\)"):
+        fwd(x, W.view(-1), t)
+    with pytest.raises(ValueError, match=r"target must be 1D \(B\*T,\)"):
+        fwd(x, W, t.view(2, 2))
+    with pytest.raises(ValueError, match="weight.shape\\[1\\] must match _input.shape\\[1\\]; got 4 != 8"):
+        fwd(x, torch.zeros(5, 4), t)
+    with pytest.raises(ValueError, match="target length must match _input rows; got 3 != 4"):
+        fwd(x, W, t[:3])
+    with pytest.raises(ValueError, match=r"bias must have shape \(5,\); got \(4,\)"):
+        fwd(x, W, t, bias=torch.zeros(4))
+    with pytest.raises(AssertionError, match="label_smoothing must be between 0.0 and 1.0"):
+        ForgeFusedLinearCrossEntropyLoss(label_smoothing=-0.1)
+    with pytest.raises(AssertionError, match="supports reduction='mean', 'sum', or 'none'"):
+        ForgeFusedLinearCrossEntropyLoss(reduction="avg")
+    with pytest.raises(AssertionError, match="softcap must greater than 0.0 or None"):
+        ForgeFusedLinearCrossEntropyLoss(softcap=0.0)
 
 
 # ---------------------------------------------------------------------------

@@ -455,3 +455,77 @@ def test_lora_qkv_varlen_positions_and_flops():
     assert len(lens) == 8 and all(512 <= n <= 4096 for n in lens)
     assert oqkv.varlen_lengths(8, 512, 4096, seed=0) == lens
     assert oqkv.flops_per_token(4096, 4096, 1024, 64) == 109_314_048
+
+
+# ---------------------------------------------------------------------------
+# fused linear + cross-entropy: pinned against autograd of the torch
+# composition F.cross_entropy(F.linear(x, W, b)) in float64 (the reference
+# tests' comparator, kernels/cross_entropy/tests/test_fused_linear_cross_entropy.py:64-96)
+# ---------------------------------------------------------------------------
+from oracle import fused_linear_ce as oflce  # noqa: E402
+
+
+def _flce_torch(x, W, b, t, ce_weight=None, ignore_index=-100, lse_square_scale=0.0, label_smoothing=0.0,
+                reduction="mean", softcap=None, token_scaling=False):
+    x = x.clone().requires_grad_(True)
+    W = W.clone().requires_grad_(True)
+    b = b.clone().requires_grad_(True) if b is not None else None
+    logits = F.linear(x, W, b)
+    if softcap is not None:
+        logits = softcap * torch.tanh(logits / softcap)
+    rows = F.cross_entropy(logits, t, weight=ce_weight, ignore_index=ignore_index, reduction="none",
+                           label_smoothing=label_smoothing)
+    mask = t != ignore_index
+    z = torch.where(mask, lse_square_scale * torch.logsumexp(logits, -1) ** 2, torch.zeros_like(rows))
+    if reduction == "mean":
+        denom = mask.sum() if ce_weight is None else ce_weight[torch.where(mask, t, 0)][mask].sum()
+        rows = rows / denom
+        z = z / mask.sum()
+    rows = rows + z
+    if token_scaling:
+        p = torch.softmax(logits.detach(), -1).gather(1, torch.where(mask, t, 0).unsqueeze(1)).squeeze(1)
+        p = torch.where(mask, p, torch.zeros_like(p))
+        rows, z = rows * p, z * p
+    loss = rows if reduction == "none" else rows.sum()
+    loss.sum().backward()
+    return loss.detach(), x.grad, W.grad, (b.grad if b is not None else None)
+
+
+@pytest.mark.parametrize("case", [
+    dict(), dict(reduction="sum"), dict(bias=False), dict(label_smoothing=0.1), dict(ce_weight=True),
+    dict(softcap=3.0, lse_square_scale=1e-2), dict(reduction="none"), dict(token_scaling=True),
+    dict(token_scaling=True, softcap=2.0, lse_square_scale=1e-3, label_smoothing=0.2),
+])
+def test_fused_linear_ce_matches_autograd_of_torch_composition(case):
+    g = torch.Generator().manual_seed(11)
+    bt, h, v = 19, 12, 37
+    x = torch.randn(bt, h, generator=g, dtype=torch.float64)
+    W = torch.randn(v, h, generator=g, dtype=torch.float64) / h ** 0.5
+    b = torch.randn(v, generator=g, dtype=torch.float64) if case.get("bias", True) else None
+    t = torch.randint(0, v, (bt,), generator=g)
+    t[::4] = -100
+    cw = torch.rand(v, generator=g, dtype=torch.float64) + 0.5 if case.get("ce_weight") else None
+    kw = dict(ce_weight=cw, lse_square_scale=case.get("lse_square_scale", 0.0),
+              label_smoothing=case.get("label_smoothing", 0.0), reduction=case.get("reduction", "mean"),
+              softcap=case.get("softcap"))
+    ref_loss, ref_dx, ref_dw, ref_db = _flce_torch(x, W, b, t, token_scaling=case.get("token_scaling", False), **kw)
+    out = oflce.fused_linear_ce(x, W, t, bias=b, use_token_scaling=case.get("token_scaling", False), **kw)
+    torch.testing.assert_close(out["loss"], ref_loss, rtol=1e-10, atol=1e-12)
+    torch.testing.assert_close(out["dX"], ref_dx, rtol=1e-10, atol=1e-12)
+    torch.testing.assert_close(out["dW"], ref_dw, rtol=1e-10, atol=1e-12)
+    if b is not None:
+        torch.testing.assert_close(out["db"], ref_db, rtol=1e-10, atol=1e-12)
+
+
+def test_fused_linear_ce_metrics_and_flops():
+    g = torch.Generator().manual_seed(5)
+    x = torch.randn(13, 8, generator=g, dtype=torch.float64)
+    W = torch.randn(21, 8, generator=g, dtype=torch.float64)
+    t = torch.randint(0, 21, (13,), generator=g)
+    t[::5] = -100
+    out = oflce.fused_linear_ce(x, W, t)
+    logits = x @ W.t()
+    pred = torch.where(t == -100, torch.full_like(t, -1), logits.argmax(-1))
+    assert torch.equal(out["predicted"], pred)
+    assert float(out["token_accuracy"]) == pytest.approx(float(((pred == t) & (t != -100)).sum() / (t != -100).sum()))
+    assert oflce.flops(8192, 4096, 128256) == 6 * 8192 * 4096 * 128256 == 25_821_343_383_552
