@@ -43,7 +43,7 @@ def _parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--kernels", default="swiglu,rope,ce,lora_mlp,lora_qkv")
+    ap.add_argument("--kernels", default="swiglu,rope,ce,lora_mlp,lora_qkv,flce")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--only-launches", action="store_true",
                     help="run only the dominant-kernel launch loop (for rocprofv3 counter runs)")
@@ -528,8 +528,64 @@ def bench_copy(args):
             "dtype": "f32"}
 
 
+def bench_flce(args):
+    """Fused linear + cross-entropy (the next row after the five configs): the
+    Llama-3-8B lm_head shape, bf16 hidden [8192, 4096] and weight
+    [128256, 4096], 5% ignore_index, mean, fwd+bwd with input and weight
+    gradients."""
+    import torch
+    from forge_hip import _lib as L
+    from kernels._lora_ops import COL, ROW, gemm
+    from kernels.cross_entropy.experiments.v2 import forge_fused_linear_cross_entropy
+    from oracle.fused_linear_ce import flops
+
+    BT, H, V = 8192, 4096, 128256
+    bf = torch.bfloat16
+    g = torch.Generator(device="cuda").manual_seed(6)
+    x = torch.randn(BT, H, device="cuda", generator=g).to(bf).requires_grad_(True)
+    W = (torch.randn(V, H, device="cuda", generator=g) / H ** 0.5).to(bf).requires_grad_(True)
+    target = torch.randint(0, V, (BT,), device="cuda", generator=g)
+    target[torch.randperm(BT, device="cuda", generator=g)[:410]] = -100
+
+    def step(i):
+        x.grad = None  # a training step after zero_grad(set_to_none=True)
+        W.grad = None
+        forge_fused_linear_cross_entropy(x, W, target).backward()
+
+    ms, wall = run_steps(args, step)
+    fl = flops(BT, H, V)
+    tf = rate(fl, ms, 1e12)
+    # dominant kernel: the LDS-DMA GEMM that computes the logits of a
+    # 4096-token chunk (X_c W^T) and, with the same symbol, dX_c = dlogits W
+    n = 4096
+    logits = torch.empty(n, V, device="cuda", dtype=bf)
+    xc, wd = x.detach()[:n], W.detach()
+    launch_ms = time_launches(lambda i: gemm(n, V, [(xc, H, wd, H, H)], ROW, COL, out=logits), max(args.steps, 10))
+    res = {
+        "config": {"workload": "fused_linear_cross_entropy_fwd_bwd", "dtype": "bf16", "tokens": BT, "hidden": H,
+                   "vocab": V, "ignored_rows": 410, "reduction": "mean", "chunk_tokens": 4096,
+                   "api": "forge_fused_linear_cross_entropy"},
+        "value": tf, "unit": "TFLOP/s", "ms_per_step": rnd(ms, 4), "wall_ms_per_step": rnd(wall, 4),
+        "frac_of_mfma_peak": rnd(tf and tf / BF16_PEAK_TFLOPS, 4), "algorithmic_flops_per_step": fl,
+        "launches_ms": {"forge_gemm logits chunk (X_c W^T, 4096 x 128256 x 4096)": round(launch_ms, 4)},
+        "roofline": _roof("mfma", 2 * n * H * V / (launch_ms * 1e-3) / 1e12, BF16_PEAK_TFLOPS, "TFLOP/s",
+                          _traffic("flce_logits_gemm")),
+        "dtype": "bf16",
+    }
+    if not (args.no_cpu_baseline or args.only_launches):
+        from oracle.fused_linear_ce import fused_linear_ce
+
+        rows = 64
+        xc_cpu, wc, tc = x.detach()[:rows].float().cpu(), W.detach().float().cpu(), target[:rows].cpu()
+        t, reps = cpu_time(lambda: fused_linear_ce(xc_cpu, wc, tc, compute_dtype=torch.float32))
+        res["cpu_baseline"] = _cpu(flops(rows, H, V) / t / 1e12, "TFLOP/s",
+                                   f"{rows} of {BT} tokens, the reference's linear + CE formulas in fp32 "
+                                   f"(torch CPU matmuls), fwd+bwd, median of {reps}")
+    return res
+
+
 BENCHES = {"copy": bench_copy, "swiglu": bench_swiglu, "rope": bench_rope, "ce": bench_ce, "lora_mlp": bench_lora_mlp,
-           "lora_qkv": bench_lora_qkv}
+           "lora_qkv": bench_lora_qkv, "flce": bench_flce}
 
 
 def main():

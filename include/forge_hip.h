@@ -312,6 +312,15 @@ int forge_splitk_reduce(const float* parts, int64_t split_stride, int n_split, i
 int forge_cast_f32_bf16(const float* src, int64_t ld_src, void* dst, int64_t ld_dst, int64_t rows,
                         int64_t cols, void* stream);
 
+/* dst[c, r] = src[r, c] for 2-byte elements (bf16 / fp16), src [rows, cols]
+ * with row pitch ld_src, dst [cols, rows] with row pitch ld_dst.  Makes the
+ * token-reduction weight gradient of the fused linear + cross-entropy path
+ * (dW = dlogits^T X, fused_linear_cross_entropy.py:211-212) a K-contiguous
+ * product for the LDS-DMA GEMM; no reference counterpart (cuBLAS reads the
+ * transposed operands directly). */
+int forge_transpose_2b(const void* src, int64_t ld_src, int64_t rows, int64_t cols, void* dst, int64_t ld_dst,
+                       void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -339,7 +339,8 @@ __device__ __forceinline__ uint4 pack8(const float (&f)[8]) {
 // Tiles and epilogues the staged epilogue serves.
 constexpr bool staged_ok(int bm, int bn, int wm, int wn, int epi) {
   return bm == 256 && bn == 256 && (256 / wm) % 32 == 0 && (256 / wn) % 32 == 0 && 256 / wm <= 128 &&
-         (epi == EPI_STORE_BF16 || epi == EPI_SWIGLU_FWD || epi == EPI_SWIGLU_BWD || epi == EPI_ROPE);
+         (epi == EPI_STORE_BF16 || epi == EPI_STORE_F32 || epi == EPI_SWIGLU_FWD || epi == EPI_SWIGLU_BWD ||
+          epi == EPI_ROPE);
 }
 
 // Workgroup barrier that waits only for this wave's LDS accesses (lgkmcnt 0),
@@ -421,7 +422,32 @@ __device__ __forceinline__ void epilogue_staged(const GemmArgs& args,
 #pragma unroll
         for (int q = 0; q < 8; ++q) v[q] = pv[q];
         const bool full = n + 8 <= N;
-        if constexpr (EPI == EPI_STORE_BF16) {
+        if constexpr (EPI == EPI_STORE_F32) {
+          // fp32 C (beta accumulation, or split z's partial slice): two
+          // 16-byte accesses per 8-column chunk
+#pragma unroll
+          for (int q = 0; q < 8; ++q) {
+            float a = ep.alpha;
+            if (ep.alpha_group > 0) {
+              const int64_t grp = (n + q) / ep.alpha_group;
+              a = ep.alphas[grp < 4 ? grp : 3];
+            }
+            v[q] *= a;
+          }
+          float* cp = (float*)ep.c + blockIdx.z * ep.split_stride + m * ep.ldc + n;
+          if (full) {
+            float4* c4 = reinterpret_cast<float4*>(cp);
+            if (ep.beta != 0.f) {
+              const float4 c0 = c4[0], c1 = c4[1];
+              v[0] += ep.beta * c0.x; v[1] += ep.beta * c0.y; v[2] += ep.beta * c0.z; v[3] += ep.beta * c0.w;
+              v[4] += ep.beta * c1.x; v[5] += ep.beta * c1.y; v[6] += ep.beta * c1.z; v[7] += ep.beta * c1.w;
+            }
+            c4[0] = make_float4(v[0], v[1], v[2], v[3]);
+            c4[1] = make_float4(v[4], v[5], v[6], v[7]);
+          } else {
+            for (int q = 0; q < 8 && n + q < N; ++q) cp[q] = ep.beta != 0.f ? v[q] + ep.beta * cp[q] : v[q];
+          }
+        } else if constexpr (EPI == EPI_STORE_BF16) {
 #pragma unroll
           for (int q = 0; q < 8; ++q) {
             float a = ep.alpha;

@@ -1,7 +1,8 @@
-// Small utility kernels used by the split-K paths: the deterministic
-// reduction of per-split fp32 partial sums, zero fill of an fp32 workspace (a
-// kernel, not hipMemsetAsync, so the sequence stays valid under stream
-// capture) and the fp32 -> bf16 cast.
+// Small utility kernels: the deterministic reduction of per-split fp32
+// partial sums, zero fill of an fp32 workspace (a kernel, not
+// hipMemsetAsync, so the sequence stays valid under stream capture), the
+// fp32 -> bf16 cast, and a 2-byte transpose (K-contiguous operands for the
+// LDS-DMA GEMM).
 #include "common.h"
 
 namespace {
@@ -63,7 +64,69 @@ int launch_reduce(const float* parts, int64_t stride, int n_split, int64_t rows,
   return FORGE_OK;
 }
 
+// out[c, r] = in[r, c] for 2-byte elements (bf16 / fp16): 64 x 64 tiles
+// through LDS (row pitch 66 elements against bank conflicts on the column
+// reads), 16-byte loads and stores when pitches and bases allow.
+__global__ __launch_bounds__(256) void transpose2_kernel(const uint16_t* in, int64_t ld_in, int64_t rows, int64_t cols,
+                                                         uint16_t* out, int64_t ld_out, int64_t tiles_c, int vec) {
+  __shared__ uint16_t tile[64][66];
+  const int64_t r0 = (blockIdx.x / tiles_c) * 64, c0 = (blockIdx.x % tiles_c) * 64;
+  const int t = threadIdx.x;
+#pragma unroll
+  for (int it = 0; it < 2; ++it) {
+    const int v = t + 256 * it, rr = v / 8, cc = (v % 8) * 8;
+    const int64_t r = r0 + rr, c = c0 + cc;
+    if (vec && r < rows && c + 8 <= cols) {
+      const uint4 q = *reinterpret_cast<const uint4*>(in + r * ld_in + c);
+      const uint32_t w[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        tile[rr][cc + 2 * j] = (uint16_t)(w[j] & 0xffff);
+        tile[rr][cc + 2 * j + 1] = (uint16_t)(w[j] >> 16);
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) tile[rr][cc + j] = (r < rows && c + j < cols) ? in[r * ld_in + c + j] : 0;
+    }
+  }
+  __syncthreads();
+#pragma unroll
+  for (int it = 0; it < 2; ++it) {
+    const int v = t + 256 * it, oc = v / 8, orr = (v % 8) * 8;  // output row = input column
+    const int64_t c = c0 + oc, r = r0 + orr;
+    if (c >= cols) continue;
+    uint16_t e[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) e[j] = tile[orr + j][oc];
+    if (vec && r + 8 <= rows) {
+      uint4 q;
+      q.x = e[0] | ((uint32_t)e[1] << 16);
+      q.y = e[2] | ((uint32_t)e[3] << 16);
+      q.z = e[4] | ((uint32_t)e[5] << 16);
+      q.w = e[6] | ((uint32_t)e[7] << 16);
+      *reinterpret_cast<uint4*>(out + c * ld_out + r) = q;
+    } else {
+      for (int j = 0; j < 8 && r + j < rows; ++j) out[c * ld_out + r + j] = e[j];
+    }
+  }
+}
+
 }  // namespace
+
+extern "C" int forge_transpose_2b(const void* src, int64_t ld_src, int64_t rows, int64_t cols, void* dst,
+                                  int64_t ld_dst, void* stream) {
+  if (rows < 0 || cols < 0 || ld_src < cols || ld_dst < rows)
+    return forge_set_error(FORGE_ERR_INVALID, "transpose_2b: shape / pitch");
+  if (rows == 0 || cols == 0) return FORGE_OK;
+  if (!src || !dst) return forge_set_error(FORGE_ERR_INVALID, "transpose_2b: null pointer");
+  const int64_t tr = (rows + 63) / 64, tc = (cols + 63) / 64;
+  if (tr * tc > 0x7fffffffLL) return forge_set_error(FORGE_ERR_INVALID, "transpose_2b: too many tiles");
+  const int vec = aligned16(src) && aligned16(dst) && ld_src % 8 == 0 && ld_dst % 8 == 0;
+  transpose2_kernel<<<(unsigned)(tr * tc), 256, 0, (hipStream_t)stream>>>(
+      (const uint16_t*)src, ld_src, rows, cols, (uint16_t*)dst, ld_dst, tc, vec);
+  FORGE_CHECK_LAUNCH();
+  return FORGE_OK;
+}
 
 extern "C" int forge_splitk_reduce(const float* parts, int64_t split_stride, int n_split, int64_t rows, int64_t cols,
                                    int64_t ld_parts, void* out, int64_t ld_out, int out_dtype, float alpha,

@@ -133,6 +133,7 @@ forge_gemm_generic = _decl(
 )
 
 forge_zero = _decl("forge_zero", [c_vp, c_i64, c_vp])
+forge_transpose_2b = _decl("forge_transpose_2b", [c_vp, c_i64, c_i64, c_i64, c_vp, c_i64, c_vp])
 forge_cast_f32_bf16 = _decl("forge_cast_f32_bf16", [c_vp, c_i64, c_vp, c_i64, c_i64, c_i64, c_vp])
 
 # Every symbol include/forge_hip.h declares (checked by the CPU test suite).
@@ -142,7 +143,7 @@ EXPORTED = [
     "forge_ce_fwd", "forge_ce_target_stats", "forge_ce_scale", "forge_sum_f32",
     "forge_gemm", "forge_lora_mlp_gate_up", "forge_lora_mlp_down_bwd", "forge_lora_qkv_rope",
     "forge_lora_a", "forge_zero", "forge_cast_f32_bf16", "forge_splitk_reduce",
-    "forge_ce_target_prob", "forge_row_scale", "forge_gemm_generic",
+    "forge_ce_target_prob", "forge_row_scale", "forge_gemm_generic", "forge_transpose_2b",
 ]
 
 # Number of successful library calls (tests use it to prove the HIP path ran).

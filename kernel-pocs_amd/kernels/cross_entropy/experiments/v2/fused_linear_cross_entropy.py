@@ -21,8 +21,10 @@ Per token chunk (all device work in libforge_hip.so):
   3. forge_ce_fwd on the chunk, in place, with the target statistics of the
      whole batch (the mean divides by the global non-ignored count)
   4. dX_c = dlogits W (MFMA on a cached, row-padded W^T, or generic),
-     dW += dlogits^T X_c (fp32, beta accumulation over chunks), db +=
-     colsum(dlogits) (generic GEMM with a ones row)
+     dW += dlogits^T X_c (fp32, beta accumulation over chunks; on the MFMA
+     path both operands are first transposed by forge_transpose_2b so the
+     product is K-contiguous for the LDS-DMA GEMM), db += colsum(dlogits)
+     (generic GEMM with a ones row)
 Chunks are sized to ~1 GiB of logits (MI355X has 288 GB of HBM): the
 reference's ~V/H-fold split (256-token chunks at the Llama-3 shape) would
 re-read and re-write the fp32 weight gradient 32 times.  Chunking changes
@@ -207,6 +209,13 @@ def fused_linear_cross_entropy_forward(
                 ones8[:, 0] = 1
                 bias8 = torch.zeros(V, 8, dtype=dtype, device=dev)
                 bias8[:, 0] = b
+        # dW = dlogits^T X_c reduces over tokens; with both operands
+        # transposed (one HBM pass each) it is a K-contiguous product for the
+        # LDS-DMA GEMM instead of a transposing register-path GEMM
+        dw_nt = fast and want_w and chunk % 8 == 0
+        if dw_nt:
+            dlT_buf = torch.empty(v_pad, chunk, dtype=dtype, device=dev)
+            xT_buf = torch.empty(H, chunk, dtype=dtype, device=dev)
         ones_row = torch.ones(1, chunk, dtype=dtype, device=dev) if want_b else None
         prob = torch.empty(chunk, dtype=torch.float32, device=dev) if use_token_scaling else None
         st = L.stream_of(x)
@@ -259,7 +268,14 @@ def fused_linear_cross_entropy_forward(
             gi = grad_input[c0:c0 + n]
             if fast:
                 gemm(n, H, [(logits, v_pad, wt, v_pad, v_pad)], ROW, COL, out=gi)
-                if want_w:
+                if dw_nt and n % 8 == 0:
+                    L.check(L.forge_transpose_2b(logits.data_ptr(), v_pad, n, v_pad, dlT_buf.data_ptr(), chunk, st),
+                            "forge_transpose_2b")
+                    L.check(L.forge_transpose_2b(x_c.data_ptr(), ld(x_c), n, H, xT_buf.data_ptr(), chunk, st),
+                            "forge_transpose_2b")
+                    gemm(v_pad, H, [(dlT_buf, chunk, xT_buf, chunk, n)], ROW, COL, out=gw32, beta=beta,
+                         out_dtype=torch.float32)
+                elif want_w:
                     gemm(v_pad, H, [(logits, v_pad, x_c, ld(x_c), n)], COL, ROW, out=gw32, beta=beta,
                          out_dtype=torch.float32)
             else:

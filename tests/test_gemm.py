@@ -155,3 +155,37 @@ def test_gemm_split_k_partials_match_single_pass():
     _gemm(M, N, [(a, K, b, K, K)], 0, 1, parts.view(split * M, N), L.DTYPE_F32, split_k=split)
     ref = A @ B
     torch.testing.assert_close(parts.sum(0).cpu(), ref, atol=1e-3 * ref.abs().max().item(), rtol=1e-3)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("a_layout,b_layout,N,ldc", [(0, 1, 520, 520), (0, 1, 300, 304), (0, 1, 300, 301),
+                                                     (1, 0, 520, 520), (1, 0, 296, 304), (1, 0, 296, 301)])
+def test_gemm_fp32_beta_epilogue(a_layout, b_layout, N, ldc):
+    """fp32 C with beta (the staged 16-byte epilogue when the pitch allows,
+    the per-element one otherwise) on both engines (LDS-DMA for A ROW x B COL,
+    register path for A^T x [K][N] B)."""
+    gen = torch.Generator().manual_seed(21)
+    M, K = 296, 264
+    a, af = _operand(M, K, a_layout, gen)
+    b, bf = _b_operand(N, K, b_layout, gen)
+    c0 = torch.randn(M, ldc, generator=gen)
+    c = c0.cuda()
+    lda = a.shape[1]
+    ldb = b.shape[1]
+    _gemm(M, N, [(a, lda, b, ldb, K)], a_layout, b_layout, c, L.DTYPE_F32, alpha=0.5, beta=-1.5)
+    ref = 0.5 * (af @ bf) - 1.5 * c0[:, :N]
+    torch.testing.assert_close(c[:, :N].cpu(), ref, rtol=1e-3, atol=1e-3 * float(ref.abs().max()))
+    assert torch.equal(c[:, N:].cpu(), c0[:, N:])  # pitch padding untouched
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("rows,cols,ld_in,ld_out", [(64, 64, 64, 64), (300, 1003, 1008, 304), (7, 129, 129, 9),
+                                                    (4096, 1024, 1024, 4096)])
+def test_transpose_2b(rows, cols, ld_in, ld_out):
+    gen = torch.Generator().manual_seed(4)
+    src = torch.randn(rows, ld_in, generator=gen).to(torch.bfloat16).cuda()
+    dst = torch.full((cols, ld_out), 7.0, dtype=torch.bfloat16).cuda()
+    L.check(L.forge_transpose_2b(src.data_ptr(), ld_in, rows, cols, dst.data_ptr(), ld_out, L.stream_of(src)),
+            "forge_transpose_2b")
+    assert torch.equal(dst[:, :rows].cpu(), src[:, :cols].t().cpu())
+    assert bool((dst[:, rows:] == 7.0).all())  # pitch padding untouched
