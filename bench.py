@@ -43,7 +43,7 @@ def _parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--kernels", default="swiglu,rope,ce,lora_mlp,lora_qkv,flce")
+    ap.add_argument("--kernels", default="swiglu,rope,ce,lora_mlp,lora_qkv,flce,geglu")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--only-launches", action="store_true",
                     help="run only the dominant-kernel launch loop (for rocprofv3 counter runs)")
@@ -584,8 +584,60 @@ def bench_flce(args):
     return res
 
 
+def bench_geglu(args):
+    """GeGLU (the next row after the five configs): the Gemma-7B MLP shape,
+    bf16 gate/up/dout [4096, 24576], tanh GELU, out = gelu(gate) * up."""
+    import torch
+    from forge_hip import _lib as L
+    from kernels.geglu import geglu
+
+    R, C = 4096, 24576
+    n = R * C
+    bf = torch.bfloat16
+    g = torch.Generator(device="cuda").manual_seed(7)
+    gate0 = torch.randn(R, C, device="cuda", generator=g).to(bf)
+    up0 = torch.randn(R, C, device="cuda", generator=g).to(bf)
+    dout = torch.randn(R, C, device="cuda", generator=g).to(bf)
+    total = args.warmup + args.steps
+    gates = [gate0.clone() for _ in range(total)]  # backward overwrites its inputs
+    ups = [up0.clone() for _ in range(total)]
+
+    def step(i):
+        gi = gates[i].requires_grad_(True)
+        ui = ups[i].requires_grad_(True)
+        geglu(gi, ui, "tanh").backward(dout)
+        gates[i] = ups[i] = None
+
+    ms, wall = run_steps(args, step)
+    bytes_step = 8 * n * 2  # fwd 3 tensors + bwd 5 tensors, bf16
+    gbs = rate(bytes_step, ms, 1e9)
+    gf, uf = gate0.clone(), up0.clone()
+    st = L.stream_of(gf)
+    bwd_ms = time_launches(lambda i: L.forge_geglu_bwd(2, dout.data_ptr(), C, gf.data_ptr(), uf.data_ptr(), C,
+                                                       gf.data_ptr(), uf.data_ptr(), C, R, C, 1, st),
+                           max(args.steps, 10))
+    res = {
+        "config": {"workload": "geglu_fwd_bwd", "dtype": "bf16", "shape": [R, C], "approximate": "tanh"},
+        "value": gbs, "unit": "GB/s", "ms_per_step": rnd(ms, 5), "wall_ms_per_step": rnd(wall, 5),
+        "frac_of_hbm_peak": rnd(gbs and gbs / HBM_PEAK_GBS, 4), "algorithmic_bytes_per_step": bytes_step,
+        "launches_ms": {"forge_geglu_bwd": round(bwd_ms, 5)},
+        "roofline": _roof("hbm", 5 * n * 2 / (bwd_ms * 1e-3) / 1e9, HBM_PEAK_GBS, "GB/s", _traffic("geglu_bwd")),
+        "dtype": "bf16",
+    }
+    if not (args.no_cpu_baseline or args.only_launches):
+        from oracle.geglu import geglu_fwd_bwd
+
+        rows = 256
+        gc, uc, dc = gate0[:rows].cpu(), up0[:rows].cpu(), dout[:rows].cpu()
+        t, reps = cpu_time(lambda: geglu_fwd_bwd(gc, uc, dc, "tanh"))
+        res["cpu_baseline"] = _cpu(8 * rows * C * 2 / t / 1e9, "GB/s",
+                                   f"{rows} of {R} rows, the reference's GeGLU formulas (float64 torch), fwd+bwd, "
+                                   f"median of {reps}")
+    return res
+
+
 BENCHES = {"copy": bench_copy, "swiglu": bench_swiglu, "rope": bench_rope, "ce": bench_ce, "lora_mlp": bench_lora_mlp,
-           "lora_qkv": bench_lora_qkv, "flce": bench_flce}
+           "lora_qkv": bench_lora_qkv, "flce": bench_flce, "geglu": bench_geglu}
 
 
 def main():

@@ -71,6 +71,26 @@ int forge_swiglu_bwd(int dtype, const void* dout, int64_t ld_dout,
                      int64_t rows, int64_t cols,
                      float gate_multiplier, float down_multiplier, void* stream);
 
+/* GeGLU: out = gelu(gate).to(dtype) * up, GELU in its tanh form
+ * (approximate_tanh != 0) or exact (erf); same layout contract as SwiGLU
+ * (rows of `cols` elements, pitches ld_*, packed gate_up via up = gate + H and
+ * ld = 2H).  Replaces `_geglu_forward_kernel` / `_geglu_packed_forward_kernel`
+ * (kernels/geglu/geglu.py:126-148, 185-213) launched by `geglu_forward` /
+ * `geglu_packed_forward` (:380-406, 440-467). */
+int forge_geglu_fwd(int dtype, const void* gate, const void* up, int64_t ld_in,
+                    void* out, int64_t ld_out, int64_t rows, int64_t cols,
+                    int approximate_tanh, void* stream);
+
+/* GeGLU backward: dup = dout * gelu(gate).to(dtype), dgate = dout * up *
+ * gelu'(gate) (fp32, rounded once); dgate/dup may alias gate/up (in place).
+ * Replaces `_geglu_backward_kernel` / `_geglu_packed_backward_kernel`
+ * (kernels/geglu/geglu.py:151-182, 216-252) launched by `geglu_backward` /
+ * `geglu_packed_backward` (:409-437, 470-498). */
+int forge_geglu_bwd(int dtype, const void* dout, int64_t ld_dout,
+                    const void* gate, const void* up, int64_t ld_in,
+                    void* dgate, void* dup, int64_t ld_dgrad,
+                    int64_t rows, int64_t cols, int approximate_tanh, void* stream);
+
 /* ------------------------------------------------------------------------
  * RoPE (half-split rotation, GQA: n_q % n_kv == 0)
  * ------------------------------------------------------------------------ */

@@ -81,6 +81,10 @@ forge_swiglu_bwd = _decl(
     "forge_swiglu_bwd",
     [c_int, c_vp, c_i64, c_vp, c_vp, c_i64, c_vp, c_vp, c_i64, c_i64, c_i64, c_f32, c_f32, c_vp],
 )
+forge_geglu_fwd = _decl("forge_geglu_fwd", [c_int, c_vp, c_vp, c_i64, c_vp, c_i64, c_i64, c_i64, c_int, c_vp])
+forge_geglu_bwd = _decl(
+    "forge_geglu_bwd", [c_int, c_vp, c_i64, c_vp, c_vp, c_i64, c_vp, c_vp, c_i64, c_i64, c_i64, c_int, c_vp]
+)
 forge_rope = _decl(
     "forge_rope",
     [c_int]
@@ -139,7 +143,7 @@ forge_cast_f32_bf16 = _decl("forge_cast_f32_bf16", [c_vp, c_i64, c_vp, c_i64, c_
 # Every symbol include/forge_hip.h declares (checked by the CPU test suite).
 EXPORTED = [
     "forge_version", "forge_last_error", "forge_arch_ok",
-    "forge_swiglu_fwd", "forge_swiglu_bwd", "forge_rope",
+    "forge_swiglu_fwd", "forge_swiglu_bwd", "forge_geglu_fwd", "forge_geglu_bwd", "forge_rope",
     "forge_ce_fwd", "forge_ce_target_stats", "forge_ce_scale", "forge_sum_f32",
     "forge_gemm", "forge_lora_mlp_gate_up", "forge_lora_mlp_down_bwd", "forge_lora_qkv_rope",
     "forge_lora_a", "forge_zero", "forge_cast_f32_bf16", "forge_splitk_reduce",

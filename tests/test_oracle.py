@@ -529,3 +529,54 @@ def test_fused_linear_ce_metrics_and_flops():
     assert torch.equal(out["predicted"], pred)
     assert float(out["token_accuracy"]) == pytest.approx(float(((pred == t) & (t != -100)).sum() / (t != -100).sum()))
     assert oflce.flops(8192, 4096, 128256) == 6 * 8192 * 4096 * 128256 == 25_821_343_383_552
+
+
+# ---------------------------------------------------------------------------
+# GeGLU: the formula restatement against torch's own GELU (forward) and
+# autograd of F.gelu (derivative), in float64
+# ---------------------------------------------------------------------------
+from oracle import geglu as ogeglu  # noqa: E402
+
+
+@pytest.mark.parametrize("approximate", ["tanh", "none"])
+def test_geglu_oracle_matches_torch_gelu_and_autograd(approximate):
+    g = torch.Generator().manual_seed(3)
+    x = (torch.randn(4096, generator=g, dtype=torch.float64) * 3).requires_grad_(True)
+    act, grad = ogeglu.gelu_and_grad(x.detach(), approximate)
+    ref = F.gelu(x, approximate=approximate)
+    ref.sum().backward()
+    torch.testing.assert_close(act, ref.detach(), rtol=1e-12, atol=1e-12)
+    torch.testing.assert_close(grad, x.grad, rtol=1e-10, atol=1e-12)
+
+
+@pytest.mark.parametrize("approximate", ["tanh", "none"])
+def test_geglu_oracle_fp32_matches_autograd_of_reference_formula(approximate):
+    """fp32 storage: out = gelu(gate) * up and its autograd gradients."""
+    g = torch.Generator().manual_seed(4)
+    gate = torch.randn(64, 33, generator=g, dtype=torch.float64)
+    up = torch.randn(64, 33, generator=g, dtype=torch.float64)
+    dout = torch.randn(64, 33, generator=g, dtype=torch.float64)
+    gv, uv = gate.clone().requires_grad_(True), up.clone().requires_grad_(True)
+    (F.gelu(gv, approximate=approximate) * uv).backward(dout)
+    out, dgate, dup = ogeglu.geglu_fwd_bwd(gate, up, dout, approximate)
+    torch.testing.assert_close(out, F.gelu(gate, approximate=approximate) * up, rtol=1e-12, atol=1e-12)
+    torch.testing.assert_close(dgate, gv.grad, rtol=1e-10, atol=1e-12)
+    torch.testing.assert_close(dup, uv.grad, rtol=1e-10, atol=1e-12)
+
+
+def test_geglu_oracle_bf16_rounds_activation_before_product():
+    """bf16: the activation is rounded before the product (a single-rounding
+    variant differs), and dup uses the rounded activation."""
+    g = torch.Generator().manual_seed(6)
+    gate = (torch.randn(8192, generator=g) * 2).to(torch.bfloat16)
+    up = torch.randn(8192, generator=g).to(torch.bfloat16)
+    out, _, _ = ogeglu.geglu_fwd_bwd(gate, up, None, "tanh")
+    ref = F.gelu(gate.float(), approximate="tanh").to(torch.bfloat16) * up  # the reference formula
+    # the oracle's float64 activation and the reference's fp32 one differ only
+    # by a bf16 rounding step, or in the far negative tail where fp32's
+    # 1 + tanh cancels (|gelu| < 1e-4 there)
+    err = (out.float() - ref.float()).abs()
+    assert bool((err <= out.float().abs() * 2 ** -7 + 1e-4).all())
+    assert bool(((out == ref) | (err <= out.float().abs() * 2 ** -7) | (gate.float() < -3.5)).all())
+    single = (F.gelu(gate.double(), approximate="tanh") * up.double()).to(torch.bfloat16)
+    assert int((single != out).sum()) > 50
