@@ -43,7 +43,7 @@ def _parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--kernels", default="swiglu,rope,ce,lora_mlp,lora_qkv,flce,geglu")
+    ap.add_argument("--kernels", default="swiglu,rope,ce,lora_mlp,lora_qkv,flce,geglu,rmsnorm")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--only-launches", action="store_true",
                     help="run only the dominant-kernel launch loop (for rocprofv3 counter runs)")
@@ -636,8 +636,83 @@ def bench_geglu(args):
     return res
 
 
+def bench_rmsnorm(args):
+    """RMSNorm (the next row after the five configs): bf16 x [8192, 4096]
+    (Llama-3-8B hidden size), llama casting, fwd+bwd with the weight
+    gradient and the in-place dY -> dX backward (v4 default)."""
+    import torch
+    from forge_hip import _lib as L
+    from kernels.rmsnorm import apply_rmsnorm_v4
+    from oracle.rmsnorm import bytes_fwd_bwd
+
+    R, H = 8192, 4096
+    bf = torch.bfloat16
+    g = torch.Generator(device="cuda").manual_seed(8)
+    x = torch.randn(R, H, device="cuda", generator=g).to(bf).requires_grad_(True)
+    w = (1 + 0.1 * torch.randn(H, device="cuda", generator=g)).to(bf).requires_grad_(True)
+    dy0 = torch.randn(R, H, device="cuda", generator=g).to(bf)
+    total = args.warmup + args.steps
+    dys = [None] * total
+
+    def prepare(i):
+        dys[i] = dy0.clone()  # the in-place backward overwrites dy with dx
+
+    def step(i):
+        x.grad = None  # a training step after zero_grad(set_to_none=True)
+        w.grad = None
+        apply_rmsnorm_v4(x, w, 1e-6, 0.0, "llama", in_place=True).backward(dys[i])
+        dys[i] = None
+
+    ms, wall = run_steps(args, step, prepare)
+    bytes_step = bytes_fwd_bwd(R, H)
+    gbs = rate(bytes_step, ms, 1e9)
+    # dominant kernel: the backward (reads x and dy, writes dx over dy, dw partials)
+    xd, wd = x.detach(), w.detach()
+    rstd = torch.empty(R, device="cuda")
+    yb = torch.empty_like(xd)
+    st = L.stream_of(xd)
+    L.check(L.forge_rmsnorm_fwd(2, 2, 2, xd.data_ptr(), H, wd.data_ptr(), yb.data_ptr(), H, rstd.data_ptr(), R, H,
+                                1e-6, 0.0, 0, st), "forge_rmsnorm_fwd")
+    dyb = dy0.clone()
+    dx = torch.empty_like(xd)
+    dw = torch.empty(H, device="cuda", dtype=bf)
+    work = torch.empty(L.forge_rmsnorm_bwd_workspace(2, R, H), device="cuda", dtype=torch.uint8)
+    bwd_ms = time_launches(lambda i: L.forge_rmsnorm_bwd(2, 2, dyb.data_ptr(), H, xd.data_ptr(), H, wd.data_ptr(),
+                                                         rstd.data_ptr(), dx.data_ptr(), H, dw.data_ptr(),
+                                                         work.data_ptr(), R, H, 0.0, 0, st), max(args.steps, 10))
+    bwd_bytes = 3 * R * H * 2 + 4 * R + 3 * H * 2
+    res = {
+        "config": {"workload": "rmsnorm_fwd_bwd", "dtype": "bf16", "shape": [R, H], "casting_mode": "llama",
+                   "offset": 0.0, "in_place": True, "weight_grad": True},
+        "value": gbs, "unit": "GB/s", "ms_per_step": rnd(ms, 5), "wall_ms_per_step": rnd(wall, 5),
+        "frac_of_hbm_peak": rnd(gbs and gbs / HBM_PEAK_GBS, 4), "algorithmic_bytes_per_step": bytes_step,
+        "launches_ms": {"forge_rmsnorm_bwd": round(bwd_ms, 5)},
+        "roofline": _roof("hbm", bwd_bytes / (bwd_ms * 1e-3) / 1e9, HBM_PEAK_GBS, "GB/s", _traffic("rmsnorm_bwd")),
+        "dtype": "bf16",
+    }
+    if not (args.no_cpu_baseline or args.only_launches):
+        from kernels.rmsnorm import torch_rmsnorm_reference_v4
+
+        rows = 512
+        xc = xd[:rows].cpu().requires_grad_(True)
+        wc = wd.cpu().requires_grad_(True)
+        gc = dy0[:rows].cpu()
+
+        def cpu_step():
+            xc.grad = None
+            wc.grad = None
+            torch_rmsnorm_reference_v4(xc, wc, 1e-6, 0.0, "llama").backward(gc)
+
+        t, reps = cpu_time(cpu_step)
+        res["cpu_baseline"] = _cpu(bytes_fwd_bwd(rows, H) / t / 1e9, "GB/s",
+                                   f"{rows} of {R} rows, the reference's PyTorch RMSNorm (bf16) fwd+bwd via "
+                                   f"autograd, median of {reps}")
+    return res
+
+
 BENCHES = {"copy": bench_copy, "swiglu": bench_swiglu, "rope": bench_rope, "ce": bench_ce, "lora_mlp": bench_lora_mlp,
-           "lora_qkv": bench_lora_qkv, "flce": bench_flce, "geglu": bench_geglu}
+           "lora_qkv": bench_lora_qkv, "flce": bench_flce, "geglu": bench_geglu,
+           "rmsnorm": bench_rmsnorm}
 
 
 def main():

@@ -191,6 +191,40 @@ int forge_row_scale(int dtype, void* x, int64_t ld, int64_t n_rows, int64_t n_co
                     void* stream);
 
 /* ------------------------------------------------------------------------
+ * RMSNorm (forward + backward, deterministic weight gradient)
+ * ------------------------------------------------------------------------ */
+
+enum { FORGE_RMS_LLAMA = 0, FORGE_RMS_GEMMA = 1, FORGE_RMS_NONE = 2 };
+
+/* y[r, :] = RMSNorm(x[r, :]) * (w + offset) with rstd[r] = rsqrt(mean(x^2) + eps)
+ * written to rstd (fp32; fp64 for fp64 x).  casting_mode FORGE_RMS_LLAMA /
+ * GEMMA / NONE selects where products are rounded to the storage dtype (see
+ * forge_rmsnorm_v4.py:73-128).  Dtypes: x, w, y all equal (fp32, fp64, bf16,
+ * fp16), or a 16-bit x with an fp32 weight and y of x's dtype or fp32.
+ * Replaces `_rmsnorm_v4_forward_kernel` (kernels/rmsnorm/forge_rmsnorm_v4.py:
+ * 73-128, launched by rmsnorm_v4_forward :242-270; the v2/v3 kernels are the
+ * same) and `_rmsnorm_v1_forward_kernel` (forge_rmsnorm_v1.py:32-58, llama
+ * mode with offset 0 and y of the promoted dtype). */
+int forge_rmsnorm_fwd(int dtype, int w_dtype, int y_dtype, const void* x, int64_t ldx, const void* w,
+                      void* y, int64_t ldy, void* rstd, int64_t rows, int64_t cols, double eps,
+                      double offset, int casting_mode, void* stream);
+
+/* dx = rstd (s - x rstd^2 sum(s x) / H) with s = dy (w + offset), written
+ * to dx (may alias dy: the in-place backward); when dw is given, dw =
+ * sum over rows of dy x rstd in w's dtype, through per-workgroup partial
+ * sums in `work` (forge_rmsnorm_bwd_workspace bytes, caller-allocated) added
+ * in a fixed order.  variant 1 = v1's roundings (s and the dw terms rounded
+ * to x's dtype).  Replaces `_rmsnorm_v4_backward_kernel`
+ * (forge_rmsnorm_v4.py:131-184) with the host reduction of its partials
+ * (:273-336), and `_rmsnorm_v1_backward_kernel` (forge_rmsnorm_v1.py:61-106). */
+int forge_rmsnorm_bwd(int dtype, int w_dtype, const void* dy, int64_t lddy, const void* x, int64_t ldx,
+                      const void* w, const void* rstd, void* dx, int64_t lddx, void* dw, void* work,
+                      int64_t rows, int64_t cols, double offset, int variant, void* stream);
+
+/* Bytes of the dw partial-sum workspace forge_rmsnorm_bwd needs. */
+int64_t forge_rmsnorm_bwd_workspace(int dtype, int64_t rows, int64_t cols);
+
+/* ------------------------------------------------------------------------
  * Generic GEMM (any strides, fp32 / fp16 / bf16 operands, fp32 accumulation)
  * ------------------------------------------------------------------------ */
 

@@ -1,0 +1,879 @@
+// RMSNorm forward/backward for gfx950.
+//
+// Reference semantics (kernels/rmsnorm/forge_rmsnorm_v4.py:73-184, the same
+// kernels as v2/v3; v1 in forge_rmsnorm_v1.py:32-106):
+//   forward   rstd = rsqrt(mean(x^2) + eps)        (fp32; fp64 for fp64 input)
+//             llama: y = (x rstd).to(dtype) * (w + offset)
+//             gemma: y = (x rstd) * (float(w) + offset)           (fp32, one rounding)
+//             none:  y = (x * rstd.to(dtype)) * (w + offset)       (dtype products)
+//   backward  s = dy (w + offset); dot = sum(s x)
+//             dx = rstd (s - x rstd^2 dot / H);  dw = sum over rows of dy x rstd
+//             (v1: s = (dy w) rounded to dtype, dw terms dy * (x rstd).to(dtype)
+//             rounded to dtype)
+//
+// Layout: rows of H elements (row pitches ld*); every row is read from HBM
+// once.  Two engines, chosen by the row's width in 16-byte vectors:
+//  * workgroup per row block (256 .. 2048 vectors, aligned rows): the 256
+//    threads of a workgroup span the row, NVT vectors each, with R = 8/NVT
+//    rows in flight per chunk; a row sum is a wave shuffle reduction plus a
+//    fixed-order sum of the four wave totals in LDS (one barrier per chunk).
+//    Each thread owns its dw columns for the whole launch, so the backward
+//    writes its per-workgroup dw partial row straight from registers.  This
+//    is the engine of Llama-class hidden sizes (2048 .. 16384 bf16).
+//  * wave per row (narrower or unaligned rows): one 64-lane wave per row,
+//    four rows per workgroup, reductions by shuffles only.  A lane's share
+//    is held in registers up to NV = 8 vectors; wider rows take a two-pass
+//    loop whose second pass hits the caches, and their dw comes from a
+//    separate column-tiled pass.  The backward combines the four waves' dw
+//    accumulators in LDS in a fixed order into one partial row per
+//    workgroup.
+// dw = a two-level fixed-order column sum of the partial rows, rounded once
+// to the weight dtype: deterministic, no atomics.  dx may alias dy (in
+// place): every thread reads its dy elements before it writes the dx
+// elements at the same addresses.
+#include <type_traits>
+
+#include "common.h"
+
+namespace {
+
+constexpr int kWaves = 4;
+enum { MODE_LLAMA = 0, MODE_GEMMA = 1, MODE_NONE = 2 };
+
+template <class T> struct Acc { typedef float type; };
+template <> struct Acc<double> { typedef double type; };
+
+template <class A> __device__ __forceinline__ A wave_sum_a(A v) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
+  return v;
+}
+__device__ __forceinline__ float rsqrt_a(float v) { return rsqrtf(v); }
+__device__ __forceinline__ double rsqrt_a(double v) { return 1.0 / sqrt(v); }
+
+// conversions between a storage type and the accumulation type
+template <class A, class T> __device__ __forceinline__ A cv(T v) { return (A)to_f32<T>(v); }
+template <> __device__ __forceinline__ double cv<double, double>(double v) { return v; }
+template <class T, class A> __device__ __forceinline__ T st(A v) { return from_f32<T>((float)v); }
+template <> __device__ __forceinline__ double st<double, double>(double v) { return v; }
+template <class T, class A> __device__ __forceinline__ A rnd(A v) { return cv<A, T>(st<T, A>(v)); }
+
+// VEC consecutive elements at p (16-byte vector when VEC > 1)
+template <class T, int VEC, class A>
+__device__ __forceinline__ void load_vec(const T* p, A (&o)[VEC]) {
+  if constexpr (VEC > 1) {
+    const Vec16<T> v = load16(p);
+#pragma unroll
+    for (int q = 0; q < VEC; ++q) o[q] = cv<A, T>(v.v[q]);
+  } else {
+    o[0] = cv<A, T>(p[0]);
+  }
+}
+// VEC raw storage elements (kept packed in registers, converted on use)
+template <class T, int VEC>
+__device__ __forceinline__ void load_raw(const T* p, T (&o)[VEC]) {
+  if constexpr (VEC > 1) {
+    const Vec16<T> v = load16(p);
+#pragma unroll
+    for (int q = 0; q < VEC; ++q) o[q] = v.v[q];
+  } else {
+    o[0] = p[0];
+  }
+}
+template <class T, int VEC, class A>
+__device__ __forceinline__ void store_vec(T* p, const A (&o)[VEC]) {
+  if constexpr (VEC > 1) {
+    Vec16<T> v;
+#pragma unroll
+    for (int q = 0; q < VEC; ++q) v.v[q] = st<T, A>(o[q]);
+    *reinterpret_cast<uint4*>(p) = v.raw;
+  } else {
+    p[0] = st<T, A>(o[0]);
+  }
+}
+// weight elements (their own dtype TW; vector loads only when TW == T)
+template <class TW, int VEC, class A>
+__device__ __forceinline__ void load_w(const TW* w, int64_t c, A (&o)[VEC], bool wvec) {
+  if constexpr (VEC * sizeof(TW) == 16) {
+    if (wvec) {
+      load_vec<TW, VEC, A>(w + c, o);
+      return;
+    }
+  }
+#pragma unroll
+  for (int q = 0; q < VEC; ++q) o[q] = cv<A, TW>(w[c + q]);
+}
+
+struct RmsArgs {
+  const void* x; int64_t ldx;
+  const void* w;
+  void* y; int64_t ldy;        // forward output
+  const void* dy; int64_t lddy;
+  void* dx; int64_t lddx;      // backward output (may alias dy)
+  void* rstd;                  // [rows] of the accumulation type
+  void* part;                  // dw partials [n_part][H] (accumulation type), or null
+  int64_t rows, H;
+  double eps, offset;
+  int mode, variant, wvec;
+};
+
+// y for one element: x and rstd in A, w as loaded (A), per casting mode
+template <class T, class TW, class TY, class A>
+__device__ __forceinline__ A fwd_elem(A x, A rstd, A w, A off, int mode) {
+  if (mode == MODE_GEMMA) return (x * rstd) * (w + off);
+  const A wo = rnd<TW, A>(w + off);
+  if (mode == MODE_LLAMA) return rnd<T, A>(x * rstd) * wo;
+  return rnd<T, A>(x * rnd<T, A>(rstd)) * wo;  // MODE_NONE
+}
+
+template <class T, class TW, class TY, int VEC, int NV>
+__global__ __launch_bounds__(256) void rms_fwd_kernel(RmsArgs a) {
+  using A = typename Acc<T>::type;
+  const int lane = threadIdx.x % 64;
+  const int64_t H = a.H;
+  const A eps = (A)a.eps, off = (A)a.offset;
+  const TW* w = (const TW*)a.w;
+  for (int64_t row = (int64_t)blockIdx.x * kWaves + threadIdx.x / 64; row < a.rows;
+       row += (int64_t)gridDim.x * kWaves) {
+    const T* xr = (const T*)a.x + row * a.ldx;
+    TY* yr = (TY*)a.y + row * a.ldy;
+    A ss = 0;
+    if constexpr (NV > 0) {
+      T xv[NV][VEC];
+#pragma unroll
+      for (int j = 0; j < NV; ++j) {
+        const int64_t c = (int64_t)(lane + 64 * j) * VEC;
+        if (c < H) {
+          load_raw<T, VEC>(xr + c, xv[j]);
+#pragma unroll
+          for (int q = 0; q < VEC; ++q) ss += cv<A, T>(xv[j][q]) * cv<A, T>(xv[j][q]);
+        }
+      }
+      ss = wave_sum_a(ss);
+      const A rstd = rsqrt_a(ss / (A)H + eps);
+      if (lane == 0) ((A*)a.rstd)[row] = rstd;
+#pragma unroll
+      for (int j = 0; j < NV; ++j) {
+        const int64_t c = (int64_t)(lane + 64 * j) * VEC;
+        if (c < H) {
+          A wv[VEC], o[VEC];
+          load_w<TW, VEC, A>(w, c, wv, a.wvec);
+#pragma unroll
+          for (int q = 0; q < VEC; ++q) o[q] = fwd_elem<T, TW, TY, A>(cv<A, T>(xv[j][q]), rstd, wv[q], off, a.mode);
+          if constexpr (sizeof(TY) == sizeof(T)) {
+            store_vec<TY, VEC, A>(yr + c, o);
+          } else {
+#pragma unroll
+            for (int q = 0; q < VEC; ++q) yr[c + q] = st<TY, A>(o[q]);
+          }
+        }
+      }
+    } else {
+      for (int64_t c = (int64_t)lane * VEC; c < H; c += 64 * VEC) {
+        A xv[VEC];
+        load_vec<T, VEC, A>(xr + c, xv);
+#pragma unroll
+        for (int q = 0; q < VEC; ++q) ss += xv[q] * xv[q];
+      }
+      ss = wave_sum_a(ss);
+      const A rstd = rsqrt_a(ss / (A)H + eps);
+      if (lane == 0) ((A*)a.rstd)[row] = rstd;
+      for (int64_t c = (int64_t)lane * VEC; c < H; c += 64 * VEC) {
+        A xv[VEC], wv[VEC], o[VEC];
+        load_vec<T, VEC, A>(xr + c, xv);
+        load_w<TW, VEC, A>(w, c, wv, a.wvec);
+#pragma unroll
+        for (int q = 0; q < VEC; ++q) o[q] = fwd_elem<T, TW, TY, A>(xv[q], rstd, wv[q], off, a.mode);
+#pragma unroll
+        for (int q = 0; q < VEC; ++q) yr[c + q] = st<TY, A>(o[q]);
+      }
+    }
+  }
+}
+
+// s = dy * (w + offset): fp32 (v2-v4) or rounded to the product dtype (v1)
+template <class T, class TW, class A>
+__device__ __forceinline__ A scaled_dy(A dy, A w, A off, int variant) {
+  if (variant == 1) return sizeof(TW) > sizeof(T) ? dy * w : rnd<T, A>(dy * w);
+  return dy * (w + off);
+}
+
+// one row's contribution to dw[c]: dy * x rstd (v2-v4, fp32); v1 rounds the
+// normalised x and the product to the storage dtype (its bf16 dy * normed)
+template <class T, class A>
+__device__ __forceinline__ A dw_term(A dy, A x, A rstd, int variant) {
+  if (variant == 1) return rnd<T, A>(dy * rnd<T, A>(x * rstd));
+  return dy * (x * rstd);
+}
+
+// Backward, NV > 0: rows in registers, dw accumulated per lane and reduced per
+// workgroup into part[blockIdx.x].  NV == 0: two passes per row, no dw (the
+// separate column pass computes it).
+template <class T, class TW, int VEC, int NV>
+__global__ __launch_bounds__(256) void rms_bwd_kernel(RmsArgs a) {
+  using A = typename Acc<T>::type;
+  constexpr int COLS = NV > 0 ? 64 * NV * VEC : 1;
+  __shared__ A red[NV > 0 ? kWaves : 1][COLS];
+  const int lane = threadIdx.x % 64, wave = threadIdx.x / 64;
+  const int64_t H = a.H;
+  const A off = (A)a.offset;
+  const A inv_h = (A)1 / (A)H;
+  const TW* w = (const TW*)a.w;
+  const bool want_dw = a.part != nullptr;
+  A dwacc[NV > 0 ? NV : 1][VEC];
+#pragma unroll
+  for (int j = 0; j < (NV > 0 ? NV : 1); ++j)
+#pragma unroll
+    for (int q = 0; q < VEC; ++q) dwacc[j][q] = 0;
+
+  for (int64_t row = (int64_t)blockIdx.x * kWaves + wave; row < a.rows; row += (int64_t)gridDim.x * kWaves) {
+    const T* xr = (const T*)a.x + row * a.ldx;
+    const T* dyr = (const T*)a.dy + row * a.lddy;
+    T* dxr = (T*)a.dx + row * a.lddx;
+    const A rstd = ((const A*)a.rstd)[row];
+    A dot = 0;
+    if constexpr (NV > 0) {
+      // x and dy stay packed in registers; s = dy (w + offset) is recomputed
+      // in the second pass from the (cached) weight
+      T xv[NV][VEC], dv[NV][VEC];
+#pragma unroll
+      for (int j = 0; j < NV; ++j) {
+        const int64_t c = (int64_t)(lane + 64 * j) * VEC;
+        if (c < H) {
+          A wv[VEC];
+          load_raw<T, VEC>(xr + c, xv[j]);
+          load_raw<T, VEC>(dyr + c, dv[j]);
+          load_w<TW, VEC, A>(w, c, wv, a.wvec);
+#pragma unroll
+          for (int q = 0; q < VEC; ++q)
+            dot += scaled_dy<T, TW, A>(cv<A, T>(dv[j][q]), wv[q], off, a.variant) * cv<A, T>(xv[j][q]);
+        }
+      }
+      dot = wave_sum_a(dot);
+      const A k = rstd * rstd * dot * inv_h;
+#pragma unroll
+      for (int j = 0; j < NV; ++j) {
+        const int64_t c = (int64_t)(lane + 64 * j) * VEC;
+        if (c < H) {
+          A wv[VEC], o[VEC];
+          load_w<TW, VEC, A>(w, c, wv, a.wvec);
+#pragma unroll
+          for (int q = 0; q < VEC; ++q) {
+            const A x = cv<A, T>(xv[j][q]), d = cv<A, T>(dv[j][q]);
+            o[q] = rstd * (scaled_dy<T, TW, A>(d, wv[q], off, a.variant) - x * k);
+            dwacc[j][q] += dw_term<T, A>(d, x, rstd, a.variant);
+          }
+          store_vec<T, VEC, A>(dxr + c, o);
+        }
+      }
+    } else {
+      for (int64_t c = (int64_t)lane * VEC; c < H; c += 64 * VEC) {
+        A xv[VEC], dv[VEC], wv[VEC];
+        load_vec<T, VEC, A>(xr + c, xv);
+        load_vec<T, VEC, A>(dyr + c, dv);
+        load_w<TW, VEC, A>(w, c, wv, a.wvec);
+#pragma unroll
+        for (int q = 0; q < VEC; ++q) dot += scaled_dy<T, TW, A>(dv[q], wv[q], off, a.variant) * xv[q];
+      }
+      dot = wave_sum_a(dot);
+      const A k = rstd * rstd * dot * inv_h;
+      for (int64_t c = (int64_t)lane * VEC; c < H; c += 64 * VEC) {
+        A xv[VEC], dv[VEC], wv[VEC], o[VEC];
+        load_vec<T, VEC, A>(xr + c, xv);
+        load_vec<T, VEC, A>(dyr + c, dv);
+        load_w<TW, VEC, A>(w, c, wv, a.wvec);
+#pragma unroll
+        for (int q = 0; q < VEC; ++q) o[q] = rstd * (scaled_dy<T, TW, A>(dv[q], wv[q], off, a.variant) - xv[q] * k);
+        store_vec<T, VEC, A>(dxr + c, o);
+      }
+    }
+  }
+
+  if constexpr (NV > 0) {
+    if (!want_dw) return;
+    // the four waves' accumulators -> one partial row, summed in wave order
+#pragma unroll
+    for (int j = 0; j < NV; ++j)
+#pragma unroll
+      for (int q = 0; q < VEC; ++q) red[wave][(lane + 64 * j) * VEC + q] = dwacc[j][q];
+    __syncthreads();
+    A* part = (A*)a.part + (int64_t)blockIdx.x * H;
+    for (int64_t c = threadIdx.x; c < H; c += 256) {
+      A s = red[0][c];
+#pragma unroll
+      for (int v = 1; v < kWaves; ++v) s += red[v][c];
+      part[c] = s;
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Workgroup-per-row-block engine (rows of 256*VEC .. 2048*VEC elements).
+// The 256 threads of a workgroup span a row: thread t owns the NVT vectors
+// at columns (t + 256 j) VEC, and a chunk of R rows is in flight at once
+// (R * NVT = 8 vectors of x and of dy per thread).  A row's sum is a wave
+// shuffle reduction plus a fixed-order sum of the four wave totals through
+// LDS (double-buffered: one barrier per chunk).  In the backward each thread
+// owns its dw columns outright, so a workgroup's dw partial row is written
+// straight from registers.
+// ---------------------------------------------------------------------------
+template <class TW, int VEC>
+__device__ __forceinline__ void load_w_raw(const TW* w, int64_t c, TW (&o)[VEC], bool wvec) {
+  constexpr int PER = 16 / sizeof(TW);
+  if constexpr (VEC >= PER && VEC % PER == 0) {
+    if (wvec) {
+#pragma unroll
+      for (int k = 0; k < VEC / PER; ++k) {
+        const Vec16<TW> v = load16(w + c + k * PER);
+#pragma unroll
+        for (int q = 0; q < PER; ++q) o[k * PER + q] = v.v[q];
+      }
+      return;
+    }
+  }
+#pragma unroll
+  for (int q = 0; q < VEC; ++q) o[q] = w[c + q];
+}
+// VEC values stored as TY: 16-byte stores when VEC*sizeof(TY) is a multiple
+// of 16 (vec > 1 guarantees the alignment), else element stores
+template <class TY, int VEC, class A>
+__device__ __forceinline__ void store_n(TY* p, const A (&o)[VEC]) {
+  constexpr int PER = 16 / sizeof(TY);
+  if constexpr (VEC >= PER && VEC % PER == 0) {
+#pragma unroll
+    for (int k = 0; k < VEC / PER; ++k) {
+      Vec16<TY> v;
+#pragma unroll
+      for (int q = 0; q < PER; ++q) v.v[q] = st<TY, A>(o[k * PER + q]);
+      *reinterpret_cast<uint4*>(p + k * PER) = v.raw;
+    }
+  } else {
+#pragma unroll
+    for (int q = 0; q < VEC; ++q) p[q] = st<TY, A>(o[q]);
+  }
+}
+
+// VEC storage elements held as 32-bit words (a 16-bit element in a scalar
+// register would take a whole VGPR): 16-byte vectors load as four words,
+// elements widen on use (bf16 by a shift or mask, fp16 by a convert).
+template <class T, int VEC>
+struct Pk {
+  static constexpr int NW = (VEC * (int)sizeof(T) + 3) / 4;
+  uint32_t w[NW];
+};
+template <class T, int VEC>
+__device__ __forceinline__ void pk_load(const T* p, Pk<T, VEC>& o) {
+  if constexpr (VEC * sizeof(T) == 16) {
+    const uint4 v = *reinterpret_cast<const uint4*>(p);
+    o.w[0] = v.x; o.w[1] = v.y; o.w[2] = v.z; o.w[3] = v.w;
+  } else if constexpr (sizeof(T) == 2) {
+    o.w[0] = *reinterpret_cast<const uint16_t*>(p);
+  } else {
+    __builtin_memcpy(o.w, p, sizeof(T));
+  }
+}
+template <class A, class T, int VEC>
+__device__ __forceinline__ A pk_get(const Pk<T, VEC>& o, int q) {
+  if constexpr (std::is_same<T, bf16_t>::value) {
+    const uint32_t u = o.w[q / 2];
+    return (A)__uint_as_float((q & 1) ? (u & 0xffff0000u) : (u << 16));
+  } else if constexpr (std::is_same<T, fp16_t>::value) {
+    const uint32_t u = o.w[q / 2];
+    return (A)(float)__builtin_bit_cast(fp16_t, (uint16_t)((q & 1) ? (u >> 16) : (u & 0xffffu)));
+  } else if constexpr (std::is_same<T, float>::value) {
+    return (A)__uint_as_float(o.w[q]);
+  } else {
+    double d;
+    __builtin_memcpy(&d, &o.w[2 * q], 8);
+    return (A)d;
+  }
+}
+// Makes the words opaque to the optimiser (an empty asm that "modifies"
+// them), so values widened before this point are not kept alive after it:
+// the second pass widens the words again (a shift per element) instead of
+// holding twice the registers across the barrier.
+template <class T, int VEC>
+__device__ __forceinline__ void keep_packed(Pk<T, VEC>& o) {
+#pragma unroll
+  for (int k = 0; k < Pk<T, VEC>::NW; ++k) asm volatile("" : "+v"(o.w[k]));
+}
+
+// sum over the workgroup of one value per row: wave shuffles, then the four
+// wave totals in wave order (every thread gets the same bits)
+template <class A, int R>
+__device__ __forceinline__ void block_row_sums(A (&v)[R], A (*buf)[R], int lane, int wave) {
+#pragma unroll
+  for (int r = 0; r < R; ++r) v[r] = wave_sum_a(v[r]);
+  if (lane == 0) {
+#pragma unroll
+    for (int r = 0; r < R; ++r) buf[wave][r] = v[r];
+  }
+  __syncthreads();
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    A s = buf[0][r];
+#pragma unroll
+    for (int k = 1; k < kWaves; ++k) s += buf[k][r];
+    v[r] = s;
+  }
+}
+
+template <class T, class TW, class TY, int VEC, int NVT, int R, int MODE>
+__global__ __launch_bounds__(256) void rms_fwd_wg_kernel(RmsArgs a) {
+  using A = typename Acc<T>::type;
+  __shared__ A sums[2][kWaves][R];
+  const int tid = threadIdx.x, lane = tid % 64, wave = tid / 64;
+  const int64_t H = a.H;
+  const A eps = (A)a.eps, off = (A)a.offset;
+  const TW* w = (const TW*)a.w;
+  const int64_t n_chunks = (a.rows + R - 1) / R;
+  int buf = 0;
+  for (int64_t ch = blockIdx.x; ch < n_chunks; ch += gridDim.x, buf ^= 1) {
+    Pk<T, VEC> xv[R][NVT];
+    A ss[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      ss[r] = 0;
+      const int64_t row = ch * R + r;
+#pragma unroll
+      for (int j = 0; j < NVT; ++j) {
+        const uint32_t c = (uint32_t)(tid + 256 * j) * VEC;
+        if (row < a.rows && (int64_t)c < H) {
+          pk_load<T, VEC>((const T*)a.x + row * a.ldx + c, xv[r][j]);
+#pragma unroll
+          for (int q = 0; q < VEC; ++q) {
+            const A x = pk_get<A>(xv[r][j], q);
+            ss[r] += x * x;
+          }
+        }
+      }
+    }
+    block_row_sums<A, R>(ss, sums[buf], lane, wave);
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+      for (int j = 0; j < NVT; ++j) keep_packed(xv[r][j]);
+#pragma unroll
+    for (int j = 0; j < NVT; ++j) {
+      const uint32_t c = (uint32_t)(tid + 256 * j) * VEC;
+      if ((int64_t)c >= H) continue;
+      TW wr[VEC];
+      load_w_raw<TW, VEC>(w, c, wr, a.wvec);
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        const int64_t row = ch * R + r;
+        if (row >= a.rows) continue;
+        const A rstd = rsqrt_a(ss[r] / (A)H + eps);
+        A o[VEC];
+#pragma unroll
+        for (int q = 0; q < VEC; ++q)
+          o[q] = fwd_elem<T, TW, TY, A>(pk_get<A>(xv[r][j], q), rstd, cv<A, TW>(wr[q]), off, MODE);
+        store_n<TY, VEC, A>((TY*)a.y + row * a.ldy + c, o);
+      }
+    }
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const int64_t row = ch * R + r;
+      if (tid == r && row < a.rows) ((A*)a.rstd)[row] = rsqrt_a(ss[r] / (A)H + eps);
+    }
+  }
+}
+
+template <class T, class TW, int VEC, int NVT, int R, int VARIANT>
+__global__ __launch_bounds__(256) void rms_bwd_wg_kernel(RmsArgs a) {
+  using A = typename Acc<T>::type;
+  __shared__ A dots[2][kWaves][R];
+  const int tid = threadIdx.x, lane = tid % 64, wave = tid / 64;
+  const int64_t H = a.H;
+  const A off = (A)a.offset;
+  const A inv_h = (A)1 / (A)H;
+  const TW* w = (const TW*)a.w;
+  A dwacc[NVT][VEC];
+#pragma unroll
+  for (int j = 0; j < NVT; ++j)
+#pragma unroll
+    for (int q = 0; q < VEC; ++q) dwacc[j][q] = 0;
+  const int64_t n_chunks = (a.rows + R - 1) / R;
+  int buf = 0;
+  for (int64_t ch = blockIdx.x; ch < n_chunks; ch += gridDim.x, buf ^= 1) {
+    Pk<T, VEC> xv[R][NVT], dv[R][NVT];
+    A dot[R], rs[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const int64_t row = ch * R + r;
+      rs[r] = row < a.rows ? ((const A*)a.rstd)[row] : (A)0;
+#pragma unroll
+      for (int j = 0; j < NVT; ++j) {
+        const uint32_t c = (uint32_t)(tid + 256 * j) * VEC;
+        if (row < a.rows && (int64_t)c < H) {
+          pk_load<T, VEC>((const T*)a.x + row * a.ldx + c, xv[r][j]);
+          pk_load<T, VEC>((const T*)a.dy + row * a.lddy + c, dv[r][j]);
+        }
+      }
+    }
+#pragma unroll
+    for (int r = 0; r < R; ++r) dot[r] = 0;
+#pragma unroll
+    for (int j = 0; j < NVT; ++j) {
+      const uint32_t c = (uint32_t)(tid + 256 * j) * VEC;
+      if ((int64_t)c >= H) continue;
+      TW wr[VEC];
+      load_w_raw<TW, VEC>(w, c, wr, a.wvec);
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        if (ch * R + r >= a.rows) continue;
+#pragma unroll
+        for (int q = 0; q < VEC; ++q)
+          dot[r] += scaled_dy<T, TW, A>(pk_get<A>(dv[r][j], q), cv<A, TW>(wr[q]), off, VARIANT) *
+                    pk_get<A>(xv[r][j], q);
+      }
+    }
+    block_row_sums<A, R>(dot, dots[buf], lane, wave);
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+      for (int j = 0; j < NVT; ++j) {
+        keep_packed(xv[r][j]);
+        keep_packed(dv[r][j]);
+      }
+#pragma unroll
+    for (int j = 0; j < NVT; ++j) {
+      const uint32_t c = (uint32_t)(tid + 256 * j) * VEC;
+      if ((int64_t)c >= H) continue;
+      TW wr[VEC];
+      load_w_raw<TW, VEC>(w, c, wr, a.wvec);
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        const int64_t row = ch * R + r;
+        if (row >= a.rows) continue;
+        const A k = rs[r] * rs[r] * dot[r] * inv_h;
+        A o[VEC];
+#pragma unroll
+        for (int q = 0; q < VEC; ++q) {
+          const A x = pk_get<A>(xv[r][j], q), d = pk_get<A>(dv[r][j], q);
+          o[q] = rs[r] * (scaled_dy<T, TW, A>(d, cv<A, TW>(wr[q]), off, VARIANT) - x * k);
+          dwacc[j][q] += dw_term<T, A>(d, x, rs[r], VARIANT);
+        }
+        store_vec<T, VEC, A>((T*)a.dx + row * a.lddx + c, o);
+      }
+    }
+  }
+  if (a.part == nullptr) return;
+  A* part = (A*)a.part + (int64_t)blockIdx.x * H;
+#pragma unroll
+  for (int j = 0; j < NVT; ++j) {
+    const uint32_t c = (uint32_t)(tid + 256 * j) * VEC;
+    if ((int64_t)c < H) store_n<A, VEC, A>(part + c, dwacc[j]);
+  }
+}
+
+// Column-tiled dw partials for rows too wide for register accumulators:
+// part[split, c] = sum over the split's rows of dy * xhat.  Runs before the
+// row kernel, which may overwrite dy with dx.
+template <class T, int VEC>
+__global__ __launch_bounds__(256) void rms_dw_kernel(RmsArgs a, int64_t rows_per_split) {
+  using A = typename Acc<T>::type;
+  const int64_t c = ((int64_t)blockIdx.x * 256 + threadIdx.x) * VEC;
+  if (c >= a.H) return;
+  const int64_t r0 = (int64_t)blockIdx.y * rows_per_split;
+  const int64_t r1 = r0 + rows_per_split < a.rows ? r0 + rows_per_split : a.rows;
+  A acc[VEC];
+#pragma unroll
+  for (int q = 0; q < VEC; ++q) acc[q] = 0;
+  for (int64_t r = r0; r < r1; ++r) {
+    const A rstd = ((const A*)a.rstd)[r];
+    A xv[VEC], dv[VEC];
+    load_vec<T, VEC, A>((const T*)a.x + r * a.ldx + c, xv);
+    load_vec<T, VEC, A>((const T*)a.dy + r * a.lddy + c, dv);
+#pragma unroll
+    for (int q = 0; q < VEC; ++q) acc[q] += dw_term<T, A>(dv[q], xv[q], rstd, a.variant);
+  }
+  A* part = (A*)a.part + (int64_t)blockIdx.y * a.H + c;
+#pragma unroll
+  for (int q = 0; q < VEC; ++q) part[q] = acc[q];
+}
+
+// The column sum of the partials in two fixed-order levels.  Level 1, in
+// place: group g of kGroup partial rows is summed into its first row
+// (part[g kGroup, c]); each (group, column) is one thread's, so the write
+// touches nothing another thread reads.  Level 2: dw[c] = sum over groups of
+// those rows, rounded once to the weight dtype.
+constexpr int kGroup = 16;
+
+template <class A>
+__global__ __launch_bounds__(256) void colsum_group_kernel(A* part, int64_t n_part, int64_t H) {
+  const int64_t c = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (c >= H) return;
+  const int64_t p0 = (int64_t)blockIdx.y * kGroup;
+  const int64_t n = n_part - p0 < kGroup ? n_part - p0 : kGroup;
+  A v[kGroup];
+#pragma unroll
+  for (int p = 0; p < kGroup; ++p) v[p] = p < n ? part[(p0 + p) * H + c] : (A)0;
+  A s = v[0];
+#pragma unroll
+  for (int p = 1; p < kGroup; ++p) s += v[p];
+  part[p0 * H + c] = s;
+}
+
+template <class A, class TO>
+__global__ __launch_bounds__(256) void colsum_kernel(const A* part, int64_t n, int64_t stride, int64_t H, TO* out) {
+  const int64_t c = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (c >= H) return;
+  A s = 0;
+#pragma unroll 8
+  for (int64_t p = 0; p < n; ++p) s += part[p * stride + c];
+  out[c] = st<TO, A>(s);
+}
+
+// ---------------------------------------------------------------------------
+// host side
+// ---------------------------------------------------------------------------
+constexpr int kMaxNV = 8;
+#ifndef RMS_BWD_WG
+#define RMS_BWD_WG 512
+#endif
+constexpr int kBwdMaxWG = RMS_BWD_WG;  // most dw partial rows (one per workgroup)
+
+// dw partial rows for a backward over `rows` rows (the workspace's row count)
+inline int64_t n_part_max(int64_t rows) {
+  const int64_t wgs = (rows + kWaves - 1) / kWaves;
+  return wgs < kBwdMaxWG ? wgs : kBwdMaxWG;
+}
+
+template <class T>
+int vec_width(const RmsArgs& a, bool bwd) {
+  constexpr int V = 16 / sizeof(T);
+  bool ok = a.H % V == 0 && aligned16(a.x) && a.ldx % V == 0;
+  if (bwd)
+    ok = ok && aligned16(a.dy) && aligned16(a.dx) && a.lddy % V == 0 && a.lddx % V == 0 &&
+         (a.part == nullptr || aligned16(a.part));
+  else
+    ok = ok && aligned16(a.y) && a.ldy % V == 0;
+  return ok ? V : 1;
+}
+
+// NV (vectors per lane) for the wave-per-row engine: smallest power of two
+// that covers the row, 0 (two-pass) beyond kMaxNV
+inline int pick_nv(int64_t H, int vec) {
+  const int64_t per_lane = (H + 64 * vec - 1) / (64 * vec);
+  for (int nv = 1; nv <= kMaxNV; nv *= 2)
+    if (per_lane <= nv) return nv;
+  return 0;
+}
+
+// NVT (vectors per thread) for the workgroup engine: 0 when the row has
+// fewer than 256 vectors (the wave-per-row engine wastes fewer lanes) or
+// more than 8 per thread
+inline int pick_nvt(int64_t H, int vec) {
+  const int64_t nvec = (H + vec - 1) / vec;
+  if (nvec < 256) return 0;
+  const int64_t per = (nvec + 255) / 256;
+  for (int n = 1; n <= 8; n *= 2)
+    if (per <= n) return n;
+  return 0;
+}
+
+template <class T, class TW, class TY, int VEC, int NVT, int R>
+void fwd_wg(const RmsArgs& a, int grid, hipStream_t s) {
+  switch (a.mode) {
+    case MODE_LLAMA: rms_fwd_wg_kernel<T, TW, TY, VEC, NVT, R, MODE_LLAMA><<<grid, 256, 0, s>>>(a); break;
+    case MODE_GEMMA: rms_fwd_wg_kernel<T, TW, TY, VEC, NVT, R, MODE_GEMMA><<<grid, 256, 0, s>>>(a); break;
+    default: rms_fwd_wg_kernel<T, TW, TY, VEC, NVT, R, MODE_NONE><<<grid, 256, 0, s>>>(a); break;
+  }
+}
+
+template <class T, class TW, class TY, int VEC>
+int fwd_v(const RmsArgs& a, hipStream_t s) {
+  const int nvt = VEC > 1 ? pick_nvt(a.H, VEC) : 0;
+  if constexpr (VEC > 1) {
+    if (nvt) {
+      const int r = 8 / nvt;
+      const int grid = grid_for((a.rows + r - 1) / r, 1, 256 * 8);
+      switch (nvt) {
+        case 1: fwd_wg<T, TW, TY, VEC, 1, 8>(a, grid, s); break;
+        case 2: fwd_wg<T, TW, TY, VEC, 2, 4>(a, grid, s); break;
+        case 4: fwd_wg<T, TW, TY, VEC, 4, 2>(a, grid, s); break;
+        default: fwd_wg<T, TW, TY, VEC, 8, 1>(a, grid, s); break;
+      }
+      FORGE_CHECK_LAUNCH();
+      return FORGE_OK;
+    }
+  }
+  const int grid = grid_for((a.rows + kWaves - 1) / kWaves, 1, 256 * 8);
+  switch (pick_nv(a.H, VEC)) {
+    case 1: rms_fwd_kernel<T, TW, TY, VEC, 1><<<grid, 256, 0, s>>>(a); break;
+    case 2: rms_fwd_kernel<T, TW, TY, VEC, 2><<<grid, 256, 0, s>>>(a); break;
+    case 4: rms_fwd_kernel<T, TW, TY, VEC, 4><<<grid, 256, 0, s>>>(a); break;
+    case 8: rms_fwd_kernel<T, TW, TY, VEC, 8><<<grid, 256, 0, s>>>(a); break;
+    default: rms_fwd_kernel<T, TW, TY, VEC, 0><<<grid, 256, 0, s>>>(a); break;
+  }
+  FORGE_CHECK_LAUNCH();
+  return FORGE_OK;
+}
+
+template <class T, class TW, class TY>
+int fwd_t(RmsArgs a, hipStream_t s) {
+  constexpr int V = 16 / sizeof(T);
+  const int vec = vec_width<T>(a, false);
+  a.wvec = vec > 1 && aligned16(a.w);
+  if (vec == V) return fwd_v<T, TW, TY, V>(a, s);
+  return fwd_v<T, TW, TY, 1>(a, s);
+}
+
+template <class T, class TW, int VEC, int NVT, int R>
+void bwd_wg(const RmsArgs& a, int grid, hipStream_t s) {
+  if (a.variant == 1) rms_bwd_wg_kernel<T, TW, VEC, NVT, R, 1><<<grid, 256, 0, s>>>(a);
+  else rms_bwd_wg_kernel<T, TW, VEC, NVT, R, 0><<<grid, 256, 0, s>>>(a);
+}
+
+// the row kernels of the backward; returns the number of dw partial rows
+// they wrote (0 when a.part is null)
+template <class T, class TW, int VEC>
+int64_t bwd_rows(RmsArgs a, hipStream_t s) {
+  const int64_t npm = n_part_max(a.rows);
+  const int nvt = VEC > 1 ? pick_nvt(a.H, VEC) : 0;
+  if constexpr (VEC > 1) {
+    if (nvt) {
+      const int64_t chunks = (a.rows + 8 / nvt - 1) / (8 / nvt);
+      const int grid = (int)(chunks < npm ? chunks : npm);
+      switch (nvt) {
+        case 1: bwd_wg<T, TW, VEC, 1, 8>(a, grid, s); break;
+        case 2: bwd_wg<T, TW, VEC, 2, 4>(a, grid, s); break;
+        case 4: bwd_wg<T, TW, VEC, 4, 2>(a, grid, s); break;
+        default: bwd_wg<T, TW, VEC, 8, 1>(a, grid, s); break;
+      }
+      return a.part ? grid : 0;
+    }
+  }
+  const int nv = pick_nv(a.H, VEC);
+  int64_t np = 0;
+  if (nv == 0 && a.part) {  // column pass first (the row pass may overwrite dy)
+    const int64_t per = (a.rows + npm - 1) / npm;
+    np = (a.rows + per - 1) / per;
+    const dim3 g2((unsigned)((a.H / VEC + 255) / 256), (unsigned)np);
+    rms_dw_kernel<T, VEC><<<g2, 256, 0, s>>>(a, per);
+    a.part = nullptr;
+  } else if (a.part) {
+    np = npm;
+  }
+  switch (nv) {
+    case 1: rms_bwd_kernel<T, TW, VEC, 1><<<(int)npm, 256, 0, s>>>(a); break;
+    case 2: rms_bwd_kernel<T, TW, VEC, 2><<<(int)npm, 256, 0, s>>>(a); break;
+    case 4: rms_bwd_kernel<T, TW, VEC, 4><<<(int)npm, 256, 0, s>>>(a); break;
+    case 8: rms_bwd_kernel<T, TW, VEC, 8><<<(int)npm, 256, 0, s>>>(a); break;
+    default: rms_bwd_kernel<T, TW, VEC, 0><<<(int)npm, 256, 0, s>>>(a); break;
+  }
+  return np;
+}
+
+template <class A, class TO>
+void colsum(A* part, int64_t np, int64_t H, TO* dw, hipStream_t s) {
+  const unsigned gx = (unsigned)((H + 255) / 256);
+  if (np > kGroup) {
+    const int64_t groups = (np + kGroup - 1) / kGroup;
+    colsum_group_kernel<A><<<dim3(gx, (unsigned)groups), 256, 0, s>>>(part, np, H);
+    colsum_kernel<A, TO><<<gx, 256, 0, s>>>(part, groups, kGroup * H, H, dw);
+  } else {
+    colsum_kernel<A, TO><<<gx, 256, 0, s>>>(part, np, H, H, dw);
+  }
+}
+
+template <class T, class TW>
+int bwd_launch(RmsArgs a, void* dw, int w_dtype, hipStream_t s) {
+  using A = typename Acc<T>::type;
+  constexpr int V = 16 / sizeof(T);
+  const int vec = vec_width<T>(a, true);
+  a.wvec = vec > 1 && aligned16(a.w);
+  const int64_t np = vec == V ? bwd_rows<T, TW, V>(a, s) : bwd_rows<T, TW, 1>(a, s);
+  FORGE_CHECK_LAUNCH();
+  if (np && dw) {
+    A* part = (A*)a.part;
+    switch (w_dtype) {
+      case FORGE_DTYPE_F32: colsum<A, float>(part, np, a.H, (float*)dw, s); break;
+      case FORGE_DTYPE_BF16: colsum<A, bf16_t>(part, np, a.H, (bf16_t*)dw, s); break;
+      case FORGE_DTYPE_F16: colsum<A, fp16_t>(part, np, a.H, (fp16_t*)dw, s); break;
+      case FORGE_DTYPE_F64: colsum<A, double>(part, np, a.H, (double*)dw, s); break;
+      default: return forge_set_error(FORGE_ERR_UNSUPPORTED, "rmsnorm_bwd: weight dtype %d", w_dtype);
+    }
+    FORGE_CHECK_LAUNCH();
+  }
+  return FORGE_OK;
+}
+
+int64_t acc_size(int dtype) { return dtype == FORGE_DTYPE_F64 ? 8 : 4; }
+
+}  // namespace
+
+extern "C" int64_t forge_rmsnorm_bwd_workspace(int dtype, int64_t rows, int64_t cols) {
+  if (rows <= 0 || cols <= 0) return 0;
+  return n_part_max(rows) * cols * acc_size(dtype);
+}
+
+extern "C" int forge_rmsnorm_fwd(int dtype, int w_dtype, int y_dtype, const void* x, int64_t ldx, const void* w,
+                                 void* y, int64_t ldy, void* rstd, int64_t rows, int64_t cols, double eps,
+                                 double offset, int casting_mode, void* stream) {
+  if (rows < 0 || cols < 0) return forge_set_error(FORGE_ERR_INVALID, "rmsnorm_fwd: negative shape");
+  if (rows == 0 || cols == 0) return FORGE_OK;
+  if (ldx < cols || ldy < cols) return forge_set_error(FORGE_ERR_INVALID, "rmsnorm_fwd: row pitch < cols");
+  if (casting_mode < MODE_LLAMA || casting_mode > MODE_NONE)
+    return forge_set_error(FORGE_ERR_INVALID, "rmsnorm_fwd: casting mode %d", casting_mode);
+  RmsArgs a = {};
+  a.x = x; a.ldx = ldx; a.w = w; a.y = y; a.ldy = ldy; a.rstd = rstd;
+  a.rows = rows; a.H = cols; a.eps = eps; a.offset = offset; a.mode = casting_mode;
+  hipStream_t s = (hipStream_t)stream;
+  const bool same_w = w_dtype == dtype, fw = w_dtype == FORGE_DTYPE_F32;
+  const bool same_y = y_dtype == dtype, fy = y_dtype == FORGE_DTYPE_F32;
+  switch (dtype) {
+    case FORGE_DTYPE_F32:
+      if (same_w && same_y) return fwd_t<float, float, float>(a, s);
+      break;
+    case FORGE_DTYPE_F64:
+      if (same_w && same_y) return fwd_t<double, double, double>(a, s);
+      break;
+    case FORGE_DTYPE_BF16:
+      if (same_w && same_y) return fwd_t<bf16_t, bf16_t, bf16_t>(a, s);
+      if (fw && same_y) return fwd_t<bf16_t, float, bf16_t>(a, s);
+      if (fw && fy) return fwd_t<bf16_t, float, float>(a, s);
+      break;
+    case FORGE_DTYPE_F16:
+      if (same_w && same_y) return fwd_t<fp16_t, fp16_t, fp16_t>(a, s);
+      if (fw && same_y) return fwd_t<fp16_t, float, fp16_t>(a, s);
+      if (fw && fy) return fwd_t<fp16_t, float, float>(a, s);
+      break;
+  }
+  return forge_set_error(FORGE_ERR_UNSUPPORTED, "rmsnorm_fwd: dtypes x %d, weight %d, y %d", dtype, w_dtype, y_dtype);
+}
+
+extern "C" int forge_rmsnorm_bwd(int dtype, int w_dtype, const void* dy, int64_t lddy, const void* x, int64_t ldx,
+                                 const void* w, const void* rstd, void* dx, int64_t lddx, void* dw, void* work,
+                                 int64_t rows, int64_t cols, double offset, int variant, void* stream) {
+  if (rows < 0 || cols < 0) return forge_set_error(FORGE_ERR_INVALID, "rmsnorm_bwd: negative shape");
+  if (rows == 0 || cols == 0) return FORGE_OK;
+  if (ldx < cols || lddy < cols || lddx < cols)
+    return forge_set_error(FORGE_ERR_INVALID, "rmsnorm_bwd: row pitch < cols");
+  if (variant != 0 && variant != 1) return forge_set_error(FORGE_ERR_INVALID, "rmsnorm_bwd: variant %d", variant);
+  if (dw && !work) return forge_set_error(FORGE_ERR_INVALID, "rmsnorm_bwd: dw needs the partial-sum workspace");
+  RmsArgs a = {};
+  a.x = x; a.ldx = ldx; a.w = w; a.dy = dy; a.lddy = lddy; a.dx = dx; a.lddx = lddx; a.rstd = const_cast<void*>(rstd);
+  a.part = dw ? work : nullptr;
+  a.rows = rows; a.H = cols; a.offset = offset; a.variant = variant;
+  hipStream_t s = (hipStream_t)stream;
+  const bool same_w = w_dtype == dtype, fw = w_dtype == FORGE_DTYPE_F32;
+  switch (dtype) {
+    case FORGE_DTYPE_F32:
+      if (same_w) return bwd_launch<float, float>(a, dw, w_dtype, s);
+      break;
+    case FORGE_DTYPE_F64:
+      if (same_w) return bwd_launch<double, double>(a, dw, w_dtype, s);
+      break;
+    case FORGE_DTYPE_BF16:
+      if (same_w) return bwd_launch<bf16_t, bf16_t>(a, dw, w_dtype, s);
+      if (fw) return bwd_launch<bf16_t, float>(a, dw, w_dtype, s);
+      break;
+    case FORGE_DTYPE_F16:
+      if (same_w) return bwd_launch<fp16_t, fp16_t>(a, dw, w_dtype, s);
+      if (fw) return bwd_launch<fp16_t, float>(a, dw, w_dtype, s);
+      break;
+  }
+  return forge_set_error(FORGE_ERR_UNSUPPORTED, "rmsnorm_bwd: dtypes x %d, weight %d", dtype, w_dtype);
+}

@@ -136,6 +136,17 @@ forge_gemm_generic = _decl(
     [c_i64, c_i64, c_i64, c_int, c_vp, c_i64, c_i64, c_vp, c_i64, c_i64, c_vp, c_i64, c_int, c_f32, c_f32, c_vp, c_vp],
 )
 
+forge_rmsnorm_fwd = _decl(
+    "forge_rmsnorm_fwd",
+    [c_int, c_int, c_int, c_vp, c_i64, c_vp, c_vp, c_i64, c_vp, c_i64, c_i64, ctypes.c_double, ctypes.c_double,
+     c_int, c_vp],
+)
+forge_rmsnorm_bwd = _decl(
+    "forge_rmsnorm_bwd",
+    [c_int, c_int, c_vp, c_i64, c_vp, c_i64, c_vp, c_vp, c_vp, c_i64, c_vp, c_vp, c_i64, c_i64, ctypes.c_double,
+     c_int, c_vp],
+)
+forge_rmsnorm_bwd_workspace = _decl("forge_rmsnorm_bwd_workspace", [c_int, c_i64, c_i64], c_i64)
 forge_zero = _decl("forge_zero", [c_vp, c_i64, c_vp])
 forge_transpose_2b = _decl("forge_transpose_2b", [c_vp, c_i64, c_i64, c_i64, c_vp, c_i64, c_vp])
 forge_cast_f32_bf16 = _decl("forge_cast_f32_bf16", [c_vp, c_i64, c_vp, c_i64, c_i64, c_i64, c_vp])
@@ -148,6 +159,7 @@ EXPORTED = [
     "forge_gemm", "forge_lora_mlp_gate_up", "forge_lora_mlp_down_bwd", "forge_lora_qkv_rope",
     "forge_lora_a", "forge_zero", "forge_cast_f32_bf16", "forge_splitk_reduce",
     "forge_ce_target_prob", "forge_row_scale", "forge_gemm_generic", "forge_transpose_2b",
+    "forge_rmsnorm_fwd", "forge_rmsnorm_bwd", "forge_rmsnorm_bwd_workspace",
 ]
 
 # Number of successful library calls (tests use it to prove the HIP path ran).
@@ -170,8 +182,10 @@ def dtype_code(dtype: torch.dtype) -> int:
 
 
 def stream_of(t: torch.Tensor) -> int:
-    """Handle of torch's current stream on t's device (launches are async on it)."""
-    return torch.cuda.current_stream(t.device).cuda_stream
+    """Handle of torch's current stream on t's device (launches are async on
+    it).  The raw accessor skips building a Stream object (2 us -> 0.1 us per
+    launch on the host)."""
+    return torch._C._cuda_getCurrentRawStream(t.device.index)
 
 
 def ptr(t):

@@ -17,6 +17,9 @@ REEXPORTS = {
         "swiglu_packed", "swiglu_packed_backward", "swiglu_packed_forward", "torch_swiglu_packed_reference",
         "torch_swiglu_reference"]),
     "forge.kernels.rope": ("kernels.rope.forge_rope_v3", ["apply_rope", "ForgeRoPEv3", "ForgeRoPEv3Function"]),
+    "forge.kernels.rmsnorm": ("kernels.rmsnorm", [
+        "ForgeRMSNormFunction", "apply_rmsnorm", "rmsnorm", "rmsnorm_backward", "rmsnorm_forward",
+        "torch_rmsnorm_reference"]),
     "forge.kernels.geglu": ("kernels.geglu", [
         "ForgeGEGLUFunction", "ForgePackedGEGLUFunction", "geglu", "geglu_backward", "geglu_forward", "geglu_packed",
         "geglu_packed_backward", "geglu_packed_forward", "torch_geglu_packed_reference", "torch_geglu_reference"]),

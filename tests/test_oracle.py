@@ -580,3 +580,50 @@ def test_geglu_oracle_bf16_rounds_activation_before_product():
     assert bool(((out == ref) | (err <= out.float().abs() * 2 ** -7) | (gate.float() < -3.5)).all())
     single = (F.gelu(gate.double(), approximate="tanh") * up.double()).to(torch.bfloat16)
     assert int((single != out).sum()) > 50
+
+
+# ---------------------------------------------------------------------------
+# RMSNorm: forward against torch's F.rms_norm, backward against autograd, in
+# float64; the casting-mode rounding points in bf16
+# ---------------------------------------------------------------------------
+from oracle import rmsnorm as orms  # noqa: E402
+
+
+@pytest.mark.parametrize("offset", [0.0, 1.0])
+def test_rmsnorm_oracle_matches_torch_rms_norm_and_autograd(offset):
+    g = torch.Generator().manual_seed(9)
+    x = torch.randn(6, 5, 40, generator=g, dtype=torch.float64).requires_grad_(True)
+    w = (torch.randn(40, generator=g, dtype=torch.float64) * 0.3).requires_grad_(True)
+    dy = torch.randn(6, 5, 40, generator=g, dtype=torch.float64)
+    ref = F.rms_norm(x, (40,), w + offset, eps=1e-6)
+    ref.backward(dy)
+    for mode in (orms.LLAMA, orms.GEMMA, orms.NONE):  # no rounding at float64
+        y, _ = orms.rms_forward(x, w, 1e-6, offset, mode)
+        torch.testing.assert_close(y, ref.detach(), rtol=1e-12, atol=1e-12)
+    dx, dw = orms.rms_backward(dy, x, w, offset, 1e-6)
+    torch.testing.assert_close(dx, x.grad, rtol=1e-10, atol=1e-12)
+    torch.testing.assert_close(dw, w.grad, rtol=1e-10, atol=1e-12)
+
+
+def test_rmsnorm_oracle_casting_modes_round_where_the_reference_does():
+    """bf16: llama rounds the normalised row before the weight product, gemma
+    rounds once at the end, none rounds rstd first; each differs from the
+    others on random data, and llama equals the reference tests' formula."""
+    g = torch.Generator().manual_seed(10)
+    x = torch.randn(64, 96, generator=g).to(torch.bfloat16)
+    w = (1 + 0.1 * torch.randn(96, generator=g)).to(torch.bfloat16)
+    ys = [orms.rms_forward(x, w, 1e-6, 0.0, m)[0] for m in (orms.LLAMA, orms.GEMMA, orms.NONE)]
+    assert not torch.equal(ys[0], ys[1]) and not torch.equal(ys[0], ys[2])
+    xf = x.float()
+    ref_llama = (xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + 1e-6)).to(torch.bfloat16) * w
+    assert int((ys[0] != ref_llama).sum()) <= 3  # float64 vs fp32 rstd: ties only
+
+
+def test_rmsnorm_oracle_scale_invariance_and_bytes():
+    g = torch.Generator().manual_seed(11)
+    x = torch.randn(4, 32, generator=g, dtype=torch.float64)
+    w = torch.randn(32, generator=g, dtype=torch.float64)
+    y1, _ = orms.rms_forward(x, w, 0.0)
+    y2, _ = orms.rms_forward(x * 37.0, w, 0.0)
+    torch.testing.assert_close(y1, y2, rtol=1e-12, atol=1e-12)
+    assert orms.bytes_fwd_bwd(8192, 4096) == 5 * 8192 * 4096 * 2 + 8 * 8192 + 3 * 4096 * 2
