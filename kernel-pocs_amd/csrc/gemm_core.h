@@ -35,6 +35,8 @@
 //   D: acc[r] (r = 0..15) of lane l is D[8 * (r / 4) + 4 * (l / 32) + r % 4][l % 32]
 #pragma once
 
+#include <type_traits>
+
 #include "common.h"
 
 namespace fgemm {
@@ -913,6 +915,96 @@ struct DmaLoader {
   }
 };
 
+// ---------------------------------------------------------------------------
+// Token-major operands on the LDS-DMA engine.  A stored [K][M] (A_LAYOUT COL)
+// or B stored [K][N] (B_LAYOUT ROW): the token-reduction products (LoRA A/B
+// gradients, the fused-CE weight gradient), whose reduction dimension K is the
+// slow one.  A stage holds BKT k-rows of BROWS elements (RB = 2 BROWS bytes
+// per k-row, no padding), DMA'd as they lie in memory; the MFMA fragments are
+// read with ds_read_b64_tr_b16, which transposes within each 16-lane group:
+// lane L of a group supplies the 8 bytes at (k0 + L/4, r0 + 4 (L%4)), and
+// result lane i receives (k0 + q, r0 + i) for q = 0..3, so two reads (k0 and
+// k0 + 4) give the 8 consecutive k of row r0 + i that the 32x32x16 MFMA takes.
+// The 16-byte chunks of k-row q are XOR-swizzled (chunk ^ swzT(q)) so that the
+// four k-rows one half-wave reads (64 bytes each) fall in distinct 64-byte
+// windows of the 256-byte bank cycle.
+// ---------------------------------------------------------------------------
+template <int CPR>
+__device__ __forceinline__ int swzT(int q) {
+  if constexpr (CPR >= 16) return 4 * (q & 3);       // k-rows of >= 256 bytes: all start at bank 0
+  else if constexpr (CPR == 8) return 4 * ((q >> 1) & 1);  // 128-byte k-rows: two per bank cycle
+  else return 0;                                     // 64-byte k-rows: four per bank cycle already
+}
+
+template <int BROWS, int BKT, int NT>
+struct DmaLoaderT {
+  static constexpr int RB = BROWS * 2;        // LDS bytes per k-row
+  static constexpr int CPR = RB / 16;         // 16-byte chunks (8 rows) per k-row
+  static constexpr int RPI = 64 / CPR;        // k-rows per wave instruction
+  static constexpr int NINST = BKT / RPI;     // wave instructions per tile
+  static constexpr int NW = NT / 64;
+  static constexpr int IPW = NINST / NW;      // instructions per wave per tile
+  static_assert(CPR >= 4 && CPR <= 64 && 64 % CPR == 0, "k-row of 4 .. 64 chunks");
+  static_assert(NINST % NW == 0 && IPW >= 1, "tile / wave split");
+  uint32_t voff[IPW];   // byte offset of this lane's chunk from the tile's first k-row (OOB = zero-fill)
+  const char* base;
+  int64_t ld_bytes;
+
+  // p: operand base, ld: pitch between k-rows (elements), panel_off: first
+  // row (element) of the tile, row_ok(r): row panel_off + r exists (rows come
+  // in whole chunks of 8: the caller guarantees a multiple-of-8 extent).
+  template <class RowOk>
+  __device__ __forceinline__ void setup(const void* p, int64_t ld, int64_t panel_off, RowOk row_ok) {
+    ld_bytes = ld * 2;
+    base = p ? (const char*)p + panel_off * 2 : nullptr;
+    const int lane = threadIdx.x % 64, wave = threadIdx.x / 64;
+#pragma unroll
+    for (int j = 0; j < IPW; ++j) {
+      const int q = (wave * IPW + j) * RPI + lane / CPR;   // k-row in the tile
+      const int chunk = (lane % CPR) ^ swzT<CPR>(q);       // source chunk of LDS slot lane % CPR
+      voff[j] = (base && row_ok(chunk * 8)) ? (uint32_t)(q * ld_bytes + chunk * 16) : OOB;
+    }
+  }
+
+  // DMA of the K tile at k0 (kvalid valid k-rows) into the LDS stage `dst`.
+  __device__ __forceinline__ void load(int64_t k0, int64_t kvalid, char* dst) {
+    const int lane = threadIdx.x % 64;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / 64);
+    const __amdgpu_buffer_rsrc_t r = make_rsrc(base + k0 * ld_bytes);
+#pragma unroll
+    for (int j = 0; j < IPW; ++j) {
+      uint32_t off = voff[j];
+      if (kvalid < BKT && (wave * IPW + j) * RPI + lane / CPR >= kvalid) off = OOB;  // segment tail
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)(dst + (wave * IPW + j) * 1024),
+                                               16, off, 0, 0, 0);
+    }
+  }
+};
+
+// Byte offset, in a token-major stage, of the 8 bytes this lane supplies to
+// ds_read_b64_tr_b16 for the fragment of rows r0 .. r0+31 at k 0..3 (or 8..11
+// for lanes 32-63); add (k_base) * RB for other k.
+template <int CPR>
+__device__ __forceinline__ int tr_lane_offset(int r0, int lane) {
+  constexpr int RB = CPR * 16;
+  const int l = lane % 16, grp = lane / 16;
+  const int q = 8 * (grp / 2) + l / 4;                  // k-row (mod 4 fixes the swizzle for every k step)
+  const int r = r0 + 16 * (grp % 2) + 4 * (l % 4);      // first of the 4 rows this lane supplies
+  return q * RB + (((r / 8) ^ swzT<CPR>(q)) * 16) + (r % 8) * 2;
+}
+
+typedef short i16x4 __attribute__((ext_vector_type(4)));
+typedef short i16x8 __attribute__((ext_vector_type(8)));
+
+// one 32x32x16 operand fragment from a token-major stage: k 0..3 from p0 and
+// k 4..7 from p1 = p0 + 4 RB (lanes 32-63: k 8..15)
+__device__ __forceinline__ bf16x8 tr_frag(const char* p0, const char* p1) {
+  const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) i16x4*)p0);
+  const i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) i16x4*)p1);
+  const i16x8 v = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+  return __builtin_bit_cast(bf16x8, v);
+}
+
 // s_waitcnt with only vmcnt constrained (gfx9 encoding: vmcnt [3:0] + [15:14],
 // expcnt [6:4] = 7 and lgkmcnt [11:8] = 15 mean "don't wait").
 template <int N>
@@ -925,7 +1017,9 @@ __device__ __forceinline__ void wait_vmcnt() {
 // wave).  The 256 x 256 tiles hold one workgroup per CU (the ring plus the
 // staged epilogue take ~130 KB of LDS): 8 waves -> WPE 2.  The skinny tiles
 // (~72 KB of LDS) hold two workgroups of 4 waves per CU: WPE 2 as well.
-template <int BM, int BN, int WAVES_M, int WAVES_N, int BMODE, int EPI, int BKT, int NSTAGE, bool STAGED, int WPE>
+// AT / BT: A stored [K][M] / B stored [K][N] (token-major, see DmaLoaderT).
+template <int BM, int BN, int WAVES_M, int WAVES_N, int BMODE, int EPI, int BKT, int NSTAGE, bool STAGED, int WPE,
+          bool AT = false, bool BT = false>
 __global__ __launch_bounds__(WAVES_M * WAVES_N * 64) __attribute__((amdgpu_waves_per_eu(WPE, WPE)))
 void gemm_dma_kernel(GemmArgs args) {
   constexpr int NT = WAVES_M * WAVES_N * 64;
@@ -934,6 +1028,7 @@ void gemm_dma_kernel(GemmArgs args) {
   constexpr int RB = BKT * 2;
   constexpr int A_BYTES = BM * RB, B_BYTES = BN * RB, STAGE = A_BYTES + B_BYTES;
   static_assert(BMODE == B_SINGLE || TN == 128, "dual mode expects 128-row wave tiles");
+  static_assert(!(BT && BMODE == B_DUAL), "dual B operands are K-contiguous");
   constexpr int STAGED_B = STAGED ? STAGED_BYTES : 0;
   constexpr int SMEM = NSTAGE * STAGE > STAGED_B ? NSTAGE * STAGE : STAGED_B;
   __shared__ __attribute__((aligned(1024))) char smem[SMEM];
@@ -971,12 +1066,20 @@ void gemm_dma_kernel(GemmArgs args) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
 
-  DmaLoader<BM, BKT, NT, false> la;
-  DmaLoader<BN, BKT, NT, BMODE == B_DUAL> lb;
+  using LoaderA = std::conditional_t<AT, DmaLoaderT<BM, BKT, NT>, DmaLoader<BM, BKT, NT, false>>;
+  using LoaderB = std::conditional_t<BT, DmaLoaderT<BN, BKT, NT>, DmaLoader<BN, BKT, NT, BMODE == B_DUAL>>;
+  LoaderA la;
+  LoaderB lb;
   auto setup_seg = [&](int s) {
     const Seg& sg = args.segs[s];
-    la.setup(sg.a, sg.a, sg.lda, m0, [&](int q, int) -> int64_t { return m0 + q < M ? q : -1; });
-    if constexpr (BMODE == B_DUAL) {
+    if constexpr (AT) la.setup(sg.a, sg.lda, m0, [&](int r) { return m0 + r < M; });
+    else la.setup(sg.a, sg.a, sg.lda, m0, [&](int q, int) -> int64_t { return m0 + q < M ? q : -1; });
+    if constexpr (BT) {
+      lb.setup(sg.b, sg.ldb, n0 - sg.n_lo, [&](int r) {
+        const int64_t n = n0 + r;
+        return n < args.N && n >= sg.n_lo && n < sg.n_hi;
+      });
+    } else if constexpr (BMODE == B_DUAL) {
       lb.setup(sg.b, sg.b2, sg.ldb, n0, [&](int q, int) -> int64_t {
         const int t4 = (q % 128) / 32;
         const int rel = (q / 128) * 64 + (t4 / 2) * 32 + q % 32;
@@ -1026,6 +1129,14 @@ void gemm_dma_kernel(GemmArgs args) {
   const int g = swz<BKT>(lane % 32) ^ hi;          // chunk ^ swz = 2 ks ^ g
   const int a_row = (wm * TM + lane % 32) * RB;
   const int b_row = A_BYTES + (wn * TN + lane % 32) * RB;
+  // token-major stages: k-row pitches and this lane's transposed-read offsets
+  constexpr int RBA = BM * 2, RBB = BN * 2;
+  int a_tr[FM], b_tr[FN];
+#pragma unroll
+  for (int i = 0; i < FM; ++i) a_tr[i] = AT ? tr_lane_offset<BM / 8>(wm * TM + 32 * i, lane) : 0;
+#pragma unroll
+  for (int j = 0; j < FN; ++j) b_tr[j] = BT ? A_BYTES + tr_lane_offset<BN / 8>(wn * TN + 32 * j, lane) : 0;
+  constexpr int RD = (AT ? 2 : 1) * FM + (BT ? 2 : 1) * FN;  // LDS read instructions per k step
   auto compute = [&](int slot) {
     const char* st = smem + slot * STAGE;
     constexpr int KS = BKT / 16;
@@ -1033,13 +1144,27 @@ void gemm_dma_kernel(GemmArgs args) {
     auto read_frags = [&](int ks, int sl) {
       const int ko = ((2 * ks) ^ g) << 4;
 #pragma unroll
-      for (int i = 0; i < FM; ++i) af[sl][i] = *reinterpret_cast<const bf16x8*>(st + a_row + i * 32 * RB + ko);
+      for (int i = 0; i < FM; ++i) {
+        if constexpr (AT) {
+          const char* p = st + a_tr[i] + 16 * ks * RBA;
+          af[sl][i] = tr_frag(p, p + 4 * RBA);
+        } else {
+          af[sl][i] = *reinterpret_cast<const bf16x8*>(st + a_row + i * 32 * RB + ko);
+        }
+      }
 #pragma unroll
-      for (int j = 0; j < FN; ++j) bfr[sl][j] = *reinterpret_cast<const bf16x8*>(st + b_row + j * 32 * RB + ko);
+      for (int j = 0; j < FN; ++j) {
+        if constexpr (BT) {
+          const char* p = st + b_tr[j] + 16 * ks * RBB;
+          bfr[sl][j] = tr_frag(p, p + 4 * RBB);
+        } else {
+          bfr[sl][j] = *reinterpret_cast<const bf16x8*>(st + b_row + j * 32 * RB + ko);
+        }
+      }
     };
     read_frags(0, 0);
     if (KS > 1) read_frags(1, 1);
-    __builtin_amdgcn_sched_group_barrier(SG_DS_READ, (KS > 1 ? 2 : 1) * (FM + FN), 0);
+    __builtin_amdgcn_sched_group_barrier(SG_DS_READ, (KS > 1 ? 2 : 1) * RD, 0);
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
       const int sl = ks & 1;
@@ -1051,12 +1176,12 @@ void gemm_dma_kernel(GemmArgs args) {
       __builtin_amdgcn_sched_group_barrier(SG_MFMA, FM * FN, 0);
       if (ks + 2 < KS) {
         read_frags(ks + 2, sl);
-        __builtin_amdgcn_sched_group_barrier(SG_DS_READ, FM + FN, 0);
+        __builtin_amdgcn_sched_group_barrier(SG_DS_READ, RD, 0);
       }
     }
   };
 
-  constexpr int PER_TILE = DmaLoader<BM, BKT, NT, false>::IPW + DmaLoader<BN, BKT, NT, BMODE == B_DUAL>::IPW;
+  constexpr int PER_TILE = LoaderA::IPW + LoaderB::IPW;
   const int n_t = t_end - t_begin;
   if (n_t > 0) {
     // prologue: tiles 0 .. NSTAGE-2 in flight

@@ -158,7 +158,7 @@ extern "C" int forge_lora_a(int64_t M, int64_t K, int64_t r, int n_proj, const v
   // tiles): split z writes fp32 partial sums to work[z] ([split_k][M][N]),
   // which one reduction pass sums in a fixed order (deterministic) and rounds
   // to bf16.
-  const int cfg = N <= 32 ? 1 /* CFG_SKINNY_N */ : 3 /* CFG_SKINNY_N64 */;
+  const int cfg = -1;  // the narrow K-contiguous tiles (64 x N, N up to 256) picked from the shape
   if (split_k <= 1) {
     a.ep.c = out;
     a.ep.ldc = ld_out;

@@ -37,7 +37,27 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* parts, 
 #pragma unroll
     for (int q = 0; q < VEC; ++q) acc[q] = 0.f;
     const float* p = parts + r * ldp + c;
-    for (int z = 0; z < n_split; ++z, p += stride) {
+    // 8 slices' loads in flight, then their adds in z order (the sum order,
+    // and so the result, is that of the plain loop)
+    constexpr int U = 8;
+    int z = 0;
+    for (; z + U <= n_split; z += U, p += U * stride) {
+      float v[U][VEC];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        if constexpr (VEC == 4) {
+          const float4 w = *reinterpret_cast<const float4*>(p + u * stride);
+          v[u][0] = w.x; v[u][1] = w.y; v[u][2] = w.z; v[u][3] = w.w;
+        } else {
+          v[u][0] = p[u * stride];
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < U; ++u)
+#pragma unroll
+        for (int q = 0; q < VEC; ++q) acc[q] += v[u][q];
+    }
+    for (; z < n_split; ++z, p += stride) {
       if constexpr (VEC == 4) {
         const float4 v = *reinterpret_cast<const float4*>(p);
         acc[0] += v.x; acc[1] += v.y; acc[2] += v.z; acc[3] += v.w;

@@ -33,13 +33,23 @@ def ld(t: torch.Tensor) -> int:
     return t.stride(0) if t.dim() == 2 and t.shape[0] > 1 else t.shape[-1]
 
 
-def skinny_split(M: int, N: int, K: int) -> int:
-    """Split-K factor for a skinny output: the 256 x 32 (N <= 32) or 256 x 64
-    tiles alone give only M/256 workgroups per column tile, too few to keep
-    HBM busy; aim for ~512 (two workgroups on each of the 256 CUs)."""
-    tile_n = 32 if N <= 32 else 64
-    tiles = max(1, (M + 255) // 256) * max(1, (N + tile_n - 1) // tile_n)
+def skinny_split(M: int, N: int, K: int, k_contiguous: bool = True) -> int:
+    """Split-K factor for a skinny output.  K-contiguous operands run on
+    64-row tiles as wide as the output (64, 128 or 256 columns): with >= 256
+    of them (one per CU) no split is needed, the fp32 partial pass would only
+    add traffic; fewer tiles split K towards ~512 workgroups.  Token-major
+    operands run on 256 x 32 / 256 x 64 tiles, which alone give only M/256
+    workgroups per column tile: aim for ~512 (two workgroups on each of the
+    256 CUs)."""
     k_tiles = max(1, (K + 63) // 64)
+    if k_contiguous:
+        tile_n = 64 if N <= 64 else 128 if N <= 128 else 256
+        tiles = max(1, (M + 63) // 64) * max(1, (N + tile_n - 1) // tile_n)
+        if tiles >= 256:
+            return 1
+    else:
+        tile_n = 32 if N <= 32 else 64
+        tiles = max(1, (M + 255) // 256) * max(1, (N + tile_n - 1) // tile_n)
     return max(1, min(16, -(-512 // tiles), k_tiles // 4))
 
 
@@ -53,7 +63,7 @@ def gemm(M: int, N: int, segs: Sequence[Tuple[torch.Tensor, int, torch.Tensor, i
     dev = device if device is not None else segs[0][0].device
     K = sum(int(k) for (_, _, _, _, k) in segs)
     if not atomic and beta == 0.0 and N <= 64 and M >= 1024 and (out is None or out.dtype == torch.bfloat16):
-        split = skinny_split(M, N, K)
+        split = skinny_split(M, N, K, a_layout == ROW and b_layout == COL)
         if split > 1:
             if out is None:
                 out = torch.empty(M, N, dtype=torch.bfloat16, device=dev)

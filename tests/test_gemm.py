@@ -1,8 +1,9 @@
 """MFMA GEMM core parity (forge_gemm through the C ABI) vs a float32 matmul
 of the same bf16 operands on the CPU.
 
-Covers every operand layout, the three tile configurations (big, skinny-N,
-skinny-M), ragged M/N edges, multi-segment K (the LoRA K-extension), beta,
+Covers every operand layout, the tile configurations (big, skinny-N and
+the 64 x 64 narrow tiles of K-contiguous products up to N = 256, skinny-M,
+and the token-major LDS-DMA variants of each), ragged M/N edges, multi-segment K (the LoRA K-extension), beta,
 fp32 output and split-K with the atomic epilogue.  Tolerance: bf16 output
 2e-2 relative to the output scale; fp32 output 1e-3 (bf16 inputs, fp32
 accumulation, different summation order).
@@ -39,7 +40,7 @@ def _b_operand(n, k, layout, gen):
 
 @pytest.mark.gpu
 @pytest.mark.parametrize("M,N,K", [(256, 256, 64), (296, 520, 264), (64, 1000, 136), (1000, 40, 512),
-                                   (16, 704, 1024), (2048, 2048, 512)])
+                                   (16, 704, 1024), (2048, 2048, 512), (1000, 192, 264), (1000, 200, 72), (600, 128, 200)])
 @pytest.mark.parametrize("a_layout", [0, 1])
 @pytest.mark.parametrize("b_layout", [0, 1])
 def test_gemm_layouts(M, N, K, a_layout, b_layout):
