@@ -8,13 +8,13 @@ namespace fgemm {
 // Tile configurations.
 enum Cfg {
   CFG_BIG = 0,       // 256 x 256: 2 x 2 waves (128 x 128 per wave); 4 x 2 on the LDS-DMA path
-  CFG_SKINNY_N = 1,  // N <= 32-ish (rank-r outputs): 64 x 64 tiles (2 x 2 waves) for K-contiguous
-                     // operands, else 256 x 32 (4 x 1 waves)
+  CFG_SKINNY_N = 1,  // N <= 32-ish (rank-r outputs): 64 x 64 tiles (2 x 2 waves) for a K-contiguous
+                     // A, else 256 x 32 (4 x 1 waves)
   CFG_SKINNY_M = 2,  // 32 x 256, 1 x 4 waves: M <= 32-ish (LoRA A gradients)
-  CFG_SKINNY_N64 = 3,  // 32 < N <= 64: 64 x 64 tiles for K-contiguous operands, 256 x 64 for
-                       // token-major ones, else 256 x 32
-  CFG_NARROW_128 = 4,  // 64 < N <= 128, K-contiguous operands: 64 x 128 tiles (2 x 2 waves)
-  CFG_NARROW_256 = 5,  // 128 < N <= 256, K-contiguous operands: 64 x 256 tiles (2 x 2 waves)
+  CFG_SKINNY_N64 = 3,  // 32 < N <= 64: 64 x 64 tiles for a K-contiguous A, 256 x 64 for
+                       // token-major operands, else 256 x 32
+  CFG_NARROW_128 = 4,  // 64 < N <= 128, K-contiguous A: 64 x 128 tiles (2 x 2 waves)
+  CFG_NARROW_256 = 5,  // 128 < N <= 256, K-contiguous A: 64 x 256 tiles (2 x 2 waves)
 };
 
 #ifndef SKINNY_NSTAGE
@@ -45,16 +45,18 @@ static int launch_cfg(const GemmArgs& a, hipStream_t s) {
       gemm_dma_kernel<BM, BN, DWM, DWN, BMODE, EPI, 64, 2, DMA_STAGE, 2><<<grid, DWM * DWN * 64, 0, s>>>(a);
     else
       gemm_dma_kernel<BM, BN, DWM, DWN, BMODE, EPI, 64, 2, false, 2><<<grid, DWM * DWN * 64, 0, s>>>(a);
-  } else if constexpr (BM == 64 && (BN == 64 || BN == 128 || BN == 256) && AL == ROW && BL == COL &&
+  } else if constexpr (BM == 64 && (BN == 64 || BN == 128 || BN == 256) && AL == ROW && (BL == COL || BL == ROW) &&
                        BMODE == B_SINGLE) {
-    // narrow outputs (N <= 256: X A^T, dY B), K-contiguous: 64-row tiles as
-    // wide as the output (so X streams once) with 4 waves; a 3-stage ring
-    // (48 / 72 KB of LDS: three / two workgroups per CU) or, at 64 x 256, two
-    // stages in 80 KB (two per CU).  M/64 tiles fill the chip without a
-    // split-K pass.
+    // narrow outputs (N <= 256: X A^T, dY B) with A K-contiguous: 64-row
+    // tiles as wide as the output (so X streams once) with 4 waves; a 3-stage
+    // ring (48 / 72 KB of LDS: three / two workgroups per CU) or, at 64 x 256,
+    // two stages in 80 KB (two per CU).  M/64 tiles fill the chip without a
+    // split-K pass.  B may be [N][K] or, read with the transposing LDS loads,
+    // [K][N] as stored (a rank-r LoRA B needs no transposed copy).
     constexpr int NS = BN == 256 ? 2 : 3;
     constexpr int WPE_N = BN == 64 ? 3 : 2;
-    gemm_dma_kernel<BM, BN, WM, WN, BMODE, EPI, 64, NS, false, WPE_N><<<grid, WM * WN * 64, 0, s>>>(a);
+    gemm_dma_kernel<BM, BN, WM, WN, BMODE, EPI, 64, NS, false, WPE_N, false, BL == ROW>
+        <<<grid, WM * WN * 64, 0, s>>>(a);
   } else if constexpr (AL == COL && BL == ROW && BMODE == B_SINGLE && BM == 256 && BN == 256) {
     // both operands token-major (A^T B reduced over tokens): the LDS-DMA
     // engine with transposing fragment reads, 8 waves as above
@@ -90,22 +92,22 @@ static int launch_layout(int cfg, const GemmArgs& a, hipStream_t s) {
     case CFG_BIG: return launch_cfg<256, 256, 2, 2, AL, BL, BMODE, EPI>(a, s);
     case CFG_SKINNY_N:
       if constexpr (BMODE == B_SINGLE) {
-        if constexpr (AL == ROW && BL == COL) return launch_cfg<64, 64, 2, 2, AL, BL, BMODE, EPI>(a, s);
+        if constexpr (AL == ROW) return launch_cfg<64, 64, 2, 2, AL, BL, BMODE, EPI>(a, s);
         return launch_cfg<256, 32, 4, 1, AL, BL, BMODE, EPI>(a, s);
       }
       break;
     case CFG_NARROW_128:
-      if constexpr (BMODE == B_SINGLE && AL == ROW && BL == COL) return launch_cfg<64, 128, 2, 2, AL, BL, BMODE, EPI>(a, s);
+      if constexpr (BMODE == B_SINGLE && AL == ROW) return launch_cfg<64, 128, 2, 2, AL, BL, BMODE, EPI>(a, s);
       break;
     case CFG_NARROW_256:
-      if constexpr (BMODE == B_SINGLE && AL == ROW && BL == COL) return launch_cfg<64, 256, 2, 2, AL, BL, BMODE, EPI>(a, s);
+      if constexpr (BMODE == B_SINGLE && AL == ROW) return launch_cfg<64, 256, 2, 2, AL, BL, BMODE, EPI>(a, s);
       break;
     case CFG_SKINNY_M:
       if constexpr (BMODE == B_SINGLE) return launch_cfg<32, 256, 1, 4, AL, BL, BMODE, EPI>(a, s);
       break;
     case CFG_SKINNY_N64:
       if constexpr (BMODE == B_SINGLE) {
-        if constexpr (AL == ROW && BL == COL) return launch_cfg<64, 64, 2, 2, AL, BL, BMODE, EPI>(a, s);
+        if constexpr (AL == ROW) return launch_cfg<64, 64, 2, 2, AL, BL, BMODE, EPI>(a, s);
         if constexpr (AL == COL && BL == ROW) return launch_cfg<256, 64, 4, 1, AL, BL, BMODE, EPI>(a, s);
         return launch_cfg<256, 32, 4, 1, AL, BL, BMODE, EPI>(a, s);
       }
@@ -123,10 +125,11 @@ static int launch_epi(int cfg, int al, int bl, const GemmArgs& a, hipStream_t s)
   return forge_set_error(FORGE_ERR_INVALID, "gemm: layout");
 }
 
-// Picks a tile shape from the output shape (K-contiguous operands take the
-// 64 x 64 tiles up to N = 256).
+// Picks a tile shape from the output shape (a K-contiguous A takes the
+// 64-row narrow tiles up to N = 256).
 static int pick_cfg(int64_t M, int64_t N, int al, int bl) {
-  if (al == ROW && bl == COL && N <= 256 && M > N) return N <= 64 ? CFG_SKINNY_N64 : N <= 128 ? CFG_NARROW_128 : CFG_NARROW_256;
+  if (al == ROW && (bl == COL || bl == ROW) && N <= 256 && M > N)
+    return N <= 64 ? CFG_SKINNY_N64 : N <= 128 ? CFG_NARROW_128 : CFG_NARROW_256;
   if (N <= 32 && M > N) return CFG_SKINNY_N;
   if (N <= 64 && M > N) return CFG_SKINNY_N64;
   if (M <= 64 && N > M) return CFG_SKINNY_M;

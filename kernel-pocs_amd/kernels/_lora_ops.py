@@ -34,8 +34,8 @@ def ld(t: torch.Tensor) -> int:
 
 
 def skinny_split(M: int, N: int, K: int, k_contiguous: bool = True) -> int:
-    """Split-K factor for a skinny output.  K-contiguous operands run on
-    64-row tiles as wide as the output (64, 128 or 256 columns): with >= 256
+    """Split-K factor for a skinny output.  A K-contiguous A (k_contiguous)
+    runs on 64-row tiles as wide as the output (64, 128 or 256 columns): with >= 256
     of them (one per CU) no split is needed, the fp32 partial pass would only
     add traffic; fewer tiles split K towards ~512 workgroups.  Token-major
     operands run on 256 x 32 / 256 x 64 tiles, which alone give only M/256
@@ -63,7 +63,7 @@ def gemm(M: int, N: int, segs: Sequence[Tuple[torch.Tensor, int, torch.Tensor, i
     dev = device if device is not None else segs[0][0].device
     K = sum(int(k) for (_, _, _, _, k) in segs)
     if not atomic and beta == 0.0 and N <= 64 and M >= 1024 and (out is None or out.dtype == torch.bfloat16):
-        split = skinny_split(M, N, K, a_layout == ROW and b_layout == COL)
+        split = skinny_split(M, N, K, a_layout == ROW)
         if split > 1:
             if out is None:
                 out = torch.empty(M, N, dtype=torch.bfloat16, device=dev)
@@ -175,6 +175,16 @@ def frozen_t(w: torch.Tensor, pitch_multiple: int = 1) -> torch.Tensor:
 def small_t(a: torch.Tensor) -> torch.Tensor:
     """A^T contiguous for a rank-r LoRA matrix (r x features: a few hundred KB)."""
     return a.detach().t().contiguous()
+
+
+def times_b(x: torch.Tensor, ldx: int, b: torch.Tensor, k: int, out: Optional[torch.Tensor] = None,
+            alpha: float = 1.0) -> torch.Tensor:
+    """alpha * x @ b for a rank-r LoRA B [k, r] as stored: the narrow tile
+    reads it in place when r is a multiple of 8, else from a transposed copy."""
+    M, r = x.shape[0], b.shape[1]
+    if r % 8 == 0:
+        return gemm(M, r, [(x, ldx, b, ld(b), k)], ROW, ROW, out=out, alpha=alpha)
+    return gemm(M, r, [(x, ldx, small_t(b), k, k)], ROW, COL, out=out, alpha=alpha)
 
 
 def split_k_for(k: int, tiles: int, target_wgs: int = 512, min_tiles_per_split: int = 4) -> int:

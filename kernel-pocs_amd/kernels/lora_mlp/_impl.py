@@ -29,7 +29,7 @@ import torch
 import torch.nn.functional as F
 
 from forge_hip import _lib as L
-from kernels._lora_ops import COL, ROW, as_operand, frozen_t, gemm, grad_at_b, ld, lora_a, small_t
+from kernels._lora_ops import COL, ROW, as_operand, frozen_t, gemm, grad_at_b, ld, lora_a, small_t, times_b
 
 
 def _w(t):
@@ -95,7 +95,7 @@ def mlp_backward(dY2, X2, e, g, W_gate, A_gate, B_gate, s_gate, W_up, A_up, B_up
     Ag, Bg, Au, Bu, Ad, Bd = (_w(t) for t in (A_gate, B_gate, A_up, B_up, A_down, B_down))
 
     # 1-2: DW = dY Wd + sd (dY Bd) Ad with the SwiGLU backward fused in place
-    td = gemm(M, r, [(dY2, ld(dY2), small_t(Bd), H, H)], ROW, COL, alpha=s_down)
+    td = times_b(dY2, ld(dY2), Bd, H, alpha=s_down)
     h = torch.empty(M, I, dtype=torch.bfloat16, device=dev)
     # K-contiguous weights (cached W^T, small A^T) put the three big GEMMs of
     # the backward on the LDS-DMA engine; a rank that is not a multiple of 8
@@ -121,8 +121,8 @@ def mlp_backward(dY2, X2, e, g, W_gate, A_gate, B_gate, s_gate, W_up, A_up, B_up
 
     # 4: up / gate LoRA grads
     v = torch.empty(M, 2 * r, dtype=torch.bfloat16, device=dev)  # [su df Bu | sg de Bg]
-    gemm(M, r, [(df, I, small_t(Bu), I, I)], ROW, COL, out=v[:, :r], alpha=s_up)
-    gemm(M, r, [(de, I, small_t(Bg), I, I)], ROW, COL, out=v[:, r:], alpha=s_gate)
+    times_b(df, I, Bu, I, out=v[:, :r], alpha=s_up)
+    times_b(de, I, Bg, I, out=v[:, r:], alpha=s_gate)
     dA_ug = grad_at_b(v, 2 * r, X2, ld(X2), 2 * r, H, M, out_dtype=dt)  # [2r, H]: rows [dAu; dAg]
     if aux is not None and "xa" in aux:
         xa = aux["xa"]                                            # [sg X Ag^T | su X Au^T]

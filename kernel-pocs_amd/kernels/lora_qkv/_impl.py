@@ -25,7 +25,7 @@ from typing import Optional
 import torch
 
 from forge_hip import _lib as L
-from kernels._lora_ops import COL, ROW, as_operand, frozen_t, gemm, grad_at_b, ld, lora_a, small_t
+from kernels._lora_ops import COL, ROW, as_operand, frozen_t, gemm, grad_at_b, ld, lora_a, small_t, times_b
 
 
 def _w(t):
@@ -86,9 +86,9 @@ def qkv_backward(dQ, dK, dV, X2, W_q, W_k, W_v, A_q, B_q, s_q, A_k, B_k, s_k, A_
     dev = X2.device
     Aq, Bq, Ak, Bk, Av, Bv = (_w(t) for t in (A_q, B_q, A_k, B_k, A_v, B_v))
     t = torch.empty(M, 3 * r, dtype=torch.bfloat16, device=dev)
-    gemm(M, r, [(dQ, ld(dQ), small_t(Bq), Hq, Hq)], ROW, COL, out=t[:, :r], alpha=s_q)
-    gemm(M, r, [(dK, ld(dK), small_t(Bk), Hkv, Hkv)], ROW, COL, out=t[:, r:2 * r], alpha=s_k)
-    gemm(M, r, [(dV, ld(dV), small_t(Bv), Hkv, Hkv)], ROW, COL, out=t[:, 2 * r:], alpha=s_v)
+    times_b(dQ, ld(dQ), Bq, Hq, out=t[:, :r], alpha=s_q)
+    times_b(dK, ld(dK), Bk, Hkv, out=t[:, r:2 * r], alpha=s_k)
+    times_b(dV, ld(dV), Bv, Hkv, out=t[:, 2 * r:], alpha=s_v)
     dt = A_q.dtype
     dA = grad_at_b(t, 3 * r, X2, ld(X2), 3 * r, K, M, out_dtype=dt)  # [3r, K] (scales included via t)
     if aux is not None and "xa" in aux:
