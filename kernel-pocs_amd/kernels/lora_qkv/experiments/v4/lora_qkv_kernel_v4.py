@@ -102,6 +102,31 @@ def _rope_rows_backward(d, n_heads, head_dim, cos, sin, positions):
     return out
 
 
+def _rope_qk_backward(dQ, dK, head_dim, cos, sin, positions):
+    """Rotates the [M, Hq] and [M, Hkv] gradients (any row pitches) by -theta
+    per token in one forge_rope launch (GQA: Hq/D a multiple of Hkv/D);
+    returns new contiguous tensors."""
+    nq, nk = dQ.shape[1] // head_dim, dK.shape[1] // head_dim
+    if nk == 0 or nq % nk != 0:
+        return (_rope_rows_backward(dQ, nq, head_dim, cos, sin, positions),
+                _rope_rows_backward(dK, nk, head_dim, cos, sin, positions))
+    M = dQ.shape[0]
+    oq = torch.empty(M, nq * head_dim, dtype=dQ.dtype, device=dQ.device)
+    ok = torch.empty(M, nk * head_dim, dtype=dK.dtype, device=dK.device)
+    L.check(
+        L.forge_rope(L.dtype_code(dQ.dtype),
+                     dQ.data_ptr(), 0, head_dim, dQ.stride(0),
+                     dK.data_ptr(), 0, head_dim, dK.stride(0),
+                     oq.data_ptr(), 0, head_dim, nq * head_dim,
+                     ok.data_ptr(), 0, head_dim, nk * head_dim,
+                     cos.data_ptr(), 0, cos.stride(0), sin.data_ptr(), 0, sin.stride(0),
+                     positions.data_ptr() if positions is not None else None,
+                     1, nq, nk, M, head_dim, 1, L.stream_of(dQ)),
+        "forge_rope(backward)",
+    )
+    return oq, ok
+
+
 class LoRAQKVRoPEFunction(torch.autograd.Function):
     """LoRA-QKV with RoPE fused into the GEMM epilogue.
 
@@ -137,8 +162,7 @@ class LoRAQKVRoPEFunction(torch.autograd.Function):
         dQ2, dK2 = _flat(dQ), _flat(dK)
         dQ2 = dQ2 if dQ2.stride(-1) == 1 else dQ2.contiguous()
         dK2 = dK2 if dK2.stride(-1) == 1 else dK2.contiguous()
-        dQu = _rope_rows_backward(dQ2, dQ2.shape[1] // D, D, cos2, sin2, pos)
-        dKu = _rope_rows_backward(dK2, dK2.shape[1] // D, D, cos2, sin2, pos)
+        dQu, dKu = _rope_qk_backward(dQ2, dK2, D, cos2, sin2, pos)
         dX, dAq, dBq, dAk, dBk, dAv, dBv = qkv_backward(dQu, dKu, _flat(dV), _flat(X), W_q, W_k, W_v,
                                                         A_q, B_q, s_q, A_k, B_k, s_k, A_v, B_v, s_v,
                                                         aux=ctx.lora_aux)
