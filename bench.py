@@ -43,7 +43,7 @@ def _parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--kernels", default="swiglu,rope,ce,lora_mlp,lora_qkv,flce,geglu,rmsnorm")
+    ap.add_argument("--kernels", default="swiglu,rope,ce,lora_mlp,lora_qkv,flce,geglu,rmsnorm,lora_patch")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--only-launches", action="store_true",
                     help="run only the dominant-kernel launch loop (for rocprofv3 counter runs)")
@@ -354,6 +354,27 @@ def _gpu_params_mlp(H, I, r, alpha, gen):
     return (W(I, H), A(H), B(I), s, W(I, H), A(H), B(I), s, W(H, I), A(I), B(H), s)
 
 
+def _gate_up_roofline(args, X2, Wg, Wu, Bg, Bu, r):
+    """(mean launch ms, roofline) of the LoRA-MLP's dominant kernel, the fused
+    gate/up GEMM + SwiGLU epilogue (forge_lora_mlp_gate_up), on X2 [M, H]."""
+    import torch
+    from forge_hip import _lib as L
+
+    M, H = X2.shape
+    I = Wg.shape[0]
+    xa = torch.randn(M, 2 * r, device="cuda").to(torch.bfloat16)
+    e = torch.empty(M, I, device="cuda", dtype=torch.bfloat16)
+    gg, hh = torch.empty_like(e), torch.empty_like(e)
+    st = L.stream_of(X2)
+    launch_ms = time_launches(lambda i: L.forge_lora_mlp_gate_up(
+        M, H, I, r, X2.data_ptr(), X2.stride(0), Wg.data_ptr(), Wu.data_ptr(), Wg.stride(0), xa.data_ptr(), 2 * r,
+        Bg.data_ptr(), Bu.data_ptr(), Bg.stride(0), e.data_ptr(), gg.data_ptr(), hh.data_ptr(), I, st),
+        max(args.steps, 10))
+    gu_flops = 4 * M * H * I + 4 * M * r * I
+    return launch_ms, _roof("mfma", gu_flops / (launch_ms * 1e-3) / 1e12, BF16_PEAK_TFLOPS, "TFLOP/s",
+                            _traffic("lora_mlp_gate_up"))
+
+
 def bench_lora_mlp(args):
     """LoRA MLP fwd+bwd, bf16, Llama-3-8B shape (M=8192, H=4096,
     I=14336), r=16, alpha=32."""
@@ -381,24 +402,15 @@ def bench_lora_mlp(args):
     fl = flops(M, H, I, r)
     tf = rate(fl, ms, 1e12)
     # dominant kernel: the fused gate/up GEMM + SwiGLU epilogue
-    X2 = X.detach().reshape(M, H)
     Wg, Ag, Bg, sg, Wu, Au, Bu, su = [t.detach() if isinstance(t, torch.Tensor) else t for t in params[:8]]
-    xa = torch.randn(M, 2 * r, device="cuda").to(torch.bfloat16)
-    e = torch.empty(M, I, device="cuda", dtype=torch.bfloat16)
-    gg, hh = torch.empty_like(e), torch.empty_like(e)
-    st = L.stream_of(X2)
-    launch_ms = time_launches(lambda i: L.forge_lora_mlp_gate_up(
-        M, H, I, r, X2.data_ptr(), H, Wg.data_ptr(), Wu.data_ptr(), H, xa.data_ptr(), 2 * r, Bg.data_ptr(),
-        Bu.data_ptr(), r, e.data_ptr(), gg.data_ptr(), hh.data_ptr(), I, st), max(args.steps, 10))
-    gu_flops = 4 * M * H * I + 4 * M * r * I
+    launch_ms, roof = _gate_up_roofline(args, X.detach().reshape(M, H), Wg, Wu, Bg, Bu, r)
     res = {
         "config": {"workload": "lora_mlp_fwd_bwd", "dtype": "bf16", "M": M, "H": H, "I": I, "rank": r, "alpha": 32,
                    "api": "LoRAMLPv6"},
         "value": tf, "unit": "TFLOP/s", "ms_per_step": rnd(ms, 4), "wall_ms_per_step": rnd(wall, 4),
         "frac_of_mfma_peak": rnd(tf and tf / BF16_PEAK_TFLOPS, 4), "algorithmic_flops_per_step": fl,
         "launches_ms": {"forge_lora_mlp_gate_up": round(launch_ms, 4)},
-        "roofline": _roof("mfma", gu_flops / (launch_ms * 1e-3) / 1e12, BF16_PEAK_TFLOPS, "TFLOP/s",
-                          _traffic("lora_mlp_gate_up")),
+        "roofline": roof,
         "dtype": "bf16",
     }
     if not (args.no_cpu_baseline or args.only_launches):
@@ -411,6 +423,106 @@ def bench_lora_mlp(args):
         res["cpu_baseline"] = _cpu(flops(ms_, H, I, r) / t / 1e12, "TFLOP/s",
                                    f"{ms_} of {M} tokens, reference LoRAMLP formulas in bf16, fwd+bwd, median of {reps}")
     return res
+
+
+class _PeftLayoutLoRA:
+    """Builds an nn.Module with peft.tuners.lora.Linear's attributes and
+    forward (base_layer, lora_A / lora_B ModuleDicts, scaling, lora_dropout,
+    active_adapters; base(x) + lora_B(lora_A(x)) * scaling): peft itself is
+    not installed on these boxes."""
+
+    @staticmethod
+    def wrap(base, r, alpha, gen):
+        import torch
+        import torch.nn as nn
+
+        class LoraLinear(nn.Module):
+            def __init__(self):
+                super().__init__()
+                self.base_layer = base
+                dev, dt = base.weight.device, base.weight.dtype
+                self.lora_A = nn.ModuleDict({"default": nn.Linear(base.in_features, r, bias=False, device=dev, dtype=dt)})
+                self.lora_B = nn.ModuleDict({"default": nn.Linear(r, base.out_features, bias=False, device=dev, dtype=dt)})
+                with torch.no_grad():
+                    self.lora_A["default"].weight.copy_(torch.randn(r, base.in_features, generator=gen, device=dev)
+                                                        / base.in_features ** 0.5)
+                    self.lora_B["default"].weight.copy_(torch.randn(base.out_features, r, generator=gen, device=dev)
+                                                        * 0.01)
+                self.lora_dropout = nn.ModuleDict({"default": nn.Identity()})
+                self.scaling = {"default": alpha / r}
+                self.active_adapters = ["default"]
+                self.disable_adapters = False
+                self.merged = False
+                base.weight.requires_grad_(False)
+
+            def forward(self, x):
+                a, b = self.lora_A["default"], self.lora_B["default"]
+                return self.base_layer(x) + b(a(x)) * self.scaling["default"]
+
+        return LoraLinear()
+
+
+def bench_lora_patch(args):
+    """The patch-layer adapter (forge/patching/kernels/lora.py) on Hugging
+    Face's LlamaMLP at the LoRA-MLP config (M=8192, H=4096, I=14336, r=16,
+    alpha=32), PEFT-layout LoRA on gate/up/down, fwd+bwd: the fused adapter
+    against the reference adapter's submodule path (PEFT projections on
+    hipBLASLt GEMMs + the SwiGLU kernel) on the same module and inputs."""
+    import copy
+
+    import torch
+
+    try:
+        from transformers import LlamaConfig
+        import transformers.models.llama.modeling_llama as ML
+    except ImportError:
+        return {"skipped": "transformers is not installed", "value": None, "unit": "TFLOP/s"}
+    from forge.patching import FORWARD_MAKERS
+    from forge.kernels.swiglu import swiglu
+    from oracle.lora_mlp import flops
+
+    M, H, I, r = 8192, 4096, 14336, 16
+    g = torch.Generator(device="cuda").manual_seed(9)
+    torch.manual_seed(9)
+    cfg = LlamaConfig(hidden_size=H, intermediate_size=I, num_attention_heads=32, num_key_value_heads=8, head_dim=128)
+    ref = ML.LlamaMLP(cfg).to("cuda", torch.bfloat16)
+    for n in ("gate_proj", "up_proj", "down_proj"):
+        setattr(ref, n, _PeftLayoutLoRA.wrap(getattr(ref, n), r, 32, g))
+    fused = copy.deepcopy(ref)
+    fused.forward = FORWARD_MAKERS["lora_mlp"](fused, {})
+    # the reference adapter's call path (lora.py:160-163): PEFT submodules + swiglu
+    ref.forward = lambda x: ref.down_proj(swiglu(ref.gate_proj(x), ref.up_proj(x)))
+    X = torch.randn(1, M, H, device="cuda", generator=g).to(torch.bfloat16).requires_grad_(True)
+    dY = torch.randn(1, M, H, device="cuda", generator=g).to(torch.bfloat16)
+
+    def stepper(mod):
+        leaves = [X] + [p for p in mod.parameters() if p.requires_grad]
+
+        def step(i):
+            for t in leaves:
+                t.grad = None
+            mod(X).backward(dY)
+        return step
+
+    ms, wall = run_steps(args, stepper(fused))
+    ms_ref, _ = run_steps(args, stepper(ref))
+    fl = flops(M, H, I, r)
+    tf, tf_ref = rate(fl, ms, 1e12), rate(fl, ms_ref, 1e12)
+    w = [getattr(ref, n).base_layer.weight.detach() for n in ("gate_proj", "up_proj")]
+    b = [getattr(ref, n).lora_B["default"].weight.detach() for n in ("gate_proj", "up_proj")]
+    launch_ms, roof = _gate_up_roofline(args, X.detach().reshape(M, H), w[0], w[1], b[0], b[1], r)
+    return {
+        "config": {"workload": "lora_mlp_patch_fwd_bwd", "dtype": "bf16", "M": M, "H": H, "I": I, "rank": r,
+                   "alpha": 32, "module": "transformers LlamaMLP, PEFT-layout LoRA on gate/up/down",
+                   "api": "forge.patching FORWARD_MAKERS['lora_mlp']"},
+        "value": tf, "unit": "TFLOP/s", "ms_per_step": rnd(ms, 4), "wall_ms_per_step": rnd(wall, 4),
+        "frac_of_mfma_peak": rnd(tf and tf / BF16_PEAK_TFLOPS, 4), "algorithmic_flops_per_step": fl,
+        "reference_submodule_path": {"value": tf_ref, "unit": "TFLOP/s", "ms_per_step": rnd(ms_ref, 4)},
+        "speedup_vs_submodule_path": rnd(ms and ms_ref / ms, 3),
+        "launches_ms": {"forge_lora_mlp_gate_up": round(launch_ms, 4)},
+        "roofline": roof,
+        "dtype": "bf16",
+    }
 
 
 def bench_lora_qkv(args):
@@ -712,7 +824,7 @@ def bench_rmsnorm(args):
 
 BENCHES = {"copy": bench_copy, "swiglu": bench_swiglu, "rope": bench_rope, "ce": bench_ce, "lora_mlp": bench_lora_mlp,
            "lora_qkv": bench_lora_qkv, "flce": bench_flce, "geglu": bench_geglu,
-           "rmsnorm": bench_rmsnorm}
+           "rmsnorm": bench_rmsnorm, "lora_patch": bench_lora_patch}
 
 
 def main():
@@ -738,7 +850,10 @@ def main():
         results[n] = fn(args)
         torch.cuda.empty_cache()
         print(f"[bench] {n}: {results[n]['value']} {results[n]['unit']}", file=sys.stderr, flush=True)
-    head = results.get("rope") or next(iter(results.values()))
+    head = results.get("rope") or next((r for r in results.values() if r.get("roofline")), None)
+    if head is None:
+        print(json.dumps({"error": "no timed workload", "kernels": results}))
+        return 1
     line = {
         "metric": METRIC,
         "value": head["value"],
