@@ -368,7 +368,7 @@ def _gate_up_roofline(args, X2, Wg, Wu, Bg, Bu, r):
     st = L.stream_of(X2)
     launch_ms = time_launches(lambda i: L.forge_lora_mlp_gate_up(
         M, H, I, r, X2.data_ptr(), X2.stride(0), Wg.data_ptr(), Wu.data_ptr(), Wg.stride(0), xa.data_ptr(), 2 * r,
-        Bg.data_ptr(), Bu.data_ptr(), Bg.stride(0), e.data_ptr(), gg.data_ptr(), hh.data_ptr(), I, st),
+        Bg.data_ptr(), Bu.data_ptr(), Bg.stride(0), e.data_ptr(), gg.data_ptr(), hh.data_ptr(), I, L.ACT_SILU, st),
         max(args.steps, 10))
     gu_flops = 4 * M * H * I + 4 * M * r * I
     return launch_ms, _roof("mfma", gu_flops / (launch_ms * 1e-3) / 1e12, BF16_PEAK_TFLOPS, "TFLOP/s",

@@ -285,37 +285,55 @@ int forge_gemm(int64_t M, int64_t N, const forge_gemm_segment* segs, int n_segs,
  * Fused LoRA entry points (bf16 storage, fp32 accumulation)
  * ------------------------------------------------------------------------ */
 
-/* LoRA-MLP forward, gate and up projections with the SwiGLU epilogue:
- *   e = X Wg^T + xa[:, :r] Bg^T,  g = X Wu^T + xa[:, r:2r] Bu^T,  h = silu(e) g
+/* Gated activation of the fused LoRA-MLP entry points. */
+enum {
+  FORGE_ACT_SILU = 0,       /* SwiGLU: h = silu(e) g */
+  FORGE_ACT_GELU_TANH = 1,  /* GeGLU, tanh-approximate GELU */
+  FORGE_ACT_GELU_ERF = 2,   /* GeGLU, exact (erf) GELU */
+};
+
+/* LoRA-MLP forward, gate and up projections with the gated-activation epilogue:
+ *   e = X Wg^T + xa[:, :r] Bg^T,  g = X Wu^T + xa[:, r:2r] Bu^T,
+ *   h = silu(e) g                        (FORGE_ACT_SILU, on the fp32 e, g)
+ *   h = round(gelu(round(e))) round(g)   (FORGE_ACT_GELU_*: forge_geglu_fwd on
+ *                                         the stored bf16 e, g)
  * X [M, H] (row pitch ldx), Wg/Wu [I, H] (pitch ldw), xa [M, 2r] holding
  * (sg X Ag^T | su X Au^T) (pitch ld_xa; NULL or r = 0 disables LoRA),
  * Bg/Bu [I, r] (pitch ldb).  Writes e, g, h [M, I] (pitch ld_out).
- * Replaces phases 1-3 of `_v6_forward_impl`
+ * SiLU replaces phases 1-3 of `_v6_forward_impl`
  * (kernels/lora_mlp/experiments/v6/lora_mlp_kernel_v6.py:373-415: two cuBLAS
- * GEMMs + `_fused_lora_swiglu_kernel`, experiments/v3/lora_mlp_kernel_v3.py:45-138). */
+ * GEMMs + `_fused_lora_swiglu_kernel`, experiments/v3/lora_mlp_kernel_v3.py:45-138);
+ * GELU replaces the Gemma path's gate_proj(x), up_proj(x) and geglu(gate, up)
+ * (forge/forge/patching/kernels/lora.py:184-188 with
+ * kernels/geglu/geglu.py:126-148). */
 int forge_lora_mlp_gate_up(int64_t M, int64_t H, int64_t I, int64_t r,
                            const void* x, int64_t ldx,
                            const void* w_gate, const void* w_up, int64_t ldw,
                            const void* xa, int64_t ld_xa,
                            const void* b_gate, const void* b_up, int64_t ldb,
-                           void* e, void* g, void* h, int64_t ld_out, void* stream);
+                           void* e, void* g, void* h, int64_t ld_out, int activation, void* stream);
 
-/* LoRA-MLP backward through the down projection and SwiGLU:
+/* LoRA-MLP backward through the down projection and the gated activation:
  *   DW = dY Wd + t Ad   (dY [M, H], Wd [H, I], t = sd dY Bd [M, r], Ad [r, I])
- *   then in place: h_out = silu(e) g,  e <- df = DW silu(e),
- *                  g <- de = DW g sig(e) (1 + e (1 - sig(e)))
+ *   then in place, with D = round(DW):
+ *   FORGE_ACT_SILU:   f = round(silu(e)), h_out = f g, e <- D f,
+ *                     g <- round(D g) sig(e) (1 + e (1 - sig(e)))
+ *   FORGE_ACT_GELU_*: a = round(gelu(e)), h_out = a g, e <- D a (d up),
+ *                     g <- D g gelu'(e) (d gate): forge_geglu_bwd with dout = D
  * w_layout FORGE_LAYOUT_ROW: w_down = Wd [H, I], a_down = Ad [r, I];
  * FORGE_LAYOUT_COL: w_down = Wd^T [I, H], a_down = Ad^T [I, r] (K-contiguous,
  * the faster engine; callers with frozen weights keep the transpose).
- * Replaces `matmul_lora(dY, W_down^T, ...)` + `_DWf_DW_dfg_kernel`
+ * SiLU replaces `matmul_lora(dY, W_down^T, ...)` + `_DWf_DW_dfg_kernel`
  * (kernels/lora_mlp/experiments/v6/lora_mlp_kernel_v6.py:632-634;
- * kernels/lora_mlp/reference/unsloth_baseline.py:34-55, 118-168). */
+ * kernels/lora_mlp/reference/unsloth_baseline.py:34-55, 118-168); GELU
+ * replaces the backward of down_proj and geglu on the Gemma path
+ * (forge/forge/patching/kernels/lora.py:186-188, kernels/geglu/geglu.py:151-182). */
 int forge_lora_mlp_down_bwd(int64_t M, int64_t H, int64_t I, int64_t r,
                             const void* dy, int64_t lddy,
                             const void* w_down, int64_t ldwd,
                             const void* t_d, int64_t ld_t,
                             const void* a_down, int64_t ld_ad, int w_layout,
-                            void* h_out, void* e_df, void* g_de, int64_t ld, void* stream);
+                            void* h_out, void* e_df, void* g_de, int64_t ld, int activation, void* stream);
 
 /* LoRA-QKV forward with GQA-asymmetric widths and optional fused RoPE:
  *   out[:, 0:hq]          = X Wq^T + xa[:, 0:r]   Bq^T   (rotated if apply_rope)

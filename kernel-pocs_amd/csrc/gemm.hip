@@ -1,6 +1,6 @@
 // Host launchers for the MFMA GEMM core: the generic forge_gemm entry point
-// and the fused LoRA entry points (LoRA-MLP gate/up + SwiGLU, LoRA-MLP
-// down-projection backward + SwiGLU backward, LoRA-QKV + RoPE).
+// and the fused LoRA entry points (LoRA-MLP gate/up + SwiGLU / GeGLU, LoRA-MLP
+// down-projection backward + SwiGLU / GeGLU backward, LoRA-QKV + RoPE).
 #include "gemm_core.h"
 
 namespace fgemm {
@@ -125,6 +125,20 @@ static int launch_epi(int cfg, int al, int bl, const GemmArgs& a, hipStream_t s)
   return forge_set_error(FORGE_ERR_INVALID, "gemm: layout");
 }
 
+// GLU epilogues (SwiGLU / GeGLU, forward and backward) on 256 x 256 tiles:
+// the forward reads the gate and up weights as one dual B (both [N][K]); the
+// backward's W_down may be [K][N] or [N][K].
+template <int EPI>
+static int launch_glu(int al, int bl, const GemmArgs& a, hipStream_t s) {
+  if constexpr (glu_fwd_epi(EPI)) {
+    if (al == ROW && bl == COL) return launch_cfg<256, 256, 2, 2, ROW, COL, B_DUAL, EPI>(a, s);
+  } else {
+    if (al == ROW && bl == ROW) return launch_cfg<256, 256, 2, 2, ROW, ROW, B_SINGLE, EPI>(a, s);
+    if (al == ROW && bl == COL) return launch_cfg<256, 256, 2, 2, ROW, COL, B_SINGLE, EPI>(a, s);
+  }
+  return forge_set_error(FORGE_ERR_UNSUPPORTED, "gemm: epilogue %d with layouts (%d, %d)", EPI, al, bl);
+}
+
 // Picks a tile shape from the output shape (a K-contiguous A takes the
 // 64-row narrow tiles up to N = 256).
 static int pick_cfg(int64_t M, int64_t N, int al, int bl) {
@@ -178,13 +192,12 @@ int run(int cfg, int al, int bl, int epi, const GemmArgs& args, hipStream_t s) {
     case EPI_STORE_BF16: return launch_epi<EPI_STORE_BF16>(cfg, al, bl, a, s);
     case EPI_STORE_F32: return launch_epi<EPI_STORE_F32>(cfg, al, bl, a, s);
     case EPI_ATOMIC_F32: return launch_epi<EPI_ATOMIC_F32>(cfg, al, bl, a, s);
-    case EPI_SWIGLU_BWD:
-      if (al == ROW && bl == ROW) return launch_layout<ROW, ROW, B_SINGLE, EPI_SWIGLU_BWD>(CFG_BIG, a, s);
-      if (al == ROW && bl == COL) return launch_layout<ROW, COL, B_SINGLE, EPI_SWIGLU_BWD>(CFG_BIG, a, s);
-      break;
-    case EPI_SWIGLU_FWD:
-      if (al == ROW && bl == COL) return launch_layout<ROW, COL, B_DUAL, EPI_SWIGLU_FWD>(CFG_BIG, a, s);
-      break;
+    case EPI_SWIGLU_FWD: return launch_glu<EPI_SWIGLU_FWD>(al, bl, a, s);
+    case EPI_SWIGLU_BWD: return launch_glu<EPI_SWIGLU_BWD>(al, bl, a, s);
+    case EPI_GEGLU_TANH_FWD: return launch_glu<EPI_GEGLU_TANH_FWD>(al, bl, a, s);
+    case EPI_GEGLU_TANH_BWD: return launch_glu<EPI_GEGLU_TANH_BWD>(al, bl, a, s);
+    case EPI_GEGLU_ERF_FWD: return launch_glu<EPI_GEGLU_ERF_FWD>(al, bl, a, s);
+    case EPI_GEGLU_ERF_BWD: return launch_glu<EPI_GEGLU_ERF_BWD>(al, bl, a, s);
     case EPI_ROPE:
       if (al == ROW && bl == COL) return launch_layout<ROW, COL, B_SINGLE, EPI_ROPE>(CFG_BIG, a, s);
       break;

@@ -38,6 +38,7 @@
 #include <type_traits>
 
 #include "common.h"
+#include "gelu.h"
 
 namespace fgemm {
 
@@ -74,7 +75,20 @@ enum Epi {
   EPI_SWIGLU_FWD = 3,   // dual: e, g, h = silu(e) * g
   EPI_SWIGLU_BWD = 4,   // DW: (DW, e, g) -> (h, df, de) in place
   EPI_ROPE = 5,         // QKV: rotate columns < rope_cols per head, store bf16
+  EPI_GEGLU_TANH_FWD = 6,  // dual: e, g, h = gelu_tanh(e) * g
+  EPI_GEGLU_TANH_BWD = 7,  // DW: (DW, e, g) -> (h, dup, dgate) in place
+  EPI_GEGLU_ERF_FWD = 8,   // as 6 with the exact (erf) GELU
+  EPI_GEGLU_ERF_BWD = 9,   // as 7 with the exact (erf) GELU
 };
+
+// Gated-linear-unit epilogues: forward (dual-B gate/up GEMM) and backward
+// (the DW = dY W_down GEMM, in place over the saved e / g).
+constexpr bool glu_fwd_epi(int epi) {
+  return epi == EPI_SWIGLU_FWD || epi == EPI_GEGLU_TANH_FWD || epi == EPI_GEGLU_ERF_FWD;
+}
+constexpr bool glu_bwd_epi(int epi) {
+  return epi == EPI_SWIGLU_BWD || epi == EPI_GEGLU_TANH_BWD || epi == EPI_GEGLU_ERF_BWD;
+}
 
 struct EpiArgs {
   void* c;
@@ -84,8 +98,8 @@ struct EpiArgs {
   // [g*alpha_group, (g+1)*alpha_group) use alphas[g] (alpha_group 0 = off)
   int64_t alpha_group;
   float alphas[4];
-  __bf16* e;   // SWIGLU: e buffer; SWIGLU_BWD: e in / df out
-  __bf16* g;   // SWIGLU: g buffer; SWIGLU_BWD: g in / de out
+  __bf16* e;   // GLU forward: e buffer; GLU backward: e in / d(up) out
+  __bf16* g;   // GLU forward: g buffer; GLU backward: g in / d(gate) out
   int64_t ld_eg;
   const __bf16* cos;
   const __bf16* sin;
@@ -281,6 +295,50 @@ __device__ __forceinline__ float sigmoid_f(float x) { return __builtin_amdgcn_rc
 __device__ __forceinline__ float silu_f(float x) { return x * sigmoid_f(x); }
 __device__ __forceinline__ float bf16r(float x) { return (float)(__bf16)x; }
 
+// h (before its bf16 rounding) of a GLU forward epilogue from the fp32
+// accumulators e (gate) and g (up).
+//  * SwiGLU: silu(e) g on the fp32 values (lora_mlp_kernel_v6.py:81-151);
+//  * GeGLU: the GeGLU kernel's forward on the bf16 e and g that are stored
+//    for the backward, round(gelu(e)) g (geglu.py:126-148), so h is what the
+//    standalone GeGLU gives on those tensors.
+template <int EPI>
+__device__ __forceinline__ float glu_fwd_h(float e, float g) {
+  if constexpr (EPI == EPI_SWIGLU_FWD) {
+    return silu_f(e) * g;
+  } else {
+    float a, d;
+    fgelu::gelu_and_grad<EPI == EPI_GEGLU_TANH_FWD>(bf16r(e), a, d);
+    return bf16r(a) * bf16r(g);
+  }
+}
+
+// GLU backward on one element: acc = DW (fp32), e / g the saved bf16 values;
+// returns h (recomputed for the down-projection gradients), du = d(up) and
+// dgt = d(gate), each before its bf16 rounding.
+//  * SwiGLU, Unsloth-style (lora_mlp_kernel_v6.py:592-672):
+//      f = round(silu(e)), h = f g, du = DW f, dgt = round(DW g) sig (1 + e (1 - sig));
+//  * GeGLU, the GeGLU kernel's backward with dout = round(DW) (geglu.py:151-182):
+//      a = round(gelu(e)), h = a g, du = DW a, dgt = DW g gelu'(e).
+template <int EPI>
+__device__ __forceinline__ void glu_bwd_vals(float acc, float e, float g, float& h, float& du, float& dgt) {
+  const float dw = bf16r(acc);
+  if constexpr (EPI == EPI_SWIGLU_BWD) {
+    const float se = sigmoid_f(e);
+    const float f = bf16r(se * e);
+    h = f * g;
+    du = dw * f;
+    const float dg = bf16r(dw * g);
+    dgt = dg * se * (1.0f + e * (1.0f - se));
+  } else {
+    float a, d;
+    fgelu::gelu_and_grad<EPI == EPI_GEGLU_TANH_BWD>(e, a, d);
+    const float ar = bf16r(a);
+    h = ar * g;
+    du = dw * ar;
+    dgt = dw * g * d;
+  }
+}
+
 // XCD-aware tile order: consecutive workgroup ids land on different XCDs
 // (round-robin dispatch), so ids are regrouped so that each XCD walks a
 // contiguous range of the tile order; within it, tiles go in groups of
@@ -341,7 +399,7 @@ __device__ __forceinline__ uint4 pack8(const float (&f)[8]) {
 // Tiles and epilogues the staged epilogue serves.
 constexpr bool staged_ok(int bm, int bn, int wm, int wn, int epi) {
   return bm == 256 && bn == 256 && (256 / wm) % 32 == 0 && (256 / wn) % 32 == 0 && 256 / wm <= 128 &&
-         (epi == EPI_STORE_BF16 || epi == EPI_STORE_F32 || epi == EPI_SWIGLU_FWD || epi == EPI_SWIGLU_BWD ||
+         (epi == EPI_STORE_BF16 || epi == EPI_STORE_F32 || glu_fwd_epi(epi) || glu_bwd_epi(epi) ||
           epi == EPI_ROPE);
 }
 
@@ -398,7 +456,7 @@ __device__ __forceinline__ void epilogue_staged(const GemmArgs& args,
         const float* pg = lds + rr * P + lc;
         float e[8], g[8], h[8];
 #pragma unroll
-        for (int q = 0; q < 8; ++q) { e[q] = pg[q]; g[q] = pg[32 + q]; h[q] = silu_f(e[q]) * g[q]; }
+        for (int q = 0; q < 8; ++q) { e[q] = pg[q]; g[q] = pg[32 + q]; h[q] = glu_fwd_h<EPI>(e[q], g[q]); }
         const int64_t off = m * ep.ld_eg + n;
         if (n + 8 <= N) {
           st16(ep.e + off, pack8(e));
@@ -475,7 +533,7 @@ __device__ __forceinline__ void epilogue_staged(const GemmArgs& args,
               cp[q] = (__bf16)o;
             }
           }
-        } else if constexpr (EPI == EPI_SWIGLU_BWD) {
+        } else if constexpr (glu_bwd_epi(EPI)) {
           const int64_t off = m * ep.ld_eg + n;
           float ev[8], gv[8], hv[8], dfv[8], dev[8];
           if (full) {
@@ -488,16 +546,7 @@ __device__ __forceinline__ void epilogue_staged(const GemmArgs& args,
             }
           }
 #pragma unroll
-          for (int q = 0; q < 8; ++q) {
-            const float dw = bf16r(v[q]);
-            const float e = ev[q], g = gv[q];
-            const float se = sigmoid_f(e);
-            const float f = bf16r(se * e);
-            hv[q] = f * g;
-            dfv[q] = dw * f;
-            const float dg = bf16r(dw * g);
-            dev[q] = dg * se * (1.0f + e * (1.0f - se));
-          }
+          for (int q = 0; q < 8; ++q) glu_bwd_vals<EPI>(v[q], ev[q], gv[q], hv[q], dfv[q], dev[q]);
           if (full) {
             st16((__bf16*)ep.c + m * ep.ldc + n, pack8(hv));
             st16(ep.e + off, pack8(dfv));
@@ -580,7 +629,7 @@ __device__ __forceinline__ void epilogue(const GemmArgs& args, f32x16 (&acc)[BM 
         }
       }
     }
-  } else if constexpr (EPI == EPI_SWIGLU_FWD) {
+  } else if constexpr (glu_fwd_epi(EPI)) {
     // wave tiles (0,1) and (2,3) are (gate, up) pairs for 32 output columns each
 #pragma unroll
     for (int jp = 0; jp < FN / 2; ++jp) {
@@ -597,13 +646,12 @@ __device__ __forceinline__ void epilogue(const GemmArgs& args, f32x16 (&acc)[BM 
           const int64_t off = m * ep.ld_eg + n;
           ep.e[off] = (__bf16)e;
           ep.g[off] = (__bf16)g;
-          ((__bf16*)ep.c)[m * ep.ldc + n] = (__bf16)(silu_f(e) * g);
+          ((__bf16*)ep.c)[m * ep.ldc + n] = (__bf16)glu_fwd_h<EPI>(e, g);
         }
       }
     }
-  } else if constexpr (EPI == EPI_SWIGLU_BWD) {
-    // Unsloth-style in-place SwiGLU backward on the DW = dY @ W_down tile:
-    //   f = silu(e) -> bf16, h = f*g, df = DW*f, de = (DW*g) * sig*(1 + e*(1-sig))
+  } else if constexpr (glu_bwd_epi(EPI)) {
+    // in-place GLU backward on the DW = dY @ W_down tile (glu_bwd_vals)
 #pragma unroll
     for (int j = 0; j < FN; ++j) {
       const int64_t n = n0 + wn * TN + j * 32 + col_in;
@@ -615,15 +663,8 @@ __device__ __forceinline__ void epilogue(const GemmArgs& args, f32x16 (&acc)[BM 
           const int64_t m = row_base + i * 32 + 8 * (r / 4) + (r % 4);
           if (m >= M) continue;
           const int64_t off = m * ep.ld_eg + n;
-          const float dw = bf16r(acc[i][j][r]);
-          const float e = (float)ep.e[off];
-          const float g = (float)ep.g[off];
-          const float se = sigmoid_f(e);
-          const float f = bf16r(se * e);
-          const float h = f * g;
-          const float df = dw * f;
-          const float dg = bf16r(dw * g);
-          const float de = dg * se * (1.0f + e * (1.0f - se));
+          float h, df, de;
+          glu_bwd_vals<EPI>(acc[i][j][r], (float)ep.e[off], (float)ep.g[off], h, df, de);
           ((__bf16*)ep.c)[m * ep.ldc + n] = (__bf16)h;
           ep.e[off] = (__bf16)df;
           ep.g[off] = (__bf16)de;

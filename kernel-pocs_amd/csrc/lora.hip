@@ -7,6 +7,9 @@
 //            h = silu(e) * g                      -> forge_lora_mlp_gate_up
 //   backward DW = dY Wd + sd (dY Bd) Ad, then the in-place SwiGLU backward
 //            (DW, e, g) -> (h, df, de)            -> forge_lora_mlp_down_bwd
+// The same two entry points take the GeGLU activation (tanh or exact GELU)
+// for Gemma MLPs, replacing the reference's layered path there (PEFT
+// projections + the GeGLU kernel, forge/forge/patching/kernels/lora.py:170-188).
 // LoRA-QKV (reference: kernels/lora_qkv/experiments/v2/lora_qkv_kernel_v2_3.py
 // :177-267 + the caller's RoPE, forge/forge/patching/kernels/lora.py:250-264):
 //   [Q | K | V] = X [Wq; Wk; Wv]^T + per-projection LoRA, RoPE on Q and K
@@ -18,13 +21,29 @@
 
 using namespace fgemm;
 
+namespace {
+
+// FORGE_ACT_* -> the forward / backward GLU epilogue (-1: unknown)
+int glu_epi(int activation, bool backward) {
+  switch (activation) {
+    case FORGE_ACT_SILU: return backward ? EPI_SWIGLU_BWD : EPI_SWIGLU_FWD;
+    case FORGE_ACT_GELU_TANH: return backward ? EPI_GEGLU_TANH_BWD : EPI_GEGLU_TANH_FWD;
+    case FORGE_ACT_GELU_ERF: return backward ? EPI_GEGLU_ERF_BWD : EPI_GEGLU_ERF_FWD;
+  }
+  return -1;
+}
+
+}  // namespace
+
 extern "C" int forge_lora_mlp_gate_up(int64_t M, int64_t H, int64_t I, int64_t r,
                                       const void* x, int64_t ldx,
                                       const void* w_gate, const void* w_up, int64_t ldw,
                                       const void* xa, int64_t ld_xa,
                                       const void* b_gate, const void* b_up, int64_t ldb,
-                                      void* e, void* g, void* h, int64_t ld_out, void* stream) {
+                                      void* e, void* g, void* h, int64_t ld_out, int activation, void* stream) {
   if (M < 0 || H < 0 || I < 0 || r < 0) return forge_set_error(FORGE_ERR_INVALID, "lora_mlp_gate_up: shape");
+  const int epi = glu_epi(activation, false);
+  if (epi < 0) return forge_set_error(FORGE_ERR_INVALID, "lora_mlp_gate_up: activation %d", activation);
   GemmArgs a = {};
   a.M = M;
   a.N = I;
@@ -45,7 +64,7 @@ extern "C" int forge_lora_mlp_gate_up(int64_t M, int64_t H, int64_t I, int64_t r
   a.ep.ld_eg = ld_out;
   if (r > 0 && xa && (ld_xa % 8 != 0 || r % 8 != 0))
     return forge_set_error(FORGE_ERR_INVALID, "lora_mlp_gate_up: rank and ld_xa must be multiples of 8");
-  return run(-1, ROW, COL, EPI_SWIGLU_FWD, a, (hipStream_t)stream);
+  return run(-1, ROW, COL, epi, a, (hipStream_t)stream);
 }
 
 extern "C" int forge_lora_mlp_down_bwd(int64_t M, int64_t H, int64_t I, int64_t r,
@@ -53,8 +72,11 @@ extern "C" int forge_lora_mlp_down_bwd(int64_t M, int64_t H, int64_t I, int64_t 
                                        const void* w_down, int64_t ldwd,
                                        const void* t_d, int64_t ld_t,
                                        const void* a_down, int64_t ld_ad, int w_layout,
-                                       void* h_out, void* e_df, void* g_de, int64_t ld, void* stream) {
+                                       void* h_out, void* e_df, void* g_de, int64_t ld, int activation,
+                                       void* stream) {
   if (M < 0 || H < 0 || I < 0 || r < 0) return forge_set_error(FORGE_ERR_INVALID, "lora_mlp_down_bwd: shape");
+  const int epi = glu_epi(activation, true);
+  if (epi < 0) return forge_set_error(FORGE_ERR_INVALID, "lora_mlp_down_bwd: activation %d", activation);
   if (w_layout != ROW && w_layout != COL) return forge_set_error(FORGE_ERR_INVALID, "lora_mlp_down_bwd: w_layout");
   GemmArgs a = {};
   a.M = M;
@@ -73,7 +95,7 @@ extern "C" int forge_lora_mlp_down_bwd(int64_t M, int64_t H, int64_t I, int64_t 
   a.ep.e = (__bf16*)e_df;
   a.ep.g = (__bf16*)g_de;
   a.ep.ld_eg = ld;
-  return run(-1, ROW, w_layout, EPI_SWIGLU_BWD, a, (hipStream_t)stream);
+  return run(-1, ROW, w_layout, epi, a, (hipStream_t)stream);
 }
 
 extern "C" int forge_lora_qkv_rope(int64_t M, int64_t K, int64_t hq, int64_t hkv, int64_t r,

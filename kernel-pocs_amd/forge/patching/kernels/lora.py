@@ -31,8 +31,10 @@ is never less general than the reference's.
 Fused paths:
   * SiLU MLP (Qwen/Llama): LoRAMLPv6 (gate/up GEMMs with the LoRA-B terms as
     extra K segments, SwiGLU in the epilogue, down GEMM with its LoRA term).
-    GeGLU MLPs (Gemma) keep the reference's layering: PEFT projections plus
-    the GeGLU kernel.
+  * GeGLU MLP (Gemma): LoRAMLPGeGLU, the same pipeline with the GeGLU
+    epilogues - the fully-fused Gemma path the reference leaves as a
+    follow-on (its adapter composes PEFT projections with the GeGLU kernel,
+    which stays the fallback here).
   * Attention without q/k norms (Llama, Qwen2 bias-free, Gemma2):
     LoRAQKVRoPEFunction - one GEMM for Q|K|V with the LoRA terms, RoPE applied
     to Q and K in its epilogue (replaces view -> transpose ->
@@ -219,7 +221,7 @@ def _fusable_input(x) -> bool:
 
 
 def mlp_fused_args(module, x):
-    """(gate, up, down) LiveLoRA of a SiLU MLP when the fused LoRA-MLP takes
+    """(gate, up, down) LiveLoRA of a gated MLP when the fused LoRA-MLP takes
     this call, else None."""
     if not _fusable_input(x):
         return None
@@ -275,13 +277,14 @@ def rope_tables(cos, sin, x, head_dim, hq, hkv):
 
 
 def make_lora_mlp_forward(module, config):
-    """PEFT LoRA MLP.forward -> fused LoRA-MLP (SiLU) or PEFT projections +
-    the GeGLU kernel (GELU), per lora.py:126-197.
+    """PEFT LoRA MLP.forward -> fused LoRA-MLP with the SwiGLU (SiLU) or GeGLU
+    (GELU, tanh or exact) epilogues; lora.py:126-197.
 
     Patch time: the activation must be recognised; SiLU needs an active
     adapter on each projection (lora.py:166-168), GeGLU extractable bias-free
     adapters (lora.py:189-191).  Call time: the fused kernel when
-    `mlp_fused_args` accepts the live tensors, else the submodules."""
+    `mlp_fused_args` accepts the live tensors, else the submodules (with the
+    SwiGLU / GeGLU kernel for the activation, as in the reference)."""
     activation = _detect_mlp_activation(module)
 
     if activation == "silu":
@@ -304,13 +307,21 @@ def make_lora_mlp_forward(module, config):
         return forward
 
     from forge.kernels.geglu import geglu
+    from forge.kernels.lora_mlp import LoRAMLPGeGLU
 
     for proj in (module.gate_proj, module.up_proj, module.down_proj):
         _lora_tensors(proj)
     approximate = "tanh" if activation == "gelu_tanh" else "none"
 
     def forward(x):
-        return module.down_proj(geglu(module.gate_proj(x), module.up_proj(x), approximate=approximate))
+        fused = mlp_fused_args(module, x)
+        if fused is None:
+            return module.down_proj(geglu(module.gate_proj(x), module.up_proj(x), approximate=approximate))
+        g, u, d = fused
+        X3 = x if x.dim() == 3 else x.reshape(1, -1, x.shape[-1])
+        out = LoRAMLPGeGLU.apply(X3, g.W, _bf16(g.A), _bf16(g.B), g.s, u.W, _bf16(u.A), _bf16(u.B), u.s,
+                                 d.W, _bf16(d.A), _bf16(d.B), d.s, approximate)
+        return out.reshape(*x.shape[:-1], out.shape[-1])
 
     return forward
 

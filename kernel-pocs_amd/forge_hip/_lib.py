@@ -35,6 +35,7 @@ c_vp = ctypes.c_void_p
 DTYPE_F32, DTYPE_F16, DTYPE_BF16, DTYPE_F64 = 0, 1, 2, 3
 LAYOUT_ROW, LAYOUT_COL = 0, 1
 EPI_STORE, EPI_ATOMIC_F32 = 0, 1
+ACT_SILU, ACT_GELU_TANH, ACT_GELU_ERF = 0, 1, 2
 
 CE_HAS_GRADIENTS = 1
 CE_HAS_WEIGHT = 2
@@ -108,11 +109,11 @@ forge_gemm = _decl(
 )
 forge_lora_mlp_gate_up = _decl(
     "forge_lora_mlp_gate_up",
-    [c_i64] * 4 + [c_vp, c_i64, c_vp, c_vp, c_i64, c_vp, c_i64, c_vp, c_vp, c_i64, c_vp, c_vp, c_vp, c_i64, c_vp],
+    [c_i64] * 4 + [c_vp, c_i64, c_vp, c_vp, c_i64, c_vp, c_i64, c_vp, c_vp, c_i64, c_vp, c_vp, c_vp, c_i64, c_int, c_vp],
 )
 forge_lora_mlp_down_bwd = _decl(
     "forge_lora_mlp_down_bwd",
-    [c_i64] * 4 + [c_vp, c_i64, c_vp, c_i64, c_vp, c_i64, c_vp, c_i64, c_int, c_vp, c_vp, c_vp, c_i64, c_vp],
+    [c_i64] * 4 + [c_vp, c_i64, c_vp, c_i64, c_vp, c_i64, c_vp, c_i64, c_int, c_vp, c_vp, c_vp, c_i64, c_int, c_vp],
 )
 forge_lora_qkv_rope = _decl(
     "forge_lora_qkv_rope",

@@ -20,9 +20,17 @@ math of kernels/lora_mlp/reference/lora_mlp_pytorch.py:145-225):
   5. dX = df Wu + de Wg + vu Au + vg Ag              forge_gemm (4 K segments)
 The saved e/g buffers are overwritten by df/de in step 2 (the reference's
 in-place contract: backward is not re-entrant).
+
+activation="gelu_tanh" / "gelu_exact" runs the same pipeline with the GeGLU
+epilogues (Gemma MLPs): h = round(gelu(e)) g in the forward and, in step 2,
+df = round(DW) round(gelu(e)), de = round(DW) g gelu'(e) - the GeGLU
+kernel's forward and backward (kernels/geglu/geglu.py:104-148) on the bf16
+e, g and DW, where the reference composes PEFT projections with that kernel
+(forge/forge/patching/kernels/lora.py:170-188).
 """
 from __future__ import annotations
 
+import math
 from typing import Optional, Tuple
 
 import torch
@@ -36,11 +44,23 @@ def _w(t):
     return None if t is None else as_operand(t)
 
 
+ACTIVATIONS = {"silu": L.ACT_SILU, "gelu_tanh": L.ACT_GELU_TANH, "gelu_exact": L.ACT_GELU_ERF}
+
+
+def _act_code(activation: str) -> int:
+    try:
+        return ACTIVATIONS[activation]
+    except KeyError:
+        raise ValueError(f"LoRA-MLP activation must be one of {sorted(ACTIVATIONS)}, got {activation!r}") from None
+
+
 def mlp_forward(X2, W_gate, A_gate, B_gate, s_gate, W_up, A_up, B_up, s_up,
-                W_down, A_down, B_down, s_down, save_eg: bool = True, aux: Optional[dict] = None):
+                W_down, A_down, B_down, s_down, save_eg: bool = True, aux: Optional[dict] = None,
+                activation: str = "silu"):
     """Returns (out [M, H], e [M, I], g [M, I]) (e, g None unless save_eg).
     aux (a dict, optional) receives the LoRA-A products the backward reuses:
     xa = [sg X Ag^T | su X Au^T] [M, 2r] and xd = sd h Ad^T [M, r]."""
+    act = _act_code(activation)
     L.require_gpu(X2, W_gate, W_up, W_down)
     X2 = as_operand(X2)
     Wg, Wu, Wd = _w(W_gate), _w(W_up), _w(W_down)
@@ -61,7 +81,7 @@ def mlp_forward(X2, W_gate, A_gate, B_gate, s_gate, W_up, A_up, B_up, s_up,
     L.check(
         L.forge_lora_mlp_gate_up(
             M, H, I, r, X2.data_ptr(), ld(X2), Wg.data_ptr(), Wu.data_ptr(), ld(Wg),
-            L.ptr(xa), 2 * r, L.ptr(Bg), L.ptr(Bu), r, e.data_ptr(), g.data_ptr(), h.data_ptr(), I, st),
+            L.ptr(xa), 2 * r, L.ptr(Bg), L.ptr(Bu), r, e.data_ptr(), g.data_ptr(), h.data_ptr(), I, act, st),
         "forge_lora_mlp_gate_up",
     )
     segs = [(h, I, Wd, ld(Wd), I)]
@@ -78,13 +98,14 @@ def mlp_forward(X2, W_gate, A_gate, B_gate, s_gate, W_up, A_up, B_up, s_up,
 
 
 def mlp_backward(dY2, X2, e, g, W_gate, A_gate, B_gate, s_gate, W_up, A_up, B_up, s_up,
-                 W_down, A_down, B_down, s_down, aux: Optional[dict] = None):
+                 W_down, A_down, B_down, s_down, aux: Optional[dict] = None, activation: str = "silu"):
     """Returns (dX [M, H], dAg, dBg, dAu, dBu, dAd, dBd).  e and g are
     overwritten with df and de.  With the forward's aux (xa, xd) the
     weight gradients of B reuse those products instead of re-reading X and h;
     xd then comes from the forward's h (fp32 e, g), which differs from the
     backward's recomputed h (bf16-rounded, lora_mlp_pytorch.py:165) only by
     rounding."""
+    act = _act_code(activation)
     dY2 = as_operand(dY2)
     X2 = as_operand(X2)
     Wg, Wu, Wd = _w(W_gate), _w(W_up), _w(W_down)
@@ -94,7 +115,7 @@ def mlp_backward(dY2, X2, e, g, W_gate, A_gate, B_gate, s_gate, W_up, A_up, B_up
     dev = X2.device
     Ag, Bg, Au, Bu, Ad, Bd = (_w(t) for t in (A_gate, B_gate, A_up, B_up, A_down, B_down))
 
-    # 1-2: DW = dY Wd + sd (dY Bd) Ad with the SwiGLU backward fused in place
+    # 1-2: DW = dY Wd + sd (dY Bd) Ad with the GLU backward fused in place
     td = times_b(dY2, ld(dY2), Bd, H, alpha=s_down)
     h = torch.empty(M, I, dtype=torch.bfloat16, device=dev)
     # K-contiguous weights (cached W^T, small A^T) put the three big GEMMs of
@@ -104,7 +125,7 @@ def mlp_backward(dY2, X2, e, g, W_gate, A_gate, B_gate, s_gate, W_up, A_up, B_up
     WdB, AdB, wl = (frozen_t(W_down), small_t(Ad), COL) if kt else (Wd, Ad, ROW)
     L.check(
         L.forge_lora_mlp_down_bwd(M, H, I, r, dY2.data_ptr(), ld(dY2), WdB.data_ptr(), ld(WdB), td.data_ptr(), r,
-                                  AdB.data_ptr(), ld(AdB), wl, h.data_ptr(), e.data_ptr(), g.data_ptr(), I,
+                                  AdB.data_ptr(), ld(AdB), wl, h.data_ptr(), e.data_ptr(), g.data_ptr(), I, act,
                                   L.stream_of(X2)),
         "forge_lora_mlp_down_bwd",
     )
@@ -144,29 +165,45 @@ def mlp_backward(dY2, X2, e, g, W_gate, A_gate, B_gate, s_gate, W_up, A_up, B_up
     return (dX, dA_ug[r:], dBg, dA_ug[:r], dBu, dAd, dBd)
 
 
-def torch_forward(X, W_gate, A_gate, B_gate, s_gate, W_up, A_up, B_up, s_up, W_down, A_down, B_down, s_down):
+def _gelu_and_grad(e, activation):
+    """(gelu(e), gelu'(e)) for the float64 path, tanh form or exact."""
+    if activation == "gelu_tanh":
+        c = math.sqrt(2.0 / math.pi)
+        t = torch.tanh(c * (e + 0.044715 * e ** 3))
+        return 0.5 * e * (1 + t), 0.5 * (1 + t) + 0.5 * e * (1 - t * t) * c * (1 + 3 * 0.044715 * e * e)
+    cdf = 0.5 * (1 + torch.erf(e / math.sqrt(2.0)))
+    return e * cdf, cdf + e * torch.exp(-0.5 * e * e) / math.sqrt(2 * math.pi)
+
+
+def torch_forward(X, W_gate, A_gate, B_gate, s_gate, W_up, A_up, B_up, s_up, W_down, A_down, B_down, s_down,
+                  activation="silu"):
     """Plain-PyTorch forward the reference uses for float64 (gradcheck)
-    inputs (kernels/lora_mlp/experiments/v6/lora_mlp_kernel_v6.py:552-557)."""
+    inputs (kernels/lora_mlp/experiments/v6/lora_mlp_kernel_v6.py:552-557);
+    GELU activations follow the same composition with h = gelu(e) g."""
     e = X @ W_gate.t() + s_gate * ((X @ A_gate.t()) @ B_gate.t())
     g = X @ W_up.t() + s_up * ((X @ A_up.t()) @ B_up.t())
-    h = F.silu(e) * g
+    h = F.silu(e) * g if activation == "silu" else _gelu_and_grad(e, activation)[0] * g
     out = h @ W_down.t() + s_down * ((h @ A_down.t()) @ B_down.t())
     return out, e, g
 
 
 def torch_backward(dY, X, e, g, W_gate, A_gate, B_gate, s_gate, W_up, A_up, B_up, s_up,
-                   W_down, A_down, B_down, s_down):
+                   W_down, A_down, B_down, s_down, activation="silu"):
     """Plain-PyTorch backward the reference uses for float64 inputs
-    (kernels/lora_mlp/experiments/v6/lora_mlp_kernel_v6.py:608-628)."""
-    sig_e = torch.sigmoid(e.float()).to(e.dtype)
-    silu_e = e * sig_e
-    h = silu_e * g
+    (kernels/lora_mlp/experiments/v6/lora_mlp_kernel_v6.py:608-628); GELU
+    activations swap silu(e) and its derivative for gelu(e) and gelu'(e)."""
+    if activation == "silu":
+        sig_e = torch.sigmoid(e.float()).to(e.dtype)
+        act_e = e * sig_e
+        dact = sig_e * (1.0 + e * (1.0 - sig_e))
+    else:
+        act_e, dact = _gelu_and_grad(e, activation)
+    h = act_e * g
     DW = dY @ W_down + s_down * ((dY @ B_down) @ A_down)
     d_downA = s_down * ((dY @ B_down).t() @ h)
     d_downB = s_down * (dY.t() @ h @ A_down.t())
-    df = DW * silu_e
-    dsilu = sig_e * (1.0 + e * (1.0 - sig_e))
-    de = DW * g * dsilu
+    df = DW * act_e
+    de = DW * g * dact
     d_upA = s_up * ((df @ B_up).t() @ X)
     d_upB = s_up * (df.t() @ X @ A_up.t())
     d_gateA = s_gate * ((de @ B_gate).t() @ X)
@@ -175,17 +212,19 @@ def torch_backward(dY, X, e, g, W_gate, A_gate, B_gate, s_gate, W_up, A_up, B_up
     return dX, d_gateA, d_gateB, d_upA, d_upB, d_downA, d_downB
 
 
-def run_forward(X, params, save_eg=True, aux=None):
+def run_forward(X, params, save_eg=True, aux=None, activation="silu"):
     """Dispatch on dtype: float64 -> the reference's PyTorch path, bf16 ->
     the HIP kernels.  Returns (out with X's leading shape, e, g); aux (a dict)
     collects the LoRA-A products for run_backward."""
+    _act_code(activation)
     if X.dtype == torch.float64:
         Xf = X.reshape(-1, X.shape[-1])
-        out, e, g = torch_forward(Xf, *params)
+        out, e, g = torch_forward(Xf, *params, activation=activation)
     else:
         if X.dtype != torch.bfloat16:
             raise TypeError(f"LoRA-MLP kernels run in bf16 (or float64 via PyTorch), got {X.dtype}")
-        out, e, g = mlp_forward(X.reshape(-1, X.shape[-1]), *params, save_eg=save_eg, aux=aux)
+        out, e, g = mlp_forward(X.reshape(-1, X.shape[-1]), *params, save_eg=save_eg, aux=aux,
+                                activation=activation)
     if X.dim() == 3:
         out = out.reshape(X.shape[0], X.shape[1], -1)
         if e is not None:
@@ -194,14 +233,14 @@ def run_forward(X, params, save_eg=True, aux=None):
     return out, e, g
 
 
-def run_backward(dY, X, e, g, params, aux=None):
+def run_backward(dY, X, e, g, params, aux=None, activation="silu"):
     dY2 = dY.reshape(-1, dY.shape[-1])
     X2 = X.reshape(-1, X.shape[-1])
     e2 = e.reshape(-1, e.shape[-1])
     g2 = g.reshape(-1, g.shape[-1])
     if X.dtype == torch.float64:
-        return torch_backward(dY2, X2, e2, g2, *params)
-    return mlp_backward(dY2, X2, e2, g2, *params, aux=aux)
+        return torch_backward(dY2, X2, e2, g2, *params, activation=activation)
+    return mlp_backward(dY2, X2, e2, g2, *params, aux=aux, activation=activation)
 
 
 def stack_lora_a(A_gate: torch.Tensor, A_up: torch.Tensor) -> torch.Tensor:

@@ -46,6 +46,11 @@ def test_status_codes_and_messages():
     assert rc == 1 and b"ld" in L.forge_last_error()
     rc = L.forge_lora_qkv_rope(16, 64, 100, 256, 0, *([16] * 20)[:14], 16, 16, 8, None, 96, 1, None)
     assert rc == 2
+    # an unknown gated activation of the fused LoRA-MLP entry points
+    rc = L.forge_lora_mlp_gate_up(16, 64, 64, 0, *([16] * 13), 64, 3, None)
+    assert rc == 1 and b"activation 3" in L.forge_last_error()
+    rc = L.forge_lora_mlp_down_bwd(16, 64, 64, 0, *([16] * 8), 0, *([16] * 3), 64, -1, None)
+    assert rc == 1 and b"activation -1" in L.forge_last_error()
 
 
 def test_zero_size_calls_are_noops():

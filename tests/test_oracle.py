@@ -353,6 +353,40 @@ def test_lora_mlp_backward_matches_autograd_float64():
         torch.testing.assert_close(got, exp, rtol=2e-5, atol=2e-6)
 
 
+@pytest.mark.parametrize("activation", ["gelu_tanh", "gelu_exact"])
+def test_lora_mlp_gelu_backward_matches_autograd_float64(activation):
+    """The GeGLU MLP oracle (lora.py:170-188 composition): hand-written
+    backward against autograd of its forward, and the forward's h against
+    torch's own F.gelu; a planted slip (gelu' without its x pdf(x) term) must
+    fail the gradient check."""
+    p = _mlp_params(seed=6)
+    g = torch.Generator().manual_seed(7)
+    X = torch.randn(7, 12, generator=g, dtype=torch.float64) * 2
+    dY = torch.randn(7, 12, generator=g, dtype=torch.float64)
+    out, e, gg = omlp.forward(X, *p, activation=activation)
+    grads = omlp.backward(dY, X, e, gg, *p, activation=activation)
+    leaves = [X.clone().requires_grad_(True)] + [t.clone().requires_grad_(True) if isinstance(t, torch.Tensor) else t
+                                                 for t in p]
+    o2, _, _ = omlp.forward(*leaves, activation=activation)
+    (o2 * dY).sum().backward()
+    expect = [leaves[0].grad, leaves[2].grad, leaves[3].grad, leaves[6].grad, leaves[7].grad, leaves[10].grad,
+              leaves[11].grad]
+    for got, exp in zip(grads, expect):
+        torch.testing.assert_close(got, exp, rtol=1e-9, atol=1e-10)
+    approx = "tanh" if activation == "gelu_tanh" else "none"
+    h = F.gelu(e, approximate=approx) * gg
+    torch.testing.assert_close(out, omlp.matmul_lora(h, *p[8:12]), rtol=1e-12, atol=1e-12)
+    assert e.min() < -2 and e.max() > 2
+
+    real = omlp._gelu
+    try:
+        omlp._gelu = lambda x, a: (real(x, a)[0], (real(x, a)[0] / x))  # Phi(x) only
+        wrong = omlp.backward(dY, X, e, gg, *p, activation=activation)
+    finally:
+        omlp._gelu = real
+    assert not torch.allclose(wrong[0], expect[0], rtol=1e-3, atol=1e-4)
+
+
 def test_lora_mlp_forward_matches_numpy():
     p = _mlp_params(seed=2)
     X = torch.randn(5, 12, generator=torch.Generator().manual_seed(3), dtype=torch.float64)

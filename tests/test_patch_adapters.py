@@ -291,9 +291,18 @@ def test_lora_mlp_fused(arch, S):
 
 
 @pytest.mark.gpu
-def test_lora_mlp_geglu_keeps_the_projection_path():
-    """Gemma2 (GeGLU): PEFT projections + the GeGLU kernel (lora.py:170-197)."""
-    _parity("gemma2", "mlp", "lora_mlp", expect_fused=None)
+@pytest.mark.parametrize("act", ["gelu_pytorch_tanh", "gelu"])
+def test_lora_mlp_geglu_fused(act):
+    """Gemma2 (GeGLU, tanh or exact GELU): the fused LoRA-GeGLU MLP in place of
+    the reference's PEFT projections + GeGLU kernel (lora.py:170-197)."""
+    _parity("gemma2", "mlp", "lora_mlp", hidden_activation=act)
+
+
+@pytest.mark.gpu
+def test_lora_mlp_geglu_fallback_keeps_the_projection_path():
+    """A GeGLU MLP whose width the fused kernel cannot take runs the
+    reference's composition (PEFT projections + the GeGLU kernel)."""
+    _parity("gemma2", "mlp", "lora_mlp", expect_fused=False, intermediate_size=1020)
 
 
 @pytest.mark.gpu
