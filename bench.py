@@ -43,7 +43,8 @@ def _parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--kernels", default="swiglu,rope,ce,lora_mlp,lora_qkv,flce,geglu,rmsnorm,lora_patch")
+    ap.add_argument("--kernels",
+                    default="swiglu,rope,ce,lora_mlp,lora_qkv,flce,geglu,rmsnorm,lora_patch,lora_mlp_geglu,lora_patch_gemma")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--only-launches", action="store_true",
                     help="run only the dominant-kernel launch loop (for rocprofv3 counter runs)")
@@ -354,9 +355,10 @@ def _gpu_params_mlp(H, I, r, alpha, gen):
     return (W(I, H), A(H), B(I), s, W(I, H), A(H), B(I), s, W(H, I), A(I), B(H), s)
 
 
-def _gate_up_roofline(args, X2, Wg, Wu, Bg, Bu, r):
+def _gate_up_roofline(args, X2, Wg, Wu, Bg, Bu, r, act=None, traffic_key="lora_mlp_gate_up"):
     """(mean launch ms, roofline) of the LoRA-MLP's dominant kernel, the fused
-    gate/up GEMM + SwiGLU epilogue (forge_lora_mlp_gate_up), on X2 [M, H]."""
+    gate/up GEMM + gated-activation epilogue (forge_lora_mlp_gate_up; SwiGLU
+    unless act names another FORGE_ACT_*), on X2 [M, H]."""
     import torch
     from forge_hip import _lib as L
 
@@ -366,24 +368,27 @@ def _gate_up_roofline(args, X2, Wg, Wu, Bg, Bu, r):
     e = torch.empty(M, I, device="cuda", dtype=torch.bfloat16)
     gg, hh = torch.empty_like(e), torch.empty_like(e)
     st = L.stream_of(X2)
+    act = L.ACT_SILU if act is None else act
     launch_ms = time_launches(lambda i: L.forge_lora_mlp_gate_up(
         M, H, I, r, X2.data_ptr(), X2.stride(0), Wg.data_ptr(), Wu.data_ptr(), Wg.stride(0), xa.data_ptr(), 2 * r,
-        Bg.data_ptr(), Bu.data_ptr(), Bg.stride(0), e.data_ptr(), gg.data_ptr(), hh.data_ptr(), I, L.ACT_SILU, st),
+        Bg.data_ptr(), Bu.data_ptr(), Bg.stride(0), e.data_ptr(), gg.data_ptr(), hh.data_ptr(), I, act, st),
         max(args.steps, 10))
     gu_flops = 4 * M * H * I + 4 * M * r * I
     return launch_ms, _roof("mfma", gu_flops / (launch_ms * 1e-3) / 1e12, BF16_PEAK_TFLOPS, "TFLOP/s",
-                            _traffic("lora_mlp_gate_up"))
+                            _traffic(traffic_key))
 
 
-def bench_lora_mlp(args):
+def bench_lora_mlp(args, activation="silu"):
     """LoRA MLP fwd+bwd, bf16, Llama-3-8B shape (M=8192, H=4096,
-    I=14336), r=16, alpha=32."""
+    I=14336), r=16, alpha=32.  activation="gelu_tanh" runs the fused
+    LoRA-GeGLU MLP (LoRAMLPGeGLU, Gemma's activation) on the same shape."""
     import torch
     from forge_hip import _lib as L
     from kernels.lora_mlp.experiments.v6.lora_mlp_kernel_v6 import LoRAMLPv6
-    from kernels.lora_mlp._impl import mlp_forward
+    from kernels.lora_mlp.geglu_mlp import LoRAMLPGeGLU
     from oracle.lora_mlp import flops
 
+    geglu = activation != "silu"
     M, H, I, r = 8192, 4096, 14336, 16
     g = torch.Generator(device="cuda").manual_seed(3)
     params = _gpu_params_mlp(H, I, r, 32, g)
@@ -395,18 +400,21 @@ def bench_lora_mlp(args):
     def step(i):
         for t in leaves:  # a training step after zero_grad(set_to_none=True)
             t.grad = None
-        out = LoRAMLPv6.apply(X, *params)
+        out = LoRAMLPGeGLU.apply(X, *params, "tanh") if geglu else LoRAMLPv6.apply(X, *params)
         out.backward(dY)
 
     ms, wall = run_steps(args, step)
     fl = flops(M, H, I, r)
     tf = rate(fl, ms, 1e12)
-    # dominant kernel: the fused gate/up GEMM + SwiGLU epilogue
+    # dominant kernel: the fused gate/up GEMM + gated-activation epilogue
     Wg, Ag, Bg, sg, Wu, Au, Bu, su = [t.detach() if isinstance(t, torch.Tensor) else t for t in params[:8]]
-    launch_ms, roof = _gate_up_roofline(args, X.detach().reshape(M, H), Wg, Wu, Bg, Bu, r)
+    launch_ms, roof = _gate_up_roofline(args, X.detach().reshape(M, H), Wg, Wu, Bg, Bu, r,
+                                        act=L.ACT_GELU_TANH if geglu else L.ACT_SILU,
+                                        traffic_key="lora_mlp_geglu_gate_up" if geglu else "lora_mlp_gate_up")
     res = {
-        "config": {"workload": "lora_mlp_fwd_bwd", "dtype": "bf16", "M": M, "H": H, "I": I, "rank": r, "alpha": 32,
-                   "api": "LoRAMLPv6"},
+        "config": {"workload": "lora_mlp_geglu_fwd_bwd" if geglu else "lora_mlp_fwd_bwd", "dtype": "bf16", "M": M,
+                   "H": H, "I": I, "rank": r, "alpha": 32,
+                   "api": "LoRAMLPGeGLU (tanh GELU)" if geglu else "LoRAMLPv6"},
         "value": tf, "unit": "TFLOP/s", "ms_per_step": rnd(ms, 4), "wall_ms_per_step": rnd(wall, 4),
         "frac_of_mfma_peak": rnd(tf and tf / BF16_PEAK_TFLOPS, 4), "algorithmic_flops_per_step": fl,
         "launches_ms": {"forge_lora_mlp_gate_up": round(launch_ms, 4)},
@@ -419,10 +427,16 @@ def bench_lora_mlp(args):
         ms_ = 512
         cpu_params = [t.detach().cpu() if isinstance(t, torch.Tensor) else t for t in params]
         Xc, dYc = X.detach()[:, :ms_].cpu(), dY[:, :ms_].cpu()
-        t, reps = cpu_time(lambda: fwd_bwd(Xc, dYc, cpu_params, compute_dtype=torch.bfloat16))
+        t, reps = cpu_time(lambda: fwd_bwd(Xc, dYc, cpu_params, compute_dtype=torch.bfloat16, activation=activation))
+        what = ("the reference's Gemma composition (LoRA projections + GeGLU)" if geglu
+                else "reference LoRAMLP formulas")
         res["cpu_baseline"] = _cpu(flops(ms_, H, I, r) / t / 1e12, "TFLOP/s",
-                                   f"{ms_} of {M} tokens, reference LoRAMLP formulas in bf16, fwd+bwd, median of {reps}")
+                                   f"{ms_} of {M} tokens, {what} in bf16, fwd+bwd, median of {reps}")
     return res
+
+
+def bench_lora_mlp_geglu(args):
+    return bench_lora_mlp(args, activation="gelu_tanh")
 
 
 class _PeftLayoutLoRA:
@@ -462,36 +476,53 @@ class _PeftLayoutLoRA:
         return LoraLinear()
 
 
-def bench_lora_patch(args):
+def bench_lora_patch(args, arch="llama"):
     """The patch-layer adapter (forge/patching/kernels/lora.py) on Hugging
     Face's LlamaMLP at the LoRA-MLP config (M=8192, H=4096, I=14336, r=16,
     alpha=32), PEFT-layout LoRA on gate/up/down, fwd+bwd: the fused adapter
     against the reference adapter's submodule path (PEFT projections on
-    hipBLASLt GEMMs + the SwiGLU kernel) on the same module and inputs."""
+    hipBLASLt GEMMs + the SwiGLU kernel) on the same module and inputs.
+    arch="gemma2": Gemma2MLP at Gemma-2-9B's MLP shape (H=3584, I=14336,
+    tanh GELU), the fused LoRA-GeGLU MLP against the reference's Gemma path
+    (PEFT projections + the GeGLU kernel, lora.py:184-188)."""
     import copy
 
     import torch
 
     try:
-        from transformers import LlamaConfig
+        from transformers import Gemma2Config, LlamaConfig
+        import transformers.models.gemma2.modeling_gemma2 as MG
         import transformers.models.llama.modeling_llama as ML
     except ImportError:
         return {"skipped": "transformers is not installed", "value": None, "unit": "TFLOP/s"}
     from forge.patching import FORWARD_MAKERS
+    from forge.kernels.geglu import geglu
     from forge.kernels.swiglu import swiglu
+    from forge_hip import _lib as L
     from oracle.lora_mlp import flops
 
-    M, H, I, r = 8192, 4096, 14336, 16
+    gemma = arch == "gemma2"
+    M, H, I, r = (8192, 3584, 14336, 16) if gemma else (8192, 4096, 14336, 16)
     g = torch.Generator(device="cuda").manual_seed(9)
     torch.manual_seed(9)
-    cfg = LlamaConfig(hidden_size=H, intermediate_size=I, num_attention_heads=32, num_key_value_heads=8, head_dim=128)
-    ref = ML.LlamaMLP(cfg).to("cuda", torch.bfloat16)
+    if gemma:
+        cfg = Gemma2Config(hidden_size=H, intermediate_size=I, num_attention_heads=16, num_key_value_heads=8,
+                           head_dim=256, hidden_activation="gelu_pytorch_tanh")
+        ref = MG.Gemma2MLP(cfg).to("cuda", torch.bfloat16)
+    else:
+        cfg = LlamaConfig(hidden_size=H, intermediate_size=I, num_attention_heads=32, num_key_value_heads=8,
+                          head_dim=128)
+        ref = ML.LlamaMLP(cfg).to("cuda", torch.bfloat16)
     for n in ("gate_proj", "up_proj", "down_proj"):
         setattr(ref, n, _PeftLayoutLoRA.wrap(getattr(ref, n), r, 32, g))
     fused = copy.deepcopy(ref)
     fused.forward = FORWARD_MAKERS["lora_mlp"](fused, {})
-    # the reference adapter's call path (lora.py:160-163): PEFT submodules + swiglu
-    ref.forward = lambda x: ref.down_proj(swiglu(ref.gate_proj(x), ref.up_proj(x)))
+    if gemma:
+        # the reference adapter's Gemma path (lora.py:184-188): PEFT submodules + geglu
+        ref.forward = lambda x: ref.down_proj(geglu(ref.gate_proj(x), ref.up_proj(x), approximate="tanh"))
+    else:
+        # the reference adapter's call path (lora.py:160-163): PEFT submodules + swiglu
+        ref.forward = lambda x: ref.down_proj(swiglu(ref.gate_proj(x), ref.up_proj(x)))
     X = torch.randn(1, M, H, device="cuda", generator=g).to(torch.bfloat16).requires_grad_(True)
     dY = torch.randn(1, M, H, device="cuda", generator=g).to(torch.bfloat16)
 
@@ -510,10 +541,14 @@ def bench_lora_patch(args):
     tf, tf_ref = rate(fl, ms, 1e12), rate(fl, ms_ref, 1e12)
     w = [getattr(ref, n).base_layer.weight.detach() for n in ("gate_proj", "up_proj")]
     b = [getattr(ref, n).lora_B["default"].weight.detach() for n in ("gate_proj", "up_proj")]
-    launch_ms, roof = _gate_up_roofline(args, X.detach().reshape(M, H), w[0], w[1], b[0], b[1], r)
+    launch_ms, roof = _gate_up_roofline(args, X.detach().reshape(M, H), w[0], w[1], b[0], b[1], r,
+                                        act=L.ACT_GELU_TANH if gemma else L.ACT_SILU,
+                                        traffic_key="lora_patch_gemma_gate_up" if gemma else "lora_mlp_gate_up")
     return {
-        "config": {"workload": "lora_mlp_patch_fwd_bwd", "dtype": "bf16", "M": M, "H": H, "I": I, "rank": r,
-                   "alpha": 32, "module": "transformers LlamaMLP, PEFT-layout LoRA on gate/up/down",
+        "config": {"workload": "lora_mlp_patch_gemma2_fwd_bwd" if gemma else "lora_mlp_patch_fwd_bwd", "dtype": "bf16",
+                   "M": M, "H": H, "I": I, "rank": r, "alpha": 32,
+                   "module": f"transformers {'Gemma2MLP (tanh GELU)' if gemma else 'LlamaMLP'}, PEFT-layout LoRA on "
+                             "gate/up/down",
                    "api": "forge.patching FORWARD_MAKERS['lora_mlp']"},
         "value": tf, "unit": "TFLOP/s", "ms_per_step": rnd(ms, 4), "wall_ms_per_step": rnd(wall, 4),
         "frac_of_mfma_peak": rnd(tf and tf / BF16_PEAK_TFLOPS, 4), "algorithmic_flops_per_step": fl,
@@ -523,6 +558,10 @@ def bench_lora_patch(args):
         "roofline": roof,
         "dtype": "bf16",
     }
+
+
+def bench_lora_patch_gemma(args):
+    return bench_lora_patch(args, arch="gemma2")
 
 
 def bench_lora_qkv(args):
@@ -823,7 +862,7 @@ def bench_rmsnorm(args):
 
 
 BENCHES = {"copy": bench_copy, "swiglu": bench_swiglu, "rope": bench_rope, "ce": bench_ce, "lora_mlp": bench_lora_mlp,
-           "lora_qkv": bench_lora_qkv, "flce": bench_flce, "geglu": bench_geglu,
+           "lora_mlp_geglu": bench_lora_mlp_geglu, "lora_patch_gemma": bench_lora_patch_gemma, "lora_qkv": bench_lora_qkv, "flce": bench_flce, "geglu": bench_geglu,
            "rmsnorm": bench_rmsnorm, "lora_patch": bench_lora_patch}
 
 
