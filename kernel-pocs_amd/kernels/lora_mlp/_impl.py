@@ -37,6 +37,7 @@ import torch
 import torch.nn.functional as F
 
 from forge_hip import _lib as L
+from kernels import _generic_lora as G
 from kernels._lora_ops import COL, ROW, as_operand, frozen_t, gemm, grad_at_b, ld, lora_a, small_t, times_b
 
 
@@ -61,6 +62,9 @@ def mlp_forward(X2, W_gate, A_gate, B_gate, s_gate, W_up, A_up, B_up, s_up,
     aux (a dict, optional) receives the LoRA-A products the backward reuses:
     xa = [sg X Ag^T | su X Au^T] [M, 2r] and xd = sd h Ad^T [M, r]."""
     act = _act_code(activation)
+    if X2.dtype in G.GENERIC_DTYPES:
+        return G.mlp_forward(X2, W_gate, A_gate, B_gate, s_gate, W_up, A_up, B_up, s_up, W_down, A_down, B_down,
+                             s_down, save_eg=save_eg, aux=aux, activation=activation)
     L.require_gpu(X2, W_gate, W_up, W_down)
     X2 = as_operand(X2)
     Wg, Wu, Wd = _w(W_gate), _w(W_up), _w(W_down)
@@ -106,6 +110,9 @@ def mlp_backward(dY2, X2, e, g, W_gate, A_gate, B_gate, s_gate, W_up, A_up, B_up
     backward's recomputed h (bf16-rounded, lora_mlp_pytorch.py:165) only by
     rounding."""
     act = _act_code(activation)
+    if X2.dtype in G.GENERIC_DTYPES:
+        return G.mlp_backward(dY2, X2, e, g, W_gate, A_gate, B_gate, s_gate, W_up, A_up, B_up, s_up, W_down, A_down,
+                              B_down, s_down, aux=aux, activation=activation)
     dY2 = as_operand(dY2)
     X2 = as_operand(X2)
     Wg, Wu, Wd = _w(W_gate), _w(W_up), _w(W_down)
@@ -214,15 +221,16 @@ def torch_backward(dY, X, e, g, W_gate, A_gate, B_gate, s_gate, W_up, A_up, B_up
 
 def run_forward(X, params, save_eg=True, aux=None, activation="silu"):
     """Dispatch on dtype: float64 -> the reference's PyTorch path, bf16 ->
-    the HIP kernels.  Returns (out with X's leading shape, e, g); aux (a dict)
-    collects the LoRA-A products for run_backward."""
+    the fused MFMA kernels, fp32 / fp16 -> the generic-GEMM kernels
+    (kernels/_generic_lora.py).  Returns (out with X's leading shape, e, g);
+    aux (a dict) collects the LoRA-A products for run_backward."""
     _act_code(activation)
     if X.dtype == torch.float64:
         Xf = X.reshape(-1, X.shape[-1])
         out, e, g = torch_forward(Xf, *params, activation=activation)
     else:
-        if X.dtype != torch.bfloat16:
-            raise TypeError(f"LoRA-MLP kernels run in bf16 (or float64 via PyTorch), got {X.dtype}")
+        if X.dtype != torch.bfloat16 and X.dtype not in G.GENERIC_DTYPES:
+            raise TypeError(f"LoRA-MLP kernels take bf16, fp32 or fp16 (float64 via PyTorch), got {X.dtype}")
         out, e, g = mlp_forward(X.reshape(-1, X.shape[-1]), *params, save_eg=save_eg, aux=aux,
                                 activation=activation)
     if X.dim() == 3:
@@ -261,6 +269,9 @@ def stack_down_lora_a(W_down, A_down):
 
 def fused_lora_a_stacked(X: torch.Tensor, A_stack: torch.Tensor, r: int) -> Tuple[torch.Tensor, torch.Tensor]:
     """X @ A_stack^T -> (xa_gate, xa_up) views of one [M, 2r] buffer (v6 :312-330)."""
+    if X.dtype in G.GENERIC_DTYPES:
+        out = G.gmm(X.reshape(-1, X.shape[-1]), A_stack[:2 * r].t())
+        return out[:, :r], out[:, r:2 * r]
     X2 = as_operand(X.reshape(-1, X.shape[-1]))
     out = lora_a(X2, [A_stack[:r], A_stack[r:2 * r]], [1.0, 1.0])
     return out[:, :r], out[:, r:2 * r]
@@ -280,10 +291,15 @@ def fused_lora_swiglu(e_base, g_base, xa_gate, xa_up, B_gate, B_up, s_gate=1.0, 
         e_full = e_base if inplace else e_base.clone()
         g_full = g_base if inplace else g_base.clone()
         r = xa_gate.shape[1]
-        xg, xu = as_operand(xa_gate), as_operand(xa_up)
-        Bg, Bu = _w(B_gate), _w(B_up)
-        gemm(M, N, [(xg, ld(xg), Bg, ld(Bg), r)], ROW, COL, out=e_full, alpha=s_gate, beta=1.0)
-        gemm(M, N, [(xu, ld(xu), Bu, ld(Bu), r)], ROW, COL, out=g_full, alpha=s_up, beta=1.0)
+        if e_full.dtype in G.GENERIC_DTYPES:
+            G.check_dtypes("fused_lora_swiglu", e_full, g_full, xa_gate, xa_up, B_gate, B_up)
+            G.gmm(xa_gate, B_gate.t(), out=e_full, alpha=s_gate, beta=1.0)
+            G.gmm(xa_up, B_up.t(), out=g_full, alpha=s_up, beta=1.0)
+        else:
+            xg, xu = as_operand(xa_gate), as_operand(xa_up)
+            Bg, Bu = _w(B_gate), _w(B_up)
+            gemm(M, N, [(xg, ld(xg), Bg, ld(Bg), r)], ROW, COL, out=e_full, alpha=s_gate, beta=1.0)
+            gemm(M, N, [(xu, ld(xu), Bu, ld(Bu), r)], ROW, COL, out=g_full, alpha=s_up, beta=1.0)
     else:
         e_full, g_full = e_base, g_base
     h = swiglu_forward(e_full, g_full)[0]

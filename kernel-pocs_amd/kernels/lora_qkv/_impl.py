@@ -25,6 +25,7 @@ from typing import Optional
 import torch
 
 from forge_hip import _lib as L
+from kernels import _generic_lora as G
 from kernels._lora_ops import COL, ROW, as_operand, frozen_t, gemm, grad_at_b, ld, lora_a, small_t, times_b
 
 
@@ -37,7 +38,11 @@ def qkv_forward(X2, W_q, W_k, W_v, A_q, B_q, s_q, A_k, B_k, s_k, A_v, B_v, s_v,
     """Returns out [M, Hq + 2 Hkv] bf16.  rope = {cos, sin, positions, head_dim}
     (bf16 tables [P, D]; int64 positions [M]) applies RoPE to Q and K.
     aux (a dict, optional) receives xa = [sq X Aq^T | sk X Ak^T | sv X Av^T]
-    for the backward's B gradients."""
+    for the backward's B gradients.  fp32 / fp16 inputs run on the generic
+    GEMM (kernels/_generic_lora.py; RoPE tables then in X's dtype) and return
+    out in X's dtype."""
+    if X2.dtype in G.GENERIC_DTYPES:
+        return G.qkv_forward(X2, W_q, W_k, W_v, A_q, B_q, s_q, A_k, B_k, s_k, A_v, B_v, s_v, rope=rope, aux=aux)
     L.require_gpu(X2, W_q, W_k, W_v)
     X2 = as_operand(X2)
     Wq, Wk, Wv = _w(W_q), _w(W_k), _w(W_v)
@@ -77,6 +82,8 @@ def qkv_backward(dQ, dK, dV, X2, W_q, W_k, W_v, A_q, B_q, s_q, A_k, B_k, s_k, A_
                  aux: Optional[dict] = None):
     """Returns (dX, dA_q, dB_q, dA_k, dB_k, dA_v, dB_v).  With the forward's
     aux the B gradients reuse its scaled xa instead of re-reading X."""
+    if X2.dtype in G.GENERIC_DTYPES:
+        return G.qkv_backward(dQ, dK, dV, X2, W_q, W_k, W_v, A_q, B_q, s_q, A_k, B_k, s_k, A_v, B_v, s_v, aux=aux)
     X2 = as_operand(X2)
     dQ, dK, dV = as_operand(dQ), as_operand(dK), as_operand(dV)
     Wq, Wk, Wv = _w(W_q), _w(W_k), _w(W_v)

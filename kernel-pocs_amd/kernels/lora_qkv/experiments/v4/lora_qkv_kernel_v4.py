@@ -132,16 +132,18 @@ class LoRAQKVRoPEFunction(torch.autograd.Function):
 
     forward(ctx, X, W_q, W_k, W_v, A_q, B_q, s_q, A_k, B_k, s_k, A_v, B_v, s_v,
             cos, sin, positions, head_dim) -> (Q_rot, K_rot, V)
-    cos/sin: bf16 tables [P, head_dim] (rows = positions); positions: int64
-    [M] (token -> table row; restarts per sequence for packed varlen)."""
+    cos/sin: tables [P, head_dim] (rows = positions; used in bf16 for bf16
+    X, else in X's dtype); positions: int64 [M] (token -> table row;
+    restarts per sequence for packed varlen)."""
 
     @staticmethod
     def forward(ctx, X, W_q, W_k, W_v, A_q, B_q, s_q, A_k, B_k, s_k, A_v, B_v, s_v, cos, sin, positions,
                 head_dim=128):
         orig_shape = X.shape
         X2 = _flat(X)
-        cos2 = cos.reshape(-1, cos.shape[-1]).to(torch.bfloat16).contiguous()
-        sin2 = sin.reshape(-1, sin.shape[-1]).to(torch.bfloat16).contiguous()
+        tdt = torch.bfloat16 if X.dtype == torch.bfloat16 else X.dtype  # fp32 / fp16: tables in X's dtype
+        cos2 = cos.reshape(-1, cos.shape[-1]).to(tdt).contiguous()
+        sin2 = sin.reshape(-1, sin.shape[-1]).to(tdt).contiguous()
         pos = positions.reshape(-1).to(device=X.device, dtype=torch.int64).contiguous() if positions is not None else None
         ctx.lora_aux = {}  # forward products reused by the backward (outside saved_tensors)
         out = qkv_forward(X2, W_q, W_k, W_v, A_q, B_q, s_q, A_k, B_k, s_k, A_v, B_v, s_v,
