@@ -20,6 +20,7 @@ using fgelu::gelu_and_grad;
 
 template <bool TANH>
 struct GeluAct {
+  static constexpr int kUnroll = 1;
   template <class T>
   __device__ __forceinline__ float fwd(float gate, float up) const {
     float a, g;

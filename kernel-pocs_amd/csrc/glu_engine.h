@@ -3,8 +3,13 @@
 //
 // Layout: rows of `cols` elements, `ld` elements apart.  The packed variant
 // (gate_up = [.., 2H]) is the same kernel with up = gate + H and ld = 2H.
-// One thread owns one 16-byte vector of each operand; kUnroll vectors are in
-// flight per thread so each CU keeps enough bytes outstanding to saturate HBM.
+// One thread owns one 16-byte vector of each operand; Act::kUnroll vectors
+// are in flight per thread, and the grid covers the tensor in one pass up to
+// kMaxBlocks workgroups (many resident workgroups keep the bytes outstanding
+// that HBM needs).  Measured fwd+bwd steps on MI355X: SwiGLU fp32
+// [2048, 11008] 5.65 -> 5.82 TB/s with 2 vectors per thread and no grid cap
+// (was 4 vectors, 8192 workgroups); GeGLU bf16 [4096, 24576] 4.9 -> 5.65
+// TB/s with 1 vector (its GELU math holds more registers per vector).
 // Loads are ordinary (the backward re-reads gate/up right after the forward,
 // largely from the Infinity Cache); stores are nontemporal, so the outputs do
 // not displace those lines and the next kernel does not pay their write-back
@@ -15,6 +20,7 @@
 // storage type T exactly where its reference materialises a tensor:
 //   template <class T> float fwd(float gate, float up) const;
 //   template <class T> void bwd(float dout, float gate, float up, float& dgate, float& dup) const;
+//   static constexpr int kUnroll;  // 16-byte vectors per thread per operand
 #pragma once
 
 #include "common.h"
@@ -23,7 +29,8 @@ namespace glu {
 
 
 constexpr int kBlock = 256;
-constexpr int kUnroll = 4;
+// Grid cap: 256 workgroups per CU; larger tensors loop (grid-stride).
+constexpr int kMaxBlocks = 256 * 256;
 
 // Index math: the flat chunk id i maps to (row, col) = (i / cpr, (i % cpr) * VEC).
 // TWO_D=false is the contiguous case (one row), which skips the division.
@@ -42,6 +49,7 @@ template <class T, int VEC, bool TWO_D, class Act>
 __global__ __launch_bounds__(kBlock) void glu_fwd_kernel(
     const T* __restrict__ gate, const T* __restrict__ up, int64_t ld_in, T* __restrict__ out,
     int64_t ld_out, int64_t n_chunks, int64_t cpr, Act act) {
+  constexpr int kUnroll = Act::kUnroll;
   const int64_t stride = (int64_t)gridDim.x * kBlock;
   for (int64_t base = (int64_t)blockIdx.x * kBlock + threadIdx.x; base < n_chunks;
        base += stride * kUnroll) {
@@ -91,6 +99,7 @@ __global__ __launch_bounds__(kBlock) void glu_bwd_kernel(
     T* dup, int64_t ld_dg, int64_t n_chunks, int64_t cpr, Act act) {
   // No __restrict__: dgate/dup alias gate/up in the default in-place mode.
   // Each element is read before it is overwritten by the same thread.
+  constexpr int kUnroll = Act::kUnroll;
   const int64_t stride = (int64_t)gridDim.x * kBlock;
   for (int64_t base = (int64_t)blockIdx.x * kBlock + threadIdx.x; base < n_chunks;
        base += stride * kUnroll) {
@@ -181,7 +190,7 @@ int launch_fwd(const void* gate, const void* up, int64_t ld_in, void* out, int64
   int vec = p.vec ? V : 1;
   int64_t n_chunks = rows * cols / vec;
   int64_t cpr = cols / vec;
-  int grid = grid_for((n_chunks + kUnroll - 1) / kUnroll, kBlock);
+  int grid = grid_for((n_chunks + Act::kUnroll - 1) / Act::kUnroll, kBlock, kMaxBlocks);
   if (p.contiguous) {
     if (p.vec)
       glu_fwd_kernel<T, V, false, Act><<<grid, kBlock, 0, s>>>(g, u, ld_in, o, ld_out, n_chunks, cpr, act);
@@ -205,7 +214,7 @@ int launch_bwd(const void* dout, int64_t ld_dout, const void* gate, const void* 
   int vec = p.vec ? V : 1;
   int64_t n_chunks = rows * cols / vec;
   int64_t cpr = cols / vec;
-  int grid = grid_for((n_chunks + kUnroll - 1) / kUnroll, kBlock);
+  int grid = grid_for((n_chunks + Act::kUnroll - 1) / Act::kUnroll, kBlock, kMaxBlocks);
   const T* d = (const T*)dout;
   const T* g = (const T*)gate;
   const T* u = (const T*)up;

@@ -17,6 +17,7 @@ __device__ __forceinline__ float silu_f32(float x) { return x / (1.0f + expf(-x)
 __device__ __forceinline__ float sigmoid_f32(float x) { return 1.0f / (1.0f + expf(-x)); }
 
 struct SiluAct {
+  static constexpr int kUnroll = 2;
   float gm, dm;
   template <class T>
   __device__ __forceinline__ float fwd(float gate, float up) const {
