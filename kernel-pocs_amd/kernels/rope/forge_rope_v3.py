@@ -35,9 +35,11 @@ def _rope_launch(q_in, k_in, q_out, k_out, cos, sin, backward_pass: bool, positi
     assert n_q % n_kv == 0, f"V3 requires n_q % n_kv == 0 (got n_q={n_q}, n_kv={n_kv})."
     L.require_gpu(q_in, k_in, cos, sin)
 
+    # one stride() tuple per tensor: the launch sits on the host's per-step path
+    qs, ks, qos, kos, cs, ss = (t.stride() for t in (q_in, k_in, q_out, k_out, cos, sin))
     cos_has_batch = cos.shape[0] == batch
-    cos_sb = cos.stride(0) if cos_has_batch else 0
-    sin_sb = sin.stride(0) if cos_has_batch else 0
+    cos_sb = cs[0] if cos_has_batch else 0
+    sin_sb = ss[0] if cos_has_batch else 0
     pos = None
     if positions is not None:
         pos = positions.reshape(-1).to(device=q_in.device, dtype=torch.int64).contiguous()
@@ -45,12 +47,12 @@ def _rope_launch(q_in, k_in, q_out, k_out, cos, sin, backward_pass: bool, positi
     L.check(
         L.forge_rope(
             L.dtype_code(q_in.dtype),
-            q_in.data_ptr(), q_in.stride(0), q_in.stride(1), q_in.stride(2),
-            k_in.data_ptr(), k_in.stride(0), k_in.stride(1), k_in.stride(2),
-            q_out.data_ptr(), q_out.stride(0), q_out.stride(1), q_out.stride(2),
-            k_out.data_ptr(), k_out.stride(0), k_out.stride(1), k_out.stride(2),
-            cos.data_ptr(), cos_sb, cos.stride(1),
-            sin.data_ptr(), sin_sb, sin.stride(1),
+            q_in.data_ptr(), qs[0], qs[1], qs[2],
+            k_in.data_ptr(), ks[0], ks[1], ks[2],
+            q_out.data_ptr(), qos[0], qos[1], qos[2],
+            k_out.data_ptr(), kos[0], kos[1], kos[2],
+            cos.data_ptr(), cos_sb, cs[1],
+            sin.data_ptr(), sin_sb, ss[1],
             None if pos is None else pos.data_ptr(),
             batch, n_q, n_kv, seq_len, head_dim, 1 if backward_pass else 0,
             L.stream_of(q_in),
