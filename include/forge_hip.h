@@ -43,7 +43,9 @@ enum {
 /* Library identity / diagnostics. */
 const char* forge_version(void);
 const char* forge_last_error(void);
-/* Number of gfx950 code objects linked in (0 means a broken build). */
+/* 1 when the current HIP device is a gfx950 (hipDeviceProp_t.gcnArchName)
+ * and this library's gfx950 code object loads on it (the attributes of a
+ * probe kernel resolve); 0 otherwise, including when no device is visible. */
 int forge_arch_ok(void);
 
 /* ------------------------------------------------------------------------
@@ -92,15 +94,22 @@ int forge_geglu_bwd(int dtype, const void* dout, int64_t ld_dout,
                     int64_t rows, int64_t cols, int approximate_tanh, void* stream);
 
 /* ------------------------------------------------------------------------
- * RoPE (half-split rotation, GQA: n_q % n_kv == 0)
+ * RoPE (half-split rotation; any n_q, n_kv)
  * ------------------------------------------------------------------------ */
 
 /* Rotates Q [B, n_q, S, D] and K [B, n_kv, S, D] given by element strides
  * (batch, head, seq; the D stride must be 1) into q_out/k_out (same
  * convention).  cos/sin rows are [D] with the given batch/seq strides
  * (batch stride 0 = broadcast); only the first D/2 entries of each row are
- * read.  If `positions` (int64, [B*S]) is non-NULL the cos/sin row of token
- * (b, s) is positions[b*S + s] instead of s.  backward != 0 rotates by -theta.
+ * read.  cos/sin are stored in `table_dtype`: q's dtype, or fp32 for any q
+ * (read as stored, math in fp32, as the reference kernel loads the table).
+ * `table_rows` is the table's extent along the position axis.  If
+ * `positions` (int64, [B*S]) is non-NULL the cos/sin row of token (b, s) is
+ * positions[b*S + s] instead of s; a position outside [0, table_rows) reads
+ * no table memory and gives NaN outputs for that token (callers validate
+ * positions first; without positions table_rows < S is an error).
+ * backward != 0 rotates by -theta.  Any q/k/out strides; in place
+ * (q_out == q, k_out == k) is allowed.
  * Replaces `_forge_rope_v3_kernel` + `_launch_kernel`
  * (kernels/rope/forge_rope_v3.py:32-132). */
 int forge_rope(int dtype,
@@ -110,6 +119,7 @@ int forge_rope(int dtype,
                void* k_out, int64_t ko_sb, int64_t ko_sh, int64_t ko_ss,
                const void* cos, int64_t cos_sb, int64_t cos_ss,
                const void* sin, int64_t sin_sb, int64_t sin_ss,
+               int table_dtype, int64_t table_rows,
                const int64_t* positions,
                int64_t batch, int64_t n_q, int64_t n_kv, int64_t seq_len,
                int64_t head_dim, int backward, void* stream);
@@ -228,8 +238,9 @@ int64_t forge_rmsnorm_bwd_workspace(int dtype, int64_t rows, int64_t cols);
  * Generic GEMM (any strides, fp32 / fp16 / bf16 operands, fp32 accumulation)
  * ------------------------------------------------------------------------ */
 
-/* C[m, n] = alpha * sum_k A[m*a_sm + k*a_sk] * B[k*b_sk + n*b_sn]
- *           + beta * C[m, n] + bias[n]   (bias of the operand dtype, optional)
+/* C[m, n] = act(alpha * sum_k A[m*a_sm + k*a_sk] * B[k*b_sk + n*b_sn]
+ *               + beta * C[m, n] + bias[n])   (bias of the operand dtype,
+ * optional; act = FORGE_GEMM_ACT_NONE, _SILU or _RELU)
  * with one fp32 fmaf per k in increasing k order (deterministic).  Operands
  * of `dtype` (fp32, fp16 or bf16); C of c_dtype = fp32 or dtype, row stride
  * ldc.  Any shape and stride: the path for fp32 / fp16 models and for K or
@@ -242,7 +253,7 @@ int forge_gemm_generic(int64_t M, int64_t N, int64_t K, int dtype,
                        const void* a, int64_t a_sm, int64_t a_sk,
                        const void* b, int64_t b_sk, int64_t b_sn,
                        void* c, int64_t ldc, int c_dtype, float alpha, float beta,
-                       const void* bias, void* stream);
+                       const void* bias, int act, void* stream);
 
 /* ------------------------------------------------------------------------
  * bf16 MFMA GEMM core (fp32 accumulation) with fused LoRA epilogues
@@ -265,10 +276,24 @@ typedef struct forge_gemm_segment {
 enum {
   FORGE_EPI_STORE = 0,          /* C = alpha*acc + beta*C (C dtype = c_dtype) */
   FORGE_EPI_ATOMIC_F32 = 1,     /* C(fp32) += alpha*acc  (split-K partials) */
+  FORGE_EPI_SILU = 2,           /* C = silu(alpha*acc + beta*C)  (split_k 1) */
+  FORGE_EPI_RELU = 3,           /* C = relu(alpha*acc + beta*C)  (split_k 1) */
+  FORGE_EPI_GELU = 4,           /* C = gelu_tanh(alpha*acc + beta*C)  (split_k 1) */
+};
+
+/* Activation of forge_gemm_generic's result. */
+enum {
+  FORGE_GEMM_ACT_NONE = 0,
+  FORGE_GEMM_ACT_SILU = 1,
+  FORGE_GEMM_ACT_RELU = 2,
 };
 
 /* C[M, N] = alpha * sum_s A_s @ B_s + beta * C.  A and B layouts are shared by
- * all segments.  c_dtype is FORGE_DTYPE_BF16 or FORGE_DTYPE_F32.  split_k > 1
+ * all segments.  c_dtype is FORGE_DTYPE_BF16 or FORGE_DTYPE_F32.  The SILU /
+ * RELU / GELU epilogues store the activation of that value (the SiLU one
+ * replaces the cuBLASLt SWISH-epilogue GEMM of the LoRA-MLP inference path,
+ * kernels/lora_mlp/experiments/v4/cublaslt_silu.cu:9-92, with the tanh GELU
+ * and ReLU of the same wrapper's epilogue map).  split_k > 1
  * partitions the K range across workgroups: with FORGE_EPI_ATOMIC_F32 they
  * accumulate into C; with FORGE_EPI_STORE and an fp32 C (beta = 0) split z
  * writes its partial sums to C + z*M*ldc (C holds split_k slices of [M, ldc]),
@@ -299,7 +324,10 @@ enum {
  *                                         the stored bf16 e, g)
  * X [M, H] (row pitch ldx), Wg/Wu [I, H] (pitch ldw), xa [M, 2r] holding
  * (sg X Ag^T | su X Au^T) (pitch ld_xa; NULL or r = 0 disables LoRA),
- * Bg/Bu [I, r] (pitch ldb).  Writes e, g, h [M, I] (pitch ld_out).
+ * Bg/Bu [I, r] (pitch ldb).  Writes e, g, h [M, I] (pitch ld_out); with
+ * e = g = NULL only h is written (the merged-weight inference path: h =
+ * silu(X Wg_eff^T) (X Wu_eff^T) in one GEMM, in place of the SWISH-epilogue
+ * GEMM, plain GEMM and product of lora_mlp_kernel_v5.py:425-460).
  * SiLU replaces phases 1-3 of `_v6_forward_impl`
  * (kernels/lora_mlp/experiments/v6/lora_mlp_kernel_v6.py:373-415: two cuBLAS
  * GEMMs + `_fused_lora_swiglu_kernel`, experiments/v3/lora_mlp_kernel_v3.py:45-138);
@@ -340,9 +368,11 @@ int forge_lora_mlp_down_bwd(int64_t M, int64_t H, int64_t I, int64_t r,
  *   out[:, hq:hq+hkv]     = X Wk^T + xa[:, r:2r]  Bk^T   (rotated if apply_rope)
  *   out[:, hq+hkv:hq+2hkv]= X Wv^T + xa[:, 2r:3r] Bv^T
  * xa holds (sq X Aq^T | sk X Ak^T | sv X Av^T).  RoPE (head_dim 64 or 128)
- * uses bf16 cos/sin tables [*, head_dim] with row pitch cs_ld and row
- * positions[m] for token m (NULL: m).  Q/K are rounded to bf16 before the
- * rotation, as in the unfused path.
+ * uses bf16 cos/sin tables [cs_rows, head_dim] with row pitch cs_ld and row
+ * positions[m] for token m (NULL: m, then cs_rows >= M is required); a
+ * position outside [0, cs_rows) reads no table memory and gives NaN in that
+ * token's Q/K (callers validate positions first).  Q/K are rounded to bf16
+ * before the rotation, as in the unfused path.
  * Replaces `lora_qkv_v2_3` (kernels/lora_qkv/experiments/v2/lora_qkv_kernel_v2_3.py
  * :177-267: one cuBLAS GEMM + `_fused_qkv_epilogue_packed_kernel`) followed by
  * the caller's RoPE (forge/forge/patching/kernels/lora.py:250-264). */
@@ -352,7 +382,7 @@ int forge_lora_qkv_rope(int64_t M, int64_t K, int64_t hq, int64_t hkv, int64_t r
                         const void* xa, int64_t ld_xa,
                         const void* b_q, const void* b_k, const void* b_v, int64_t ldb,
                         void* out, int64_t ld_out,
-                        const void* cos, const void* sin, int64_t cs_ld,
+                        const void* cos, const void* sin, int64_t cs_ld, int64_t cs_rows,
                         const int64_t* positions, int64_t head_dim, int apply_rope,
                         void* stream);
 

@@ -1,6 +1,7 @@
 // Library identity and error reporting for the C ABI.
 #include <stdarg.h>
 #include <stdio.h>
+#include <string.h>
 
 #include "common.h"
 
@@ -28,9 +29,26 @@ extern "C" const char* forge_version(void) { return "forge-hip 0.1 (gfx950)"; }
 
 extern "C" const char* forge_last_error(void) { return g_last_error; }
 
-// Host-side check that the gfx950 code object is present: the probe kernel's
-// function handle resolves only if the fat binary carries a matching image.
+// 1 when the current device is a gfx950 and this library's code object for
+// it loads (the probe kernel's attributes resolve on that device); 0 when no
+// device is visible, the device is another architecture, or the fat binary
+// has no gfx950 image.
 extern "C" int forge_arch_ok(void) {
-  const void* fn = reinterpret_cast<const void*>(&arch_probe_kernel);
-  return fn != nullptr ? 1 : 0;
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0) {
+    (void)hipGetLastError();
+    return 0;
+  }
+  hipDeviceProp_t prop;
+  if (hipGetDeviceProperties(&prop, dev) != hipSuccess) {
+    (void)hipGetLastError();
+    return 0;
+  }
+  if (strncmp(prop.gcnArchName, "gfx950", 6) != 0) return 0;
+  hipFuncAttributes attr;
+  if (hipFuncGetAttributes(&attr, reinterpret_cast<const void*>(&arch_probe_kernel)) != hipSuccess) {
+    (void)hipGetLastError();
+    return 0;
+  }
+  return 1;
 }

@@ -451,7 +451,9 @@ void ce_resident_kernel(CeArgs a) {
       const float p0 = fast_exp2(fmaf(x0, kLog2e, -ml2));
       const float p1 = fast_exp2(fmaf(x1, kLog2e, -ml2));
       d += p0 + p1;
-      w[j / 2] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(p0, p1));
+      // round to nearest (not toward zero): the stored p carries no bias
+      const half2_t ph = {(__fp16)p0, (__fp16)p1};
+      w[j / 2] = __builtin_bit_cast(uint32_t, ph);
     }
     v = make_uint4(w[0], w[1], w[2], w[3]);
   };

@@ -240,7 +240,13 @@ extern "C" int forge_gemm(int64_t M, int64_t N, const forge_gemm_segment* segs, 
     if (c_dtype != FORGE_DTYPE_F32)
       return forge_set_error(FORGE_ERR_INVALID, "gemm: atomic epilogue needs an fp32 C");
     epi = EPI_ATOMIC_F32;
-  } else if (epilogue == FORGE_EPI_STORE) {
+  } else if (epilogue == FORGE_EPI_STORE || epilogue == FORGE_EPI_SILU || epilogue == FORGE_EPI_RELU ||
+             epilogue == FORGE_EPI_GELU) {
+    a.ep.act = epilogue == FORGE_EPI_SILU ? ACT_SILU
+             : epilogue == FORGE_EPI_RELU ? ACT_RELU
+             : epilogue == FORGE_EPI_GELU ? ACT_GELU : ACT_NONE;
+    if (a.ep.act != ACT_NONE && split_k != 1)
+      return forge_set_error(FORGE_ERR_INVALID, "gemm: an activation epilogue needs split_k == 1");
     if (c_dtype == FORGE_DTYPE_BF16) {
       if (split_k != 1)
         return forge_set_error(FORGE_ERR_INVALID, "gemm: split_k needs an fp32 C (partials) or the atomic epilogue");

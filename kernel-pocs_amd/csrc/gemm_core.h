@@ -104,12 +104,17 @@ struct EpiArgs {
   const __bf16* cos;
   const __bf16* sin;
   int64_t cs_ld;             // cos/sin row pitch (elements)
+  int64_t cs_rows;           // cos/sin rows; a position outside [0, cs_rows) gives NaN (no read)
   const int64_t* positions;  // per output row (token); nullptr = row index
   int64_t rope_cols;         // columns [0, rope_cols) are rotated
   int head_dim;              // 64 or 128
   int vec_ok;                // every output / side buffer 16-byte aligned with pitches % 8 == 0
   int64_t split_stride;      // STORE_F32 with split-K: split z writes its partial sums at c + z * split_stride
+  int act;                   // STORE epilogues: activation of the result (ACT_NONE / ACT_SILU / ACT_RELU / ACT_GELU)
 };
+
+// Activations of the STORE epilogues, applied to alpha * acc + beta * C.
+enum EpiAct { ACT_NONE = 0, ACT_SILU = 1, ACT_RELU = 2, ACT_GELU = 3 };
 
 struct GemmArgs {
   int64_t M, N;  // N = output columns
@@ -295,6 +300,15 @@ __device__ __forceinline__ float sigmoid_f(float x) { return __builtin_amdgcn_rc
 __device__ __forceinline__ float silu_f(float x) { return x * sigmoid_f(x); }
 __device__ __forceinline__ float bf16r(float x) { return (float)(__bf16)x; }
 
+// Activation of a STORE epilogue (act is uniform across the launch).
+__device__ __forceinline__ float epi_act(int act, float v) {
+  if (act == ACT_SILU) return silu_f(v);
+  if (act == ACT_RELU) return v > 0.f ? v : 0.f;
+  float a, d;  // ACT_GELU: tanh-approximate GELU
+  fgelu::gelu_and_grad<true>(v, a, d);
+  return a;
+}
+
 // h (before its bf16 rounding) of a GLU forward epilogue from the fp32
 // accumulators e (gate) and g (up).
 //  * SwiGLU: silu(e) g on the fp32 values (lora_mlp_kernel_v6.py:81-151);
@@ -459,13 +473,17 @@ __device__ __forceinline__ void epilogue_staged(const GemmArgs& args,
         for (int q = 0; q < 8; ++q) { e[q] = pg[q]; g[q] = pg[32 + q]; h[q] = glu_fwd_h<EPI>(e[q], g[q]); }
         const int64_t off = m * ep.ld_eg + n;
         if (n + 8 <= N) {
-          st16(ep.e + off, pack8(e));
-          st16(ep.g + off, pack8(g));
+          if (ep.e) {  // training saves e and g; inference (e = g = null) stores h only
+            st16(ep.e + off, pack8(e));
+            st16(ep.g + off, pack8(g));
+          }
           st16((__bf16*)ep.c + m * ep.ldc + n, pack8(h));
         } else {
           for (int q = 0; q < 8 && n + q < N; ++q) {
-            ep.e[off + q] = (__bf16)e[q];
-            ep.g[off + q] = (__bf16)g[q];
+            if (ep.e) {
+              ep.e[off + q] = (__bf16)e[q];
+              ep.g[off + q] = (__bf16)g[q];
+            }
             ((__bf16*)ep.c)[m * ep.ldc + n + q] = (__bf16)h[q];
           }
         }
@@ -502,10 +520,16 @@ __device__ __forceinline__ void epilogue_staged(const GemmArgs& args,
               v[0] += ep.beta * c0.x; v[1] += ep.beta * c0.y; v[2] += ep.beta * c0.z; v[3] += ep.beta * c0.w;
               v[4] += ep.beta * c1.x; v[5] += ep.beta * c1.y; v[6] += ep.beta * c1.z; v[7] += ep.beta * c1.w;
             }
+            if (ep.act)
+#pragma unroll
+              for (int q = 0; q < 8; ++q) v[q] = epi_act(ep.act, v[q]);
             c4[0] = make_float4(v[0], v[1], v[2], v[3]);
             c4[1] = make_float4(v[4], v[5], v[6], v[7]);
           } else {
-            for (int q = 0; q < 8 && n + q < N; ++q) cp[q] = ep.beta != 0.f ? v[q] + ep.beta * cp[q] : v[q];
+            for (int q = 0; q < 8 && n + q < N; ++q) {
+              float o = ep.beta != 0.f ? v[q] + ep.beta * cp[q] : v[q];
+              cp[q] = ep.act ? epi_act(ep.act, o) : o;
+            }
           }
         } else if constexpr (EPI == EPI_STORE_BF16) {
 #pragma unroll
@@ -525,11 +549,15 @@ __device__ __forceinline__ void epilogue_staged(const GemmArgs& args,
 #pragma unroll
               for (int q = 0; q < 8; ++q) v[q] += ep.beta * cv[q];
             }
+            if (ep.act)
+#pragma unroll
+              for (int q = 0; q < 8; ++q) v[q] = epi_act(ep.act, v[q]);
             st16(cp, pack8(v));
           } else {
             for (int q = 0; q < 8 && n + q < N; ++q) {
               float o = v[q];
               if (ep.beta != 0.f) o += ep.beta * (float)cp[q];
+              if (ep.act) o = epi_act(ep.act, o);
               cp[q] = (__bf16)o;
             }
           }
@@ -568,8 +596,13 @@ __device__ __forceinline__ void epilogue_staged(const GemmArgs& args,
             const int d = in_head % half;
             const int64_t pos = ep.positions ? ep.positions[m] : m;
             float cs[8], sn[8];
-            unpack8(ld16(ep.cos + pos * ep.cs_ld + d), cs);
-            unpack8(ld16(ep.sin + pos * ep.cs_ld + d), sn);
+            if (pos >= 0 && pos < ep.cs_rows) {
+              unpack8(ld16(ep.cos + pos * ep.cs_ld + d), cs);
+              unpack8(ld16(ep.sin + pos * ep.cs_ld + d), sn);
+            } else {
+#pragma unroll
+              for (int q = 0; q < 8; ++q) cs[q] = sn[q] = __builtin_nanf("");
+            }
 #pragma unroll
             for (int q = 0; q < 8; ++q) {
               const float x = bf16r(v[q]), xp = bf16r(pp[q]);
@@ -617,11 +650,13 @@ __device__ __forceinline__ void epilogue(const GemmArgs& args, f32x16 (&acc)[BM 
             __bf16* cp = (__bf16*)ep.c + m * ep.ldc + n;
             float o = v;
             if (ep.beta != 0.f) o += ep.beta * (float)(*cp);
+            if (ep.act) o = epi_act(ep.act, o);
             *cp = (__bf16)o;
           } else if constexpr (EPI == EPI_STORE_F32) {
             float* cp = (float*)ep.c + (int64_t)blockIdx.z * ep.split_stride + m * ep.ldc + n;
             float o = v;
             if (ep.beta != 0.f) o += ep.beta * (*cp);
+            if (ep.act) o = epi_act(ep.act, o);
             *cp = o;
           } else {
             atomicAdd((float*)ep.c + m * ep.ldc + n, v);
@@ -644,8 +679,10 @@ __device__ __forceinline__ void epilogue(const GemmArgs& args, f32x16 (&acc)[BM 
           const float e = acc[i][2 * jp][r];
           const float g = acc[i][2 * jp + 1][r];
           const int64_t off = m * ep.ld_eg + n;
-          ep.e[off] = (__bf16)e;
-          ep.g[off] = (__bf16)g;
+          if (ep.e) {
+            ep.e[off] = (__bf16)e;
+            ep.g[off] = (__bf16)g;
+          }
           ((__bf16*)ep.c)[m * ep.ldc + n] = (__bf16)glu_fwd_h<EPI>(e, g);
         }
       }
@@ -683,6 +720,7 @@ __device__ __forceinline__ void epilogue(const GemmArgs& args, f32x16 (&acc)[BM 
         const int64_t m = row_base + i * 32 + 8 * (r / 4) + (r % 4);
         if (m >= M) continue;
         const int64_t pos = ep.positions ? ep.positions[m] : m;
+        const bool pos_ok = pos >= 0 && pos < ep.cs_rows;
 #pragma unroll
         for (int j = 0; j < FN; ++j) {
           const int64_t n = n0 + wn * TN + j * 32 + col_in;
@@ -697,8 +735,8 @@ __device__ __forceinline__ void epilogue(const GemmArgs& args, f32x16 (&acc)[BM 
             for (int q = 0; q < FN; ++q)
               if (q == partner) pv = acc[i][q][r];
             const int d = (int)(n % ep.head_dim) % (ep.head_dim / 2);
-            const float c = (float)ep.cos[pos * ep.cs_ld + d];
-            const float s = (float)ep.sin[pos * ep.cs_ld + d];
+            const float c = pos_ok ? (float)ep.cos[pos * ep.cs_ld + d] : __builtin_nanf("");
+            const float s = pos_ok ? (float)ep.sin[pos * ep.cs_ld + d] : __builtin_nanf("");
             // round the projection to bf16 first: RoPE is applied to the
             // materialised Q/K in the unfused reference path
             const float x = bf16r(v), xp = bf16r(pv);

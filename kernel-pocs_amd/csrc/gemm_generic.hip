@@ -1,4 +1,4 @@
-// Generic GEMM: C[M, N] = alpha * sum_k A(m, k) B(k, n) + beta * C + bias[n].
+// Generic GEMM: C[M, N] = act(alpha * sum_k A(m, k) B(k, n) + beta * C + bias[n]).
 //
 // Any strides (so every layout: X W^T, dY W, dY^T X), fp32 / fp16 / bf16
 // operands, fp32 accumulation with one fmaf per k in increasing k order
@@ -24,7 +24,14 @@ struct GenArgs {
   int64_t ldc;
   const void* bias;
   float alpha, beta;
+  int act;  // FORGE_GEMM_ACT_*: activation applied to the result
 };
+
+__device__ __forceinline__ float gen_act(int act, float v) {
+  if (act == FORGE_GEMM_ACT_SILU) return v * __builtin_amdgcn_rcpf(1.0f + __expf(-v));
+  if (act == FORGE_GEMM_ACT_RELU) return v > 0.f ? v : 0.f;
+  return v;
+}
 
 constexpr int GBM = 64, GBN = 64, GBK = 16;
 
@@ -87,6 +94,7 @@ __global__ __launch_bounds__(256) void generic_gemm_kernel(GenArgs g, int64_t ti
       float v = g.alpha * acc[i][j];
       if (g.beta != 0.f) v += g.beta * to_f32<TC>(C[m * g.ldc + n]);
       if (bias) v += to_f32<T>(bias[n]);
+      if (g.act) v = gen_act(g.act, v);
       C[m * g.ldc + n] = from_f32<TC>(v);
     }
   }
@@ -109,15 +117,18 @@ int launch_generic(const GenArgs& g, int c_dtype, hipStream_t s) {
 
 extern "C" int forge_gemm_generic(int64_t M, int64_t N, int64_t K, int dtype, const void* a, int64_t a_sm,
                                   int64_t a_sk, const void* b, int64_t b_sk, int64_t b_sn, void* c, int64_t ldc,
-                                  int c_dtype, float alpha, float beta, const void* bias, void* stream) {
+                                  int c_dtype, float alpha, float beta, const void* bias, int act,
+                                  void* stream) {
   if (M < 0 || N < 0 || K < 0) return forge_set_error(FORGE_ERR_INVALID, "gemm_generic: negative shape");
   if (dtype != FORGE_DTYPE_F32 && dtype != FORGE_DTYPE_F16 && dtype != FORGE_DTYPE_BF16)
     return forge_set_error(FORGE_ERR_UNSUPPORTED, "gemm_generic: dtype %d", dtype);
   if (c_dtype != FORGE_DTYPE_F32 && c_dtype != dtype)
     return forge_set_error(FORGE_ERR_UNSUPPORTED, "gemm_generic: C dtype %d with operands %d", c_dtype, dtype);
+  if (act != FORGE_GEMM_ACT_NONE && act != FORGE_GEMM_ACT_SILU && act != FORGE_GEMM_ACT_RELU)
+    return forge_set_error(FORGE_ERR_UNSUPPORTED, "gemm_generic: activation %d", act);
   if (M == 0 || N == 0) return FORGE_OK;
   if (!c || (K > 0 && (!a || !b))) return forge_set_error(FORGE_ERR_INVALID, "gemm_generic: null operand");
-  GenArgs g{M, N, K, a, a_sm, a_sk, b, b_sk, b_sn, c, ldc, bias, alpha, beta};
+  GenArgs g{M, N, K, a, a_sm, a_sk, b, b_sk, b_sn, c, ldc, bias, alpha, beta, act};
   hipStream_t s = (hipStream_t)stream;
   switch (dtype) {
     case FORGE_DTYPE_F32: return launch_generic<float>(g, c_dtype, s);

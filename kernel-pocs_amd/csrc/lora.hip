@@ -44,6 +44,8 @@ extern "C" int forge_lora_mlp_gate_up(int64_t M, int64_t H, int64_t I, int64_t r
   if (M < 0 || H < 0 || I < 0 || r < 0) return forge_set_error(FORGE_ERR_INVALID, "lora_mlp_gate_up: shape");
   const int epi = glu_epi(activation, false);
   if (epi < 0) return forge_set_error(FORGE_ERR_INVALID, "lora_mlp_gate_up: activation %d", activation);
+  if ((e == nullptr) != (g == nullptr))
+    return forge_set_error(FORGE_ERR_INVALID, "lora_mlp_gate_up: e and g are both given or both NULL");
   GemmArgs a = {};
   a.M = M;
   a.N = I;
@@ -105,8 +107,8 @@ extern "C" int forge_lora_qkv_rope(int64_t M, int64_t K, int64_t hq, int64_t hkv
                                    const void* b_q, const void* b_k, const void* b_v, int64_t ldb,
                                    void* out, int64_t ld_out,
                                    const void* cos, const void* sin, int64_t cs_ld,
-                                   const int64_t* positions, int64_t head_dim, int apply_rope,
-                                   void* stream) {
+                                   int64_t cs_rows, const int64_t* positions, int64_t head_dim,
+                                   int apply_rope, void* stream) {
   if (M < 0 || K < 0 || hq < 0 || hkv < 0 || r < 0)
     return forge_set_error(FORGE_ERR_INVALID, "lora_qkv_rope: shape");
   if (apply_rope && !(head_dim == 64 || head_dim == 128))
@@ -116,6 +118,9 @@ extern "C" int forge_lora_qkv_rope(int64_t M, int64_t K, int64_t hq, int64_t hkv
     return forge_set_error(FORGE_ERR_UNSUPPORTED,
                            "lora_qkv_rope: projection widths must be multiples of 256 (got %lld, %lld)",
                            (long long)hq, (long long)hkv);
+  if (apply_rope && !positions && cs_rows < M)
+    return forge_set_error(FORGE_ERR_INVALID, "lora_qkv_rope: cos/sin have %lld rows for %lld tokens",
+                           (long long)cs_rows, (long long)M);
   GemmArgs a = {};
   a.M = M;
   a.N = hq + 2 * hkv;
@@ -137,6 +142,7 @@ extern "C" int forge_lora_qkv_rope(int64_t M, int64_t K, int64_t hq, int64_t hkv
   a.ep.cos = (const __bf16*)cos;
   a.ep.sin = (const __bf16*)sin;
   a.ep.cs_ld = cs_ld;
+  a.ep.cs_rows = cs_rows;
   a.ep.positions = positions;
   a.ep.rope_cols = apply_rope ? k1 : 0;
   a.ep.head_dim = (int)(head_dim > 0 ? head_dim : 128);

@@ -36,12 +36,35 @@ struct RopeArgs {
   const void* cos; int64_t cos_sb, cos_ss;
   const void* sin; int64_t sin_sb, sin_ss;
   const int64_t* positions;
+  int64_t table_rows;  // rows of cos/sin along the position axis
   int64_t seq_len, n_q, n_heads, half, chunks, n_hgroups, n_items;
   float sign;  // +1 forward, -1 backward
 };
 
-// I: index type of the item / x offset math (int32_t when every offset fits).
-template <class T, int VEC, class I>
+// VEC table values of type TC, as fp32 (times `scale`).  With kVec the
+// VEC * sizeof(TC) bytes are 16-byte aligned and read as 16-byte vectors.
+template <class TC, int VEC, bool kVec>
+__device__ __forceinline__ void load_table(const TC* p, float scale, float (&out)[VEC]) {
+  constexpr int BYTES = VEC * (int)sizeof(TC);
+  if constexpr (kVec && BYTES % 16 == 0) {
+    constexpr int PER = 16 / (int)sizeof(TC);
+#pragma unroll
+    for (int k = 0; k < BYTES / 16; ++k) {
+      Vec16<TC> v = load16(p + k * PER);
+#pragma unroll
+      for (int j = 0; j < PER; ++j) out[k * PER + j] = scale * to_f32(v.v[j]);
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < VEC; ++j) out[j] = scale * to_f32(p[j]);
+  }
+}
+
+// T: q/k storage type; TC: cos/sin storage type (T, or fp32 tables with
+// narrower q/k: the table is read as stored and the math is fp32, as in the
+// reference kernel).  I: index type of the item / x offset math (int32_t
+// when every offset fits).
+template <class T, class TC, int VEC, class I>
 __global__ __launch_bounds__(kBlock) void rope_kernel(RopeArgs a) {
   constexpr bool kVec16 = VEC * sizeof(T) == 16;
   const I stride = (I)gridDim.x * kBlock;
@@ -61,17 +84,14 @@ __global__ __launch_bounds__(kBlock) void rope_kernel(RopeArgs a) {
     const int64_t sno = (int64_t)b * a.sin_sb + pos * a.sin_ss + col;
 
     float cs[VEC], sn[VEC];
-    {
-      const T* cp = (const T*)a.cos + cso;
-      const T* sp = (const T*)a.sin + sno;
-      if constexpr (kVec16) {
-        Vec16<T> cv = load16(cp), sv = load16(sp);
+    if (pos >= 0 && pos < a.table_rows) {
+      load_table<TC, VEC, kVec16>((const TC*)a.cos + cso, 1.0f, cs);
+      load_table<TC, VEC, kVec16>((const TC*)a.sin + sno, a.sign, sn);
+    } else {
+      // a position outside the table: no table read, the token's outputs
+      // are NaN (the host wrappers reject such positions before launching)
 #pragma unroll
-        for (int j = 0; j < VEC; ++j) { cs[j] = to_f32(cv.v[j]); sn[j] = a.sign * to_f32(sv.v[j]); }
-      } else {
-#pragma unroll
-        for (int j = 0; j < VEC; ++j) { cs[j] = to_f32(cp[j]); sn[j] = a.sign * to_f32(sp[j]); }
-      }
+      for (int j = 0; j < VEC; ++j) { cs[j] = __builtin_nanf(""); sn[j] = cs[j]; }
     }
 
     const I h0 = hg * kHPT;
@@ -127,7 +147,7 @@ int64_t max_offset(int64_t sb, int64_t sh, int64_t ss, int64_t nb, int64_t nh, i
   return ext(sb, nb) + ext(sh, nh) + ext(ss, ns) + d;
 }
 
-template <class T>
+template <class T, class TC>
 int launch(RopeArgs a, bool all_aligned, bool offsets_fit32, hipStream_t s) {
   constexpr int V = 16 / sizeof(T);
   const bool vec = all_aligned && (a.half % V == 0);
@@ -141,11 +161,11 @@ int launch(RopeArgs a, bool all_aligned, bool offsets_fit32, hipStream_t s) {
   const bool i32 = offsets_fit32 && a.n_items + (int64_t)kMaxBlocks * kBlock < 0x7fffffffLL;
   const dim3 grid((unsigned)blocks);
   if (vec) {
-    if (i32) rope_kernel<T, V, int32_t><<<grid, kBlock, 0, s>>>(a);
-    else rope_kernel<T, V, int64_t><<<grid, kBlock, 0, s>>>(a);
+    if (i32) rope_kernel<T, TC, V, int32_t><<<grid, kBlock, 0, s>>>(a);
+    else rope_kernel<T, TC, V, int64_t><<<grid, kBlock, 0, s>>>(a);
   } else {
-    if (i32) rope_kernel<T, 1, int32_t><<<grid, kBlock, 0, s>>>(a);
-    else rope_kernel<T, 1, int64_t><<<grid, kBlock, 0, s>>>(a);
+    if (i32) rope_kernel<T, TC, 1, int32_t><<<grid, kBlock, 0, s>>>(a);
+    else rope_kernel<T, TC, 1, int64_t><<<grid, kBlock, 0, s>>>(a);
   }
   FORGE_CHECK_LAUNCH();
   return FORGE_OK;
@@ -158,13 +178,20 @@ extern "C" int forge_rope(int dtype, const void* q, int64_t q_sb, int64_t q_sh, 
                           int64_t qo_sb, int64_t qo_sh, int64_t qo_ss, void* k_out, int64_t ko_sb,
                           int64_t ko_sh, int64_t ko_ss, const void* cos, int64_t cos_sb,
                           int64_t cos_ss, const void* sin, int64_t sin_sb, int64_t sin_ss,
-                          const int64_t* positions, int64_t batch, int64_t n_q, int64_t n_kv,
-                          int64_t seq_len, int64_t head_dim, int backward, void* stream) {
+                          int table_dtype, int64_t table_rows, const int64_t* positions,
+                          int64_t batch, int64_t n_q, int64_t n_kv, int64_t seq_len,
+                          int64_t head_dim, int backward, void* stream) {
   if (batch < 0 || n_q < 0 || n_kv < 0 || seq_len < 0 || head_dim < 0)
     return forge_set_error(FORGE_ERR_INVALID, "rope: negative shape");
   if (head_dim % 2 != 0) return forge_set_error(FORGE_ERR_INVALID, "rope: head_dim must be even");
-  if (n_kv > 0 && n_q % n_kv != 0)
-    return forge_set_error(FORGE_ERR_INVALID, "rope: n_q %% n_kv != 0");
+  if (table_dtype != dtype && table_dtype != FORGE_DTYPE_F32)
+    return forge_set_error(FORGE_ERR_UNSUPPORTED,
+                           "rope: cos/sin dtype %d with q dtype %d (tables are q's dtype or fp32)",
+                           table_dtype, dtype);
+  if (table_rows < 0) return forge_set_error(FORGE_ERR_INVALID, "rope: negative table_rows");
+  if (!positions && table_rows < seq_len)
+    return forge_set_error(FORGE_ERR_INVALID, "rope: cos/sin have %lld rows for seq_len %lld",
+                           (long long)table_rows, (long long)seq_len);
   if (batch == 0 || seq_len == 0 || head_dim == 0 || (n_q + n_kv) == 0) return FORGE_OK;
 
   RopeArgs a;
@@ -175,6 +202,7 @@ extern "C" int forge_rope(int dtype, const void* q, int64_t q_sb, int64_t q_sh, 
   a.cos = cos; a.cos_sb = cos_sb; a.cos_ss = cos_ss;
   a.sin = sin; a.sin_sb = sin_sb; a.sin_ss = sin_ss;
   a.positions = positions;
+  a.table_rows = table_rows;
   a.seq_len = seq_len;
   a.n_q = n_q;
   a.n_heads = n_q + n_kv;
@@ -183,13 +211,14 @@ extern "C" int forge_rope(int dtype, const void* q, int64_t q_sb, int64_t q_sh, 
   a.sign = backward ? -1.0f : 1.0f;
 
   // 16-byte vectors need every base pointer and every non-unit stride aligned.
-  const size_t es = dtype_size(dtype);
+  const size_t es = dtype_size(dtype), ets = dtype_size(table_dtype);
   const int64_t V = es ? (int64_t)(16 / es) : 1;
+  const int64_t Vt = ets ? (int64_t)(16 / ets) : 1;
   bool al = aligned16(q) && aligned16(k) && aligned16(q_out) && aligned16(k_out) &&
             aligned16(cos) && aligned16(sin);
-  for (int64_t st : {q_sb, q_sh, q_ss, k_sb, k_sh, k_ss, qo_sb, qo_sh, qo_ss, ko_sb, ko_sh, ko_ss,
-                     cos_sb, cos_ss, sin_sb, sin_ss})
+  for (int64_t st : {q_sb, q_sh, q_ss, k_sb, k_sh, k_ss, qo_sb, qo_sh, qo_ss, ko_sb, ko_sh, ko_ss})
     al = al && (st % V == 0);
+  for (int64_t st : {cos_sb, cos_ss, sin_sb, sin_ss}) al = al && (st % Vt == 0);
 
   // 32-bit x offsets when every Q / K / output address fits
   const int64_t lim = 0x7fffffffLL;
@@ -200,11 +229,15 @@ extern "C" int forge_rope(int dtype, const void* q, int64_t q_sb, int64_t q_sh, 
                      batch * seq_len < lim;
 
   hipStream_t s = (hipStream_t)stream;
+  const bool f32_table = table_dtype != dtype;
   switch (dtype) {
-    case FORGE_DTYPE_F32: return launch<float>(a, al, fit32, s);
-    case FORGE_DTYPE_BF16: return launch<bf16_t>(a, al, fit32, s);
-    case FORGE_DTYPE_F16: return launch<fp16_t>(a, al, fit32, s);
-    case FORGE_DTYPE_F64: return launch<double>(a, al, fit32, s);
+    case FORGE_DTYPE_F32: return launch<float, float>(a, al, fit32, s);
+    case FORGE_DTYPE_BF16:
+      return f32_table ? launch<bf16_t, float>(a, al, fit32, s) : launch<bf16_t, bf16_t>(a, al, fit32, s);
+    case FORGE_DTYPE_F16:
+      return f32_table ? launch<fp16_t, float>(a, al, fit32, s) : launch<fp16_t, fp16_t>(a, al, fit32, s);
+    case FORGE_DTYPE_F64:
+      return f32_table ? launch<double, float>(a, al, fit32, s) : launch<double, double>(a, al, fit32, s);
     default: return forge_set_error(FORGE_ERR_UNSUPPORTED, "rope: dtype %d", dtype);
   }
 }

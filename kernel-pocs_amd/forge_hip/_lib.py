@@ -34,7 +34,8 @@ c_vp = ctypes.c_void_p
 
 DTYPE_F32, DTYPE_F16, DTYPE_BF16, DTYPE_F64 = 0, 1, 2, 3
 LAYOUT_ROW, LAYOUT_COL = 0, 1
-EPI_STORE, EPI_ATOMIC_F32 = 0, 1
+EPI_STORE, EPI_ATOMIC_F32, EPI_SILU, EPI_RELU, EPI_GELU = 0, 1, 2, 3, 4
+GEMM_ACT_NONE, GEMM_ACT_SILU, GEMM_ACT_RELU = 0, 1, 2
 ACT_SILU, ACT_GELU_TANH, ACT_GELU_ERF = 0, 1, 2
 
 CE_HAS_GRADIENTS = 1
@@ -91,6 +92,7 @@ forge_rope = _decl(
     [c_int]
     + [c_vp, c_i64, c_i64, c_i64] * 4
     + [c_vp, c_i64, c_i64] * 2
+    + [c_int, c_i64]
     + [c_vp, c_i64, c_i64, c_i64, c_i64, c_i64, c_int, c_vp],
 )
 forge_ce_fwd = _decl(
@@ -119,7 +121,7 @@ forge_lora_qkv_rope = _decl(
     "forge_lora_qkv_rope",
     [c_i64] * 5
     + [c_vp, c_i64, c_vp, c_vp, c_vp, c_i64, c_vp, c_i64, c_vp, c_vp, c_vp, c_i64, c_vp, c_i64]
-    + [c_vp, c_vp, c_i64, c_vp, c_i64, c_int, c_vp],
+    + [c_vp, c_vp, c_i64, c_i64, c_vp, c_i64, c_int, c_vp],
 )
 
 forge_lora_a = _decl(
@@ -134,7 +136,8 @@ forge_ce_target_prob = _decl(
 forge_row_scale = _decl("forge_row_scale", [c_int, c_vp, c_i64, c_i64, c_i64, c_vp, c_vp])
 forge_gemm_generic = _decl(
     "forge_gemm_generic",
-    [c_i64, c_i64, c_i64, c_int, c_vp, c_i64, c_i64, c_vp, c_i64, c_i64, c_vp, c_i64, c_int, c_f32, c_f32, c_vp, c_vp],
+    [c_i64, c_i64, c_i64, c_int, c_vp, c_i64, c_i64, c_vp, c_i64, c_i64, c_vp, c_i64, c_int, c_f32, c_f32, c_vp, c_int,
+     c_vp],
 )
 
 forge_rmsnorm_fwd = _decl(

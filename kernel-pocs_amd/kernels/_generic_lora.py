@@ -54,7 +54,8 @@ def gmm(a: torch.Tensor, b: torch.Tensor, out: Optional[torch.Tensor] = None, al
     assert out.stride(1) == 1 or N == 1
     L.check(L.forge_gemm_generic(M, N, K, L.dtype_code(a.dtype), a.data_ptr(), a.stride(0), a.stride(1),
                                  b.data_ptr(), b.stride(0), b.stride(1), out.data_ptr(), out.stride(0),
-                                 L.dtype_code(out.dtype), float(alpha), float(beta), None, L.stream_of(out)),
+                                 L.dtype_code(out.dtype), float(alpha), float(beta), None, L.GEMM_ACT_NONE,
+                                 L.stream_of(out)),
             "forge_gemm_generic")
     return out
 
@@ -168,6 +169,7 @@ def qkv_forward(X2, W_q, W_k, W_v, A_q, B_q, s_q, A_k, B_k, s_k, A_v, B_v, s_v, 
                              q.data_ptr(), 0, D, out.stride(0), k.data_ptr(), 0, D, out.stride(0),
                              q.data_ptr(), 0, D, out.stride(0), k.data_ptr(), 0, D, out.stride(0),
                              cos.data_ptr(), 0, cos.stride(0), sin.data_ptr(), 0, sin.stride(0),
+                             L.dtype_code(cos.dtype), cos.shape[0],
                              None if pos is None else pos.data_ptr(), 1, Hq // D, Hkv // D, M, D, 0,
                              L.stream_of(out)), "forge_rope")
     return out

@@ -26,7 +26,7 @@ def _mfma_ok(*ts: torch.Tensor) -> bool:
 def _generic(M, N, K, a, a_sm, a_sk, b, b_sk, b_sn, c, ldc, bias=None):
     L.check(L.forge_gemm_generic(M, N, K, L.dtype_code(a.dtype), a.data_ptr(), a_sm, a_sk, b.data_ptr(), b_sk,
                                  b_sn, c.data_ptr(), ldc, L.dtype_code(c.dtype), 1.0, 0.0, L.ptr(bias),
-                                 L.stream_of(c)), "forge_gemm_generic")
+                                 L.GEMM_ACT_NONE, L.stream_of(c)), "forge_gemm_generic")
 
 
 def linear_forward(x2: torch.Tensor, w: torch.Tensor, b: Optional[torch.Tensor]) -> torch.Tensor:

@@ -172,6 +172,29 @@ def frozen_t(w: torch.Tensor, pitch_multiple: int = 1) -> torch.Tensor:
     return wt
 
 
+_CAT_CACHE = {}
+
+
+def frozen_cat(ws: Sequence[torch.Tensor]) -> torch.Tensor:
+    """torch.cat(ws, 0) of frozen base weights, kept like frozen_t: made once
+    and reused while every weight is alive, unmodified (tensor._version) and
+    on the same storage (data_ptr)."""
+    key = tuple(id(w) for w in ws)
+    ent = _CAT_CACHE.get(key)
+    if ent is not None:
+        refs, vers, ptrs, cat = ent
+        if all(r() is w and v == w._version and p == w.data_ptr() for r, v, p, w in zip(refs, vers, ptrs, ws)):
+            return cat
+    cat = torch.cat([w.detach() for w in ws], 0)
+
+    def _drop(_ref, key=key):
+        _CAT_CACHE.pop(key, None)
+
+    _CAT_CACHE[key] = (tuple(weakref.ref(w, _drop) for w in ws), tuple(w._version for w in ws),
+                       tuple(w.data_ptr() for w in ws), cat)
+    return cat
+
+
 def small_t(a: torch.Tensor) -> torch.Tensor:
     """A^T contiguous for a rank-r LoRA matrix (r x features: a few hundred KB)."""
     return a.detach().t().contiguous()

@@ -69,7 +69,7 @@ def _fast_path(x: torch.Tensor, weight: torch.Tensor) -> bool:
 def _generic(M, N, K, dtype, a, a_sm, a_sk, b, b_sk, b_sn, c, ldc, c_dtype, beta=0.0, bias=None):
     L.check(L.forge_gemm_generic(M, N, K, L.dtype_code(dtype), a.data_ptr(), a_sm, a_sk, b.data_ptr(), b_sk, b_sn,
                                  c.data_ptr(), ldc, L.dtype_code(c_dtype), 1.0, float(beta), L.ptr(bias),
-                                 L.stream_of(c)),
+                                 L.GEMM_ACT_NONE, L.stream_of(c)),
             "forge_gemm_generic")
 
 

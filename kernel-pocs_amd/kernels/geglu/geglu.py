@@ -26,9 +26,6 @@ import torch.nn.functional as F
 from forge_hip import _lib as L
 from kernels._linear import linear
 
-FLAT_BLOCK_SIZE = 1024
-INT32_SAFETY_BUFFER = 2**31 - FLAT_BLOCK_SIZE * 4
-
 
 def _check_same_shape_inputs(gate: torch.Tensor, up: torch.Tensor) -> None:
     """geglu.py:19-27."""
@@ -89,11 +86,6 @@ def _check_optional_bias(name, bias, out_features, device=None, dtype=None) -> N
         raise ValueError(f"{name} must be on device {device}, got {bias.device}")
     if dtype is not None and bias.dtype != dtype:
         raise TypeError(f"{name} must have dtype {dtype}, got {bias.dtype}")
-
-
-def _uses_long_indexing(num_elements: int) -> bool:
-    """geglu.py:86-87 (kept for API parity; the HIP kernels index in 64 bits)."""
-    return num_elements > INT32_SAFETY_BUFFER
 
 
 def torch_geglu_reference(gate: torch.Tensor, up: torch.Tensor, approximate: str = "tanh") -> torch.Tensor:

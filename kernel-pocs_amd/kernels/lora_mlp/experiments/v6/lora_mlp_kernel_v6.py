@@ -28,6 +28,14 @@ from kernels.lora_mlp._impl import (  # noqa: F401
     stack_gate_lora_a,
     stack_lora_a,
 )
+from kernels.lora_mlp.experiments.v5.lora_mlp_kernel_v5 import (  # noqa: F401
+    lora_mlp_v5_inference,
+    merge_lora_weights,
+    prepare_inference_weights,
+)
+
+# v6 shares v5's merged-weight inference path (reference v6 :158)
+lora_mlp_v6_inference = lora_mlp_v5_inference
 
 
 def fused_lora_swiglu_inplace(e_base, g_base, xa_gate, xa_up, B_gate, B_up, s_gate=1.0, s_up=1.0, save_eg=True):
@@ -140,5 +148,5 @@ class LoRAMLPv6Module(nn.Module):
 
 __all__ = [
     "LoRAMLPv6", "LoRAMLPv6Module", "lora_mlp_v6", "stack_lora_a", "stack_gate_lora_a", "stack_down_lora_a",
-    "fused_lora_a_stacked", "fused_lora_swiglu_inplace",
+    "fused_lora_a_stacked", "fused_lora_swiglu_inplace", "lora_mlp_v6_inference", "prepare_inference_weights",
 ]

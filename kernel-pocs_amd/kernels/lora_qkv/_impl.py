@@ -34,13 +34,21 @@ def _w(t):
 
 
 def qkv_forward(X2, W_q, W_k, W_v, A_q, B_q, s_q, A_k, B_k, s_k, A_v, B_v, s_v,
-                rope: Optional[dict] = None, aux: Optional[dict] = None):
+                rope: Optional[dict] = None, aux: Optional[dict] = None, a_packed=None):
     """Returns out [M, Hq + 2 Hkv] bf16.  rope = {cos, sin, positions, head_dim}
-    (bf16 tables [P, D]; int64 positions [M]) applies RoPE to Q and K.
+    (tables [P, D]; int64 positions [M], validated by the caller) applies
+    RoPE to Q and K: bf16 tables in the GEMM epilogue, fp32 tables by an
+    in-place forge_rope pass over the stored Q/K (the unfused composition).
     aux (a dict, optional) receives xa = [sq X Aq^T | sk X Ak^T | sv X Av^T]
     for the backward's B gradients.  fp32 / fp16 inputs run on the generic
-    GEMM (kernels/_generic_lora.py; RoPE tables then in X's dtype) and return
-    out in X's dtype."""
+    GEMM (kernels/_generic_lora.py; RoPE tables in X's dtype or fp32) and
+    return out in X's dtype.  a_packed = [A_q; A_k; A_v] (optional) is read
+    as the stacked LoRA-A operand instead of stacking the three."""
+    if rope is not None and X2.dtype == torch.bfloat16 and rope["cos"].dtype != torch.bfloat16:
+        out = qkv_forward(X2, W_q, W_k, W_v, A_q, B_q, s_q, A_k, B_k, s_k, A_v, B_v, s_v, aux=aux,
+                          a_packed=a_packed)
+        rope_qk_inplace(out, W_q.shape[0], W_k.shape[0], rope)
+        return out
     if X2.dtype in G.GENERIC_DTYPES:
         return G.qkv_forward(X2, W_q, W_k, W_v, A_q, B_q, s_q, A_k, B_k, s_k, A_v, B_v, s_v, rope=rope, aux=aux)
     L.require_gpu(X2, W_q, W_k, W_v)
@@ -54,7 +62,8 @@ def qkv_forward(X2, W_q, W_k, W_v, A_q, B_q, s_q, A_k, B_k, s_k, A_v, B_v, s_v,
     xa = None
     Bq = Bk = Bv = None
     if has_lora:
-        xa = lora_a(X2, [A_q, A_k, A_v], [s_q, s_k, s_v])
+        mats = [A_q, A_k, A_v] if a_packed is None else [a_packed[:r], a_packed[r:2 * r], a_packed[2 * r:]]
+        xa = lora_a(X2, mats, [s_q, s_k, s_v])
         Bq, Bk, Bv = _w(B_q), _w(B_k), _w(B_v)
         if aux is not None:
             aux["xa"] = xa
@@ -62,20 +71,36 @@ def qkv_forward(X2, W_q, W_k, W_v, A_q, B_q, s_q, A_k, B_k, s_k, A_v, B_v, s_v,
         cos, sin = rope["cos"], rope["sin"]
         pos = rope.get("positions")
         hd = rope["head_dim"]
-        cos_p, sin_p, cs_ld = cos.data_ptr(), sin.data_ptr(), cos.stride(0)
+        cos_p, sin_p, cs_ld, cs_rows = cos.data_ptr(), sin.data_ptr(), cos.stride(0), cos.shape[0]
         pos_p = None if pos is None else pos.data_ptr()
         apply = 1
     else:
         cos_p = sin_p = pos_p = None
-        cs_ld, hd, apply = 0, 128, 0
+        cs_ld, cs_rows, hd, apply = 0, 0, 128, 0
     L.check(
         L.forge_lora_qkv_rope(
             M, K, Hq, Hkv, r, X2.data_ptr(), ld(X2), Wq.data_ptr(), Wk.data_ptr(), Wv.data_ptr(), ld(Wq),
             L.ptr(xa), 3 * r, L.ptr(Bq), L.ptr(Bk), L.ptr(Bv), r, out.data_ptr(), ld(out),
-            cos_p, sin_p, cs_ld, pos_p, hd, apply, L.stream_of(X2)),
+            cos_p, sin_p, cs_ld, cs_rows, pos_p, hd, apply, L.stream_of(X2)),
         "forge_lora_qkv_rope",
     )
     return out
+
+
+def rope_qk_inplace(out, Hq, Hkv, rope, backward=False):
+    """Rotates the Q and K column blocks of a packed [M, Hq + 2 Hkv] buffer
+    in place with forge_rope (tables in out's dtype or fp32)."""
+    D = rope["head_dim"]
+    cos, sin, pos = rope["cos"], rope["sin"], rope.get("positions")
+    M, ldo = out.shape[0], out.stride(0)
+    q, k = out[:, :Hq], out[:, Hq:Hq + Hkv]
+    L.check(L.forge_rope(L.dtype_code(out.dtype),
+                         q.data_ptr(), 0, D, ldo, k.data_ptr(), 0, D, ldo,
+                         q.data_ptr(), 0, D, ldo, k.data_ptr(), 0, D, ldo,
+                         cos.data_ptr(), 0, cos.stride(0), sin.data_ptr(), 0, sin.stride(0),
+                         L.dtype_code(cos.dtype), cos.shape[0],
+                         None if pos is None else pos.data_ptr(), 1, Hq // D, Hkv // D, M, D,
+                         1 if backward else 0, L.stream_of(out)), "forge_rope")
 
 
 def qkv_backward(dQ, dK, dV, X2, W_q, W_k, W_v, A_q, B_q, s_q, A_k, B_k, s_k, A_v, B_v, s_v,

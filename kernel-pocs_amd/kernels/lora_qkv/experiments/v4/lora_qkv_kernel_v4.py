@@ -4,9 +4,11 @@ Drop-in for kernels/lora_qkv/experiments/v4/lora_qkv_kernel_v4.py of
 Forge-researchlab/kernel-POCs: `LoRAQKVv4Function` (16 forward arguments,
 saves (X, A_q, B_q, A_k, B_k, A_v, B_v, W_dX_packed, A_packed),
 ctx.scalings / ctx.dims, 16-tuple backward), `lora_qkv_v4`,
-`pack_weights_backward`, `pack_lora_a`.  The packed weights are accepted and
-saved when given; they are not built when absent (the backward reads
-W_q/W_k/W_v as separate K segments, so no [Hq+2Hkv, K] copy is made).
+`pack_weights_backward`, `pack_lora_a`.  As in the reference (:209-214) the
+packed matrices are built when not given and saved: A_packed = [A_q; A_k;
+A_v] is also the forward's stacked LoRA-A operand, and W_dX_packed =
+[W_q; W_k; W_v] of the frozen base weights is built once per weight triple
+and reused (the HIP backward reads the cached W^T of each weight).
 
 `LoRAQKVRoPEFunction` / `lora_qkv_rope` add the fusion of the caller's RoPE
 (forge/forge/patching/kernels/lora.py:250-264 for models without q/k norm):
@@ -19,6 +21,8 @@ from __future__ import annotations
 import torch
 
 from forge_hip import _lib as L
+from kernels._lora_ops import frozen_cat
+from kernels._positions import check_positions
 from kernels.lora_qkv._impl import (  # noqa: F401
     pack_lora_a,
     pack_weights_backward,
@@ -44,8 +48,15 @@ class LoRAQKVv4Function(torch.autograd.Function):
         orig_shape = X.shape
         X2 = _flat(X)
         ctx.lora_aux = {}  # forward products reused by the backward (outside saved_tensors)
+        # the packed matrices of the reference's save contract (:209-214)
+        if W_dX_packed is None:
+            W_dX_packed = frozen_cat((W_q, W_k, W_v))
+        a_stack = None  # a caller's A_packed is only saved; the one built here is the stacked operand
+        if A_packed is None:
+            A_packed = a_stack = pack_lora_a(A_q.detach(), A_k.detach(), A_v.detach())
         if use_hip:
-            out = qkv_forward(X2, W_q, W_k, W_v, A_q, B_q, s_q, A_k, B_k, s_k, A_v, B_v, s_v, aux=ctx.lora_aux)
+            out = qkv_forward(X2, W_q, W_k, W_v, A_q, B_q, s_q, A_k, B_k, s_k, A_v, B_v, s_v, aux=ctx.lora_aux,
+                              a_packed=a_stack)
             Q, K, V = split_views(out, W_q.shape[0], W_k.shape[0], orig_shape)
         else:
             Q, K, V = torch_qkv_forward(X2, W_q, W_k, W_v, A_q, B_q, s_q, A_k, B_k, s_k, A_v, B_v, s_v)
@@ -95,6 +106,7 @@ def _rope_rows_backward(d, n_heads, head_dim, cos, sin, positions):
                      out.data_ptr(), 0, head_dim, n_heads * head_dim,
                      out.data_ptr(), 0, head_dim, n_heads * head_dim,
                      cos.data_ptr(), 0, cos.stride(0), sin.data_ptr(), 0, sin.stride(0),
+                     L.dtype_code(cos.dtype), cos.shape[0],
                      positions.data_ptr() if positions is not None else None,
                      1, n_heads, 0, M, head_dim, 1, st),
         "forge_rope(backward)",
@@ -120,6 +132,7 @@ def _rope_qk_backward(dQ, dK, head_dim, cos, sin, positions):
                      oq.data_ptr(), 0, head_dim, nq * head_dim,
                      ok.data_ptr(), 0, head_dim, nk * head_dim,
                      cos.data_ptr(), 0, cos.stride(0), sin.data_ptr(), 0, sin.stride(0),
+                     L.dtype_code(cos.dtype), cos.shape[0],
                      positions.data_ptr() if positions is not None else None,
                      1, nq, nk, M, head_dim, 1, L.stream_of(dQ)),
         "forge_rope(backward)",
@@ -127,24 +140,37 @@ def _rope_qk_backward(dQ, dK, head_dim, cos, sin, positions):
     return oq, ok
 
 
+def _qkv_tables(cos, sin, x_dtype):
+    """2-D contiguous cos/sin in one dtype the kernels read as stored:
+    X's dtype or fp32 (another dtype, or a mixed pair, is widened to fp32)."""
+    cos2, sin2 = cos.reshape(-1, cos.shape[-1]), sin.reshape(-1, sin.shape[-1])
+    if not (cos2.dtype == sin2.dtype and cos2.dtype in (x_dtype, torch.float32)):
+        cos2, sin2 = cos2.float(), sin2.float()
+    return cos2.contiguous(), sin2.contiguous()
+
+
 class LoRAQKVRoPEFunction(torch.autograd.Function):
     """LoRA-QKV with RoPE fused into the GEMM epilogue.
 
     forward(ctx, X, W_q, W_k, W_v, A_q, B_q, s_q, A_k, B_k, s_k, A_v, B_v, s_v,
             cos, sin, positions, head_dim) -> (Q_rot, K_rot, V)
-    cos/sin: tables [P, head_dim] (rows = positions; used in bf16 for bf16
-    X, else in X's dtype); positions: int64 [M] (token -> table row;
-    restarts per sequence for packed varlen)."""
+    cos/sin: tables [P, head_dim] (rows = positions), read as stored when in
+    X's dtype or fp32 (fp32 math either way), else widened to fp32; bf16
+    tables with bf16 X rotate in the GEMM epilogue, fp32 tables in a
+    forge_rope pass over the stored Q/K.  positions: int64 [M] in [0, P)
+    (token -> table row; restarts per sequence for packed varlen;
+    IndexError otherwise); None means row m for token m."""
 
     @staticmethod
     def forward(ctx, X, W_q, W_k, W_v, A_q, B_q, s_q, A_k, B_k, s_k, A_v, B_v, s_v, cos, sin, positions,
                 head_dim=128):
         orig_shape = X.shape
         X2 = _flat(X)
-        tdt = torch.bfloat16 if X.dtype == torch.bfloat16 else X.dtype  # fp32 / fp16: tables in X's dtype
-        cos2 = cos.reshape(-1, cos.shape[-1]).to(tdt).contiguous()
-        sin2 = sin.reshape(-1, sin.shape[-1]).to(tdt).contiguous()
-        pos = positions.reshape(-1).to(device=X.device, dtype=torch.int64).contiguous() if positions is not None else None
+        cos2, sin2 = _qkv_tables(cos, sin, X.dtype)
+        pos = None
+        if positions is not None:
+            check_positions(positions, cos2.shape[0])
+            pos = positions.reshape(-1).to(device=X.device, dtype=torch.int64).contiguous()
         ctx.lora_aux = {}  # forward products reused by the backward (outside saved_tensors)
         out = qkv_forward(X2, W_q, W_k, W_v, A_q, B_q, s_q, A_k, B_k, s_k, A_v, B_v, s_v,
                           rope={"cos": cos2, "sin": sin2, "positions": pos, "head_dim": int(head_dim)},

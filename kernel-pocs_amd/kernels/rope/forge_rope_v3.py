@@ -12,7 +12,12 @@ Differences that keep values identical:
     no `.contiguous()` copy (reference :179-180 copies).  Outputs are allocated
     with `torch.empty_like`, i.e. in the input's memory layout.
   * `apply_rope(..., positions=...)` (optional, int64 [B*S] or [B, S]) selects
-    the cos/sin row per token, for packed variable-length sequences.
+    the cos/sin row per token, for packed variable-length sequences; every
+    position must lie in [0, cos.shape[-2]) (IndexError otherwise).
+  * cos/sin are read as stored: a table in q's dtype or in fp32 goes to the
+    kernel unchanged (fp32 math either way, as the reference kernel loads
+    the table and computes in fp32); another table dtype is widened to fp32,
+    which is exact.
 """
 from __future__ import annotations
 
@@ -22,17 +27,25 @@ from typing import Optional
 import torch
 
 from forge_hip import _lib as L
+from kernels._positions import check_positions
 
 # launch geometry of csrc/rope.hip (fixed; there is no autotuning)
 _BLOCK = 256
 _HEADS_PER_ITEM = 4
 
 
-def _rope_launch(q_in, k_in, q_out, k_out, cos, sin, backward_pass: bool, positions=None):
-    """Replaces `_launch_kernel` (kernels/rope/forge_rope_v3.py:99-132)."""
+_V3_DIVISIBLE = "V3 requires n_q % n_kv == 0 (got n_q={n_q}, n_kv={n_kv})."
+
+
+def _rope_launch(q_in, k_in, q_out, k_out, cos, sin, backward_pass: bool, positions=None,
+                 divisible_msg=_V3_DIVISIBLE):
+    """Replaces `_launch_kernel` (kernels/rope/forge_rope_v3.py:99-132; v2's
+    forge_rope_v2.py:103-136 with its own message; v1's forge_rope_v1.py:
+    98-124 has no divisibility check)."""
     batch, n_q, seq_len, head_dim = q_in.shape
     n_kv = k_in.shape[1]
-    assert n_q % n_kv == 0, f"V3 requires n_q % n_kv == 0 (got n_q={n_q}, n_kv={n_kv})."
+    if divisible_msg is not None:
+        assert n_q % n_kv == 0, divisible_msg.format(n_q=n_q, n_kv=n_kv)
     L.require_gpu(q_in, k_in, cos, sin)
 
     # one stride() tuple per tensor: the launch sits on the host's per-step path
@@ -53,6 +66,7 @@ def _rope_launch(q_in, k_in, q_out, k_out, cos, sin, backward_pass: bool, positi
             k_out.data_ptr(), kos[0], kos[1], kos[2],
             cos.data_ptr(), cos_sb, cs[1],
             sin.data_ptr(), sin_sb, ss[1],
+            L.dtype_code(cos.dtype), cos.shape[1],
             None if pos is None else pos.data_ptr(),
             batch, n_q, n_kv, seq_len, head_dim, 1 if backward_pass else 0,
             L.stream_of(q_in),
@@ -67,9 +81,19 @@ def _unit_last(t: torch.Tensor) -> torch.Tensor:
 
 
 def _cos_sin_like(cos: torch.Tensor, q: torch.Tensor) -> torch.Tensor:
-    # the reference kernel reads cos/sin as stored and computes in fp32; a
-    # table in another dtype than q is cast once so the kernel reads one type
-    return _unit_last(cos if cos.dtype == q.dtype else cos.to(q.dtype))
+    # the reference kernel reads cos/sin as stored and computes in fp32: a
+    # table in q's dtype or fp32 is passed as is, any other is widened to
+    # fp32 (exact for bf16 / fp16; float64 rounds as the reference's load does)
+    if cos.dtype not in (q.dtype, torch.float32):
+        cos = cos.to(torch.float32)
+    return _unit_last(cos)
+
+
+def _tables(cos: torch.Tensor, sin: torch.Tensor, q: torch.Tensor):
+    cos, sin = _cos_sin_like(cos, q), _cos_sin_like(sin, q)
+    if cos.dtype != sin.dtype:  # the kernel reads both tables in one dtype
+        cos, sin = cos.float(), sin.float()
+    return cos, sin
 
 
 def get_autotune_cache_for(q, k, cos, sin, backward_pass: bool = False):
@@ -87,6 +111,7 @@ def get_autotune_cache_for(q, k, cos, sin, backward_pass: bool = False):
 
 
 def _rope_forward(ctx, q, k, cos, sin, positions):
+    """v3's checks (kernels/rope/forge_rope_v3.py:165-176), then the launch."""
     assert q.dim() == 4
     assert k.dim() == 4
     assert cos.dim() == 3 and sin.dim() == 3
@@ -102,17 +127,26 @@ def _rope_forward(ctx, q, k, cos, sin, positions):
         assert cos.shape[2] == head_dim
     assert sin.shape == cos.shape
     assert head_dim & (head_dim - 1) == 0
+    if positions is not None:
+        check_positions(positions, cos.shape[1])
+    return rope_forward_checked(ctx, q, k, cos, sin, positions, _V3_DIVISIBLE)
 
+
+def rope_forward_checked(ctx, q, k, cos, sin, positions=None, divisible_msg=_V3_DIVISIBLE):
+    """The forward launch shared by the v1 / v2 / v3 Functions once their
+    own shape checks have passed: out-of-place outputs in q/k's layout,
+    (cos, sin) saved as given."""
     q = _unit_last(q)
     k = _unit_last(k)
-    cos = _cos_sin_like(cos, q)
-    sin = _cos_sin_like(sin, q)
+    cos_t, sin_t = _tables(cos, sin, q)
 
     out_q = torch.empty_like(q)
     out_k = torch.empty_like(k)
-    pos = _rope_launch(q, k, out_q, out_k, cos, sin, backward_pass=False, positions=positions)
-    ctx.save_for_backward(cos, sin)
+    pos = _rope_launch(q, k, out_q, out_k, cos_t, sin_t, backward_pass=False, positions=positions,
+                       divisible_msg=divisible_msg)
+    ctx.save_for_backward(cos, sin)  # the caller's tables, as the reference saves them
     ctx.positions = pos
+    ctx.divisible_msg = divisible_msg
     return out_q, out_k
 
 
@@ -120,9 +154,11 @@ def _rope_backward(ctx, dq, dk):
     cos, sin = ctx.saved_tensors
     dq = _unit_last(dq)
     dk = _unit_last(dk)
+    cos, sin = _tables(cos, sin, dq)
     dq_in = torch.empty_like(dq)
     dk_in = torch.empty_like(dk)
-    _rope_launch(dq, dk, dq_in, dk_in, cos, sin, backward_pass=True, positions=ctx.positions)
+    _rope_launch(dq, dk, dq_in, dk_in, cos, sin, backward_pass=True, positions=ctx.positions,
+                 divisible_msg=getattr(ctx, "divisible_msg", _V3_DIVISIBLE))
     return dq_in, dk_in
 
 
@@ -185,4 +221,5 @@ def rope_cos_sin(positions: torch.Tensor, head_dim: int, base: float = 10000.0,
     return emb.cos().to(dtype), emb.sin().to(dtype)
 
 
-__all__ = ["apply_rope", "ForgeRoPEv3Function", "ForgeRoPEPositionsFunction", "ForgeRoPEv3", "get_autotune_cache_for", "rope_cos_sin"]
+__all__ = ["apply_rope", "ForgeRoPEv3Function", "ForgeRoPEPositionsFunction", "ForgeRoPEv3", "get_autotune_cache_for",
+           "rope_cos_sin"]

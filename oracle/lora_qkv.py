@@ -91,3 +91,14 @@ def flops_per_token(K, Hq, Hkv, r):
     forward 2KN + 6Kr + 2rN, backward 2NK + 2Nr + 18Kr + 2Nr, N = Hq + 2Hkv."""
     N = Hq + 2 * Hkv
     return 4 * K * N + 6 * r * N + 24 * K * r
+
+
+def lora_grads(dQ, dK, dV, X, W_q, W_k, W_v, A_q, B_q, s_q, A_k, B_k, s_k, A_v, B_v, s_v):
+    """The LoRA-parameter part of `backward` alone (lora_qkv_pytorch.py:
+    196-211): (dA_q, dB_q, dA_k, dB_k, dA_v, dB_v) with dA = s (dY B)^T X and
+    dB = s dY^T (X A^T).  It skips backward's [T, K] dX products, so it runs
+    over tens of thousands of tokens on the CPU."""
+    out = []
+    for dY, A, B, s in ((dQ, A_q, B_q, s_q), (dK, A_k, B_k, s_k), (dV, A_v, B_v, s_v)):
+        out += [s * ((dY @ B).t() @ X), s * (dY.t() @ (X @ A.t()))]
+    return tuple(out)

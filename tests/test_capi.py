@@ -5,6 +5,8 @@ import ctypes
 import re
 from pathlib import Path
 
+import pytest
+
 from forge_hip import _lib as L
 
 HEADER = Path(__file__).resolve().parents[1] / "include" / "forge_hip.h"
@@ -31,7 +33,23 @@ def test_library_exports_every_declared_symbol():
 
 def test_identity():
     assert L.forge_version().startswith(b"forge-hip")
-    assert L.forge_arch_ok() == 1
+
+
+def test_arch_check_reports_no_device_without_a_gpu():
+    import torch
+
+    if torch.cuda.is_available():
+        pytest.skip("a GPU is visible: covered by test_arch_check_on_the_gpu")
+    assert L.forge_arch_ok() == 0
+
+
+@pytest.mark.gpu
+def test_arch_check_on_the_gpu():
+    import torch
+
+    torch.cuda.init()
+    name = torch.cuda.get_device_properties(0).gcnArchName
+    assert L.forge_arch_ok() == (1 if name.startswith("gfx950") else 0)
 
 
 def test_status_codes_and_messages():
@@ -40,12 +58,19 @@ def test_status_codes_and_messages():
     assert rc == 2 and b"dtype" in L.forge_last_error()
     rc = L.forge_swiglu_fwd(0, 16, 16, 4, 16, 8, 4, 8, 1.0, 1.0, None)  # ld < cols
     assert rc == 1
-    rc = L.forge_rope(2, *([16, 0, 0, 0] * 4), *([16, 0, 0] * 2), None, 1, 4, 3, 8, 128, 0, None)
-    assert rc == 1 and b"n_q" in L.forge_last_error()
+    rc = L.forge_rope(2, *([16, 0, 0, 0] * 4), *([16, 0, 0] * 2), 2, 8, None, 1, 4, 3, 8, 127, 0, None)
+    assert rc == 1 and b"even" in L.forge_last_error()
+    # cos/sin dtype other than q's or fp32; too few table rows without positions
+    rc = L.forge_rope(2, *([16, 0, 0, 0] * 4), *([16, 0, 0] * 2), 1, 8, None, 1, 4, 2, 8, 128, 0, None)
+    assert rc == 2 and b"cos/sin dtype" in L.forge_last_error()
+    rc = L.forge_rope(2, *([16, 0, 0, 0] * 4), *([16, 0, 0] * 2), 2, 7, None, 1, 4, 2, 8, 128, 0, None)
+    assert rc == 1 and b"7 rows" in L.forge_last_error()
     rc = L.forge_ce_fwd(2, 16, 4, 2, 8, 16, 1, None, None, None, None, None, -100, *([0.0] * 6), 0, None, None)
     assert rc == 1 and b"ld" in L.forge_last_error()
-    rc = L.forge_lora_qkv_rope(16, 64, 100, 256, 0, *([16] * 20)[:14], 16, 16, 8, None, 96, 1, None)
+    rc = L.forge_lora_qkv_rope(16, 64, 100, 256, 0, *([16] * 20)[:14], 16, 16, 8, 16, None, 96, 1, None)
     assert rc == 2
+    rc = L.forge_lora_qkv_rope(16, 64, 256, 256, 0, *([16] * 20)[:14], 16, 16, 8, 15, None, 128, 1, None)
+    assert rc == 1 and b"15 rows" in L.forge_last_error()
     # an unknown gated activation of the fused LoRA-MLP entry points
     rc = L.forge_lora_mlp_gate_up(16, 64, 64, 0, *([16] * 13), 64, 3, None)
     assert rc == 1 and b"activation 3" in L.forge_last_error()

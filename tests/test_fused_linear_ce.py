@@ -261,13 +261,13 @@ def test_gemm_generic_layouts(dtype, layout):
     C = C0.to(DEV)
     L.check(L.forge_gemm_generic(M, N, K, L.dtype_code(dtype), a.data_ptr(), a_sm, a_sk, b.data_ptr(), b_sk, b_sn,
                                  C.data_ptr(), N, L.DTYPE_F32, 0.5, 2.0, bias.to(DEV).data_ptr(),
-                                 L.stream_of(C)), "forge_gemm_generic")
+                                 L.GEMM_ACT_NONE, L.stream_of(C)), "forge_gemm_generic")
     torch.testing.assert_close(C.cpu().double(), ref, rtol=1e-5, atol=1e-4)
 
 
 def test_gemm_generic_rejects_bad_arguments():
     assert L.forge_gemm_generic(2, 2, 2, L.DTYPE_F64, None, 2, 1, None, 2, 1, None, 2, L.DTYPE_F32, 1.0, 0.0,
-                                None, None) != 0
+                                None, 0, None) != 0
     assert b"dtype" in L.forge_last_error()
 
 

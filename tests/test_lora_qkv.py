@@ -137,3 +137,107 @@ def test_lora_qkv_fp64_gradcheck_uses_reference_torch_path():
         return LoRAQKVv4Function.apply(x, params[0], params[1], params[2], aq, bq, params[5], ak, bk, params[8],
                                        av, bv, params[11])
     assert torch.autograd.gradcheck(f, (X, *lora))
+
+
+def _baseline_rows(lens, T, tile=256):
+    """Token rows checked at full size: the first and last rows of every
+    sequence (and their neighbours), the first rows of the batch, and the
+    last partial 256-row GEMM tile."""
+    rows = set(range(0, 48))
+    start = 0
+    for n in lens:
+        for r in (start, start + 1, start + 2, start + n - 3, start + n - 2, start + n - 1):
+            if 0 <= r < T:
+                rows.add(r)
+        start += n
+    last_tile = (T // tile) * tile
+    rows.update(range(max(0, last_tile - 8), min(T, last_tile + 24)))
+    rows.update(range(T - 48, T))
+    return torch.tensor(sorted(rows))
+
+
+@pytest.mark.gpu
+def test_lora_qkv_rope_baseline_config():
+    """BASELINE configs[4] at its own size: hidden 4096, 32 Q / 8 KV heads,
+    head_dim 128, r = 64, alpha = 128, RoPE base 500000, 8 packed sequences
+    with lengths U[512, 4096] from seed 4 (T = 22954, as bench.py builds it).
+    Q/K/V and dX rows depend only on the same token rows, so the oracle runs
+    on sequence starts/ends and the last partial tile; the LoRA gradients
+    are token sums, so they are checked over ALL tokens against the oracle's
+    LoRA-gradient products fed with dQ/dK rotated back by -theta (the
+    adjoint rotation, pinned in tests/test_oracle.py)."""
+    K, Hq, Hkv, D, r, alpha = 4096, 4096, 1024, 128, 64, 128
+    lens = orc.varlen_lengths(8, 512, 4096, seed=4)
+    pos = orc.positions_for(lens)
+    T = int(pos.numel())
+    assert T == 22954
+    print(f"lora_qkv_rope baseline: T={T} lens={lens}", flush=True)
+    gen = torch.Generator().manual_seed(4)
+    params = orc.make_params(K, Hq, Hkv, r, alpha, gen)
+    X = torch.randn(T, K, generator=gen).to(torch.bfloat16)
+    dQ = torch.randn(T, Hq, generator=gen).to(torch.bfloat16)
+    dK = torch.randn(T, Hkv, generator=gen).to(torch.bfloat16)
+    dV = torch.randn(T, Hkv, generator=gen).to(torch.bfloat16)
+    c, s = cos_sin(torch.arange(max(lens)), D, 500000.0, torch.bfloat16)
+
+    p = _cuda(params)
+    x = X.cuda().requires_grad_(True)
+    Q, K_, V = lora_qkv_rope(x, p[0], p[3], p[4], p[5], p[1], p[6], p[7], p[8], p[2], p[9], p[10], p[11],
+                             c.cuda(), s.cuda(), pos.cuda(), D)
+    torch.autograd.backward((Q, K_, V), (dQ.cuda(), dK.cuda(), dV.cuda()))
+    torch.cuda.synchronize()
+
+    rows = _baseline_rows(lens, T)
+    pr = pos[rows]
+    (Qr, Kr, Vr), ref_grads = orc.qkv_rope_fwd_bwd(X[rows], dQ[rows], dK[rows], dV[rows], params,
+                                                    c[pr], s[pr], D)
+    rc = rows.cuda()
+    for a, b, n in ((Q[rc], Qr, "Q rows"), (K_[rc], Kr, "K rows"), (V[rc], Vr, "V rows"),
+                    (x.grad[rc], ref_grads[0], "dX rows")):
+        _close_bf16(a, b, n)
+
+    # LoRA gradients over every token
+    f = lambda t: t.float() if isinstance(t, torch.Tensor) else t  # noqa: E731
+    pf = [f(t) for t in params]
+    ct, st = c[pos].float(), s[pos].float()
+    dQu = orc.rope_rows(dQ.float(), ct, -st, D)
+    dKu = orc.rope_rows(dK.float(), ct, -st, D)
+    ref_lora = orc.lora_grads(dQu, dKu, dV.float(), X.float(), *pf)
+    got = [p[3].grad, p[4].grad, p[6].grad, p[7].grad, p[9].grad, p[10].grad]
+    for n, a, b in zip(NAMES[1:], got, ref_lora):
+        _close_bf16(a, b, n + " (all tokens)")
+
+
+def test_lora_qkv_rope_positions_out_of_range_raise():
+    """Token positions index the cos/sin rows: out-of-range values raise
+    IndexError before any launch (CPU tensors here)."""
+    gen = torch.Generator().manual_seed(3)
+    params = orc.make_params(64, 128, 128, 4, 8, gen)
+    X = torch.randn(5, 64, generator=gen).to(torch.bfloat16)
+    c, s = cos_sin(torch.arange(6), 64, 10000.0, torch.bfloat16)
+    p = list(params)
+    with pytest.raises(IndexError, match=r"\[0, 6\)"):
+        lora_qkv_rope(X, p[0], p[3], p[4], p[5], p[1], p[6], p[7], p[8], p[2], p[9], p[10], p[11],
+                      c, s, torch.tensor([0, 1, 2, 6, 0]), 64)
+
+
+@pytest.mark.gpu
+def test_lora_qkv_v4_saves_packed_matrices():
+    """v4's save_for_backward contract (reference lora_qkv_kernel_v4.py:
+    209-214): (X, A_q, B_q, A_k, B_k, A_v, B_v, W_dX_packed, A_packed), with
+    the packed matrices built when not given; given ones are saved as is."""
+    gen = torch.Generator().manual_seed(12)
+    T, K, Hq, Hkv, r = 64, 256, 256, 128, 16
+    p = _cuda(orc.make_params(K, Hq, Hkv, r, 32, gen))
+    x = torch.randn(T, K, generator=gen).to(torch.bfloat16).cuda().requires_grad_(True)
+    Q, _, _ = LoRAQKVv4Function.apply(x, *p)
+    saved = Q.grad_fn.saved_tensors
+    assert len(saved) == 9
+    assert saved[0] is x or torch.equal(saved[0], x)
+    assert torch.equal(saved[7], torch.cat([p[0], p[1], p[2]]))
+    assert torch.equal(saved[8], torch.cat([p[3], p[6], p[9]]))
+    W_dX, A_pack = pack_weights_backward(p[0], p[1], p[2]), pack_lora_a(p[3], p[6], p[9]).detach()
+    Q2, _, _ = LoRAQKVv4Function.apply(x, *p, None, W_dX, A_pack)
+    s2 = Q2.grad_fn.saved_tensors
+    assert s2[7].data_ptr() == W_dX.data_ptr() and s2[8].data_ptr() == A_pack.data_ptr()
+    torch.testing.assert_close(Q2, Q, rtol=0, atol=0)

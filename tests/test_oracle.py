@@ -470,6 +470,23 @@ def test_lora_qkv_rope_backward_is_adjoint_rotation():
         torch.testing.assert_close(got, exp, rtol=1e-10, atol=1e-12)
 
 
+def test_lora_qkv_lora_grads_equal_backward_parts():
+    """lora_grads is backward's LoRA-parameter part (backward is pinned by
+    autograd above); a slip in one of its products (e.g. dB from X instead of
+    X A^T) would not keep the shapes and values equal."""
+    p = _qkv_params(seed=11)
+    g = torch.Generator().manual_seed(12)
+    X = torch.randn(7, 16, generator=g, dtype=torch.float64)
+    dQ = torch.randn(7, 16, generator=g, dtype=torch.float64)
+    dK = torch.randn(7, 8, generator=g, dtype=torch.float64)
+    dV = torch.randn(7, 8, generator=g, dtype=torch.float64)
+    full = oqkv.backward(dQ, dK, dV, X, *p)
+    part = oqkv.lora_grads(dQ, dK, dV, X, *p)
+    assert len(part) == 6
+    for got, exp in zip(part, full[1:]):
+        torch.testing.assert_close(got, exp, rtol=1e-12, atol=1e-12)
+
+
 def test_lora_qkv_rope_rows_matches_complex_rotation():
     D = 8
     Y = torch.randn(4, 3 * D, generator=torch.Generator().manual_seed(8), dtype=torch.float64)

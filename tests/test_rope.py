@@ -120,6 +120,93 @@ def test_rope_varlen_positions():
     _close(ok, rk.to(dtype), dtype)
 
 
+def test_rope_positions_out_of_range_raise_before_launch():
+    """Positions index the cos/sin rows: values outside [0, P) are rejected
+    (IndexError) before any launch, here on CPU tensors."""
+    from kernels._positions import check_positions
+
+    q = torch.zeros(1, 2, 6, 64)
+    k = torch.zeros(1, 1, 6, 64)
+    c, s = cos_sin(torch.arange(8), 64, 10000.0, torch.float32)
+    c, s = c.unsqueeze(0), s.unsqueeze(0)
+    for bad in ([0, 1, 2, 3, 4, 8], [0, -1, 2, 3, 4, 5]):
+        with pytest.raises(IndexError, match=r"positions must lie in \[0, 8\)"):
+            apply_rope(q, k, c, s, positions=torch.tensor(bad))
+    # a valid buffer is checked once per version; writing into it re-checks
+    pos = torch.tensor([0, 1, 2, 3, 4, 7])
+    check_positions(pos, 8)
+    pos[5] = 9
+    with pytest.raises(IndexError, match="max 9"):
+        check_positions(pos, 8)
+    with pytest.raises(TypeError):
+        check_positions(torch.zeros(3), 8)
+
+
+@pytest.mark.gpu
+def test_rope_fp32_tables_with_bf16_q_are_read_as_stored():
+    """fp32 cos/sin with bf16 q/k: the kernel reads the fp32 table (no bf16
+    rounding of cos/sin) and computes in fp32, as the reference kernel does.
+    The result equals the fp32-math oracle rounded once (all but a few
+    elements bit-equal, the rest within one bf16 ulp), while a bf16-rounded table
+    gives a visibly different result."""
+    b, nq, nkv, S, d = 2, 8, 2, 256, 128
+    g = torch.Generator().manual_seed(21)
+    q = torch.randn(b, nq, S, d, generator=g).to(torch.bfloat16)
+    k = torch.randn(b, nkv, S, d, generator=g).to(torch.bfloat16)
+    c32, s32 = cos_sin(torch.arange(S) * 37, d, 10000.0, torch.float32)  # large angles: cos/sin far from bf16 grid
+    dq = torch.randn(q.shape, generator=g).to(torch.bfloat16)
+    dk = torch.randn(k.shape, generator=g).to(torch.bfloat16)
+    rq, rk, rdq, rdk = rope_fwd_bwd(q, k, c32.unsqueeze(0), s32.unsqueeze(0), dq, dk)
+    qg = q.cuda().requires_grad_(True)
+    kg = k.cuda().requires_grad_(True)
+    oq, ok = apply_rope(qg, kg, c32.unsqueeze(0).cuda(), s32.unsqueeze(0).cuda())
+    torch.autograd.backward((oq, ok), (dq.cuda(), dk.cuda()))
+    for a, ref in ((oq, rq), (ok, rk), (qg.grad, rdq), (kg.grad, rdk)):
+        a = a.detach().cpu()
+        diff = (a.float() - ref.float()).abs()
+        # one bf16 ulp, plus 1e-5 absolute where x cos - y sin cancels (the
+        # fp32 evaluation order then moves a tiny result by more than an ulp)
+        ulp = ref.float().abs() * 2.0 ** -7 + 1e-5
+        assert bool((diff <= ulp).all())
+        assert (a == ref).float().mean().item() > 0.99
+    cb, sb = c32.to(torch.bfloat16), s32.to(torch.bfloat16)
+    oq_b, _ = apply_rope(q.cuda(), k.cuda(), cb.unsqueeze(0).cuda(), sb.unsqueeze(0).cuda())
+    assert (oq_b.cpu() != oq.detach().cpu()).float().mean().item() > 0.05
+
+
+@pytest.mark.gpu
+def test_rope_c_abi_position_outside_table_reads_nothing():
+    """Called through the C ABI directly (no host validation), a position
+    outside [0, table_rows) gives NaN for that token and reads no table
+    memory; every other token is rotated as usual."""
+    from forge_hip import _lib as L
+
+    T, nq, nkv, d, P = 64, 4, 2, 128, 40
+    g = torch.Generator().manual_seed(5)
+    q = torch.randn(1, nq, T, d, generator=g).to(torch.bfloat16).cuda()
+    k = torch.randn(1, nkv, T, d, generator=g).to(torch.bfloat16).cuda()
+    c, s = (t.cuda() for t in cos_sin(torch.arange(P), d, 10000.0, torch.bfloat16))
+    pos = torch.randint(0, P, (T,), generator=g)
+    pos[3], pos[60] = P, -2
+    pos = pos.cuda()
+    oq, ok = torch.empty_like(q), torch.empty_like(k)
+    qs, ks = q.stride(), k.stride()
+    L.check(L.forge_rope(L.DTYPE_BF16, q.data_ptr(), qs[0], qs[1], qs[2], k.data_ptr(), ks[0], ks[1], ks[2],
+                         oq.data_ptr(), qs[0], qs[1], qs[2], ok.data_ptr(), ks[0], ks[1], ks[2],
+                         c.data_ptr(), 0, d, s.data_ptr(), 0, d, L.DTYPE_BF16, P, pos.data_ptr(),
+                         1, nq, nkv, T, d, 0, L.stream_of(q)), "forge_rope")
+    torch.cuda.synchronize()
+    bad = torch.zeros(T, dtype=torch.bool)
+    bad[3] = bad[60] = True
+    assert bool(torch.isnan(oq[0][:, bad.cuda()]).all()) and bool(torch.isnan(ok[0][:, bad.cuda()]).all())
+    good = (~bad).cuda()
+    pc = pos.clamp(0, P - 1).cpu()
+    rq, rk = hf_apply_rotary_pos_emb(q.float().cpu(), k.float().cpu(), c.cpu()[pc].float().unsqueeze(0),
+                                     s.cpu()[pc].float().unsqueeze(0))
+    _close(oq[:, :, good], rq.to(torch.bfloat16)[:, :, good.cpu()], torch.bfloat16)
+    _close(ok[:, :, good], rk.to(torch.bfloat16)[:, :, good.cpu()], torch.bfloat16)
+
+
 @pytest.mark.gpu
 @pytest.mark.parametrize("base", [10000.0, 500000.0])
 def test_rope_baseline_config(base):
@@ -165,3 +252,69 @@ def test_rope_cos_sin_builder_matches_oracle():
         c, s = rope_cos_sin(pos, 128, base, torch.float32)
         rc, rs = cos_sin(pos, 128, base, torch.float32)
         assert torch.equal(c, rc) and torch.equal(s, rs)
+
+
+# --- v1 / v2 APIs (kernels/rope/forge_rope_v1.py, forge_rope_v2.py): same
+# rotation kernel, their own Function names, assert messages and checks ---
+from kernels.rope.forge_rope_v1 import ForgeRoPEv1, ForgeRoPEv1Function  # noqa: E402
+from kernels.rope.forge_rope_v1 import apply_rope as apply_rope_v1  # noqa: E402
+from kernels.rope.forge_rope_v2 import ForgeRoPEv2, ForgeRoPEv2Function  # noqa: E402
+from kernels.rope.forge_rope_v2 import apply_rope as apply_rope_v2  # noqa: E402
+
+
+def test_rope_v1_v2_shape_messages():
+    q = torch.zeros(1, 6, 8, 64)
+    k = torch.zeros(1, 4, 8, 64)
+    c, s = cos_sin(torch.arange(8), 64, 10000.0, torch.float32)
+    c, s = c.unsqueeze(0), s.unsqueeze(0)
+    with pytest.raises(AssertionError, match=r"V2 requires n_q % n_kv == 0 \(got n_q=6, n_kv=4\)"):
+        apply_rope_v2(q, k, c, s)
+    with pytest.raises(AssertionError, match="q must be 4D"):
+        apply_rope_v1(q[0], k, c, s)
+    with pytest.raises(AssertionError, match=r"cos shape \(1, 8, 64\) mismatch \(expected \(.,9,64\)\)"):
+        apply_rope_v1(torch.zeros(1, 6, 9, 64), torch.zeros(1, 4, 9, 64), c, s)
+    with pytest.raises(AssertionError, match="sin/cos shape mismatch"):
+        apply_rope_v2(q[:, :4], k, c, s[:, :4])
+    with pytest.raises(AssertionError, match="head_dim must be a power of 2"):
+        apply_rope_v1(torch.zeros(1, 2, 8, 48), torch.zeros(1, 2, 8, 48), c[..., :48], s[..., :48])
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("version", ["v1", "v2"])
+@pytest.mark.parametrize("label,b,nq,nkv,s,d", SHAPES[:3] + SHAPES[4:])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_rope_v1_v2_forward_backward(version, label, b, nq, nkv, s, d, dtype):
+    q, k, c, sn = _inputs(b, nq, nkv, s, d, dtype, seed=3)
+    dq = torch.randn(q.shape).to(dtype)
+    dk = torch.randn(k.shape).to(dtype)
+    rq, rk, rdq, rdk = rope_fwd_bwd(q, k, c, sn, dq, dk)
+    qg = q.cuda().requires_grad_(True)
+    kg = k.cuda().requires_grad_(True)
+    fn = apply_rope_v1 if version == "v1" else apply_rope_v2
+    oq, ok = fn(qg, kg, c.cuda(), sn.cuda())
+    assert type(oq.grad_fn).__name__.startswith("ForgeRoPE" + version + "Function")
+    _close(oq, rq, dtype)
+    _close(ok, rk, dtype)
+    torch.autograd.backward((oq, ok), (dq.cuda(), dk.cuda()))
+    _close(qg.grad, rdq, dtype)
+    _close(kg.grad, rdk, dtype)
+
+
+@pytest.mark.gpu
+def test_rope_v1_non_divisible_gqa_and_gradcheck():
+    """v1 accepts n_q % n_kv != 0 (its reference grid needs no grouping);
+    fp64 gradcheck through ForgeRoPEv1Function and the Module form."""
+    q, k, c, sn = _inputs(2, 6, 4, 40, 64, torch.bfloat16, seed=9)
+    rq, rk = hf_apply_rotary_pos_emb(q.float(), k.float(), c.float(), sn.float())
+    oq, ok = ForgeRoPEv1()(q.cuda(), k.cuda(), c.cuda(), sn.cuda())
+    _close(oq, rq.to(torch.bfloat16), torch.bfloat16)
+    _close(ok, rk.to(torch.bfloat16), torch.bfloat16)
+    q, k, c, sn = _inputs(1, 4, 2, 6, 16, torch.float64, seed=10)
+    qg = q.cuda().requires_grad_(True)
+    kg = k.cuda().requires_grad_(True)
+    # fp32 math inside, so the reference test's gradcheck settings (test_v1.py:273-340)
+    kw = dict(eps=1e-3, atol=1e-2, rtol=1e-2, nondet_tol=1e-3)
+    assert torch.autograd.gradcheck(lambda a, b_: ForgeRoPEv1Function.apply(a, b_, c.cuda(), sn.cuda()), (qg, kg), **kw)
+    assert torch.autograd.gradcheck(lambda a, b_: ForgeRoPEv2Function.apply(a, b_, c.cuda(), sn.cuda()), (qg, kg), **kw)
+    oq2, _ = ForgeRoPEv2()(qg, kg, c.cuda(), sn.cuda())
+    torch.testing.assert_close(oq2, apply_rope(qg, kg, c.cuda(), sn.cuda())[0], rtol=0, atol=0)
