@@ -661,7 +661,7 @@ def bench_lora_qkv(args):
     launch_ms = time_launches(lambda i: L.forge_lora_qkv_rope(
         T, K, Hq, Hkv, r, Xd.data_ptr(), K, Wq.data_ptr(), Wk.data_ptr(), Wv.data_ptr(), K, xa.data_ptr(), 3 * r,
         Bq.data_ptr(), Bk.data_ptr(), Bv.data_ptr(), r, out.data_ptr(), Hq + 2 * Hkv, c.data_ptr(), sn.data_ptr(),
-        c.stride(0), pos.data_ptr(), D, 1, st), max(args.steps, 10))
+        c.stride(0), c.shape[0], pos.data_ptr(), D, 1, st), max(args.steps, 10))
     fwd_flops = 2 * T * K * (Hq + 2 * Hkv) + 2 * T * r * (Hq + 2 * Hkv)
     res = {
         "config": {"workload": "lora_qkv_rope_fwd_bwd", "dtype": "bf16", "tokens": T, "seq_lens": lens,
