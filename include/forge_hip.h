@@ -400,6 +400,22 @@ int forge_lora_a(int64_t M, int64_t K, int64_t r, int n_proj, const void* x, int
                  const void* const* a_mats, int64_t lda, const float* scales, void* out,
                  int64_t ld_out, float* work, int split_k, void* stream);
 
+/* Bytes of the per-GPU scratch array behind forge_lora_a_noalloc. */
+#define FORGE_LORA_A_SCRATCH_BYTES (16LL * 1024 * 1024)
+
+/* forge_lora_a with no workspace argument and no allocation: the split-K
+ * partials live in a file-scope device array of FORGE_LORA_A_SCRATCH_BYTES
+ * per GPU (held until the process ends), so split_k * M * n_proj * r fp32
+ * values must fit in it (larger calls return FORGE_ERR_INVALID).  Calls no
+ * hipMalloc / hipFree.  Calls that overlap on one GPU (different streams)
+ * share the array and race; serialise them.  Same results as forge_lora_a,
+ * bit for bit.  No counterpart in the reference: it is for callers that
+ * cannot allocate (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc). */
+int forge_lora_a_noalloc(int64_t M, int64_t K, int64_t r, int n_proj, const void* x, int64_t ldx,
+                         const void* const* a_mats, int64_t lda, const float* scales, void* out,
+                         int64_t ld_out, int split_k, void* stream);
+
 /* Utilities for split-K reductions (no counterpart in the reference, which
  * delegates these to cuBLAS): zero an fp32 workspace with a fill kernel, and
  * cast a reduced fp32 [rows, cols] block to bf16. */

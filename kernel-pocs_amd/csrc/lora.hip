@@ -17,6 +17,8 @@
 // The LoRA-A products (X A^T, dY B, ...) arrive pre-scaled by s from the
 // caller (computed with forge_gemm); the LoRA-B product rides along the base
 // GEMM as one more K segment.
+#include <mutex>
+
 #include "gemm_core.h"
 
 using namespace fgemm;
@@ -197,4 +199,59 @@ extern "C" int forge_lora_a(int64_t M, int64_t K, int64_t r, int n_proj, const v
   a.ep.split_stride = M * N;
   if (int e = run(cfg, ROW, COL, EPI_STORE_F32, a, s)) return e;
   return forge_splitk_reduce(work, M * N, split_k, M, N, N, out, ld_out, FORGE_DTYPE_BF16, 1.0f, stream);
+}
+
+// ---------------------------------------------------------------------------
+// forge_lora_a without a caller workspace: the split-K partial sums go to a
+// file-scope device array (one per GPU, resident until the process ends).
+// Every split writes its whole [M, N] slice before the reduction reads it, so
+// the array needs no clearing between calls; calls that overlap on one GPU
+// (two streams) share it and race.
+// ---------------------------------------------------------------------------
+namespace {
+
+constexpr int64_t kScratchFloats = FORGE_LORA_A_SCRATCH_BYTES / 4;
+static __device__ __align__(256) float scratch[kScratchFloats];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+float* g_scratch_ptr[kMaxDevices] = {};
+
+// Device address of this GPU's `scratch`, looked up once per device with that
+// device current (host code must never pass the symbol itself to a kernel).
+int scratch_for_current_device(float** out) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices)
+    return forge_set_error(FORGE_ERR_HIP, "lora_a_noalloc: no current device (or device index >= %d)", kMaxDevices);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p)
+      return forge_set_error(FORGE_ERR_HIP, "lora_a_noalloc: hipGetSymbolAddress(scratch) failed on device %d: %s",
+                             dev, hipGetErrorString(e));
+    g_scratch_ptr[dev] = static_cast<float*>(p);
+  }
+  *out = g_scratch_ptr[dev];
+  return FORGE_OK;
+}
+
+}  // namespace
+
+extern "C" int forge_lora_a_noalloc(int64_t M, int64_t K, int64_t r, int n_proj, const void* x, int64_t ldx,
+                                    const void* const* a_mats, int64_t lda, const float* scales, void* out,
+                                    int64_t ld_out, int split_k, void* stream) {
+  if (M < 0 || K < 0 || r <= 0 || n_proj < 1 || n_proj > 4)
+    return forge_set_error(FORGE_ERR_INVALID, "lora_a_noalloc: shape (r > 0, 1 <= n_proj <= 4)");
+  if (split_k <= 1)
+    return forge_lora_a(M, K, r, n_proj, x, ldx, a_mats, lda, scales, out, ld_out, nullptr, 1, stream);
+  const int64_t need = (int64_t)split_k * M * r * n_proj;
+  if (need > kScratchFloats)
+    return forge_set_error(FORGE_ERR_INVALID,
+                           "lora_a_noalloc: split_k * M * n_proj * r = %lld fp32 partials exceed the %lld-byte scratch "
+                           "(use forge_lora_a with a workspace, or a smaller split_k)",
+                           (long long)need, (long long)FORGE_LORA_A_SCRATCH_BYTES);
+  float* work = nullptr;
+  if (int e = scratch_for_current_device(&work)) return e;
+  return forge_lora_a(M, K, r, n_proj, x, ldx, a_mats, lda, scales, out, ld_out, work, split_k, stream);
 }

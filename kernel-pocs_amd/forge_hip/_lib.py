@@ -130,6 +130,13 @@ forge_lora_a = _decl(
      c_vp, c_int, c_vp],
 )
 
+forge_lora_a_noalloc = _decl(
+    "forge_lora_a_noalloc",
+    [c_i64, c_i64, c_i64, c_int, c_vp, c_i64, ctypes.POINTER(c_vp), c_i64, ctypes.POINTER(c_f32), c_vp, c_i64,
+     c_int, c_vp],
+)
+LORA_A_SCRATCH_BYTES = 16 * 1024 * 1024
+
 forge_ce_target_prob = _decl(
     "forge_ce_target_prob", [c_int, c_vp, c_i64, c_i64, c_i64, c_vp, c_i64, c_i64, c_f32, c_vp, c_vp]
 )
@@ -161,7 +168,7 @@ EXPORTED = [
     "forge_swiglu_fwd", "forge_swiglu_bwd", "forge_geglu_fwd", "forge_geglu_bwd", "forge_rope",
     "forge_ce_fwd", "forge_ce_target_stats", "forge_ce_scale", "forge_sum_f32",
     "forge_gemm", "forge_lora_mlp_gate_up", "forge_lora_mlp_down_bwd", "forge_lora_qkv_rope",
-    "forge_lora_a", "forge_zero", "forge_cast_f32_bf16", "forge_splitk_reduce",
+    "forge_lora_a", "forge_lora_a_noalloc", "forge_zero", "forge_cast_f32_bf16", "forge_splitk_reduce",
     "forge_ce_target_prob", "forge_row_scale", "forge_gemm_generic", "forge_transpose_2b",
     "forge_rmsnorm_fwd", "forge_rmsnorm_bwd", "forge_rmsnorm_bwd_workspace",
 ]
