@@ -4,14 +4,21 @@
                     [--no-cpu-baseline] [--only-launches]
 
 A step is one fwd+bwd pass of a kernel's drop-in autograd path over one batch
-of synthetic input already resident in HBM.  Steps
-are timed back to back in one HIP-event bracket; inputs a step overwrites
-(SwiGLU's fast backward, RMSNorm's in-place backward) are cloned per step
-before the bracket.  The exception is the 2.1 GB CE logits: they are
-restored into one buffer before each step, outside the timed interval, a
-read of a 512 MB buffer then leaves the Infinity Cache holding none of
-them, and each CE step is timed alone with HIP events, as the reference's
-CE benchmark times a rep.  Every kernel is timed; the headline `value` is the RoPE fwd+bwd
+of synthetic input already resident in HBM.  Every
+step is timed cold and alone: a read of a 512 MB buffer (twice the 256 MB
+Infinity Cache) precedes it outside the timed interval, so no input of the
+step is cached when it starts, and HIP events bracket the step (the
+reference's RoPE benchmark flushes a 256 MB buffer before every rep,
+kernels/rope/benchmarks/bench_v3.py:310, 371; its CE benchmark times a rep
+alone, kernels/cross_entropy/benchmarks/bench_cross_entropy.py:197-210).
+Reuse inside a step (the backward re-reading what the forward just touched)
+is part of the step.  Inputs a step overwrites (SwiGLU's fast backward,
+RMSNorm's in-place backward) are cloned per step beforehand; the 2.1 GB CE
+logits are restored into one buffer before each step.  The HBM-bound legs
+also report `warm`: the same steps back to back in one event bracket, with
+inputs reused from step to step (partly served by the Infinity Cache).  The
+dominant-kernel launch loops behind `roofline` are cold the same way.
+Every kernel is timed; the headline `value` is the RoPE fwd+bwd
 throughput on configs[1] (B=4, S=4096, 32/8 heads, D=128, bf16, bases 10000
 and 500000 alternate by step), the others are reported under "kernels".
 
@@ -66,8 +73,8 @@ def _sync():
 
 
 def time_steps(step_fn, steps, warmup):
-    """Runs warmup + steps; returns (event ms per step over the timed
-    bracket, wall ms per step)."""
+    """Warm timing: warmup + steps back to back; returns (event ms per step
+    over one timed bracket, wall ms per step)."""
     import torch
 
     for i in range(warmup):
@@ -86,35 +93,45 @@ def time_steps(step_fn, steps, warmup):
 
 
 SCRUB_BYTES = 512 << 20  # twice the 256 MB Infinity Cache
+_SCRUB = []
 
 
-def time_steps_restored(step_fn, restore_fn, steps, warmup):
-    """Per-step timing for a step that overwrites its input in place, the way
-    the reference's benchmarks time one rep (a fresh clone of the base
-    input per rep, HIP events around the rep alone:
-    kernels/cross_entropy/benchmarks/bench_cross_entropy.py:197-210,
-    kernels/swiglu/benchmarks/benchmark_swiglu.py:97-120).
-    restore_fn(i) rewrites the input buffer the step works on (the same
-    buffer every step, as a training step gets the same block back from the
-    caching allocator); a read of a 512 MB buffer then evicts the restored
-    bytes from the Infinity Cache, so each step starts from HBM.  The host
-    queues restore, read and step without waiting, so the events time the
-    step's device work (the reference synchronizes before each rep, which
-    also puts the host's launch latency inside its interval).
-    Returns (mean event ms over the K steps, wall ms per step including the
-    restores)."""
+def scrub():
+    """Queues a read of a 512 MB buffer: afterwards neither the L2s nor the
+    Infinity Cache hold any of the previous working set."""
     import torch
 
-    scrub = torch.zeros(SCRUB_BYTES // 4, device="cuda")
+    if not _SCRUB:
+        _SCRUB.append(torch.zeros(SCRUB_BYTES // 4, device="cuda"))
+    _SCRUB[0].sum()
+
+
+def time_steps_cold(step_fn, steps, warmup, restore_fn=None):
+    """Per-step cold timing, the way the reference's benchmarks time one rep
+    (a cache flush before each rep, HIP events around the rep alone:
+    kernels/rope/benchmarks/bench_v3.py:310, 371;
+    kernels/cross_entropy/benchmarks/bench_cross_entropy.py:197-210).
+    restore_fn(i), if given, first rewrites the input buffer the step
+    overwrites (the same buffer every step, as a training step gets the same
+    block back from the caching allocator).  The 512 MB read then evicts
+    everything the step will touch.  The host queues restore, read and step
+    without waiting, so the events time the step's device work (the
+    reference synchronizes before each rep, which also puts the host's
+    launch latency inside its interval).  Returns (mean event ms over the K
+    steps, wall ms per step including restores and reads)."""
+    import torch
+
     for i in range(warmup):
-        restore_fn(i)
+        if restore_fn is not None:
+            restore_fn(i)
         step_fn(i)
     _sync()
     evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
     t0 = time.perf_counter()
     for j, (a, b) in enumerate(evs):
-        restore_fn(warmup + j)
-        scrub.sum()
+        if restore_fn is not None:
+            restore_fn(warmup + j)
+        scrub()
         a.record()
         step_fn(warmup + j)
         b.record()
@@ -124,8 +141,9 @@ def time_steps_restored(step_fn, restore_fn, steps, warmup):
 
 
 def time_launches(launch_fn, n, warmup=3):
-    """Average duration (ms) of one device launch, from events recorded on
-    torch's current stream (the stream every forge_* call launches on)."""
+    """Average duration (ms) of one device launch, cold (a 512 MB read before
+    each, untimed), from events recorded on torch's current stream (the
+    stream every forge_* call launches on)."""
     import torch
 
     for i in range(warmup):
@@ -133,6 +151,7 @@ def time_launches(launch_fn, n, warmup=3):
     _sync()
     evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(n)]
     for i, (a, b) in enumerate(evs):
+        scrub()
         a.record()
         launch_fn(i)
         b.record()
@@ -141,13 +160,21 @@ def time_launches(launch_fn, n, warmup=3):
 
 
 def run_steps(args, step_fn, restore=None):
-    """time_steps, or time_steps_restored for a step that overwrites its
-    input (restore(i) rewrites it); (None, None) with --only-launches."""
+    """Cold per-step timing (time_steps_cold); (None, None) with
+    --only-launches."""
     if args.only_launches:
         return None, None
-    if restore is not None:
-        return time_steps_restored(step_fn, restore, args.steps, args.warmup)
-    return time_steps(step_fn, args.steps, args.warmup)
+    return time_steps_cold(step_fn, args.steps, args.warmup, restore)
+
+
+def warm_steps(args, step_fn, bytes_step):
+    """The HBM legs' warm figure: steps back to back with inputs reused
+    across steps (labelled, not the claim)."""
+    if args.only_launches:
+        return None
+    ms, _ = time_steps(step_fn, args.steps, args.warmup)
+    return {"value": rate(bytes_step, ms, 1e9), "unit": "GB/s", "ms_per_step": rnd(ms, 5),
+            "timing": "steps back to back, inputs reused across steps (partly cached)"}
 
 
 def rate(amount, ms, scale):
@@ -202,8 +229,11 @@ def bench_swiglu(args):
     up0 = torch.randn(R, C, device="cuda", generator=g)
     dout = torch.randn(R, C, device="cuda", generator=g)
     total = args.warmup + args.steps
-    gates = [gate0.clone() for _ in range(total)]  # backward overwrites its inputs
-    ups = [up0.clone() for _ in range(total)]
+    gates, ups = [], []
+
+    def fresh():  # the backward overwrites its inputs: one clone pair per step
+        gates[:] = [gate0.clone() for _ in range(total)]
+        ups[:] = [up0.clone() for _ in range(total)]
 
     def step(i):
         gi = gates[i].requires_grad_(True)
@@ -212,9 +242,14 @@ def bench_swiglu(args):
         out.backward(dout)
         gates[i] = ups[i] = None
 
-    ms, wall = run_steps(args, step)
     bytes_step = 8 * n * 4  # fwd 3 tensors + bwd 5 tensors, fp32
+    fresh()
+    ms, wall = run_steps(args, step)
     gbs = rate(bytes_step, ms, 1e9)
+    fresh()
+    warm = warm_steps(args, step, bytes_step)
+    gates.clear()
+    ups.clear()
     # dominant kernel: backward (5 tensor passes)
     gf, uf, out = gate0.clone(), up0.clone(), torch.empty_like(gate0)
     st = L.stream_of(gf)
@@ -229,6 +264,7 @@ def bench_swiglu(args):
                    "down_multiplier": 1.0, "preserve_inputs": False},
         "value": gbs, "unit": "GB/s", "ms_per_step": rnd(ms, 5), "wall_ms_per_step": rnd(wall, 5),
         "frac_of_hbm_peak": rnd(gbs and gbs / HBM_PEAK_GBS, 4), "algorithmic_bytes_per_step": bytes_step,
+        "timing": "cold: each step alone after a 512 MB read", "warm": warm,
         "launches_ms": {"forge_swiglu_fwd": round(fwd_ms, 5), "forge_swiglu_bwd": round(bwd_ms, 5)},
         "roofline": _roof("hbm", bwd_bytes / (bwd_ms * 1e-3) / 1e9, HBM_PEAK_GBS, "GB/s", _traffic("swiglu_bwd")),
         "dtype": "f32",
@@ -285,6 +321,7 @@ def bench_rope(args):
     bytes_dir = 2 * elems * 2 + 2 * S * D * 2  # read+write Q,K + cos/sin (the reference's formula)
     bytes_step = 2 * bytes_dir
     gbs = rate(bytes_step, ms, 1e9)
+    warm = warm_steps(args, step, bytes_step)
     oq, ok = torch.empty_like(qv), torch.empty_like(kv)
     launch_ms = time_launches(lambda i: _rope_launch(qv, kv, oq, ok, tabs[i % 2][0], tabs[i % 2][1], bool(i % 2)),
                               max(2 * args.steps, 20))
@@ -293,6 +330,7 @@ def bench_rope(args):
                    "layout": "BSHD memory, HF transpose(1,2) view", "bases": [10000, 500000]},
         "value": gbs, "unit": "GB/s", "ms_per_step": rnd(ms, 5), "wall_ms_per_step": rnd(wall, 5),
         "frac_of_hbm_peak": rnd(gbs and gbs / HBM_PEAK_GBS, 4), "algorithmic_bytes_per_step": bytes_step,
+        "timing": "cold: each step alone after a 512 MB read", "warm": warm,
         "launches_ms": {"forge_rope": round(launch_ms, 5)},
         "roofline": _roof("hbm", bytes_dir / (launch_ms * 1e-3) / 1e9, HBM_PEAK_GBS, "GB/s", _traffic("rope")),
         "dtype": "bf16",
@@ -792,8 +830,11 @@ def bench_geglu(args):
     up0 = torch.randn(R, C, device="cuda", generator=g).to(bf)
     dout = torch.randn(R, C, device="cuda", generator=g).to(bf)
     total = args.warmup + args.steps
-    gates = [gate0.clone() for _ in range(total)]  # backward overwrites its inputs
-    ups = [up0.clone() for _ in range(total)]
+    gates, ups = [], []
+
+    def fresh():  # the backward overwrites its inputs: one clone pair per step
+        gates[:] = [gate0.clone() for _ in range(total)]
+        ups[:] = [up0.clone() for _ in range(total)]
 
     def step(i):
         gi = gates[i].requires_grad_(True)
@@ -801,9 +842,14 @@ def bench_geglu(args):
         geglu(gi, ui, "tanh").backward(dout)
         gates[i] = ups[i] = None
 
-    ms, wall = run_steps(args, step)
     bytes_step = 8 * n * 2  # fwd 3 tensors + bwd 5 tensors, bf16
+    fresh()
+    ms, wall = run_steps(args, step)
     gbs = rate(bytes_step, ms, 1e9)
+    fresh()
+    warm = warm_steps(args, step, bytes_step)
+    gates.clear()
+    ups.clear()
     gf, uf = gate0.clone(), up0.clone()
     st = L.stream_of(gf)
     bwd_ms = time_launches(lambda i: L.forge_geglu_bwd(2, dout.data_ptr(), C, gf.data_ptr(), uf.data_ptr(), C,
@@ -813,6 +859,7 @@ def bench_geglu(args):
         "config": {"workload": "geglu_fwd_bwd", "dtype": "bf16", "shape": [R, C], "approximate": "tanh"},
         "value": gbs, "unit": "GB/s", "ms_per_step": rnd(ms, 5), "wall_ms_per_step": rnd(wall, 5),
         "frac_of_hbm_peak": rnd(gbs and gbs / HBM_PEAK_GBS, 4), "algorithmic_bytes_per_step": bytes_step,
+        "timing": "cold: each step alone after a 512 MB read", "warm": warm,
         "launches_ms": {"forge_geglu_bwd": round(bwd_ms, 5)},
         "roofline": _roof("hbm", 5 * n * 2 / (bwd_ms * 1e-3) / 1e9, HBM_PEAK_GBS, "GB/s", _traffic("geglu_bwd")),
         "dtype": "bf16",
@@ -845,7 +892,10 @@ def bench_rmsnorm(args):
     w = (1 + 0.1 * torch.randn(H, device="cuda", generator=g)).to(bf).requires_grad_(True)
     dy0 = torch.randn(R, H, device="cuda", generator=g).to(bf)
     total = args.warmup + args.steps
-    dys = [dy0.clone() for _ in range(total)]  # the in-place backward overwrites dy with dx
+    dys = []
+
+    def fresh():  # the in-place backward overwrites dy with dx: one clone per step
+        dys[:] = [dy0.clone() for _ in range(total)]
 
     def step(i):
         x.grad = None  # a training step after zero_grad(set_to_none=True)
@@ -853,9 +903,13 @@ def bench_rmsnorm(args):
         apply_rmsnorm_v4(x, w, 1e-6, 0.0, "llama", in_place=True).backward(dys[i])
         dys[i] = None
 
-    ms, wall = run_steps(args, step)
     bytes_step = bytes_fwd_bwd(R, H)
+    fresh()
+    ms, wall = run_steps(args, step)
     gbs = rate(bytes_step, ms, 1e9)
+    fresh()
+    warm = warm_steps(args, step, bytes_step)
+    dys.clear()
     # dominant kernel: the backward (reads x and dy, writes dx over dy, dw partials)
     xd, wd = x.detach(), w.detach()
     rstd = torch.empty(R, device="cuda")
@@ -876,6 +930,7 @@ def bench_rmsnorm(args):
                    "offset": 0.0, "in_place": True, "weight_grad": True},
         "value": gbs, "unit": "GB/s", "ms_per_step": rnd(ms, 5), "wall_ms_per_step": rnd(wall, 5),
         "frac_of_hbm_peak": rnd(gbs and gbs / HBM_PEAK_GBS, 4), "algorithmic_bytes_per_step": bytes_step,
+        "timing": "cold: each step alone after a 512 MB read", "warm": warm,
         "launches_ms": {"forge_rmsnorm_bwd": round(bwd_ms, 5)},
         "roofline": _roof("hbm", bwd_bytes / (bwd_ms * 1e-3) / 1e9, HBM_PEAK_GBS, "GB/s", _traffic("rmsnorm_bwd")),
         "dtype": "bf16",
@@ -946,6 +1001,8 @@ def main():
         "dtype": head["dtype"],
         "data": "synthetic",
         "config": head["config"],
+        "timing": head.get("timing"),
+        "warm": head.get("warm"),
         "roofline": head["roofline"],
         "cpu_baseline": head.get("cpu_baseline"),
         "kernels": results,

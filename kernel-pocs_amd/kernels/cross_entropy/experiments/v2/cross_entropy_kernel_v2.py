@@ -9,9 +9,15 @@ writes dloss/dlogits over the logits buffer, which is what backward returns.
 Features: class weights, ignore_index, label smoothing, z-loss, softcap,
 token accuracy, predicted tokens, mean/sum/none reductions.
 
-Device work: `forge_ce_fwd` (row kernel), `forge_sum_f32` (loss reduction)
-and `forge_ce_scale` (grad_output != 1) in libforge_hip.so
-(csrc/cross_entropy.hip).
+Device work: `forge_ce_target_stats` (target count and range), `forge_ce_fwd`
+(row kernel, reading the count from the statistics on the device),
+`forge_sum_f32` (loss reduction) and `forge_ce_scale` (grad_output != 1) in
+libforge_hip.so (csrc/cross_entropy.hip).  The host queues the statistics
+kernel and the row kernel back to back, and only then copies the four
+statistics to pinned host memory on a side stream (for the reference's
+bounds assert), so the device does not wait for host work between the two.
+With class weights the host needs the validated count before the launch (as
+the reference), so there it waits for the copy first.
 
 Numerics: per-row losses are kept in fp32 and summed in fp32, then cast to the
 logits dtype once (the reference rounds every row to the logits dtype before
@@ -37,23 +43,27 @@ class CrossEntropyOutput:
     predicted_tokens: Optional[torch.Tensor] = None
 
 
-def _target_stats_async(target: torch.Tensor, ignore_index: int, n_cols: int):
-    """Queues forge_ce_target_stats and a copy of its 4 values to pinned host
-    memory; returns (device stats, host stats, event).  The reference reads
-    the same values with `.item()` (:374-387) before launching; here the main
-    kernel is queued first and the host waits only for this copy."""
+def _target_stats_launch(target: torch.Tensor, ignore_index: int, n_cols: int):
+    """Queues forge_ce_target_stats and an event after it; returns (device
+    stats, event).  The reference reads the same values with `.item()`
+    (:374-387) before launching."""
     stats = torch.empty(4, dtype=torch.int64, device=target.device)
     L.check(
         L.forge_ce_target_stats(target.data_ptr(), target.stride(-1), target.numel(), int(ignore_index), int(n_cols),
                                 stats.data_ptr(), L.stream_of(target)),
         "forge_ce_target_stats",
     )
-    # the copy runs on a side stream so the main stream goes straight on to
-    # the CE kernel (no copy packet between the two)
-    main = torch.cuda.current_stream(target.device)
     ready = torch.cuda.Event()
-    ready.record(main)
-    side = _side_stream(target.device)
+    ready.record(torch.cuda.current_stream(target.device))
+    return stats, ready
+
+
+
+def _target_stats_to_host(stats: torch.Tensor, ready):
+    """Copies the 4 statistics to pinned host memory on a side stream that
+    waits only for the statistics kernel (`ready`), not for the row kernel
+    queued after it; returns (host stats, done event)."""
+    side = _side_stream(stats.device)
     side.wait_event(ready)
     host = torch.empty(4, dtype=torch.int64, pin_memory=True)
     with torch.cuda.stream(side):
@@ -61,6 +71,14 @@ def _target_stats_async(target: torch.Tensor, ignore_index: int, n_cols: int):
         done = torch.cuda.Event()
         done.record(side)
     stats.record_stream(side)
+    return host, done
+
+
+def _target_stats_async(target: torch.Tensor, ignore_index: int, n_cols: int):
+    """Statistics kernel and its host copy together -> (stats, host, event)
+    (used where the host needs the values before the next launch)."""
+    stats, ready = _target_stats_launch(target, ignore_index, n_cols)
+    host, done = _target_stats_to_host(stats, ready)
     return stats, host, done
 
 
@@ -126,15 +144,16 @@ def _cross_entropy_forward_impl(
     if _input.stride(-1) != 1:
         _input = _input.contiguous()
 
-    stats = None
+    stats = ready = None
     n_non_ignore = 0
     if BT > 0:
-        stats, stats_host, stats_ev = _target_stats_async(target, ignore_index, V)
+        stats, ready = _target_stats_launch(target, ignore_index, V)
     sum_non_ignore_weight = 0.0
     weight_sum = 0.0
     if weight is not None:
         # the weighted sums need validated targets: check first, as the reference does
         if BT > 0:
+            stats_host, stats_ev = _target_stats_to_host(stats, ready)
             n_non_ignore = _check_targets(stats_host, stats_ev, V)
         assert weight.shape[0] == V, f"If given, weight has to be a Tensor of size V. Got: {weight.shape}"
         assert torch.is_floating_point(weight), (
@@ -163,6 +182,7 @@ def _cross_entropy_forward_impl(
 
     if BT > 0:
         # n_non_ignore (unweighted) is read by the kernel from `stats`
+        st = L.stream_of(_input)
         L.check(
             L.forge_ce_fwd(
                 L.dtype_code(_input.dtype), _input.data_ptr(), _input.stride(-2), BT, V,
@@ -170,12 +190,13 @@ def _cross_entropy_forward_impl(
                 loss_1d.data_ptr(), L.ptr(z_loss_1d), L.ptr(token_accuracy_1d), L.ptr(predicted_tokens_1d),
                 int(ignore_index), float(n_non_ignore), float(sum_non_ignore_weight), float(weight_sum),
                 float(lse_square_scale), float(label_smoothing), float(softcap or 0.0), flags,
-                stats.data_ptr(), L.stream_of(_input),
+                stats.data_ptr(), st,
             ),
             "forge_ce_fwd",
         )
         if weight is None:
             # the kernel is already queued (and writes nothing if this fails)
+            stats_host, stats_ev = _target_stats_to_host(stats, ready)
             n_non_ignore = _check_targets(stats_host, stats_ev, V)
 
     if reduction == "none":
