@@ -14,7 +14,8 @@ enum Cfg {
   CFG_SKINNY_N64 = 3,  // 32 < N <= 64: 64 x 64 tiles for a K-contiguous A, 256 x 64 for
                        // token-major operands, else 256 x 32
   CFG_NARROW_128 = 4,  // 64 < N <= 128, K-contiguous A: 64 x 128 tiles (2 x 2 waves)
-  CFG_NARROW_256 = 5,  // 128 < N <= 256, K-contiguous A: 64 x 256 tiles (2 x 2 waves)
+  CFG_NARROW_256 = 5,  // 192 < N <= 256, K-contiguous A: 64 x 256 tiles (2 x 2 waves)
+  CFG_NARROW_192 = 6,  // 128 < N <= 192, K-contiguous A: 64 x 192 tiles (2 x 2 waves, 32 x 96 per wave)
 };
 
 #ifndef SKINNY_NSTAGE
@@ -45,15 +46,16 @@ static int launch_cfg(const GemmArgs& a, hipStream_t s) {
       gemm_dma_kernel<BM, BN, DWM, DWN, BMODE, EPI, 64, 2, DMA_STAGE, 2><<<grid, DWM * DWN * 64, 0, s>>>(a);
     else
       gemm_dma_kernel<BM, BN, DWM, DWN, BMODE, EPI, 64, 2, false, 2><<<grid, DWM * DWN * 64, 0, s>>>(a);
-  } else if constexpr (BM == 64 && (BN == 64 || BN == 128 || BN == 256) && AL == ROW && (BL == COL || BL == ROW) &&
-                       BMODE == B_SINGLE) {
+  } else if constexpr (BM == 64 && (BN == 64 || BN == 128 || BN == 192 || BN == 256) && AL == ROW &&
+                       (BL == COL || (BL == ROW && BN != 192)) && BMODE == B_SINGLE) {
     // narrow outputs (N <= 256: X A^T, dY B) with A K-contiguous: 64-row
     // tiles as wide as the output (so X streams once) with 4 waves; a 3-stage
     // ring (48 / 72 KB of LDS: three / two workgroups per CU) or, at 64 x 256,
-    // two stages in 80 KB (two per CU).  M/64 tiles fill the chip without a
-    // split-K pass.  B may be [N][K] or, read with the transposing LDS loads,
-    // [K][N] as stored (a rank-r LoRA B needs no transposed copy).
-    constexpr int NS = BN == 256 ? 2 : 3;
+    // two stages in 80 KB (two per CU); 64 x 192 (three rank-64 LoRA-A
+    // products) two stages in 64 KB, with no padded columns.  M/64 tiles fill
+    // the chip without a split-K pass.  B may be [N][K] or, read with the
+    // transposing LDS loads, [K][N] as stored.
+    constexpr int NS = BN >= 192 ? 2 : 3;
     constexpr int WPE_N = BN == 64 ? 3 : 2;
     gemm_dma_kernel<BM, BN, WM, WN, BMODE, EPI, 64, NS, false, WPE_N, false, BL == ROW>
         <<<grid, WM * WN * 64, 0, s>>>(a);
@@ -102,6 +104,9 @@ static int launch_layout(int cfg, const GemmArgs& a, hipStream_t s) {
     case CFG_NARROW_256:
       if constexpr (BMODE == B_SINGLE && AL == ROW) return launch_cfg<64, 256, 2, 2, AL, BL, BMODE, EPI>(a, s);
       break;
+    case CFG_NARROW_192:  // B as [N][K] only (a 192-wide k-row is not a whole number of transposing reads)
+      if constexpr (BMODE == B_SINGLE && AL == ROW && BL == COL) return launch_cfg<64, 192, 2, 2, AL, BL, BMODE, EPI>(a, s);
+      break;
     case CFG_SKINNY_M:
       if constexpr (BMODE == B_SINGLE) return launch_cfg<32, 256, 1, 4, AL, BL, BMODE, EPI>(a, s);
       break;
@@ -143,7 +148,7 @@ static int launch_glu(int al, int bl, const GemmArgs& a, hipStream_t s) {
 // 64-row narrow tiles up to N = 256).
 static int pick_cfg(int64_t M, int64_t N, int al, int bl) {
   if (al == ROW && (bl == COL || bl == ROW) && N <= 256 && M > N)
-    return N <= 64 ? CFG_SKINNY_N64 : N <= 128 ? CFG_NARROW_128 : CFG_NARROW_256;
+    return N <= 64 ? CFG_SKINNY_N64 : N <= 128 ? CFG_NARROW_128 : (N <= 192 && bl == COL) ? CFG_NARROW_192 : CFG_NARROW_256;
   if (N <= 32 && M > N) return CFG_SKINNY_N;
   if (N <= 64 && M > N) return CFG_SKINNY_N64;
   if (M <= 64 && N > M) return CFG_SKINNY_M;

@@ -9,24 +9,28 @@
 // Backward is the same rotation with -sin.
 //
 // Work decomposition: one work item = (token t, 16-byte column chunk c of the
-// lo half, group of HPT heads).  The item loads its cos/sin chunk once and
-// rotates that chunk in HPT heads (Q heads first, then K heads), so every
-// thread keeps 2*HPT independent 16-byte loads in flight; the lanes that
-// share (t, head group) cover a head's half rows, so for head_dim 128 every
-// load and store instruction consumes whole 128-byte lines.  Any element
+// lo half, group of HPT heads, HPT = 1).  The item loads its cos/sin chunk
+// (L2-resident: the table is a few MB) and rotates that chunk of its head
+// (Q heads first, then K heads); the lanes that share (t, head) cover the
+// head's half rows, so for head_dim 128 every load and store instruction
+// consumes whole 128-byte lines.  Measured on MI355X, cold, on the BASELINE
+// shape: one head per item with up to 64 workgroups per CU streams 5.8-5.96
+// TB/s, against 5.4-5.6 with 4 heads per item and 8 workgroups per CU, 5.9
+// with 2 heads and 32-64 per CU, 5.1 with 8 heads (more items in flight beat
+// fewer cos/sin reads).  Any element
 // strides for (batch, head, seq) are accepted, so the HF `transpose(1, 2)`
 // view of a [B, S, H, D] projection is rotated in place of memory order, with
 // no copy.  Index math runs in 32 bits whenever every offset fits (the usual
 // case); x is touched once, so its 16-byte loads and stores are nontemporal.
-// The grid is capped at 8 workgroups per CU and strides over the items: on
-// MI355X that measured faster than one item per thread.
+// The grid is capped at 64 workgroups per CU and strides over the items
+// beyond that.
 #include "common.h"
 
 namespace {
 
 constexpr int kBlock = 256;
-constexpr int kHPT = 4;           // heads per work item
-constexpr int kMaxBlocks = 2048;  // 8 workgroups per CU
+constexpr int kHPT = 1;            // heads per work item
+constexpr int kMaxBlocks = 16384;  // 64 workgroups per CU
 
 struct RopeArgs {
   const void* q; int64_t q_sb, q_sh, q_ss;

@@ -31,7 +31,7 @@ from kernels._positions import check_positions
 
 # launch geometry of csrc/rope.hip (fixed; there is no autotuning)
 _BLOCK = 256
-_HEADS_PER_ITEM = 4
+_HEADS_PER_ITEM = 1
 
 
 _V3_DIVISIBLE = "V3 requires n_q % n_kv == 0 (got n_q={n_q}, n_kv={n_kv})."

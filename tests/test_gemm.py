@@ -40,7 +40,8 @@ def _b_operand(n, k, layout, gen):
 
 @pytest.mark.gpu
 @pytest.mark.parametrize("M,N,K", [(256, 256, 64), (296, 520, 264), (64, 1000, 136), (1000, 40, 512),
-                                   (16, 704, 1024), (2048, 2048, 512), (1000, 192, 264), (1000, 200, 72), (600, 128, 200)])
+                                   (16, 704, 1024), (2048, 2048, 512), (1000, 192, 264), (1000, 200, 72), (600, 128, 200),
+                                   (2000, 160, 520)])
 @pytest.mark.parametrize("a_layout", [0, 1])
 @pytest.mark.parametrize("b_layout", [0, 1])
 def test_gemm_layouts(M, N, K, a_layout, b_layout):
