@@ -488,6 +488,72 @@ __device__ __forceinline__ void epilogue_staged(const GemmArgs& args,
           }
         }
       }
+    } else if constexpr (EPI == EPI_ROPE) {
+      // A thread's chunks share one column chunk c (rows tid / 32 + 16 it), so
+      // d and the lo / hi half are fixed: the positions of all its rows are
+      // read first, then the cos / sin chunks of four rows at a time, then
+      // those four rows are rotated and stored.  Issuing the table loads ahead
+      // keeps several in flight (one row at a time left the epilogue waiting
+      // on each load).
+      static_assert(NT % 32 == 0, "rows of 32 chunk-threads");
+      constexpr int IT = 128 * 32 / NT, RSTEP = NT / 32, GRP = IT >= 4 ? 4 : IT;
+      const int c = (tid % 32) * 8;
+      const int64_t n = n0 + c;
+      const bool rot = n < N && n < ep.rope_cols;
+      const int half = ep.head_dim / 2;
+      const int in_head = (int)(n % ep.head_dim);
+      const bool lo = in_head < half;
+      const int d = in_head % half;
+      int64_t posv[IT];
+#pragma unroll
+      for (int it = 0; it < IT; ++it) {
+        const int64_t m = mrow0 + it * RSTEP + tid / 32;
+        posv[it] = (rot && m < M) ? (ep.positions ? ep.positions[m] : m) : -1;
+      }
+#pragma unroll
+      for (int g0 = 0; g0 < IT; g0 += GRP) {
+        uint4 cv[GRP], sv[GRP];
+#pragma unroll
+        for (int j = 0; j < GRP; ++j) {
+          const int64_t pos = posv[g0 + j];
+          if (pos >= 0 && pos < ep.cs_rows) {
+            cv[j] = ld16(ep.cos + pos * ep.cs_ld + d);
+            sv[j] = ld16(ep.sin + pos * ep.cs_ld + d);
+          }
+        }
+#pragma unroll
+        for (int j = 0; j < GRP; ++j) {
+          const int rr = (g0 + j) * RSTEP + tid / 32;
+          const int64_t m = mrow0 + rr;
+          if (m >= M || n >= N) continue;
+          const float* pv = lds + rr * P + c;
+          float v[8];
+#pragma unroll
+          for (int q = 0; q < 8; ++q) v[q] = pv[q];
+          if (rot) {
+            // the 128-column wave tile holds whole heads: partner half in LDS
+            const float* pp = lds + rr * P + (lo ? c + half : c - half);
+            const int64_t pos = posv[g0 + j];
+            float cs[8], sn[8];
+            if (pos >= 0 && pos < ep.cs_rows) {
+              unpack8(cv[j], cs);
+              unpack8(sv[j], sn);
+            } else {
+#pragma unroll
+              for (int q = 0; q < 8; ++q) cs[q] = sn[q] = __builtin_nanf("");
+            }
+#pragma unroll
+            for (int q = 0; q < 8; ++q) {
+              const float x = bf16r(v[q]), xp = bf16r(pp[q]);
+              v[q] = lo ? x * cs[q] - xp * sn[q] : x * cs[q] + xp * sn[q];
+            }
+          }
+          __bf16* cp = (__bf16*)ep.c + m * ep.ldc + n;
+          if (n + 8 <= N) st16(cp, pack8(v));
+          else
+            for (int q = 0; q < 8 && n + q < N; ++q) cp[q] = (__bf16)v[q];
+        }
+      }
     } else {
 #pragma unroll 2
       for (int it = 0; it < 128 * 32 / NT; ++it) {
@@ -586,33 +652,6 @@ __device__ __forceinline__ void epilogue_staged(const GemmArgs& args,
               ep.g[off + q] = (__bf16)dev[q];
             }
           }
-        } else if constexpr (EPI == EPI_ROPE) {
-          if (n < ep.rope_cols) {
-            // the 128-column wave tile holds whole heads: partner half in LDS
-            const int half = ep.head_dim / 2;
-            const int in_head = (int)(n % ep.head_dim);
-            const bool lo = in_head < half;
-            const float* pp = lds + rr * P + (lo ? c + half : c - half);
-            const int d = in_head % half;
-            const int64_t pos = ep.positions ? ep.positions[m] : m;
-            float cs[8], sn[8];
-            if (pos >= 0 && pos < ep.cs_rows) {
-              unpack8(ld16(ep.cos + pos * ep.cs_ld + d), cs);
-              unpack8(ld16(ep.sin + pos * ep.cs_ld + d), sn);
-            } else {
-#pragma unroll
-              for (int q = 0; q < 8; ++q) cs[q] = sn[q] = __builtin_nanf("");
-            }
-#pragma unroll
-            for (int q = 0; q < 8; ++q) {
-              const float x = bf16r(v[q]), xp = bf16r(pp[q]);
-              v[q] = lo ? x * cs[q] - xp * sn[q] : x * cs[q] + xp * sn[q];
-            }
-          }
-          __bf16* cp = (__bf16*)ep.c + m * ep.ldc + n;
-          if (full) st16(cp, pack8(v));
-          else
-            for (int q = 0; q < 8 && n + q < N; ++q) cp[q] = (__bf16)v[q];
         }
       }
     }
