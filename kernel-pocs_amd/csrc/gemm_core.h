@@ -488,6 +488,59 @@ __device__ __forceinline__ void epilogue_staged(const GemmArgs& args,
           }
         }
       }
+    } else if constexpr (glu_bwd_epi(EPI)) {
+      // As for RoPE below: a thread's chunks share one column chunk c, so the
+      // saved e / g chunks of four rows are read before any of them is used
+      // (one row at a time left the epilogue waiting on each load).
+      static_assert(NT % 32 == 0, "rows of 32 chunk-threads");
+      constexpr int IT = 128 * 32 / NT, RSTEP = NT / 32, GRP = IT >= 4 ? 4 : IT;
+      const int c = (tid % 32) * 8;
+      const int64_t n = n0 + c;
+      const bool full = n + 8 <= N;
+#pragma unroll
+      for (int g0 = 0; g0 < IT; g0 += GRP) {
+        uint4 ew[GRP], gw[GRP];
+#pragma unroll
+        for (int j = 0; j < GRP; ++j) {
+          const int64_t m = mrow0 + (g0 + j) * RSTEP + tid / 32;
+          if (m < M && full) {
+            const int64_t off = m * ep.ld_eg + n;
+            ew[j] = ld16(ep.e + off);
+            gw[j] = ld16(ep.g + off);
+          }
+        }
+#pragma unroll
+        for (int j = 0; j < GRP; ++j) {
+          const int rr = (g0 + j) * RSTEP + tid / 32;
+          const int64_t m = mrow0 + rr;
+          if (m >= M || n >= N) continue;
+          const float* pv = lds + rr * P + c;
+          const int64_t off = m * ep.ld_eg + n;
+          float ev[8], gv[8], hv[8], dfv[8], dev[8];
+          if (full) {
+            unpack8(ew[j], ev);
+            unpack8(gw[j], gv);
+          } else {
+            for (int q = 0; q < 8; ++q) {
+              ev[q] = n + q < N ? (float)ep.e[off + q] : 0.f;
+              gv[q] = n + q < N ? (float)ep.g[off + q] : 0.f;
+            }
+          }
+#pragma unroll
+          for (int q = 0; q < 8; ++q) glu_bwd_vals<EPI>(pv[q], ev[q], gv[q], hv[q], dfv[q], dev[q]);
+          if (full) {
+            st16((__bf16*)ep.c + m * ep.ldc + n, pack8(hv));
+            st16(ep.e + off, pack8(dfv));
+            st16(ep.g + off, pack8(dev));
+          } else {
+            for (int q = 0; q < 8 && n + q < N; ++q) {
+              ((__bf16*)ep.c)[m * ep.ldc + n + q] = (__bf16)hv[q];
+              ep.e[off + q] = (__bf16)dfv[q];
+              ep.g[off + q] = (__bf16)dev[q];
+            }
+          }
+        }
+      }
     } else if constexpr (EPI == EPI_ROPE) {
       // A thread's chunks share one column chunk c (rows tid / 32 + 16 it), so
       // d and the lo / hi half are fixed: the positions of all its rows are
@@ -625,31 +678,6 @@ __device__ __forceinline__ void epilogue_staged(const GemmArgs& args,
               if (ep.beta != 0.f) o += ep.beta * (float)cp[q];
               if (ep.act) o = epi_act(ep.act, o);
               cp[q] = (__bf16)o;
-            }
-          }
-        } else if constexpr (glu_bwd_epi(EPI)) {
-          const int64_t off = m * ep.ld_eg + n;
-          float ev[8], gv[8], hv[8], dfv[8], dev[8];
-          if (full) {
-            unpack8(ld16(ep.e + off), ev);
-            unpack8(ld16(ep.g + off), gv);
-          } else {
-            for (int q = 0; q < 8; ++q) {
-              ev[q] = n + q < N ? (float)ep.e[off + q] : 0.f;
-              gv[q] = n + q < N ? (float)ep.g[off + q] : 0.f;
-            }
-          }
-#pragma unroll
-          for (int q = 0; q < 8; ++q) glu_bwd_vals<EPI>(v[q], ev[q], gv[q], hv[q], dfv[q], dev[q]);
-          if (full) {
-            st16((__bf16*)ep.c + m * ep.ldc + n, pack8(hv));
-            st16(ep.e + off, pack8(dfv));
-            st16(ep.g + off, pack8(dev));
-          } else {
-            for (int q = 0; q < 8 && n + q < N; ++q) {
-              ((__bf16*)ep.c)[m * ep.ldc + n + q] = (__bf16)hv[q];
-              ep.e[off + q] = (__bf16)dfv[q];
-              ep.g[off + q] = (__bf16)dev[q];
             }
           }
         }
