@@ -16,8 +16,16 @@ is part of the step.  Inputs a step overwrites (SwiGLU's fast backward,
 RMSNorm's in-place backward) are cloned per step beforehand; the 2.1 GB CE
 logits are restored into one buffer before each step.  The HBM-bound legs
 also report `warm`: the same steps back to back in one event bracket, with
-inputs reused from step to step (partly served by the Infinity Cache).  The
-dominant-kernel launch loops behind `roofline` are cold the same way.
+inputs reused from step to step (partly served by the Infinity Cache).
+
+The launch loops behind `roofline` time one launch of the dominant kernel.
+For the HBM-bound legs they are sustained: launches back to back over
+rotating buffer sets whose footprint (> 1.2 GB) is several times the
+Infinity Cache, so no input is cached and earlier launches' writes drain to
+HBM during later ones (a cold launch after a read-only flush can instead
+leave its writes in the Infinity Cache past its end event).  These legs also
+report `copy_ceiling`: a plain device copy of the same byte count timed both
+ways.  The MFMA-bound launch loops are cold (a 512 MB read before each).
 Every kernel is timed; the headline `value` is the RoPE fwd+bwd
 throughput on configs[1] (B=4, S=4096, 32/8 heads, D=128, bf16, bases 10000
 and 500000 alternate by step), the others are reported under "kernels".
@@ -159,6 +167,71 @@ def time_launches(launch_fn, n, warmup=3):
     return statistics.mean(a.elapsed_time(b) for a, b in evs)
 
 
+SUSTAINED_FOOTPRINT = 1200 * 10 ** 6  # bytes of rotating buffers: > 4x the Infinity Cache
+SUSTAINED_LABEL = "sustained: launches back to back over rotating buffer sets of > 1.2 GB"
+
+
+def n_sets(set_bytes):
+    """Buffer sets a sustained launch loop rotates over: at least two, and
+    enough that their footprint exceeds SUSTAINED_FOOTPRINT."""
+    return max(2, -(-SUSTAINED_FOOTPRINT // max(1, set_bytes)))
+
+
+def time_sustained(launch_fn, n, warmup=4):
+    """Average duration (ms) of one launch at steady state: launches run back
+    to back, launch i on buffer set i % K (launch_fn picks it), where the K
+    sets (> 1.2 GB) are several times the 256 MB Infinity Cache, so no input
+    is cached when a launch reads it and the writes of earlier launches drain
+    to HBM during later ones.  HIP events on torch's current stream (the
+    stream every forge_* call launches on) bracket each launch."""
+    import torch
+
+    for i in range(warmup):
+        launch_fn(i)
+    _sync()
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(n)]
+    for i, (a, b) in enumerate(evs):
+        a.record()
+        launch_fn(warmup + i)
+        b.record()
+    _sync()
+    return statistics.mean(a.elapsed_time(b) for a, b in evs)
+
+
+def copy_ceiling(args, nbytes, n=20):
+    """Plain device copies moving nbytes in all (between buffers of nbytes / 2),
+    timed both ways a kernel of the same byte count is: cold (after a 512 MB
+    read, as the steps) and sustained (rotating sets, as the roofline
+    launches).  Two copies: forge_copy (16-byte nontemporal loads and stores)
+    and torch's elementwise kernel (y = x * 1 in bf16); the ceiling is the
+    faster of the two.  A cold launch's writes can land in the Infinity Cache
+    and drain after its end event; the copies are timed the same way, so the
+    rates compare."""
+    import torch
+    from forge_hip import _lib as L
+
+    if args.only_launches:
+        return None
+    half = nbytes // 2 // 16 * 16
+    k = n_sets(2 * half)
+    srcs = [torch.ones(half // 2, dtype=torch.bfloat16, device="cuda") for _ in range(k)]
+    dsts = [torch.empty_like(s) for s in srcs]
+    st = L.stream_of(srcs[0])
+    fns = {
+        "forge_copy": lambda i: L.forge_copy(dsts[i % k].data_ptr(), srcs[i % k].data_ptr(), half, st),
+        "torch_mul": lambda i: torch.mul(srcs[i % k], 1, out=dsts[i % k]),
+    }
+    res = {"unit": "GB/s", "bytes": 2 * half}
+    for name, fn in fns.items():
+        cold_ms = time_launches(lambda i: fn(0), n)
+        sus_ms = time_sustained(fn, n)
+        res[name] = {"cold": rate(2 * half, cold_ms, 1e9), "sustained": rate(2 * half, sus_ms, 1e9)}
+    res["cold"] = max(v["cold"] for v in (res["forge_copy"], res["torch_mul"]))
+    res["sustained"] = max(v["sustained"] for v in (res["forge_copy"], res["torch_mul"]))
+    del srcs, dsts
+    return res
+
+
 def run_steps(args, step_fn, restore=None):
     """Cold per-step timing (time_steps_cold); (None, None) with
     --only-launches."""
@@ -250,23 +323,34 @@ def bench_swiglu(args):
     warm = warm_steps(args, step, bytes_step)
     gates.clear()
     ups.clear()
-    # dominant kernel: backward (5 tensor passes)
-    gf, uf, out = gate0.clone(), up0.clone(), torch.empty_like(gate0)
-    st = L.stream_of(gf)
-    bwd_ms = time_launches(lambda i: L.forge_swiglu_bwd(0, dout.data_ptr(), C, gf.data_ptr(), uf.data_ptr(), C,
-                                                        gf.data_ptr(), uf.data_ptr(), C, R, C, 1.0, 1.0, st),
-                           max(args.steps, 10))
-    fwd_ms = time_launches(lambda i: L.forge_swiglu_fwd(0, gate0.data_ptr(), up0.data_ptr(), C, out.data_ptr(), C,
-                                                        R, C, 1.0, 1.0, st), max(args.steps, 10))
+    # dominant kernel: backward (5 tensor passes), sustained over rotating
+    # sets of (gate, up, dout, out)
     bwd_bytes = 5 * n * 4
+    k = n_sets(bwd_bytes)
+    sets = [(gate0.clone(), up0.clone(), dout.clone(), torch.empty_like(gate0)) for _ in range(k)]
+    st = L.stream_of(gate0)
+
+    def bwd(i):
+        gf, uf, df, _ = sets[i % k]
+        L.forge_swiglu_bwd(0, df.data_ptr(), C, gf.data_ptr(), uf.data_ptr(), C, gf.data_ptr(), uf.data_ptr(), C,
+                           R, C, 1.0, 1.0, st)
+
+    def fwd(i):
+        gf, uf, _, out = sets[i % k]
+        L.forge_swiglu_fwd(0, gf.data_ptr(), uf.data_ptr(), C, out.data_ptr(), C, R, C, 1.0, 1.0, st)
+
+    bwd_ms = time_sustained(bwd, max(args.steps, 20))
+    fwd_ms = time_sustained(fwd, max(args.steps, 20))
+    del sets
     res = {
         "config": {"workload": "swiglu_fwd_bwd", "dtype": "fp32", "shape": [R, C], "gate_multiplier": 1.0,
                    "down_multiplier": 1.0, "preserve_inputs": False},
         "value": gbs, "unit": "GB/s", "ms_per_step": rnd(ms, 5), "wall_ms_per_step": rnd(wall, 5),
         "frac_of_hbm_peak": rnd(gbs and gbs / HBM_PEAK_GBS, 4), "algorithmic_bytes_per_step": bytes_step,
-        "timing": "cold: each step alone after a 512 MB read", "warm": warm,
+        "timing": "cold: each step alone after a 512 MB read", "warm": warm, "launch_timing": SUSTAINED_LABEL,
         "launches_ms": {"forge_swiglu_fwd": round(fwd_ms, 5), "forge_swiglu_bwd": round(bwd_ms, 5)},
         "roofline": _roof("hbm", bwd_bytes / (bwd_ms * 1e-3) / 1e9, HBM_PEAK_GBS, "GB/s", _traffic("swiglu_bwd")),
+        "copy_ceiling": copy_ceiling(args, bwd_bytes),
         "dtype": "f32",
     }
     if not (args.no_cpu_baseline or args.only_launches):
@@ -322,17 +406,30 @@ def bench_rope(args):
     bytes_step = 2 * bytes_dir
     gbs = rate(bytes_step, ms, 1e9)
     warm = warm_steps(args, step, bytes_step)
-    oq, ok = torch.empty_like(qv), torch.empty_like(kv)
-    launch_ms = time_launches(lambda i: _rope_launch(qv, kv, oq, ok, tabs[i % 2][0], tabs[i % 2][1], bool(i % 2)),
-                              max(2 * args.steps, 20))
+    # one direction, sustained over rotating sets of (q, k, q_out, k_out),
+    # each a fresh HF transpose(1, 2) view of BSHD memory; the base and the
+    # direction alternate as in the steps
+    nk = n_sets(bytes_dir)
+    sets = []
+    for _ in range(nk):
+        qs, ks = q.clone().transpose(1, 2), k.clone().transpose(1, 2)
+        sets.append((qs, ks, torch.empty_like(qs), torch.empty_like(ks)))
+
+    def launch(i):
+        qs, ks, oq, ok = sets[i % nk]
+        _rope_launch(qs, ks, oq, ok, tabs[i % 2][0], tabs[i % 2][1], bool(i % 2))
+
+    launch_ms = time_sustained(launch, max(2 * args.steps, 40))
+    del sets
     res = {
         "config": {"workload": "rope_fwd_bwd", "dtype": "bf16", "q": [B, NQ, S, D], "k": [B, NKV, S, D],
                    "layout": "BSHD memory, HF transpose(1,2) view", "bases": [10000, 500000]},
         "value": gbs, "unit": "GB/s", "ms_per_step": rnd(ms, 5), "wall_ms_per_step": rnd(wall, 5),
         "frac_of_hbm_peak": rnd(gbs and gbs / HBM_PEAK_GBS, 4), "algorithmic_bytes_per_step": bytes_step,
-        "timing": "cold: each step alone after a 512 MB read", "warm": warm,
+        "timing": "cold: each step alone after a 512 MB read", "warm": warm, "launch_timing": SUSTAINED_LABEL,
         "launches_ms": {"forge_rope": round(launch_ms, 5)},
         "roofline": _roof("hbm", bytes_dir / (launch_ms * 1e-3) / 1e9, HBM_PEAK_GBS, "GB/s", _traffic("rope")),
+        "copy_ceiling": copy_ceiling(args, bytes_dir),
         "dtype": "bf16",
     }
     if not (args.no_cpu_baseline or args.only_launches):
@@ -379,23 +476,33 @@ def bench_ce(args):
     ms, wall = run_steps(args, step, restore)
     bytes_step = V * 2 * (2 * n_valid + n_ign) + 8 * BT
     gbs = rate(bytes_step, ms, 1e9)
+    # sustained over two 2.1 GB logits buffers (the steps' buffer and one more)
+    xbuf.copy_(logits0)
     xb = logits0.clone()
+    sets = [xbuf, xb]
     loss1d = torch.empty(BT, device="cuda")
     st = L.stream_of(xb)
     flags = L.CE_HAS_GRADIENTS | L.CE_REDUCTION_MEAN
-    launch_ms = time_launches(
-        lambda i: L.forge_ce_fwd(2, xb.data_ptr(), V, BT, V, target.data_ptr(), 1, None, loss1d.data_ptr(), None,
-                                 None, None, -100, float(n_valid), float(n_valid), 0.0, 0.0, 0.0, 0.0, flags, None, st),
-        max(args.steps, 10))
+    launch_ms = time_sustained(
+        lambda i: L.forge_ce_fwd(2, sets[i % 2].data_ptr(), V, BT, V, target.data_ptr(), 1, None, loss1d.data_ptr(),
+                                 None, None, None, -100, float(n_valid), float(n_valid), 0.0, 0.0, 0.0, 0.0, flags,
+                                 None, st),
+        max(args.steps, 20))
+    del sets
     res = {
         "config": {"workload": "cross_entropy_fwd_bwd", "dtype": "bf16", "logits": [BT, V], "ignored_rows": n_ign,
                    "reduction": "mean", "grad_output": 1.0},
         "value": gbs, "unit": "GB/s", "ms_per_step": rnd(ms, 5), "wall_ms_per_step": rnd(wall, 5),
         "frac_of_hbm_peak": rnd(gbs and gbs / HBM_PEAK_GBS, 4), "algorithmic_bytes_per_step": bytes_step,
+        "timing": "cold: each step alone after its logits are restored and a 512 MB read",
+        "launch_timing": SUSTAINED_LABEL,
         "launches_ms": {"forge_ce_fwd": round(launch_ms, 5)},
         "roofline": _roof("hbm", bytes_step / (launch_ms * 1e-3) / 1e9, HBM_PEAK_GBS, "GB/s", _traffic("ce_fwd")),
+        "copy_ceiling": None,
         "dtype": "bf16",
     }
+    del xb
+    res["copy_ceiling"] = copy_ceiling(args, bytes_step)
     if not (args.no_cpu_baseline or args.only_launches):
         import torch.nn.functional as F
 
@@ -850,18 +957,26 @@ def bench_geglu(args):
     warm = warm_steps(args, step, bytes_step)
     gates.clear()
     ups.clear()
-    gf, uf = gate0.clone(), up0.clone()
-    st = L.stream_of(gf)
-    bwd_ms = time_launches(lambda i: L.forge_geglu_bwd(2, dout.data_ptr(), C, gf.data_ptr(), uf.data_ptr(), C,
-                                                       gf.data_ptr(), uf.data_ptr(), C, R, C, 1, st),
-                           max(args.steps, 10))
+    # the backward, sustained over rotating sets of (gate, up, dout)
+    k = n_sets(5 * n * 2)
+    sets = [(gate0.clone(), up0.clone(), dout.clone()) for _ in range(k)]
+    st = L.stream_of(gate0)
+
+    def bwd(i):
+        gf, uf, df = sets[i % k]
+        L.forge_geglu_bwd(2, df.data_ptr(), C, gf.data_ptr(), uf.data_ptr(), C, gf.data_ptr(), uf.data_ptr(), C,
+                          R, C, 1, st)
+
+    bwd_ms = time_sustained(bwd, max(args.steps, 20))
+    del sets
     res = {
         "config": {"workload": "geglu_fwd_bwd", "dtype": "bf16", "shape": [R, C], "approximate": "tanh"},
         "value": gbs, "unit": "GB/s", "ms_per_step": rnd(ms, 5), "wall_ms_per_step": rnd(wall, 5),
         "frac_of_hbm_peak": rnd(gbs and gbs / HBM_PEAK_GBS, 4), "algorithmic_bytes_per_step": bytes_step,
-        "timing": "cold: each step alone after a 512 MB read", "warm": warm,
+        "timing": "cold: each step alone after a 512 MB read", "warm": warm, "launch_timing": SUSTAINED_LABEL,
         "launches_ms": {"forge_geglu_bwd": round(bwd_ms, 5)},
         "roofline": _roof("hbm", 5 * n * 2 / (bwd_ms * 1e-3) / 1e9, HBM_PEAK_GBS, "GB/s", _traffic("geglu_bwd")),
+        "copy_ceiling": copy_ceiling(args, 5 * n * 2),
         "dtype": "bf16",
     }
     if not (args.no_cpu_baseline or args.only_launches):
@@ -917,22 +1032,29 @@ def bench_rmsnorm(args):
     st = L.stream_of(xd)
     L.check(L.forge_rmsnorm_fwd(2, 2, 2, xd.data_ptr(), H, wd.data_ptr(), yb.data_ptr(), H, rstd.data_ptr(), R, H,
                                 1e-6, 0.0, 0, st), "forge_rmsnorm_fwd")
-    dyb = dy0.clone()
-    dx = torch.empty_like(xd)
+    bwd_bytes = 3 * R * H * 2 + 4 * R + 3 * H * 2
+    # sustained over rotating sets of (x, dy, dx) (rstd and the weight are shared)
+    k = n_sets(bwd_bytes)
+    sets = [(xd.clone(), dy0.clone(), torch.empty_like(xd)) for _ in range(k)]
     dw = torch.empty(H, device="cuda", dtype=bf)
     work = torch.empty(L.forge_rmsnorm_bwd_workspace(2, R, H), device="cuda", dtype=torch.uint8)
-    bwd_ms = time_launches(lambda i: L.forge_rmsnorm_bwd(2, 2, dyb.data_ptr(), H, xd.data_ptr(), H, wd.data_ptr(),
-                                                         rstd.data_ptr(), dx.data_ptr(), H, dw.data_ptr(),
-                                                         work.data_ptr(), R, H, 0.0, 0, st), max(args.steps, 10))
-    bwd_bytes = 3 * R * H * 2 + 4 * R + 3 * H * 2
+
+    def bwd(i):
+        xs, dys, dxs = sets[i % k]
+        L.forge_rmsnorm_bwd(2, 2, dys.data_ptr(), H, xs.data_ptr(), H, wd.data_ptr(), rstd.data_ptr(), dxs.data_ptr(),
+                            H, dw.data_ptr(), work.data_ptr(), R, H, 0.0, 0, st)
+
+    bwd_ms = time_sustained(bwd, max(args.steps, 20))
+    del sets
     res = {
         "config": {"workload": "rmsnorm_fwd_bwd", "dtype": "bf16", "shape": [R, H], "casting_mode": "llama",
                    "offset": 0.0, "in_place": True, "weight_grad": True},
         "value": gbs, "unit": "GB/s", "ms_per_step": rnd(ms, 5), "wall_ms_per_step": rnd(wall, 5),
         "frac_of_hbm_peak": rnd(gbs and gbs / HBM_PEAK_GBS, 4), "algorithmic_bytes_per_step": bytes_step,
-        "timing": "cold: each step alone after a 512 MB read", "warm": warm,
+        "timing": "cold: each step alone after a 512 MB read", "warm": warm, "launch_timing": SUSTAINED_LABEL,
         "launches_ms": {"forge_rmsnorm_bwd": round(bwd_ms, 5)},
         "roofline": _roof("hbm", bwd_bytes / (bwd_ms * 1e-3) / 1e9, HBM_PEAK_GBS, "GB/s", _traffic("rmsnorm_bwd")),
+        "copy_ceiling": copy_ceiling(args, bwd_bytes),
         "dtype": "bf16",
     }
     if not (args.no_cpu_baseline or args.only_launches):
@@ -1004,6 +1126,7 @@ def main():
         "timing": head.get("timing"),
         "warm": head.get("warm"),
         "roofline": head["roofline"],
+        "copy_ceiling": head.get("copy_ceiling"),
         "cpu_baseline": head.get("cpu_baseline"),
         "kernels": results,
     }

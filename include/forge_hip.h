@@ -421,6 +421,13 @@ int forge_lora_a_noalloc(int64_t M, int64_t K, int64_t r, int n_proj, const void
  * cast a reduced fp32 [rows, cols] block to bf16. */
 int forge_zero(void* ptr, int64_t bytes, void* stream);
 
+/* Copies `bytes` bytes from src to dst (both 16-byte aligned, not
+ * overlapping) with 16-byte nontemporal loads and stores.  No counterpart in
+ * the reference: a plain device copy with the access pattern of this
+ * library's streaming kernels, the ceiling that the HBM-bound kernels' rates
+ * are read against. */
+int forge_copy(void* dst, const void* src, int64_t bytes, void* stream);
+
 /* out[m, n] = alpha * sum_{z < n_split} parts[z*split_stride + m*ld_parts + n],
  * summed in z order (deterministic), rounded once to out_dtype (fp32, bf16 or
  * fp16).  The reduction of forge_gemm / forge_lora_a split-K partials; no

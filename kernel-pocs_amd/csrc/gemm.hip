@@ -27,6 +27,15 @@ enum Cfg {
 #ifndef SKINNY_WPE
 #define SKINNY_WPE 2
 #endif
+#ifndef NARROW64_NSTAGE
+#define NARROW64_NSTAGE 3
+#endif
+#ifndef NARROW64_WPE
+#define NARROW64_WPE 3
+#endif
+#ifndef NARROW_WIDE_NSTAGE
+#define NARROW_WIDE_NSTAGE 2
+#endif
 
 template <int BM, int BN, int WM, int WN, int AL, int BL, int BMODE, int EPI>
 static int launch_cfg(const GemmArgs& a, hipStream_t s) {
@@ -55,8 +64,8 @@ static int launch_cfg(const GemmArgs& a, hipStream_t s) {
     // products) two stages in 64 KB, with no padded columns.  M/64 tiles fill
     // the chip without a split-K pass.  B may be [N][K] or, read with the
     // transposing LDS loads, [K][N] as stored.
-    constexpr int NS = BN >= 192 ? 2 : 3;
-    constexpr int WPE_N = BN == 64 ? 3 : 2;
+    constexpr int NS = BN >= 192 ? NARROW_WIDE_NSTAGE : BN == 64 ? NARROW64_NSTAGE : 3;
+    constexpr int WPE_N = BN == 64 ? NARROW64_WPE : 2;
     gemm_dma_kernel<BM, BN, WM, WN, BMODE, EPI, 64, NS, false, WPE_N, false, BL == ROW>
         <<<grid, WM * WN * 64, 0, s>>>(a);
   } else if constexpr (AL == COL && BL == ROW && BMODE == B_SINGLE && BM == 256 && BN == 256) {

@@ -13,6 +13,23 @@ __global__ __launch_bounds__(256) void zero_kernel(uint4* p, int64_t n16, uint8_
   if (blockIdx.x == 0 && threadIdx.x < ntail) tail[threadIdx.x] = 0;
 }
 
+// Plain device copy: 16-byte nontemporal loads and stores with two vectors in
+// flight per thread, the access pattern of this library's streaming kernels;
+// the last bytes % 16 bytes are copied by workgroup 0.
+__global__ __launch_bounds__(256) void copy_kernel(const uint4* src, uint4* dst, int64_t n16, const uint8_t* src_tail,
+                                                   uint8_t* dst_tail, int64_t ntail) {
+  const int64_t stride = (int64_t)gridDim.x * 512;
+  for (int64_t i = (int64_t)blockIdx.x * 512 + threadIdx.x; i < n16; i += stride) {
+    const bool two = i + 256 < n16;
+    const u32x4_t a = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(src + i));
+    u32x4_t b = a;
+    if (two) b = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(src + i + 256));
+    __builtin_nontemporal_store(a, reinterpret_cast<u32x4_t*>(dst + i));
+    if (two) __builtin_nontemporal_store(b, reinterpret_cast<u32x4_t*>(dst + i + 256));
+  }
+  if (blockIdx.x == 0 && threadIdx.x < ntail) dst_tail[threadIdx.x] = src_tail[threadIdx.x];
+}
+
 __global__ __launch_bounds__(256) void cast_f32_bf16_kernel(const float* src, int64_t lds, bf16_t* dst,
                                                             int64_t ldd, int64_t rows, int64_t cols) {
   const int64_t n = rows * cols;
@@ -168,6 +185,24 @@ extern "C" int forge_zero(void* ptr, int64_t bytes, void* stream) {
   const int64_t n16 = bytes / 16;
   zero_kernel<<<grid_for(n16 > 0 ? n16 : 1, 256, 2048), 256, 0, (hipStream_t)stream>>>(
       (uint4*)ptr, n16, (uint8_t*)ptr + n16 * 16, bytes - n16 * 16);
+  FORGE_CHECK_LAUNCH();
+  return FORGE_OK;
+}
+
+extern "C" int forge_copy(void* dst, const void* src, int64_t bytes, void* stream) {
+  if (bytes <= 0) return FORGE_OK;
+  if (!dst || !src) return forge_set_error(FORGE_ERR_INVALID, "copy: null pointer");
+  if (!aligned16(dst) || !aligned16(src)) return forge_set_error(FORGE_ERR_INVALID, "copy: pointers not 16-byte aligned");
+  const uintptr_t d = (uintptr_t)dst, s = (uintptr_t)src;
+  if (d < s + (uintptr_t)bytes && s < d + (uintptr_t)bytes)
+    return forge_set_error(FORGE_ERR_INVALID, "copy: source and destination overlap");
+  const int64_t n16 = bytes / 16;
+  int64_t blocks = (n16 + 511) / 512;
+  if (blocks < 1) blocks = 1;
+  if (blocks > 65536) blocks = 65536;
+  copy_kernel<<<(unsigned)blocks, 256, 0, (hipStream_t)stream>>>((const uint4*)src, (uint4*)dst, n16,
+                                                                 (const uint8_t*)src + n16 * 16,
+                                                                 (uint8_t*)dst + n16 * 16, bytes - n16 * 16);
   FORGE_CHECK_LAUNCH();
   return FORGE_OK;
 }

@@ -81,3 +81,23 @@ def test_status_codes_and_messages():
 def test_zero_size_calls_are_noops():
     assert L.forge_swiglu_fwd(0, None, None, 0, None, 0, 0, 0, 1.0, 1.0, None) == 0
     assert L.forge_ce_fwd(2, None, 0, 0, 0, None, 1, None, None, None, None, None, -100, *([0.0] * 6), 0, None, None) == 0
+
+
+def test_copy_argument_errors():
+    # misaligned pointers and overlapping ranges are rejected before any launch
+    assert L.forge_copy(16, 24, 64, None) == 1 and b"aligned" in L.forge_last_error()
+    assert L.forge_copy(16, 32, 64, None) == 1 and b"overlap" in L.forge_last_error()
+    assert L.forge_copy(None, None, 0, None) == 0
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("nbytes", [1, 15, 16, 4096 + 7, 512 * 16 * 3 + 5, (1 << 24) + 9])
+def test_copy_is_exact(nbytes):
+    import torch
+
+    src = torch.randint(0, 256, (nbytes,), dtype=torch.uint8, device="cuda")
+    dst = torch.zeros(nbytes + 16, dtype=torch.uint8, device="cuda")
+    L.check(L.forge_copy(dst.data_ptr(), src.data_ptr(), nbytes, L.stream_of(src)), "forge_copy")
+    torch.cuda.synchronize()
+    assert torch.equal(dst[:nbytes], src)
+    assert int(dst[nbytes:].sum()) == 0  # nothing written past the end
