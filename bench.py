@@ -182,20 +182,23 @@ def time_sustained(launch_fn, n, warmup=4):
     to back, launch i on buffer set i % K (launch_fn picks it), where the K
     sets (> 1.2 GB) are several times the 256 MB Infinity Cache, so no input
     is cached when a launch reads it and the writes of earlier launches drain
-    to HBM during later ones.  HIP events on torch's current stream (the
-    stream every forge_* call launches on) bracket each launch."""
+    to HBM during later ones.  One pair of HIP events on torch's current
+    stream (the stream every forge_* call launches on) brackets the n
+    launches, which run with no gap between them; the mean is total / n.
+    (An event pair around each launch would add the ~3-6 us that each event
+    puts between two kernels.)"""
     import torch
 
     for i in range(warmup):
         launch_fn(i)
     _sync()
-    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(n)]
-    for i, (a, b) in enumerate(evs):
-        a.record()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record()
+    for i in range(n):
         launch_fn(warmup + i)
-        b.record()
+    b.record()
     _sync()
-    return statistics.mean(a.elapsed_time(b) for a, b in evs)
+    return a.elapsed_time(b) / n
 
 
 def copy_ceiling(args, nbytes, n=20):

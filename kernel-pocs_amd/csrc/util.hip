@@ -13,19 +13,24 @@ __global__ __launch_bounds__(256) void zero_kernel(uint4* p, int64_t n16, uint8_
   if (blockIdx.x == 0 && threadIdx.x < ntail) tail[threadIdx.x] = 0;
 }
 
-// Plain device copy: 16-byte nontemporal loads and stores with two vectors in
-// flight per thread, the access pattern of this library's streaming kernels;
-// the last bytes % 16 bytes are copied by workgroup 0.
+// Plain device copy: 16-byte nontemporal loads and stores, VPT vectors in
+// flight per thread (the access pattern of this library's streaming kernels);
+// the last bytes % 16 bytes are copied by workgroup 0.  Measured sustained on
+// MI355X (rotating buffers): one vector per thread streams 6.3-6.4 TB/s for
+// copies of 0.3-0.5 GB, two 6.2; at 2 GB two vectors are best (6.2 against
+// 6.0).
+template <int VPT>
 __global__ __launch_bounds__(256) void copy_kernel(const uint4* src, uint4* dst, int64_t n16, const uint8_t* src_tail,
                                                    uint8_t* dst_tail, int64_t ntail) {
-  const int64_t stride = (int64_t)gridDim.x * 512;
-  for (int64_t i = (int64_t)blockIdx.x * 512 + threadIdx.x; i < n16; i += stride) {
-    const bool two = i + 256 < n16;
-    const u32x4_t a = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(src + i));
-    u32x4_t b = a;
-    if (two) b = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(src + i + 256));
-    __builtin_nontemporal_store(a, reinterpret_cast<u32x4_t*>(dst + i));
-    if (two) __builtin_nontemporal_store(b, reinterpret_cast<u32x4_t*>(dst + i + 256));
+  const int64_t stride = (int64_t)gridDim.x * 256 * VPT;
+  for (int64_t i = (int64_t)blockIdx.x * 256 * VPT + threadIdx.x; i < n16; i += stride) {
+    u32x4_t v[VPT];
+#pragma unroll
+    for (int j = 0; j < VPT; ++j)
+      if (i + j * 256 < n16) v[j] = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(src + i + j * 256));
+#pragma unroll
+    for (int j = 0; j < VPT; ++j)
+      if (i + j * 256 < n16) __builtin_nontemporal_store(v[j], reinterpret_cast<u32x4_t*>(dst + i + j * 256));
   }
   if (blockIdx.x == 0 && threadIdx.x < ntail) dst_tail[threadIdx.x] = src_tail[threadIdx.x];
 }
@@ -197,12 +202,19 @@ extern "C" int forge_copy(void* dst, const void* src, int64_t bytes, void* strea
   if (d < s + (uintptr_t)bytes && s < d + (uintptr_t)bytes)
     return forge_set_error(FORGE_ERR_INVALID, "copy: source and destination overlap");
   const int64_t n16 = bytes / 16;
-  int64_t blocks = (n16 + 511) / 512;
+  const bool one = n16 <= (64LL << 20);  // up to 1 GiB: one vector per thread
+  const int vpt = one ? 1 : 2;
+  int64_t blocks = (n16 + 256 * vpt - 1) / (256 * vpt);
   if (blocks < 1) blocks = 1;
   if (blocks > 65536) blocks = 65536;
-  copy_kernel<<<(unsigned)blocks, 256, 0, (hipStream_t)stream>>>((const uint4*)src, (uint4*)dst, n16,
-                                                                 (const uint8_t*)src + n16 * 16,
-                                                                 (uint8_t*)dst + n16 * 16, bytes - n16 * 16);
+  const uint8_t* st = (const uint8_t*)src + n16 * 16;
+  uint8_t* dt = (uint8_t*)dst + n16 * 16;
+  if (one)
+    copy_kernel<1><<<(unsigned)blocks, 256, 0, (hipStream_t)stream>>>((const uint4*)src, (uint4*)dst, n16, st, dt,
+                                                                      bytes - n16 * 16);
+  else
+    copy_kernel<2><<<(unsigned)blocks, 256, 0, (hipStream_t)stream>>>((const uint4*)src, (uint4*)dst, n16, st, dt,
+                                                                      bytes - n16 * 16);
   FORGE_CHECK_LAUNCH();
   return FORGE_OK;
 }

@@ -91,7 +91,7 @@ def test_copy_argument_errors():
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("nbytes", [1, 15, 16, 4096 + 7, 512 * 16 * 3 + 5, (1 << 24) + 9])
+@pytest.mark.parametrize("nbytes", [1, 15, 16, 4096 + 7, 512 * 16 * 3 + 5, (1 << 24) + 9, (1 << 30) + 16 * 300 + 3])
 def test_copy_is_exact(nbytes):
     import torch
 
