@@ -27,15 +27,6 @@ enum Cfg {
 #ifndef SKINNY_WPE
 #define SKINNY_WPE 2
 #endif
-#ifndef NARROW64_NSTAGE
-#define NARROW64_NSTAGE 3
-#endif
-#ifndef NARROW64_WPE
-#define NARROW64_WPE 3
-#endif
-#ifndef NARROW_WIDE_NSTAGE
-#define NARROW_WIDE_NSTAGE 2
-#endif
 
 template <int BM, int BN, int WM, int WN, int AL, int BL, int BMODE, int EPI>
 static int launch_cfg(const GemmArgs& a, hipStream_t s) {
@@ -64,8 +55,10 @@ static int launch_cfg(const GemmArgs& a, hipStream_t s) {
     // products) two stages in 64 KB, with no padded columns.  M/64 tiles fill
     // the chip without a split-K pass.  B may be [N][K] or, read with the
     // transposing LDS loads, [K][N] as stored.
-    constexpr int NS = BN >= 192 ? NARROW_WIDE_NSTAGE : BN == 64 ? NARROW64_NSTAGE : 3;
-    constexpr int WPE_N = BN == 64 ? NARROW64_WPE : 2;
+    // (measured cold on MI355X: 4 or 5 stages at 64 x 64 and 3 at 64 x 192 were
+    // no faster; 64 x 64 or 64 x 128 tiles for the 192-wide product were slower)
+    constexpr int NS = BN >= 192 ? 2 : 3;
+    constexpr int WPE_N = BN == 64 ? 3 : 2;
     gemm_dma_kernel<BM, BN, WM, WN, BMODE, EPI, 64, NS, false, WPE_N, false, BL == ROW>
         <<<grid, WM * WN * 64, 0, s>>>(a);
   } else if constexpr (AL == COL && BL == ROW && BMODE == B_SINGLE && BM == 256 && BN == 256) {

@@ -182,12 +182,12 @@ extern "C" int forge_lora_a(int64_t M, int64_t K, int64_t r, int n_proj, const v
   a.ep.alpha = 1.f;
   a.ep.alpha_group = r;
   for (int p = 0; p < 4; ++p) a.ep.alphas[p] = p < n_proj ? scales[p] : 1.f;
-  // 256 x 32 tiles for N <= 32, else 256 x 64 (X A^T is K-contiguous: both
-  // run on the LDS-DMA ring).  With split_k the K range is spread over
-  // split_k workgroups per tile (the skinny output alone gives only M/256
-  // tiles): split z writes fp32 partial sums to work[z] ([split_k][M][N]),
-  // which one reduction pass sums in a fixed order (deterministic) and rounds
-  // to bf16.
+  // 64-row tiles as wide as the output (64, 128, 192 or 256 columns: X A^T
+  // is K-contiguous, on the LDS-DMA ring).  With split_k the K range is
+  // spread over split_k workgroups per tile (when M / 64 tiles alone do not
+  // fill the chip): split z writes fp32 partial sums to work[z]
+  // ([split_k][M][N]), which one reduction pass sums in a fixed order
+  // (deterministic) and rounds to bf16.
   const int cfg = -1;  // the narrow K-contiguous tiles (64 x N, N up to 256) picked from the shape
   if (split_k <= 1) {
     a.ep.c = out;
