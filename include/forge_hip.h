@@ -264,13 +264,18 @@ int forge_gemm_generic(int64_t M, int64_t N, int64_t K, int dtype,
  * i.e. an nn.Linear weight used as W^T), ROW = [K][N] (N contiguous). */
 enum { FORGE_LAYOUT_ROW = 0, FORGE_LAYOUT_COL = 1 };
 
-/* One K-segment of a multi-segment product C = sum_s A_s @ B_s. */
+/* One K-segment of a multi-segment product C = sum_s A_s @ B_s.  With
+ * n_lo < n_hi the segment applies only to output columns [n_lo, n_hi) and B's
+ * first column (row, for B as [N][K]) is output column n_lo; n_lo = n_hi = 0
+ * means every column.  Segments with disjoint column ranges make several
+ * independent products one launch (e.g. [dQ B_q | dK B_k | dV B_v]). */
 typedef struct forge_gemm_segment {
   const void* a;  /* bf16 */
   int64_t lda;
   const void* b;  /* bf16 */
   int64_t ldb;
   int64_t k;      /* extent of this segment along K (multiple of 8) */
+  int64_t n_lo, n_hi;
 } forge_gemm_segment;
 
 enum {
@@ -445,6 +450,15 @@ int forge_cast_f32_bf16(const float* src, int64_t ld_src, void* dst, int64_t ld_
  * transposed operands directly). */
 int forge_transpose_2b(const void* src, int64_t ld_src, int64_t rows, int64_t cols, void* dst, int64_t ld_dst,
                        void* stream);
+
+/* Up to FORGE_TRANSPOSE_BATCH_MAX of the above in one launch: matrix i is
+ * src[i] [rows[i], cols[i]] (pitch ld_src[i]) -> dst[i] [cols[i], rows[i]]
+ * (pitch ld_dst[i]).  The transposed rank-r LoRA matrices that the backward
+ * passes read K-contiguous (B^T for dY B, A^T for the dX LoRA segments), in
+ * one launch per backward instead of one each; no reference counterpart. */
+#define FORGE_TRANSPOSE_BATCH_MAX 8
+int forge_transpose_2b_batch(int n, const void* const* src, const int64_t* ld_src, const int64_t* rows,
+                             const int64_t* cols, void* const* dst, const int64_t* ld_dst, void* stream);
 
 #ifdef __cplusplus
 }

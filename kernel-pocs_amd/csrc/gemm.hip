@@ -227,6 +227,8 @@ extern "C" int forge_gemm(int64_t M, int64_t N, const forge_gemm_segment* segs, 
   a.M = M;
   a.N = N;
   a.n_segs = n_segs;
+  bool ranged = false;
+  int64_t width = 0;  // widest column range of a segment
   for (int i = 0; i < n_segs; ++i) {
     a.segs[i].a = (const __bf16*)segs[i].a;
     a.segs[i].lda = segs[i].lda;
@@ -234,9 +236,22 @@ extern "C" int forge_gemm(int64_t M, int64_t N, const forge_gemm_segment* segs, 
     a.segs[i].b2 = nullptr;
     a.segs[i].ldb = segs[i].ldb;
     a.segs[i].k = segs[i].k;
-    a.segs[i].n_lo = 0;
-    a.segs[i].n_hi = N;
+    if (segs[i].n_lo == 0 && segs[i].n_hi == 0) {
+      a.segs[i].n_lo = 0;
+      a.segs[i].n_hi = N;
+    } else {
+      if (segs[i].n_lo < 0 || segs[i].n_hi <= segs[i].n_lo || segs[i].n_hi > N)
+        return forge_set_error(FORGE_ERR_INVALID, "gemm: segment %d columns [%lld, %lld) outside [0, %lld)", i,
+                               (long long)segs[i].n_lo, (long long)segs[i].n_hi, (long long)N);
+      a.segs[i].n_lo = segs[i].n_lo;
+      a.segs[i].n_hi = segs[i].n_hi;
+      ranged = true;
+    }
+    if (a.segs[i].n_hi - a.segs[i].n_lo > width) width = a.segs[i].n_hi - a.segs[i].n_lo;
   }
+  // column-ranged segments: tiles sized for the widest range, so that
+  // independent products side by side get tiles of their own
+  const int cfg = ranged ? pick_cfg(M, width, a_layout, b_layout) : -1;
   a.split_k = split_k;
   a.ep.c = c;
   a.ep.ldc = ldc;
@@ -270,5 +285,5 @@ extern "C" int forge_gemm(int64_t M, int64_t N, const forge_gemm_segment* segs, 
   } else {
     return forge_set_error(FORGE_ERR_INVALID, "gemm: epilogue %d", epilogue);
   }
-  return run(-1, a_layout, b_layout, epi, a, (hipStream_t)stream);
+  return run(cfg, a_layout, b_layout, epi, a, (hipStream_t)stream);
 }

@@ -106,13 +106,13 @@ int launch_reduce(const float* parts, int64_t stride, int n_split, int64_t rows,
   return FORGE_OK;
 }
 
-// out[c, r] = in[r, c] for 2-byte elements (bf16 / fp16): 64 x 64 tiles
-// through LDS (row pitch 66 elements against bank conflicts on the column
-// reads), 16-byte loads and stores when pitches and bases allow.
-__global__ __launch_bounds__(256) void transpose2_kernel(const uint16_t* in, int64_t ld_in, int64_t rows, int64_t cols,
-                                                         uint16_t* out, int64_t ld_out, int64_t tiles_c, int vec) {
-  __shared__ uint16_t tile[64][66];
-  const int64_t r0 = (blockIdx.x / tiles_c) * 64, c0 = (blockIdx.x % tiles_c) * 64;
+// out[c, r] = in[r, c] for 2-byte elements (bf16 / fp16), one 64 x 64 tile
+// (index `tidx`) through LDS (row pitch 66 elements against bank conflicts on
+// the column reads), 16-byte loads and stores when pitches and bases allow.
+__device__ __forceinline__ void transpose_tile(const uint16_t* in, int64_t ld_in, int64_t rows, int64_t cols,
+                                               uint16_t* out, int64_t ld_out, int64_t tiles_c, int vec,
+                                               int64_t tidx, uint16_t (&tile)[64][66]) {
+  const int64_t r0 = (tidx / tiles_c) * 64, c0 = (tidx % tiles_c) * 64;
   const int t = threadIdx.x;
 #pragma unroll
   for (int it = 0; it < 2; ++it) {
@@ -153,6 +153,34 @@ __global__ __launch_bounds__(256) void transpose2_kernel(const uint16_t* in, int
   }
 }
 
+__global__ __launch_bounds__(256) void transpose2_kernel(const uint16_t* in, int64_t ld_in, int64_t rows, int64_t cols,
+                                                         uint16_t* out, int64_t ld_out, int64_t tiles_c, int vec) {
+  __shared__ uint16_t tile[64][66];
+  transpose_tile(in, ld_in, rows, cols, out, ld_out, tiles_c, vec, blockIdx.x, tile);
+}
+
+// Up to FORGE_TRANSPOSE_BATCH_MAX transposes in one launch: workgroup b takes
+// tile b - first[i] of matrix i, first[i] <= b < first[i + 1].
+struct TransposeBatch {
+  int n;
+  const uint16_t* in[FORGE_TRANSPOSE_BATCH_MAX];
+  uint16_t* out[FORGE_TRANSPOSE_BATCH_MAX];
+  int64_t ld_in[FORGE_TRANSPOSE_BATCH_MAX], ld_out[FORGE_TRANSPOSE_BATCH_MAX];
+  int64_t rows[FORGE_TRANSPOSE_BATCH_MAX], cols[FORGE_TRANSPOSE_BATCH_MAX];
+  int64_t tiles_c[FORGE_TRANSPOSE_BATCH_MAX];
+  int64_t first[FORGE_TRANSPOSE_BATCH_MAX + 1];
+  int vec[FORGE_TRANSPOSE_BATCH_MAX];
+};
+
+__global__ __launch_bounds__(256) void transpose2_batch_kernel(TransposeBatch b) {
+  __shared__ uint16_t tile[64][66];
+  const int64_t blk = blockIdx.x;
+  int i = 0;
+  while (i + 1 < b.n && blk >= b.first[i + 1]) ++i;
+  transpose_tile(b.in[i], b.ld_in[i], b.rows[i], b.cols[i], b.out[i], b.ld_out[i], b.tiles_c[i], b.vec[i],
+                 blk - b.first[i], tile);
+}
+
 }  // namespace
 
 extern "C" int forge_transpose_2b(const void* src, int64_t ld_src, int64_t rows, int64_t cols, void* dst,
@@ -166,6 +194,37 @@ extern "C" int forge_transpose_2b(const void* src, int64_t ld_src, int64_t rows,
   const int vec = aligned16(src) && aligned16(dst) && ld_src % 8 == 0 && ld_dst % 8 == 0;
   transpose2_kernel<<<(unsigned)(tr * tc), 256, 0, (hipStream_t)stream>>>(
       (const uint16_t*)src, ld_src, rows, cols, (uint16_t*)dst, ld_dst, tc, vec);
+  FORGE_CHECK_LAUNCH();
+  return FORGE_OK;
+}
+
+extern "C" int forge_transpose_2b_batch(int n, const void* const* src, const int64_t* ld_src, const int64_t* rows,
+                                        const int64_t* cols, void* const* dst, const int64_t* ld_dst, void* stream) {
+  if (n < 0 || n > FORGE_TRANSPOSE_BATCH_MAX)
+    return forge_set_error(FORGE_ERR_INVALID, "transpose_2b_batch: 0..%d matrices", FORGE_TRANSPOSE_BATCH_MAX);
+  TransposeBatch b = {};
+  b.n = n;
+  int64_t tiles = 0;
+  for (int i = 0; i < n; ++i) {
+    if (rows[i] < 0 || cols[i] < 0 || ld_src[i] < cols[i] || ld_dst[i] < rows[i])
+      return forge_set_error(FORGE_ERR_INVALID, "transpose_2b_batch: shape / pitch of matrix %d", i);
+    if (rows[i] > 0 && cols[i] > 0 && (!src[i] || !dst[i]))
+      return forge_set_error(FORGE_ERR_INVALID, "transpose_2b_batch: null pointer (matrix %d)", i);
+    b.in[i] = (const uint16_t*)src[i];
+    b.out[i] = (uint16_t*)dst[i];
+    b.ld_in[i] = ld_src[i];
+    b.ld_out[i] = ld_dst[i];
+    b.rows[i] = rows[i];
+    b.cols[i] = cols[i];
+    b.tiles_c[i] = (cols[i] + 63) / 64;
+    b.vec[i] = aligned16(src[i]) && aligned16(dst[i]) && ld_src[i] % 8 == 0 && ld_dst[i] % 8 == 0;
+    b.first[i] = tiles;
+    tiles += (rows[i] > 0 && cols[i] > 0) ? ((rows[i] + 63) / 64) * b.tiles_c[i] : 0;
+  }
+  b.first[n] = tiles;
+  if (tiles == 0) return FORGE_OK;
+  if (tiles > 0x7fffffffLL) return forge_set_error(FORGE_ERR_INVALID, "transpose_2b_batch: too many tiles");
+  transpose2_batch_kernel<<<(unsigned)tiles, 256, 0, (hipStream_t)stream>>>(b);
   FORGE_CHECK_LAUNCH();
   return FORGE_OK;
 }

@@ -63,6 +63,8 @@ class GemmSegment(ctypes.Structure):
         ("b", c_vp),
         ("ldb", c_i64),
         ("k", c_i64),
+        ("n_lo", c_i64),  # output columns [n_lo, n_hi); 0, 0 = every column
+        ("n_hi", c_i64),
     ]
 
 
@@ -161,6 +163,8 @@ forge_rmsnorm_bwd_workspace = _decl("forge_rmsnorm_bwd_workspace", [c_int, c_i64
 forge_zero = _decl("forge_zero", [c_vp, c_i64, c_vp])
 forge_copy = _decl("forge_copy", [c_vp, c_vp, c_i64, c_vp])
 forge_transpose_2b = _decl("forge_transpose_2b", [c_vp, c_i64, c_i64, c_i64, c_vp, c_i64, c_vp])
+forge_transpose_2b_batch = _decl("forge_transpose_2b_batch", [c_int, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp])
+TRANSPOSE_BATCH_MAX = 8
 forge_cast_f32_bf16 = _decl("forge_cast_f32_bf16", [c_vp, c_i64, c_vp, c_i64, c_i64, c_i64, c_vp])
 
 # Every symbol include/forge_hip.h declares (checked by the CPU test suite).
@@ -170,7 +174,7 @@ EXPORTED = [
     "forge_ce_fwd", "forge_ce_target_stats", "forge_ce_scale", "forge_sum_f32",
     "forge_gemm", "forge_lora_mlp_gate_up", "forge_lora_mlp_down_bwd", "forge_lora_qkv_rope",
     "forge_lora_a", "forge_lora_a_noalloc", "forge_zero", "forge_copy", "forge_cast_f32_bf16", "forge_splitk_reduce",
-    "forge_ce_target_prob", "forge_row_scale", "forge_gemm_generic", "forge_transpose_2b",
+    "forge_ce_target_prob", "forge_row_scale", "forge_gemm_generic", "forge_transpose_2b", "forge_transpose_2b_batch",
     "forge_rmsnorm_fwd", "forge_rmsnorm_bwd", "forge_rmsnorm_bwd_workspace",
 ]
 

@@ -53,15 +53,27 @@ def skinny_split(M: int, N: int, K: int, k_contiguous: bool = True) -> int:
     return max(1, min(16, -(-512 // tiles), k_tiles // 4))
 
 
+def _segments(segs) -> ctypes.Array:
+    """forge_gemm_segment array from (A, lda, B, ldb, K) tuples, optionally
+    extended by (n_lo, n_hi): the output columns the segment applies to."""
+    arr = (L.GemmSegment * len(segs))()
+    for i, sg in enumerate(segs):
+        a, lda, b, ldb, k = sg[:5]
+        n_lo, n_hi = (int(sg[5]), int(sg[6])) if len(sg) > 5 else (0, 0)
+        arr[i] = L.GemmSegment(a.data_ptr(), int(lda), b.data_ptr(), int(ldb), int(k), n_lo, n_hi)
+    return arr
+
+
 def gemm(M: int, N: int, segs: Sequence[Tuple[torch.Tensor, int, torch.Tensor, int, int]], a_layout: int,
          b_layout: int, out: Optional[torch.Tensor] = None, alpha: float = 1.0, beta: float = 0.0,
          out_dtype=torch.bfloat16, atomic: bool = False, split_k: int = 1, device=None) -> torch.Tensor:
-    """C[M, N] = alpha * sum_s A_s @ B_s (+ beta C).  segs: (A, lda, B, ldb, K).
-    atomic=True accumulates into a zero-initialised fp32 C over split_k
+    """C[M, N] = alpha * sum_s A_s @ B_s (+ beta C).  segs: (A, lda, B, ldb, K),
+    or (A, lda, B, ldb, K, n_lo, n_hi) for a segment that applies to output
+    columns [n_lo, n_hi) only (B's first row is column n_lo).  atomic=True accumulates into a zero-initialised fp32 C over split_k
     K partitions.  A skinny bf16 output (N <= 64, beta = 0) is split over K
     into fp32 partial slices, then summed in a fixed order and rounded."""
     dev = device if device is not None else segs[0][0].device
-    K = sum(int(k) for (_, _, _, _, k) in segs)
+    K = sum(int(sg[4]) for sg in segs)
     if not atomic and beta == 0.0 and N <= 64 and M >= 1024 and (out is None or out.dtype == torch.bfloat16):
         split = skinny_split(M, N, K, a_layout == ROW)
         if split > 1:
@@ -74,9 +86,7 @@ def gemm(M: int, N: int, segs: Sequence[Tuple[torch.Tensor, int, torch.Tensor, i
             L.check(L.forge_zero(out.data_ptr(), out.numel() * 4, L.stream_of(out)), "forge_zero")
         else:
             out = torch.empty(M, N, dtype=out_dtype, device=dev)
-    arr = (L.GemmSegment * len(segs))()
-    for i, (a, lda, b, ldb, k) in enumerate(segs):
-        arr[i] = L.GemmSegment(a.data_ptr(), int(lda), b.data_ptr(), int(ldb), int(k))
+    arr = _segments(segs)
     c_dtype = L.DTYPE_F32 if out.dtype == torch.float32 else L.DTYPE_BF16
     L.check(
         L.forge_gemm(M, N, arr, len(segs), a_layout, b_layout, out.data_ptr(), ld(out), c_dtype, float(alpha),
@@ -94,9 +104,7 @@ def split_gemm(M: int, N: int, segs, a_layout: int, b_layout: int, split: int, o
     once to out's dtype."""
     dev = device if device is not None else out.device
     parts = torch.empty(split, M, N, dtype=torch.float32, device=dev)
-    arr = (L.GemmSegment * len(segs))()
-    for i, (a, lda, b, ldb, k) in enumerate(segs):
-        arr[i] = L.GemmSegment(a.data_ptr(), int(lda), b.data_ptr(), int(ldb), int(k))
+    arr = _segments(segs)
     st = L.stream_of(parts)
     L.check(L.forge_gemm(M, N, arr, len(segs), a_layout, b_layout, parts.data_ptr(), N, L.DTYPE_F32, float(alpha),
                          0.0, L.EPI_STORE, int(split), st), "forge_gemm")
@@ -200,15 +208,42 @@ def small_t(a: torch.Tensor) -> torch.Tensor:
     return a.detach().t().contiguous()
 
 
+def small_t_batch(mats: Sequence[torch.Tensor]) -> list:
+    """small_t of each 2-byte matrix in one launch (forge_transpose_2b_batch)
+    instead of one copy kernel each; the transposes share one buffer."""
+    mats = [as_operand(m.detach()) for m in mats]
+    if len(mats) > L.TRANSPOSE_BATCH_MAX or any(m.element_size() != 2 or m.dim() != 2 for m in mats):
+        return [small_t(m) for m in mats]
+    sizes = [m.numel() for m in mats]
+    # each transposed matrix starts on a 16-byte boundary of the shared buffer
+    offs, o = [], 0
+    for n in sizes:
+        offs.append(o)
+        o += -(-n // 8) * 8
+    buf = torch.empty(o, dtype=mats[0].dtype, device=mats[0].device)
+    outs = [buf[off:off + n].view(m.shape[1], m.shape[0]) for off, n, m in zip(offs, sizes, mats)]
+    k = len(mats)
+    src = (ctypes.c_void_p * k)(*[m.data_ptr() for m in mats])
+    dst = (ctypes.c_void_p * k)(*[t.data_ptr() for t in outs])
+    ld_src = (ctypes.c_int64 * k)(*[ld(m) for m in mats])
+    rows = (ctypes.c_int64 * k)(*[m.shape[0] for m in mats])
+    cols = (ctypes.c_int64 * k)(*[m.shape[1] for m in mats])
+    ld_dst = (ctypes.c_int64 * k)(*[m.shape[0] for m in mats])
+    L.check(L.forge_transpose_2b_batch(k, src, ld_src, rows, cols, dst, ld_dst, L.stream_of(buf)),
+            "forge_transpose_2b_batch")
+    return outs
+
+
 def times_b(x: torch.Tensor, ldx: int, b: torch.Tensor, k: int, out: Optional[torch.Tensor] = None,
-            alpha: float = 1.0) -> torch.Tensor:
+            alpha: float = 1.0, b_t: Optional[torch.Tensor] = None) -> torch.Tensor:
     """alpha * x @ b for a rank-r LoRA B [k, r], from a transposed copy
-    B^T [r, k] (a few hundred KB): with both operands K-contiguous the
-    narrow tiles stream x faster than when they read B [k][r] as stored
-    (measured cold on MI355X: [8192, 14336] x [14336, 16] 68.5 -> 51.1 us,
-    [22954, 4096] x [4096, 64] 70.0 -> 52.8 us)."""
+    B^T [r, k] (a few hundred KB; b_t if the caller made it already): with
+    both operands K-contiguous the narrow tiles stream x faster than when
+    they read B [k][r] as stored (measured cold on MI355X: [8192, 14336] x
+    [14336, 16] 68.5 -> 51.1 us, [22954, 4096] x [4096, 64] 70.0 -> 52.8 us)."""
     M = x.shape[0]
-    return gemm(M, b.shape[1], [(x, ldx, small_t(b), k, k)], ROW, COL, out=out, alpha=alpha)
+    bt = b_t if b_t is not None else small_t(b)
+    return gemm(M, b.shape[1], [(x, ldx, bt, k, k)], ROW, COL, out=out, alpha=alpha)
 
 
 def split_k_for(k: int, tiles: int, target_wgs: int = 512, min_tiles_per_split: int = 4) -> int:

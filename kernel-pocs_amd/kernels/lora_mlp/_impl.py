@@ -38,7 +38,7 @@ import torch.nn.functional as F
 
 from forge_hip import _lib as L
 from kernels import _generic_lora as G
-from kernels._lora_ops import COL, ROW, as_operand, frozen_t, gemm, grad_at_b, ld, lora_a, small_t, times_b
+from kernels._lora_ops import COL, ROW, as_operand, frozen_t, gemm, grad_at_b, ld, lora_a, small_t_batch, times_b
 
 
 def _w(t):
@@ -122,14 +122,19 @@ def mlp_backward(dY2, X2, e, g, W_gate, A_gate, B_gate, s_gate, W_up, A_up, B_up
     dev = X2.device
     Ag, Bg, Au, Bu, Ad, Bd = (_w(t) for t in (A_gate, B_gate, A_up, B_up, A_down, B_down))
 
-    # 1-2: DW = dY Wd + sd (dY Bd) Ad with the GLU backward fused in place
-    td = times_b(dY2, ld(dY2), Bd, H, alpha=s_down)
-    h = torch.empty(M, I, dtype=torch.bfloat16, device=dev)
     # K-contiguous weights (cached W^T, small A^T) put the three big GEMMs of
     # the backward on the LDS-DMA engine; a rank that is not a multiple of 8
-    # keeps the [K][N] layout
+    # keeps the [K][N] layout.  The six small transposes (B^T for the dY B
+    # products, A^T for the LoRA segments) are one launch.
     kt = r % 8 == 0
-    WdB, AdB, wl = (frozen_t(W_down), small_t(Ad), COL) if kt else (Wd, Ad, ROW)
+    BdT = BuT = BgT = None
+    if kt:
+        BdT, AdT, BuT, BgT, AuT, AgT = small_t_batch([Bd, Ad, Bu, Bg, Au, Ag])
+
+    # 1-2: DW = dY Wd + sd (dY Bd) Ad with the GLU backward fused in place
+    td = times_b(dY2, ld(dY2), Bd, H, alpha=s_down, b_t=BdT)
+    h = torch.empty(M, I, dtype=torch.bfloat16, device=dev)
+    WdB, AdB, wl = (frozen_t(W_down), AdT, COL) if kt else (Wd, Ad, ROW)
     L.check(
         L.forge_lora_mlp_down_bwd(M, H, I, r, dY2.data_ptr(), ld(dY2), WdB.data_ptr(), ld(WdB), td.data_ptr(), r,
                                   AdB.data_ptr(), ld(AdB), wl, h.data_ptr(), e.data_ptr(), g.data_ptr(), I, act,
@@ -149,8 +154,11 @@ def mlp_backward(dY2, X2, e, g, W_gate, A_gate, B_gate, s_gate, W_up, A_up, B_up
 
     # 4: up / gate LoRA grads
     v = torch.empty(M, 2 * r, dtype=torch.bfloat16, device=dev)  # [su df Bu | sg de Bg]
-    times_b(df, I, Bu, I, out=v[:, :r], alpha=s_up)
-    times_b(de, I, Bg, I, out=v[:, r:], alpha=s_gate)
+    if kt and s_up == s_gate:  # both products in one launch (column-ranged segments)
+        gemm(M, 2 * r, [(df, I, BuT, I, I, 0, r), (de, I, BgT, I, I, r, 2 * r)], ROW, COL, out=v, alpha=s_up)
+    else:
+        times_b(df, I, Bu, I, out=v[:, :r], alpha=s_up, b_t=BuT)
+        times_b(de, I, Bg, I, out=v[:, r:], alpha=s_gate, b_t=BgT)
     dA_ug = grad_at_b(v, 2 * r, X2, ld(X2), 2 * r, H, M, out_dtype=dt)  # [2r, H]: rows [dAu; dAg]
     if aux is not None and "xa" in aux:
         xa = aux["xa"]                                            # [sg X Ag^T | su X Au^T]
@@ -163,7 +171,7 @@ def mlp_backward(dY2, X2, e, g, W_gate, A_gate, B_gate, s_gate, W_up, A_up, B_up
 
     # 5: dX
     if kt:
-        WuT, WgT, AuT, AgT = frozen_t(W_up), frozen_t(W_gate), small_t(Au), small_t(Ag)
+        WuT, WgT = frozen_t(W_up), frozen_t(W_gate)
         dX = gemm(M, H, [(df, I, WuT, I, I), (de, I, WgT, I, I),
                          (v[:, :r], 2 * r, AuT, r, r), (v[:, r:], 2 * r, AgT, r, r)], ROW, COL)
     else:

@@ -26,7 +26,7 @@ import torch
 
 from forge_hip import _lib as L
 from kernels import _generic_lora as G
-from kernels._lora_ops import COL, ROW, as_operand, frozen_t, gemm, grad_at_b, ld, lora_a, small_t, times_b
+from kernels._lora_ops import COL, ROW, as_operand, frozen_t, gemm, grad_at_b, ld, lora_a, small_t_batch, times_b
 
 
 def _w(t):
@@ -117,10 +117,18 @@ def qkv_backward(dQ, dK, dV, X2, W_q, W_k, W_v, A_q, B_q, s_q, A_k, B_k, s_k, A_
     r = A_q.shape[0]
     dev = X2.device
     Aq, Bq, Ak, Bk, Av, Bv = (_w(t) for t in (A_q, B_q, A_k, B_k, A_v, B_v))
+    kt = r % 8 == 0  # K-contiguous operands for the LDS-DMA engine (cached W^T, small A^T / B^T)
+    BqT = BkT = BvT = None
+    if kt:  # the six small transposes in one launch
+        BqT, BkT, BvT, AqT, AkT, AvT = small_t_batch([Bq, Bk, Bv, Aq, Ak, Av])
     t = torch.empty(M, 3 * r, dtype=torch.bfloat16, device=dev)
-    times_b(dQ, ld(dQ), Bq, Hq, out=t[:, :r], alpha=s_q)
-    times_b(dK, ld(dK), Bk, Hkv, out=t[:, r:2 * r], alpha=s_k)
-    times_b(dV, ld(dV), Bv, Hkv, out=t[:, 2 * r:], alpha=s_v)
+    if kt and s_q == s_k == s_v:  # [dQ Bq | dK Bk | dV Bv] in one launch (column-ranged segments)
+        gemm(M, 3 * r, [(dQ, ld(dQ), BqT, Hq, Hq, 0, r), (dK, ld(dK), BkT, Hkv, Hkv, r, 2 * r),
+                        (dV, ld(dV), BvT, Hkv, Hkv, 2 * r, 3 * r)], ROW, COL, out=t, alpha=s_q)
+    else:
+        times_b(dQ, ld(dQ), Bq, Hq, out=t[:, :r], alpha=s_q, b_t=BqT)
+        times_b(dK, ld(dK), Bk, Hkv, out=t[:, r:2 * r], alpha=s_k, b_t=BkT)
+        times_b(dV, ld(dV), Bv, Hkv, out=t[:, 2 * r:], alpha=s_v, b_t=BvT)
     dt = A_q.dtype
     dA = grad_at_b(t, 3 * r, X2, ld(X2), 3 * r, K, M, out_dtype=dt)  # [3r, K] (scales included via t)
     if aux is not None and "xa" in aux:
@@ -130,10 +138,10 @@ def qkv_backward(dQ, dK, dV, X2, W_q, W_k, W_v, A_q, B_q, s_q, A_k, B_k, s_k, A_
     dBq = grad_at_b(dQ, ld(dQ), xa[:, :r], 3 * r, Hq, r, M, alpha=sc[0], out_dtype=dt)
     dBk = grad_at_b(dK, ld(dK), xa[:, r:2 * r], 3 * r, Hkv, r, M, alpha=sc[1], out_dtype=dt)
     dBv = grad_at_b(dV, ld(dV), xa[:, 2 * r:], 3 * r, Hkv, r, M, alpha=sc[2], out_dtype=dt)
-    if r % 8 == 0:  # K-contiguous weights: the LDS-DMA engine (cached W^T, small A^T)
+    if kt:
         dX = gemm(M, K, [(dQ, ld(dQ), frozen_t(W_q), Hq, Hq), (dK, ld(dK), frozen_t(W_k), Hkv, Hkv),
-                         (dV, ld(dV), frozen_t(W_v), Hkv, Hkv), (t[:, :r], 3 * r, small_t(Aq), r, r),
-                         (t[:, r:2 * r], 3 * r, small_t(Ak), r, r), (t[:, 2 * r:], 3 * r, small_t(Av), r, r)],
+                         (dV, ld(dV), frozen_t(W_v), Hkv, Hkv), (t[:, :r], 3 * r, AqT, r, r),
+                         (t[:, r:2 * r], 3 * r, AkT, r, r), (t[:, 2 * r:], 3 * r, AvT, r, r)],
                   ROW, COL)
     else:
         dX = gemm(M, K, [(dQ, ld(dQ), Wq, ld(Wq), Hq), (dK, ld(dK), Wk, ld(Wk), Hkv),

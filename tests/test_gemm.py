@@ -191,3 +191,79 @@ def test_transpose_2b(rows, cols, ld_in, ld_out):
             "forge_transpose_2b")
     assert torch.equal(dst[:, :rows].cpu(), src[:, :cols].t().cpu())
     assert bool((dst[:, rows:] == 7.0).all())  # pitch padding untouched
+
+
+@pytest.mark.gpu
+def test_transpose_2b_batch_matches_single_transposes():
+    """One launch, matrices of different shapes, pitches and alignments (a
+    zero-size one included); every output equals src^T and pitch padding is
+    untouched."""
+    import ctypes
+
+    gen = torch.Generator().manual_seed(5)
+    shapes = [(16, 14336, 14336, 16), (4096, 64, 64, 4096), (7, 129, 130, 9), (0, 5, 5, 0), (300, 1003, 1008, 304),
+              (64, 64, 64, 64)]
+    srcs = [torch.randn(r, ldi, generator=gen).to(torch.bfloat16).cuda() for r, _, ldi, _ in shapes]
+    dsts = [torch.full((c, max(ldo, 1)), 7.0, dtype=torch.bfloat16).cuda() for _, c, _, ldo in shapes]
+    n = len(shapes)
+    arr = lambda t, vals: (t * n)(*vals)  # noqa: E731
+    L.check(L.forge_transpose_2b_batch(
+        n, arr(ctypes.c_void_p, [s.data_ptr() for s in srcs]), arr(ctypes.c_int64, [s[2] for s in shapes]),
+        arr(ctypes.c_int64, [s[0] for s in shapes]), arr(ctypes.c_int64, [s[1] for s in shapes]),
+        arr(ctypes.c_void_p, [d.data_ptr() for d in dsts]), arr(ctypes.c_int64, [s[3] for s in shapes]),
+        L.stream_of(srcs[0])), "forge_transpose_2b_batch")
+    for (r, c, _, ldo), s, d in zip(shapes, srcs, dsts):
+        assert torch.equal(d[:, :r].cpu(), s[:, :c].t().cpu())
+        assert bool((d[:, r:] == 7.0).all())
+
+
+def test_transpose_2b_batch_rejects_bad_arguments_without_gpu():
+    import ctypes
+
+    one = lambda t, v: (t * 1)(v)  # noqa: E731
+    rc = L.forge_transpose_2b_batch(9, None, None, None, None, None, None, None)
+    assert rc == 1 and b"matrices" in L.forge_last_error()
+    rc = L.forge_transpose_2b_batch(1, one(ctypes.c_void_p, 16), one(ctypes.c_int64, 4), one(ctypes.c_int64, 8),
+                                    one(ctypes.c_int64, 8), one(ctypes.c_void_p, 16), one(ctypes.c_int64, 8), None)
+    assert rc == 1 and b"pitch" in L.forge_last_error()
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("M,r,split", [(2048, 16, 1), (2048, 16, 4), (300, 64, 1), (1000, 8, 3)])
+def test_gemm_column_ranged_segments(M, r, split):
+    """Independent products side by side in one launch: out[:, p r:(p+1) r] =
+    A_p B_p^T with a different K per product (segments restricted to their
+    columns), against float32 matmuls of the same bf16 operands; with split-K
+    the fp32 partials are summed by forge_splitk_reduce."""
+    gen = torch.Generator().manual_seed(6)
+    Ks = [512, 128, 136]
+    As = [torch.randn(M, k, generator=gen).to(torch.bfloat16) for k in Ks]
+    Bs = [torch.randn(r, k, generator=gen).to(torch.bfloat16) for k in Ks]  # B^T [r][K] (layout COL)
+    N = r * len(Ks)
+    segs = (L.GemmSegment * len(Ks))()
+    dA, dB = [a.cuda() for a in As], [b.cuda() for b in Bs]
+    for p, (a, b, k) in enumerate(zip(dA, dB, Ks)):
+        segs[p] = L.GemmSegment(a.data_ptr(), k, b.data_ptr(), k, k, p * r, (p + 1) * r)
+    ref = torch.cat([a.float() @ b.float().t() for a, b in zip(As, Bs)], 1)
+    if split == 1:
+        c = torch.zeros(M, N, dtype=torch.bfloat16).cuda()
+        L.check(L.forge_gemm(M, N, segs, len(Ks), L.LAYOUT_ROW, L.LAYOUT_COL, c.data_ptr(), N, L.DTYPE_BF16, 1.0,
+                             0.0, L.EPI_STORE, 1, L.stream_of(c)), "forge_gemm")
+        got = c.float().cpu()
+    else:
+        parts = torch.empty(split, M, N).cuda()
+        L.check(L.forge_gemm(M, N, segs, len(Ks), L.LAYOUT_ROW, L.LAYOUT_COL, parts.data_ptr(), N, L.DTYPE_F32,
+                             1.0, 0.0, L.EPI_STORE, split, L.stream_of(parts)), "forge_gemm")
+        got = parts.sum(0).cpu()
+    scale = ref.abs().max()
+    torch.testing.assert_close(got / scale, ref / scale, atol=2e-2, rtol=0)
+
+
+def test_gemm_rejects_bad_column_ranges_without_gpu():
+    seg = (L.GemmSegment * 1)()
+    seg[0] = L.GemmSegment(16, 8, 16, 8, 8, 4, 40)  # [4, 40) outside N = 32
+    rc = L.forge_gemm(64, 32, seg, 1, 0, 1, 16, 32, L.DTYPE_BF16, 1.0, 0.0, L.EPI_STORE, 1, None)
+    assert rc == 1 and b"columns" in L.forge_last_error()
+    seg[0] = L.GemmSegment(16, 8, 16, 8, 8, 8, 8)  # empty range with n_lo != 0
+    rc = L.forge_gemm(64, 32, seg, 1, 0, 1, 16, 32, L.DTYPE_BF16, 1.0, 0.0, L.EPI_STORE, 1, None)
+    assert rc == 1

@@ -140,3 +140,21 @@ def test_lora_mlp_baseline_config():
     _, g2 = _run(lambda x, *p: LoRAMLPv6.apply(x, *p), X[:, h:], dY[:, h:], params)
     for name, a, b1, b2 in zip(NAMES[1:], grads[1:], g1[1:], g2[1:]):
         _close_bf16(a, b1.float() + b2.float(), name + " additivity")
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("scales", [(2.0, 2.0, 2.0), (1.5, 0.5, 3.0)])
+def test_lora_mlp_per_projection_scales(scales):
+    """Equal gate / up scales take the one-launch [df B_u | de B_g] product,
+    different ones a launch each; both against the oracle."""
+    B, S, H, I, r = 2, 300, 512, 1536, 16
+    gen = torch.Generator().manual_seed(23)
+    params = list(orc.make_params(H, I, r, 2 * r, gen))
+    params[3], params[7], params[11] = scales
+    X = torch.randn(B, S, H, generator=gen).to(torch.bfloat16)
+    dY = torch.randn(B, S, H, generator=gen).to(torch.bfloat16)
+    ref_out, ref_grads = orc.fwd_bwd(X, dY, params)
+    out, grads = _run(lambda x, *p: LoRAMLPv6.apply(x, *p), X, dY, params)
+    _close_bf16(out.reshape(-1, H), ref_out, "out")
+    for n, a, b in zip(NAMES, grads, ref_grads):
+        _close_bf16(a.reshape(b.shape), b, n)

@@ -241,3 +241,28 @@ def test_lora_qkv_v4_saves_packed_matrices():
     s2 = Q2.grad_fn.saved_tensors
     assert s2[7].data_ptr() == W_dX.data_ptr() and s2[8].data_ptr() == A_pack.data_ptr()
     torch.testing.assert_close(Q2, Q, rtol=0, atol=0)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("scales", [(2.0, 2.0, 2.0), (1.5, 0.5, 3.0)])
+def test_lora_qkv_per_projection_scales(scales):
+    """Equal scales take the one-launch [dQ B_q | dK B_k | dV B_v] product,
+    different ones a launch per projection; both against the oracle."""
+    T, K, Hq, Hkv, r = 1100, 512, 512, 128, 64
+    gen = torch.Generator().manual_seed(17)
+    params = list(orc.make_params(K, Hq, Hkv, r, 2 * r, gen))
+    params[5], params[8], params[11] = scales
+    X = torch.randn(T, K, generator=gen).to(torch.bfloat16)
+    dQ = torch.randn(T, Hq, generator=gen).to(torch.bfloat16)
+    dK = torch.randn(T, Hkv, generator=gen).to(torch.bfloat16)
+    dV = torch.randn(T, Hkv, generator=gen).to(torch.bfloat16)
+    f = lambda t: t.float() if isinstance(t, torch.Tensor) else t  # noqa: E731
+    pf = [f(t) for t in params]
+    ref_grads = orc.backward(dQ.float(), dK.float(), dV.float(), X.float(), *pf)
+    p = _cuda(params)
+    x = X.cuda().requires_grad_(True)
+    Q, K_, V = LoRAQKVv4Function.apply(x, *p)
+    torch.autograd.backward((Q, K_, V), (dQ.cuda(), dK.cuda(), dV.cuda()))
+    got = [x.grad, p[3].grad, p[4].grad, p[6].grad, p[7].grad, p[9].grad, p[10].grad]
+    for n, a, b in zip(NAMES, got, ref_grads):
+        _close_bf16(a, b, n)
