@@ -211,9 +211,9 @@ def small_t(a: torch.Tensor) -> torch.Tensor:
 def small_t_batch(mats: Sequence[torch.Tensor]) -> list:
     """small_t of each 2-byte matrix in one launch (forge_transpose_2b_batch)
     instead of one copy kernel each; the transposes share one buffer."""
-    mats = [as_operand(m.detach()) for m in mats]
-    if len(mats) > L.TRANSPOSE_BATCH_MAX or any(m.element_size() != 2 or m.dim() != 2 for m in mats):
+    if len(mats) > L.TRANSPOSE_BATCH_MAX or any(m.dtype != torch.bfloat16 or m.dim() != 2 for m in mats):
         return [small_t(m) for m in mats]
+    mats = [as_operand(m.detach()) for m in mats]
     sizes = [m.numel() for m in mats]
     # each transposed matrix starts on a 16-byte boundary of the shared buffer
     offs, o = [], 0
@@ -270,3 +270,30 @@ def grad_at_b(a_t: torch.Tensor, lda: int, b: torch.Tensor, ldb: int, rows: int,
     split = split_k_for(k, tiles_m * tiles_n, target_wgs=256 if big else 512)
     out = torch.empty(rows, cols, dtype=out_dtype, device=a_t.device)
     return split_gemm(rows, cols, [(a_t, lda, b, ldb, k)], COL, ROW, split, out, alpha)
+
+
+def grad_at_b_group(pairs: Sequence[Tuple[torch.Tensor, int, torch.Tensor, int, int]], r: int, k: int,
+                    alpha: float = 1.0) -> list:
+    """[alpha * D_p^T @ U_p for each pair] (each [w_p, r] bf16), where U_p is
+    stored [k][r] (pitch ldu) and D_p [k][w_p] (pitch ldd), both token-major:
+    the LoRA B gradients of one backward in one launch.  Computed transposed,
+    out^T [r, sum w_p] = [U_p^T D_p], as one product with column-ranged
+    segments split over k (fp32 partials, fixed-order reduction, one
+    rounding), then the blocks transposed in one launch (measured cold on
+    MI355X, the three LoRA-QKV B gradients at T = 22954, r = 64: 138 -> 82 us
+    against a launch per projection).  pairs: (U_p, ldu, D_p, ldd, w_p)."""
+    widths = [int(p[4]) for p in pairs]
+    N = sum(widths)
+    dev = pairs[0][0].device
+    split = split_k_for(k, ((r + 31) // 32) * ((N + 255) // 256), target_wgs=512)
+    segs, lo = [], 0
+    for (u, ldu, d, ldd, w) in pairs:
+        segs.append((u, ldu, d, ldd, k, lo, lo + w))
+        lo += w
+    out_t = torch.empty(r, N, dtype=torch.bfloat16, device=dev)
+    split_gemm(r, N, segs, COL, ROW, split, out_t, alpha)
+    blocks, lo = [], 0
+    for w in widths:
+        blocks.append(out_t[:, lo:lo + w])
+        lo += w
+    return small_t_batch(blocks)

@@ -38,7 +38,8 @@ import torch.nn.functional as F
 
 from forge_hip import _lib as L
 from kernels import _generic_lora as G
-from kernels._lora_ops import COL, ROW, as_operand, frozen_t, gemm, grad_at_b, ld, lora_a, small_t_batch, times_b
+from kernels._lora_ops import (COL, ROW, as_operand, frozen_t, gemm, grad_at_b, grad_at_b_group, ld, lora_a,
+                               small_t_batch, times_b)
 
 
 def _w(t):
@@ -146,7 +147,12 @@ def mlp_backward(dY2, X2, e, g, W_gate, A_gate, B_gate, s_gate, W_up, A_up, B_up
     # 3: down-projection LoRA grads
     dt = A_gate.dtype
     dAd = grad_at_b(td, r, h, I, r, I, M, out_dtype=dt)          # [r, I] = (sd dY Bd)^T h
-    if aux is not None and "xd" in aux:
+    # with the forward's scaled products the three B gradients are one
+    # launch (step 4); otherwise each is its own
+    grouped = aux is not None and "xd" in aux and "xa" in aux and dt == torch.bfloat16
+    if grouped:
+        dBd = None
+    elif aux is not None and "xd" in aux:
         dBd = grad_at_b(dY2, ld(dY2), aux["xd"], r, H, r, M, out_dtype=dt)  # [H, r] = dY^T (sd h Ad^T)
     else:
         u = lora_a(h, [Ad], [1.0])                                # h Ad^T [M, r]
@@ -160,7 +166,11 @@ def mlp_backward(dY2, X2, e, g, W_gate, A_gate, B_gate, s_gate, W_up, A_up, B_up
         times_b(df, I, Bu, I, out=v[:, :r], alpha=s_up, b_t=BuT)
         times_b(de, I, Bg, I, out=v[:, r:], alpha=s_gate, b_t=BgT)
     dA_ug = grad_at_b(v, 2 * r, X2, ld(X2), 2 * r, H, M, out_dtype=dt)  # [2r, H]: rows [dAu; dAg]
-    if aux is not None and "xa" in aux:
+    if grouped:
+        xa = aux["xa"]                                            # [sg X Ag^T | su X Au^T]
+        dBd, dBu, dBg = grad_at_b_group([(aux["xd"], r, dY2, ld(dY2), H), (xa[:, r:], 2 * r, df, I, I),
+                                         (xa[:, :r], 2 * r, de, I, I)], r, M)
+    elif aux is not None and "xa" in aux:
         xa = aux["xa"]                                            # [sg X Ag^T | su X Au^T]
         dBu = grad_at_b(df, I, xa[:, r:], 2 * r, I, r, M, out_dtype=dt)
         dBg = grad_at_b(de, I, xa[:, :r], 2 * r, I, r, M, out_dtype=dt)

@@ -26,7 +26,8 @@ import torch
 
 from forge_hip import _lib as L
 from kernels import _generic_lora as G
-from kernels._lora_ops import COL, ROW, as_operand, frozen_t, gemm, grad_at_b, ld, lora_a, small_t_batch, times_b
+from kernels._lora_ops import (COL, ROW, as_operand, frozen_t, gemm, grad_at_b, grad_at_b_group, ld, lora_a,
+                               small_t_batch, times_b)
 
 
 def _w(t):
@@ -135,9 +136,13 @@ def qkv_backward(dQ, dK, dV, X2, W_q, W_k, W_v, A_q, B_q, s_q, A_k, B_k, s_k, A_
         xa, sc = aux["xa"], (1.0, 1.0, 1.0)            # scaled s_p X A_p^T from the forward
     else:
         xa, sc = lora_a(X2, [Aq, Ak, Av], [1.0, 1.0, 1.0]), (s_q, s_k, s_v)
-    dBq = grad_at_b(dQ, ld(dQ), xa[:, :r], 3 * r, Hq, r, M, alpha=sc[0], out_dtype=dt)
-    dBk = grad_at_b(dK, ld(dK), xa[:, r:2 * r], 3 * r, Hkv, r, M, alpha=sc[1], out_dtype=dt)
-    dBv = grad_at_b(dV, ld(dV), xa[:, 2 * r:], 3 * r, Hkv, r, M, alpha=sc[2], out_dtype=dt)
+    if dt == torch.bfloat16 and sc[0] == sc[1] == sc[2]:  # the three B gradients in one launch
+        dBq, dBk, dBv = grad_at_b_group([(xa[:, :r], 3 * r, dQ, ld(dQ), Hq), (xa[:, r:2 * r], 3 * r, dK, ld(dK), Hkv),
+                                         (xa[:, 2 * r:], 3 * r, dV, ld(dV), Hkv)], r, M, alpha=sc[0])
+    else:
+        dBq = grad_at_b(dQ, ld(dQ), xa[:, :r], 3 * r, Hq, r, M, alpha=sc[0], out_dtype=dt)
+        dBk = grad_at_b(dK, ld(dK), xa[:, r:2 * r], 3 * r, Hkv, r, M, alpha=sc[1], out_dtype=dt)
+        dBv = grad_at_b(dV, ld(dV), xa[:, 2 * r:], 3 * r, Hkv, r, M, alpha=sc[2], out_dtype=dt)
     if kt:
         dX = gemm(M, K, [(dQ, ld(dQ), frozen_t(W_q), Hq, Hq), (dK, ld(dK), frozen_t(W_k), Hkv, Hkv),
                          (dV, ld(dV), frozen_t(W_v), Hkv, Hkv), (t[:, :r], 3 * r, AqT, r, r),
