@@ -798,18 +798,17 @@ def bench_lora_qkv(args):
     ms, wall = run_steps(args, step)
     fl = T * flops_per_token(K, Hq, Hkv, r)
     tf = rate(fl, ms, 1e12)
-    # dominant kernel: the forward GEMM (X [Wq;Wk;Wv]^T + LoRA-B segment, RoPE epilogue)
-    from forge_hip import _lib as L
+    # dominant kernel: the forward GEMM (X [Wq;Wk;Wv]^T + LoRA-B segment, RoPE
+    # epilogue), forge_lora_qkv_rope
     from kernels._lora_ops import lora_a
+    from kernels.lora_qkv._impl import qkv_gemm
 
     Xd = X.detach()
     xa = lora_a(Xd, [Aq.detach(), Ak.detach(), Av.detach()], [s, s, s])  # the forward's LoRA-A product
     out = torch.empty(T, Hq + 2 * Hkv, device="cuda", dtype=bf)
-    st = L.stream_of(Xd)
-    launch_ms = time_launches(lambda i: L.forge_lora_qkv_rope(
-        T, K, Hq, Hkv, r, Xd.data_ptr(), K, Wq.data_ptr(), Wk.data_ptr(), Wv.data_ptr(), K, xa.data_ptr(), 3 * r,
-        Bq.data_ptr(), Bk.data_ptr(), Bv.data_ptr(), r, out.data_ptr(), Hq + 2 * Hkv, c.data_ptr(), sn.data_ptr(),
-        c.stride(0), c.shape[0], pos.data_ptr(), D, 1, st), max(args.steps, 10))
+    rope = {"cos": c, "sin": sn, "positions": pos, "head_dim": D}
+    launch_ms = time_launches(lambda i: qkv_gemm(Xd, Wq, Wk, Wv, xa, Bq.detach(), Bk.detach(), Bv.detach(), r, rope,
+                                                 out), max(args.steps, 10))
     fwd_flops = 2 * T * K * (Hq + 2 * Hkv) + 2 * T * r * (Hq + 2 * Hkv)
     res = {
         "config": {"workload": "lora_qkv_rope_fwd_bwd", "dtype": "bf16", "tokens": T, "seq_lens": lens,

@@ -68,6 +68,20 @@ def qkv_forward(X2, W_q, W_k, W_v, A_q, B_q, s_q, A_k, B_k, s_k, A_v, B_v, s_v,
         Bq, Bk, Bv = _w(B_q), _w(B_k), _w(B_v)
         if aux is not None:
             aux["xa"] = xa
+    qkv_gemm(X2, Wq, Wk, Wv, xa, Bq, Bk, Bv, r, rope, out)
+    return out
+
+
+def qkv_gemm(X2, Wq, Wk, Wv, xa, Bq, Bk, Bv, r: int, rope: Optional[dict], out: torch.Tensor) -> None:
+    """out = [X Wq^T + xa_q Bq^T | X Wk^T + xa_k Bk^T | X Wv^T + xa_v Bv^T]
+    (xa = [sq X Aq^T | sk X Ak^T | sv X Av^T], None without LoRA), Q and K
+    rotated in the epilogue when rope (bf16 tables) is given: one
+    forge_lora_qkv_rope launch.  (Splitting the rows of a last, partly
+    filled round of 256 x 256 tiles over K was measured on MI355X at the
+    BASELINE shape, 2160 tiles on 256 CUs: no faster, since the chip clocks
+    up while fewer CUs are busy.)"""
+    M, K = X2.shape
+    Hq, Hkv = Wq.shape[0], Wk.shape[0]
     if rope is not None:
         cos, sin = rope["cos"], rope["sin"]
         pos = rope.get("positions")
@@ -85,7 +99,6 @@ def qkv_forward(X2, W_q, W_k, W_v, A_q, B_q, s_q, A_k, B_k, s_k, A_v, B_v, s_v,
             cos_p, sin_p, cs_ld, cs_rows, pos_p, hd, apply, L.stream_of(X2)),
         "forge_lora_qkv_rope",
     )
-    return out
 
 
 def rope_qk_inplace(out, Hq, Hkv, rope, backward=False):
