@@ -1088,7 +1088,7 @@ def main():
     args = _parse()
     if args.gpus != 1:
         print(json.dumps({"error": f"--gpus {args.gpus}: this build measures one GPU only (single-GPU box); "
-                                   "multi-GPU sharding is described in DESIGN.md, not run"}))
+                                   "multi-GPU sharding is designed, not run here"}))
         return 2
     import torch
 

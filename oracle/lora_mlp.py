@@ -101,7 +101,7 @@ def make_params(H, I, r, alpha, gen, dtype=torch.bfloat16):
 
 def flops(M, H, I, r):
     """Algorithmic FLOPs of one forward + backward (2 per multiply-add), the
-    accounting BASELINE.md quotes (5,821,828,169,728 at M=8192, H=4096,
+    accounting the published benchmark quotes (5,821,828,169,728 at M=8192, H=4096,
     I=14336, r=16):
       base GEMMs      forward 3 * 2MHI, backward 3 * 2MHI
       LoRA forward    X A^T and xa B^T for gate/up, h Ad^T and xd Bd^T = 6 M r (H + I)

@@ -86,8 +86,8 @@ def positions_for(lengths):
 
 
 def flops_per_token(K, Hq, Hkv, r):
-    """Algorithmic FLOPs per token of one forward + backward, BASELINE.md's
-    accounting (109,314,048 at K=4096, Hq=4096, Hkv=1024, r=64):
+    """Algorithmic FLOPs per token of one forward + backward, the published
+    benchmark's accounting (109,314,048 at K=4096, Hq=4096, Hkv=1024, r=64):
     forward 2KN + 6Kr + 2rN, backward 2NK + 2Nr + 18Kr + 2Nr, N = Hq + 2Hkv."""
     N = Hq + 2 * Hkv
     return 4 * K * N + 6 * r * N + 24 * K * r
