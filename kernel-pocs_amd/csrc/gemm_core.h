@@ -1015,7 +1015,7 @@ __device__ __forceinline__ int swz(int row) {
   else return (row >> 2) & 3;                      // BKT == 32: 4 rows per 256 bytes
 }
 
-template <int BROWS, int BKT, int NT, bool DUAL>
+template <int BROWS, int BKT, int NT, bool DUAL, int AUX = 0>
 struct DmaLoader {
   static constexpr int RB = BKT * 2;          // LDS bytes per row
   static constexpr int CPR = RB / 16;         // 16-byte chunks per row
@@ -1064,7 +1064,7 @@ struct DmaLoader {
       const int sel = DUAL ? (((wave * IPW + j) * RPI) / 32) % 2 : 0;
       __builtin_amdgcn_raw_ptr_buffer_load_lds(sel ? r1 : r0,
                                                (__attribute__((address_space(3))) void*)(dst + (wave * IPW + j) * 1024),
-                                               16, off, 0, 0, 0);
+                                               16, off, 0, 0, AUX);
     }
   }
 };
@@ -1090,7 +1090,7 @@ __device__ __forceinline__ int swzT(int q) {
   else return 0;                                     // 64-byte k-rows: four per bank cycle already
 }
 
-template <int BROWS, int BKT, int NT>
+template <int BROWS, int BKT, int NT, int AUX = 0>
 struct DmaLoaderT {
   static constexpr int RB = BROWS * 2;        // LDS bytes per k-row
   static constexpr int CPR = RB / 16;         // 16-byte chunks (8 rows) per k-row
@@ -1130,7 +1130,7 @@ struct DmaLoaderT {
       uint32_t off = voff[j];
       if (kvalid < BKT && (wave * IPW + j) * RPI + lane / CPR >= kvalid) off = OOB;  // segment tail
       __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)(dst + (wave * IPW + j) * 1024),
-                                               16, off, 0, 0, 0);
+                                               16, off, 0, 0, AUX);
     }
   }
 };
@@ -1172,8 +1172,10 @@ __device__ __forceinline__ void wait_vmcnt() {
 // staged epilogue take ~130 KB of LDS): 8 waves -> WPE 2.  The skinny tiles
 // (~72 KB of LDS) hold two workgroups of 4 waves per CU: WPE 2 as well.
 // AT / BT: A stored [K][M] / B stored [K][N] (token-major, see DmaLoaderT).
+// CPA / CPB: cache-policy bits of the A / B buffer loads (0 = default; 2 =
+// nontemporal, for an operand that no other workgroup reads again).
 template <int BM, int BN, int WAVES_M, int WAVES_N, int BMODE, int EPI, int BKT, int NSTAGE, bool STAGED, int WPE,
-          bool AT = false, bool BT = false>
+          bool AT = false, bool BT = false, int CPA = 0, int CPB = 0>
 __global__ __launch_bounds__(WAVES_M * WAVES_N * 64) __attribute__((amdgpu_waves_per_eu(WPE, WPE)))
 void gemm_dma_kernel(GemmArgs args) {
   constexpr int NT = WAVES_M * WAVES_N * 64;
@@ -1220,8 +1222,8 @@ void gemm_dma_kernel(GemmArgs args) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
 
-  using LoaderA = std::conditional_t<AT, DmaLoaderT<BM, BKT, NT>, DmaLoader<BM, BKT, NT, false>>;
-  using LoaderB = std::conditional_t<BT, DmaLoaderT<BN, BKT, NT>, DmaLoader<BN, BKT, NT, BMODE == B_DUAL>>;
+  using LoaderA = std::conditional_t<AT, DmaLoaderT<BM, BKT, NT, CPA>, DmaLoader<BM, BKT, NT, false, CPA>>;
+  using LoaderB = std::conditional_t<BT, DmaLoaderT<BN, BKT, NT, CPB>, DmaLoader<BN, BKT, NT, BMODE == B_DUAL, CPB>>;
   LoaderA la;
   LoaderB lb;
   auto setup_seg = [&](int s) {
