@@ -15,7 +15,7 @@ enum Cfg {
                        // token-major operands, else 256 x 32
   CFG_NARROW_128 = 4,  // 64 < N <= 128, K-contiguous A: 64 x 128 tiles (2 x 2 waves)
   CFG_NARROW_256 = 5,  // 192 < N <= 256, K-contiguous A: 64 x 256 tiles (2 x 2 waves)
-  CFG_NARROW_192 = 6,  // 128 < N <= 192, K-contiguous A: 64 x 192 tiles (2 x 2 waves, 32 x 96 per wave)
+  CFG_NARROW_192 = 6,  // 128 < N <= 192, K-contiguous A: 96 x 192 tiles (3 x 2 waves, 32 x 96 per wave)
 };
 
 #ifndef SKINNY_NSTAGE
@@ -31,12 +31,42 @@ enum Cfg {
 // bit, 2, of the gfx950 buffer instruction's cache-policy field)
 constexpr int CP_STREAM = 2;
 
+// Column tiles of unequal K work (column-ranged segments of different
+// lengths, e.g. [dQ B_q | dK B_k | dV B_v] with K = 4096, 1024, 1024) are
+// dispatched heaviest first, so that the long tiles do not start in the last
+// round; equal work keeps the default order.
+static void order_columns(GemmArgs& a, int64_t out_bn, int64_t tn) {
+  a.n_col_order = 0;
+  if (tn < 2 || tn > MAX_COL_ORDER) return;
+  int64_t work[MAX_COL_ORDER];
+  int idx[MAX_COL_ORDER];
+  bool uniform = true;
+  for (int j = 0; j < tn; ++j) {
+    const int64_t lo = j * out_bn, hi = lo + out_bn;
+    work[j] = 0;
+    for (int s = 0; s < a.n_segs; ++s)
+      if (a.segs[s].n_hi > lo && a.segs[s].n_lo < hi) work[j] += a.segs[s].k;
+    uniform = uniform && work[j] == work[0];
+    idx[j] = j;
+  }
+  if (uniform) return;
+  for (int i = 1; i < tn; ++i)  // stable insertion sort, heaviest first
+    for (int j = i; j > 0 && work[idx[j]] > work[idx[j - 1]]; --j) {
+      const int t = idx[j];
+      idx[j] = idx[j - 1];
+      idx[j - 1] = t;
+    }
+  a.n_col_order = (int)tn;
+  for (int j = 0; j < tn; ++j) a.col_order[j] = (uint8_t)idx[j];
+}
+
 template <int BM, int BN, int WM, int WN, int AL, int BL, int BMODE, int EPI>
-static int launch_cfg(const GemmArgs& a, hipStream_t s) {
+static int launch_cfg(GemmArgs a, hipStream_t s) {
   constexpr int OUT_BN = (BMODE == B_DUAL) ? BN / 2 : BN;
   const int64_t tm = (a.M + BM - 1) / BM;
   const int64_t tn = (a.N + OUT_BN - 1) / OUT_BN;
   if (tm * tn > 0x7fffffffLL) return forge_set_error(FORGE_ERR_INVALID, "gemm: too many tiles");
+  order_columns(a, OUT_BN, tn);
   dim3 grid((unsigned)(tm * tn), 1, (unsigned)a.split_k);
   constexpr bool CAN_STAGE = staged_ok(BM, BN, WM, WN, EPI);
   const bool staged = CAN_STAGE && a.ep.vec_ok;
@@ -49,22 +79,29 @@ static int launch_cfg(const GemmArgs& a, hipStream_t s) {
       gemm_dma_kernel<BM, BN, DWM, DWN, BMODE, EPI, 64, 2, DMA_STAGE, 2><<<grid, DWM * DWN * 64, 0, s>>>(a);
     else
       gemm_dma_kernel<BM, BN, DWM, DWN, BMODE, EPI, 64, 2, false, 2><<<grid, DWM * DWN * 64, 0, s>>>(a);
-  } else if constexpr (BM == 64 && (BN == 64 || BN == 128 || BN == 192 || BN == 256) && AL == ROW &&
-                       (BL == COL || (BL == ROW && BN != 192)) && BMODE == B_SINGLE) {
+  } else if constexpr (BM == 64 && (BN == 64 || BN == 128 || BN == 256) && AL == ROW &&
+                       (BL == COL || BL == ROW) && BMODE == B_SINGLE) {
     // narrow outputs (N <= 256: X A^T, dY B) with A K-contiguous: 64-row
     // tiles as wide as the output (so X streams once) with 4 waves; a 3-stage
     // ring (48 / 72 KB of LDS: three / two workgroups per CU) or, at 64 x 256,
-    // two stages in 80 KB (two per CU); 64 x 192 (three rank-64 LoRA-A
-    // products) two stages in 64 KB, with no padded columns.  M/64 tiles fill
-    // the chip without a split-K pass.  B may be [N][K] or, read with the
-    // transposing LDS loads, [K][N] as stored.
-    // (measured cold on MI355X: 4 or 5 stages at 64 x 64 and 3 at 64 x 192 were
-    // no faster; 64 x 64 or 64 x 128 tiles for the 192-wide product were slower)
-    constexpr int NS = BN >= 192 ? 2 : 3;
+    // two stages in 80 KB (two per CU).  M/64 tiles fill the chip without a
+    // split-K pass.  B may be [N][K] or, read with the transposing LDS loads,
+    // [K][N] as stored.
+    // (measured cold on MI355X: 4 or 5 stages at 64 x 64 were no faster)
+    constexpr int NS = BN == 256 ? 2 : 3;
     constexpr int WPE_N = BN == 64 ? 3 : 2;
     // (nontemporal loads of A, read by one column of tiles, measured 0.2% slower)
     gemm_dma_kernel<BM, BN, WM, WN, BMODE, EPI, 64, NS, false, WPE_N, false, BL == ROW>
         <<<grid, WM * WN * 64, 0, s>>>(a);
+  } else if constexpr (BM == 96 && BN == 192 && AL == ROW && BL == COL && BMODE == B_SINGLE) {
+    // 129..192 output columns (the three stacked rank-64 LoRA-A products of
+    // LoRA-QKV): 96-row tiles of 3 x 2 waves and a 3-stage ring (108 KB, one
+    // workgroup per CU; 240 tiles at 22954 tokens, one round on 256 CUs),
+    // with no padded columns.  Measured cold on MI355X against 64 x 192 tiles
+    // with two stages (two workgroups per CU): [22954, 4096] x [4096, 192]
+    // 116 -> 94 us, [4096, 4096] x [4096, 192] 78 -> 61 us, bitwise-equal
+    // output; 4 stages no faster than 3; 64 x 64 or 64 x 128 tiles slower.
+    gemm_dma_kernel<96, 192, 3, 2, BMODE, EPI, 64, 3, false, 2><<<grid, 384, 0, s>>>(a);
   } else if constexpr (AL == COL && BL == ROW && BMODE == B_SINGLE && BM == 256 && BN == 256) {
     // both operands token-major (A^T B reduced over tokens): the LDS-DMA
     // engine with transposing fragment reads, 8 waves as above
@@ -115,7 +152,7 @@ static int launch_layout(int cfg, const GemmArgs& a, hipStream_t s) {
       if constexpr (BMODE == B_SINGLE && AL == ROW) return launch_cfg<64, 256, 2, 2, AL, BL, BMODE, EPI>(a, s);
       break;
     case CFG_NARROW_192:  // B as [N][K] only (a 192-wide k-row is not a whole number of transposing reads)
-      if constexpr (BMODE == B_SINGLE && AL == ROW && BL == COL) return launch_cfg<64, 192, 2, 2, AL, BL, BMODE, EPI>(a, s);
+      if constexpr (BMODE == B_SINGLE && AL == ROW && BL == COL) return launch_cfg<96, 192, 3, 2, AL, BL, BMODE, EPI>(a, s);
       break;
     case CFG_SKINNY_M:
       if constexpr (BMODE == B_SINGLE) return launch_cfg<32, 256, 1, 4, AL, BL, BMODE, EPI>(a, s);

@@ -116,12 +116,19 @@ struct EpiArgs {
 // Activations of the STORE epilogues, applied to alpha * acc + beta * C.
 enum EpiAct { ACT_NONE = 0, ACT_SILU = 1, ACT_RELU = 2, ACT_GELU = 3 };
 
+constexpr int MAX_COL_ORDER = 8;
 struct GemmArgs {
   int64_t M, N;  // N = output columns
   int n_segs;
   Seg segs[MAX_SEGS];
   int split_k;   // number of K partitions (grid z)
   EpiArgs ep;
+  // Dispatch order of the column tiles when their K work differs (column-
+  // ranged segments of different lengths): n_col_order = tiles_n (at most
+  // MAX_COL_ORDER) and col_order[i] = the i-th column tile, heaviest first;
+  // 0 = the default XCD-aware order.
+  int n_col_order;
+  uint8_t col_order[MAX_COL_ORDER];
 };
 
 __device__ __forceinline__ uint32_t perm_lo(uint32_t a, uint32_t b) {
@@ -357,7 +364,17 @@ __device__ __forceinline__ void glu_bwd_vals(float acc, float e, float g, float&
 // (round-robin dispatch), so ids are regrouped so that each XCD walks a
 // contiguous range of the tile order; within it, tiles go in groups of
 // GROUP_M row-panels to share A and B panels in that XCD's L2.
-__device__ __forceinline__ void tile_coords(int64_t tiles_m, int64_t tiles_n, int& tm, int& tn) {
+// With a column order (column tiles of unequal K work), the tiles go column
+// by column in that order instead, so the long tiles are dispatched first
+// and the short ones fill in behind them.
+__device__ __forceinline__ void tile_coords(int64_t tiles_m, int64_t tiles_n, int& tm, int& tn,
+                                            const GemmArgs& args) {
+  if (args.n_col_order > 0 && args.n_col_order == tiles_n) {
+    const int64_t id = blockIdx.x;
+    tm = (int)(id % tiles_m);
+    tn = args.col_order[id / tiles_m];
+    return;
+  }
   constexpr int NXCD = 8;
   constexpr int GROUP_M = 8;
   const int64_t total = tiles_m * tiles_n;
@@ -844,7 +861,7 @@ void gemm_kernel(GemmArgs args) {
   const int64_t tiles_m = (M + BM - 1) / BM;
   const int64_t tiles_n = (args.N + OUT_BN - 1) / OUT_BN;
   int tmi, tni;
-  tile_coords(tiles_m, tiles_n, tmi, tni);
+  tile_coords(tiles_m, tiles_n, tmi, tni, args);
   const int64_t m0 = (int64_t)tmi * BM;
   const int64_t n0 = (int64_t)tni * OUT_BN;
 
@@ -1194,7 +1211,7 @@ void gemm_dma_kernel(GemmArgs args) {
   const int64_t tiles_m = (M + BM - 1) / BM;
   const int64_t tiles_n = (args.N + OUT_BN - 1) / OUT_BN;
   int tmi, tni;
-  tile_coords(tiles_m, tiles_n, tmi, tni);
+  tile_coords(tiles_m, tiles_n, tmi, tni, args);
   const int64_t m0 = (int64_t)tmi * BM;
   const int64_t n0 = (int64_t)tni * OUT_BN;
   const int lane = threadIdx.x % 64;

@@ -229,12 +229,14 @@ def test_transpose_2b_batch_rejects_bad_arguments_without_gpu():
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("M,r,split", [(2048, 16, 1), (2048, 16, 4), (300, 64, 1), (1000, 8, 3)])
+@pytest.mark.parametrize("M,r,split", [(2048, 16, 1), (2048, 16, 4), (300, 64, 1), (700, 64, 2), (1000, 8, 3)])
 def test_gemm_column_ranged_segments(M, r, split):
     """Independent products side by side in one launch: out[:, p r:(p+1) r] =
     A_p B_p^T with a different K per product (segments restricted to their
     columns), against float32 matmuls of the same bf16 operands; with split-K
-    the fp32 partials are summed by forge_splitk_reduce."""
+    the fp32 partials are summed by forge_splitk_reduce.  At r = 64 each
+    product has column tiles of its own, dispatched heaviest first (K = 512,
+    136, 128: a reordered grid)."""
     gen = torch.Generator().manual_seed(6)
     Ks = [512, 128, 136]
     As = [torch.randn(M, k, generator=gen).to(torch.bfloat16) for k in Ks]
