@@ -126,19 +126,24 @@ def lora_a(x: torch.Tensor, mats: Sequence[torch.Tensor], scales: Sequence[float
     M, K = x.shape
     r = mats[0].shape[0]
     n = len(mats)
-    if out is None:
-        out = torch.empty(M, n * r, dtype=torch.bfloat16, device=x.device)
     mats = [as_operand(a) for a in mats]
     if n > 1 and not _row_stacked(mats):
-        # one [n r, K] buffer: the kernel then streams x once per column tile
+        # one [n r, K] buffer (contiguous: A_p is rows p r .. p r + r - 1):
+        # the kernel then streams x once per column tile
         stack = torch.cat([a.detach() for a in mats], 0)
-        mats = [stack[p * r:(p + 1) * r] for p in range(n)]
-    ptrs = (ctypes.c_void_p * n)(*[a.data_ptr() for a in mats])
+        lda = ld(stack)
+        addrs = [stack.data_ptr() + p * r * lda * stack.element_size() for p in range(n)]
+    else:
+        lda = ld(mats[0])
+        addrs = [a.data_ptr() for a in mats]
+    if out is None:
+        out = torch.empty(M, n * r, dtype=torch.bfloat16, device=x.device)
+    ptrs = (ctypes.c_void_p * n)(*addrs)
     sc = (ctypes.c_float * n)(*[float(s) for s in scales])
     split = skinny_split(M, n * r, K) if M >= 1024 else 1
     work = torch.empty(split, M, n * r, dtype=torch.float32, device=x.device) if split > 1 else None
     L.check(
-        L.forge_lora_a(M, K, r, n, x.data_ptr(), ld(x), ptrs, ld(mats[0]), sc, out.data_ptr(), ld(out),
+        L.forge_lora_a(M, K, r, n, x.data_ptr(), ld(x), ptrs, lda, sc, out.data_ptr(), ld(out),
                        L.ptr(work), split, L.stream_of(x)),
         "forge_lora_a",
     )

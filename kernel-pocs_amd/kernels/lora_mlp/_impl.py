@@ -74,14 +74,14 @@ def mlp_forward(X2, W_gate, A_gate, B_gate, s_gate, W_up, A_up, B_up, s_up,
     has_lora = A_gate is not None and B_gate is not None
     r = A_gate.shape[0] if has_lora else 0
     dev = X2.device
+    xa = None
+    Bg = Bu = None
+    if has_lora:  # the first launch; the gate/up GEMM needs its result
+        xa = lora_a(X2, [A_gate, A_up], [s_gate, s_up])
+        Bg, Bu = _w(B_gate), _w(B_up)
     e = torch.empty(M, I, dtype=torch.bfloat16, device=dev)
     g = torch.empty(M, I, dtype=torch.bfloat16, device=dev)
     h = torch.empty(M, I, dtype=torch.bfloat16, device=dev)
-    xa = None
-    Bg = Bu = None
-    if has_lora:
-        xa = lora_a(X2, [A_gate, A_up], [s_gate, s_up])
-        Bg, Bu = _w(B_gate), _w(B_up)
     st = L.stream_of(X2)
     L.check(
         L.forge_lora_mlp_gate_up(

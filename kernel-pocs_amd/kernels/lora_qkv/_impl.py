@@ -35,40 +35,47 @@ def _w(t):
 
 
 def qkv_forward(X2, W_q, W_k, W_v, A_q, B_q, s_q, A_k, B_k, s_k, A_v, B_v, s_v,
-                rope: Optional[dict] = None, aux: Optional[dict] = None, a_packed=None):
+                rope=None, aux: Optional[dict] = None, a_packed=None):
     """Returns out [M, Hq + 2 Hkv] bf16.  rope = {cos, sin, positions, head_dim}
     (tables [P, D]; int64 positions [M], validated by the caller) applies
     RoPE to Q and K: bf16 tables in the GEMM epilogue, fp32 tables by an
     in-place forge_rope pass over the stored Q/K (the unfused composition).
+    rope may also be a callable that returns that dict (or None): it is
+    called once the LoRA-A product is queued, so the host prepares the
+    tables while the device already works.
     aux (a dict, optional) receives xa = [sq X Aq^T | sk X Ak^T | sv X Av^T]
     for the backward's B gradients.  fp32 / fp16 inputs run on the generic
     GEMM (kernels/_generic_lora.py; RoPE tables in X's dtype or fp32) and
     return out in X's dtype.  a_packed = [A_q; A_k; A_v] (optional) is read
     as the stacked LoRA-A operand instead of stacking the three."""
-    if rope is not None and X2.dtype == torch.bfloat16 and rope["cos"].dtype != torch.bfloat16:
-        out = qkv_forward(X2, W_q, W_k, W_v, A_q, B_q, s_q, A_k, B_k, s_k, A_v, B_v, s_v, aux=aux,
-                          a_packed=a_packed)
-        rope_qk_inplace(out, W_q.shape[0], W_k.shape[0], rope)
-        return out
     if X2.dtype in G.GENERIC_DTYPES:
+        rope = rope() if callable(rope) else rope
         return G.qkv_forward(X2, W_q, W_k, W_v, A_q, B_q, s_q, A_k, B_k, s_k, A_v, B_v, s_v, rope=rope, aux=aux)
     L.require_gpu(X2, W_q, W_k, W_v)
     X2 = as_operand(X2)
-    Wq, Wk, Wv = _w(W_q), _w(W_k), _w(W_v)
-    M, K = X2.shape
-    Hq, Hkv = Wq.shape[0], Wk.shape[0]
     has_lora = A_q is not None and B_q is not None
     r = A_q.shape[0] if has_lora else 0
-    out = torch.empty(M, Hq + 2 * Hkv, dtype=torch.bfloat16, device=X2.device)
     xa = None
-    Bq = Bk = Bv = None
-    if has_lora:
+    if has_lora:  # the first launch; the QKV GEMM needs its result
         mats = [A_q, A_k, A_v] if a_packed is None else [a_packed[:r], a_packed[r:2 * r], a_packed[2 * r:]]
         xa = lora_a(X2, mats, [s_q, s_k, s_v])
-        Bq, Bk, Bv = _w(B_q), _w(B_k), _w(B_v)
         if aux is not None:
             aux["xa"] = xa
-    qkv_gemm(X2, Wq, Wk, Wv, xa, Bq, Bk, Bv, r, rope, out)
+    if callable(rope):
+        rope = rope()
+    Wq, Wk, Wv = _w(W_q), _w(W_k), _w(W_v)
+    M = X2.shape[0]
+    Hq, Hkv = Wq.shape[0], Wk.shape[0]
+    out = torch.empty(M, Hq + 2 * Hkv, dtype=torch.bfloat16, device=X2.device)
+    Bq = Bk = Bv = None
+    if has_lora:
+        Bq, Bk, Bv = _w(B_q), _w(B_k), _w(B_v)
+    if rope is not None and rope["cos"].dtype != torch.bfloat16:
+        # fp32 tables: the unfused composition, a forge_rope pass over the stored Q/K
+        qkv_gemm(X2, Wq, Wk, Wv, xa, Bq, Bk, Bv, r, None, out)
+        rope_qk_inplace(out, Hq, Hkv, rope)
+    else:
+        qkv_gemm(X2, Wq, Wk, Wv, xa, Bq, Bk, Bv, r, rope, out)
     return out
 
 

@@ -166,15 +166,22 @@ class LoRAQKVRoPEFunction(torch.autograd.Function):
                 head_dim=128):
         orig_shape = X.shape
         X2 = _flat(X)
-        cos2, sin2 = _qkv_tables(cos, sin, X.dtype)
-        pos = None
-        if positions is not None:
-            check_positions(positions, cos2.shape[0])
-            pos = positions.reshape(-1).to(device=X.device, dtype=torch.int64).contiguous()
+        if positions is not None:  # validated before any launch
+            check_positions(positions, cos.reshape(-1, cos.shape[-1]).shape[0])
+        tables = []
+
+        def rope_args():  # called by qkv_forward once the LoRA-A product is queued
+            cos2, sin2 = _qkv_tables(cos, sin, X.dtype)
+            pos = None
+            if positions is not None:
+                pos = positions.reshape(-1).to(device=X.device, dtype=torch.int64).contiguous()
+            tables.extend((cos2, sin2, pos))
+            return {"cos": cos2, "sin": sin2, "positions": pos, "head_dim": int(head_dim)}
+
         ctx.lora_aux = {}  # forward products reused by the backward (outside saved_tensors)
         out = qkv_forward(X2, W_q, W_k, W_v, A_q, B_q, s_q, A_k, B_k, s_k, A_v, B_v, s_v,
-                          rope={"cos": cos2, "sin": sin2, "positions": pos, "head_dim": int(head_dim)},
-                          aux=ctx.lora_aux)
+                          rope=rope_args, aux=ctx.lora_aux)
+        cos2, sin2, pos = tables
         ctx.save_for_backward(X, A_q, B_q, A_k, B_k, A_v, B_v, cos2, sin2, pos)
         ctx.scalings = (s_q, s_k, s_v)
         ctx.base_weights = (W_q, W_k, W_v)
