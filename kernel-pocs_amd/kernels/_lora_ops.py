@@ -113,6 +113,17 @@ def split_gemm(M: int, N: int, segs, a_layout: int, b_layout: int, split: int, o
     return out
 
 
+def pad_rank(A: Optional[torch.Tensor], B: Optional[torch.Tensor]):
+    """Zero-pads a LoRA pair (A [r, K], B [N, r]) to the next rank that is a
+    multiple of 8, which the MFMA core's K segments need.  The added rows of
+    A and columns of B are zero, so every product and every gradient of the
+    original rows / columns is unchanged (the extra terms add exact zeros)."""
+    if A is None or B is None or A.shape[0] % 8 == 0:
+        return A, B
+    extra = -A.shape[0] % 8
+    return torch.nn.functional.pad(A, (0, 0, 0, extra)), torch.nn.functional.pad(B, (0, extra))
+
+
 def _row_stacked(mats: Sequence[torch.Tensor]) -> bool:
     """True when mats are consecutive row blocks of one buffer (same pitch)."""
     r, pitch, base = mats[0].shape[0], ld(mats[0]), mats[0].data_ptr()

@@ -39,7 +39,7 @@ import torch.nn.functional as F
 from forge_hip import _lib as L
 from kernels import _generic_lora as G
 from kernels._lora_ops import (COL, ROW, as_operand, frozen_t, gemm, grad_at_b, grad_at_b_group, ld, lora_a,
-                               small_t_batch, times_b)
+                               pad_rank, small_t_batch, times_b)
 
 
 def _w(t):
@@ -67,6 +67,9 @@ def mlp_forward(X2, W_gate, A_gate, B_gate, s_gate, W_up, A_up, B_up, s_up,
         return G.mlp_forward(X2, W_gate, A_gate, B_gate, s_gate, W_up, A_up, B_up, s_up, W_down, A_down, B_down,
                              s_down, save_eg=save_eg, aux=aux, activation=activation)
     L.require_gpu(X2, W_gate, W_up, W_down)
+    if A_gate is not None and A_gate.shape[0] % 8:  # rank padded to a multiple of 8 (exact)
+        (A_gate, B_gate), (A_up, B_up), (A_down, B_down) = (
+            pad_rank(a, b) for a, b in ((A_gate, B_gate), (A_up, B_up), (A_down, B_down)))
     X2 = as_operand(X2)
     Wg, Wu, Wd = _w(W_gate), _w(W_up), _w(W_down)
     M, H = X2.shape
@@ -114,6 +117,14 @@ def mlp_backward(dY2, X2, e, g, W_gate, A_gate, B_gate, s_gate, W_up, A_up, B_up
     if X2.dtype in G.GENERIC_DTYPES:
         return G.mlp_backward(dY2, X2, e, g, W_gate, A_gate, B_gate, s_gate, W_up, A_up, B_up, s_up, W_down, A_down,
                               B_down, s_down, aux=aux, activation=activation)
+    if A_gate.shape[0] % 8:  # rank padded to a multiple of 8 (exact); the padding's gradients are dropped
+        r0 = A_gate.shape[0]
+        (Ag8, Bg8), (Au8, Bu8), (Ad8, Bd8) = (
+            pad_rank(a, b) for a, b in ((A_gate, B_gate), (A_up, B_up), (A_down, B_down)))
+        dX, dAg, dBg, dAu, dBu, dAd, dBd = mlp_backward(dY2, X2, e, g, W_gate, Ag8, Bg8, s_gate, W_up, Au8, Bu8, s_up,
+                                                        W_down, Ad8, Bd8, s_down, aux=aux, activation=activation)
+        return (dX, dAg[:r0].contiguous(), dBg[:, :r0].contiguous(), dAu[:r0].contiguous(),
+                dBu[:, :r0].contiguous(), dAd[:r0].contiguous(), dBd[:, :r0].contiguous())
     dY2 = as_operand(dY2)
     X2 = as_operand(X2)
     Wg, Wu, Wd = _w(W_gate), _w(W_up), _w(W_down)

@@ -27,7 +27,7 @@ import torch
 from forge_hip import _lib as L
 from kernels import _generic_lora as G
 from kernels._lora_ops import (COL, ROW, as_operand, frozen_t, gemm, grad_at_b, grad_at_b_group, ld, lora_a,
-                               small_t_batch, times_b)
+                               pad_rank, small_t_batch, times_b)
 
 
 def _w(t):
@@ -52,6 +52,9 @@ def qkv_forward(X2, W_q, W_k, W_v, A_q, B_q, s_q, A_k, B_k, s_k, A_v, B_v, s_v,
         rope = rope() if callable(rope) else rope
         return G.qkv_forward(X2, W_q, W_k, W_v, A_q, B_q, s_q, A_k, B_k, s_k, A_v, B_v, s_v, rope=rope, aux=aux)
     L.require_gpu(X2, W_q, W_k, W_v)
+    if A_q is not None and A_q.shape[0] % 8:  # rank padded to a multiple of 8 (exact)
+        (A_q, B_q), (A_k, B_k), (A_v, B_v) = (pad_rank(a, b) for a, b in ((A_q, B_q), (A_k, B_k), (A_v, B_v)))
+        a_packed = None
     X2 = as_operand(X2)
     has_lora = A_q is not None and B_q is not None
     r = A_q.shape[0] if has_lora else 0
@@ -70,13 +73,22 @@ def qkv_forward(X2, W_q, W_k, W_v, A_q, B_q, s_q, A_k, B_k, s_k, A_v, B_v, s_v,
     Bq = Bk = Bv = None
     if has_lora:
         Bq, Bk, Bv = _w(B_q), _w(B_k), _w(B_v)
-    if rope is not None and rope["cos"].dtype != torch.bfloat16:
-        # fp32 tables: the unfused composition, a forge_rope pass over the stored Q/K
+    if rope is not None and not rope_fusable(rope, Hq, Hkv):
+        # the unfused composition: a forge_rope pass over the stored Q/K
         qkv_gemm(X2, Wq, Wk, Wv, xa, Bq, Bk, Bv, r, None, out)
         rope_qk_inplace(out, Hq, Hkv, rope)
     else:
         qkv_gemm(X2, Wq, Wk, Wv, xa, Bq, Bk, Bv, r, rope, out)
     return out
+
+
+def rope_fusable(rope: dict, Hq: int, Hkv: int) -> bool:
+    """Whether forge_lora_qkv_rope can rotate Q/K in its GEMM epilogue: bf16
+    tables, head_dim 64 or 128, and Q and K widths that are whole 256-column
+    tiles (a tile then holds whole heads of one projection).  Otherwise the
+    forward stores Q/K unrotated and rotates them with forge_rope."""
+    return (rope["cos"].dtype == torch.bfloat16 and rope["head_dim"] in (64, 128)
+            and Hq % 256 == 0 and Hkv % 256 == 0)
 
 
 def qkv_gemm(X2, Wq, Wk, Wv, xa, Bq, Bk, Bv, r: int, rope: Optional[dict], out: torch.Tensor) -> None:
@@ -130,6 +142,13 @@ def qkv_backward(dQ, dK, dV, X2, W_q, W_k, W_v, A_q, B_q, s_q, A_k, B_k, s_k, A_
     aux the B gradients reuse its scaled xa instead of re-reading X."""
     if X2.dtype in G.GENERIC_DTYPES:
         return G.qkv_backward(dQ, dK, dV, X2, W_q, W_k, W_v, A_q, B_q, s_q, A_k, B_k, s_k, A_v, B_v, s_v, aux=aux)
+    if A_q.shape[0] % 8:  # rank padded to a multiple of 8 (exact); the padding's gradients are dropped
+        r0 = A_q.shape[0]
+        (Aq8, Bq8), (Ak8, Bk8), (Av8, Bv8) = (pad_rank(a, b) for a, b in ((A_q, B_q), (A_k, B_k), (A_v, B_v)))
+        dX, dAq, dBq, dAk, dBk, dAv, dBv = qkv_backward(dQ, dK, dV, X2, W_q, W_k, W_v, Aq8, Bq8, s_q, Ak8, Bk8, s_k,
+                                                        Av8, Bv8, s_v, aux=aux)
+        return (dX, dAq[:r0].contiguous(), dBq[:, :r0].contiguous(), dAk[:r0].contiguous(),
+                dBk[:, :r0].contiguous(), dAv[:r0].contiguous(), dBv[:, :r0].contiguous())
     X2 = as_operand(X2)
     dQ, dK, dV = as_operand(dQ), as_operand(dK), as_operand(dV)
     Wq, Wk, Wv = _w(W_q), _w(W_k), _w(W_v)

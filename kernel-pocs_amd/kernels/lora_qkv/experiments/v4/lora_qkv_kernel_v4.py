@@ -156,8 +156,9 @@ class LoRAQKVRoPEFunction(torch.autograd.Function):
             cos, sin, positions, head_dim) -> (Q_rot, K_rot, V)
     cos/sin: tables [P, head_dim] (rows = positions), read as stored when in
     X's dtype or fp32 (fp32 math either way), else widened to fp32; bf16
-    tables with bf16 X rotate in the GEMM epilogue, fp32 tables in a
-    forge_rope pass over the stored Q/K.  positions: int64 [M] in [0, P)
+    tables with bf16 X rotate in the GEMM epilogue (head_dim 64 or 128, Q and
+    K widths multiples of 256), other cases in a forge_rope pass over the
+    stored Q/K.  positions: int64 [M] in [0, P)
     (token -> table row; restarts per sequence for packed varlen;
     IndexError otherwise); None means row m for token m."""
 

@@ -266,3 +266,37 @@ def test_lora_qkv_per_projection_scales(scales):
     got = [x.grad, p[3].grad, p[4].grad, p[6].grad, p[7].grad, p[9].grad, p[10].grad]
     for n, a, b in zip(NAMES, got, ref_grads):
         _close_bf16(a, b, n)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("Hq,Hkv,head_dim,r,table_dtype", [(256, 128, 64, 16, torch.bfloat16),
+                                                            (128, 64, 64, 4, torch.bfloat16),
+                                                            (512, 256, 32, 12, torch.bfloat16),
+                                                            (256, 128, 128, 8, torch.float32)])
+def test_lora_qkv_rope_unfused_shapes_and_ranks(Hq, Hkv, head_dim, r, table_dtype):
+    """Q/K widths that are not whole 256-column tiles, head_dim other than 64 /
+    128, fp32 tables, and ranks that are not multiples of 8 (zero-padded
+    inside): the forward rotates Q/K in a forge_rope pass after the GEMM, and
+    everything still matches the oracle."""
+    gen = torch.Generator().manual_seed(Hq + Hkv + head_dim + r)
+    lens = [70, 33]
+    pos = orc.positions_for(lens)
+    T, K = int(pos.numel()), 256
+    params = orc.make_params(K, Hq, Hkv, r, 2 * r, gen)
+    X = torch.randn(T, K, generator=gen).to(torch.bfloat16)
+    dQ = torch.randn(T, Hq, generator=gen).to(torch.bfloat16)
+    dK = torch.randn(T, Hkv, generator=gen).to(torch.bfloat16)
+    dV = torch.randn(T, Hkv, generator=gen).to(torch.bfloat16)
+    c, s = cos_sin(torch.arange(128), head_dim, 10000.0, table_dtype)
+    (Qr, Kr, Vr), ref_grads = orc.qkv_rope_fwd_bwd(X, dQ, dK, dV, params, c[pos], s[pos], head_dim)
+    p = _cuda(params)
+    x = X.cuda().requires_grad_(True)
+    Q, K_, V = lora_qkv_rope(x, p[0], p[3], p[4], p[5], p[1], p[6], p[7], p[8], p[2], p[9], p[10], p[11],
+                             c.cuda(), s.cuda(), pos.cuda(), head_dim)
+    for a, b, n in ((Q, Qr, "Q"), (K_, Kr, "K"), (V, Vr, "V")):
+        _close_bf16(a, b, n)
+    torch.autograd.backward((Q, K_, V), (dQ.cuda(), dK.cuda(), dV.cuda()))
+    got = [x.grad, p[3].grad, p[4].grad, p[6].grad, p[7].grad, p[9].grad, p[10].grad]
+    for n, a, b in zip(NAMES, got, ref_grads):
+        assert a.shape == b.shape, n
+        _close_bf16(a, b, n)
