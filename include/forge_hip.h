@@ -271,9 +271,9 @@ enum { FORGE_LAYOUT_ROW = 0, FORGE_LAYOUT_COL = 1 };
  * independent products one launch (e.g. [dQ B_q | dK B_k | dV B_v]). */
 typedef struct forge_gemm_segment {
   const void* a;  /* bf16 */
-  int64_t lda;
+  int64_t lda;    /* multiple of 8, at most 4,194,303 (256 rows < 2^31 bytes) */
   const void* b;  /* bf16 */
-  int64_t ldb;
+  int64_t ldb;    /* as lda */
   int64_t k;      /* extent of this segment along K (multiple of 8) */
   int64_t n_lo, n_hi;
 } forge_gemm_segment;

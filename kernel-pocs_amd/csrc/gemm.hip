@@ -202,6 +202,9 @@ static int pick_cfg(int64_t M, int64_t N, int al, int bl) {
   return CFG_BIG;
 }
 
+// Largest operand pitch (elements of 2 bytes): 256 rows of it span < 2^31 bytes.
+constexpr int64_t kMaxLd = (int64_t(1) << 31) / (256 * 2) - 1;
+
 static int check_segs(const GemmArgs& a, int al, int bl) {
   if (a.n_segs < 1 || a.n_segs > MAX_SEGS)
     return forge_set_error(FORGE_ERR_INVALID, "gemm: 1..%d segments", MAX_SEGS);
@@ -217,6 +220,12 @@ static int check_segs(const GemmArgs& a, int al, int bl) {
       return forge_set_error(FORGE_ERR_INVALID, "gemm: segment %d operand not 16-byte aligned", i);
     if (s.lda % 8 != 0 || s.ldb % 8 != 0)
       return forge_set_error(FORGE_ERR_INVALID, "gemm: segment %d leading dims must be multiples of 8", i);
+    // A lane's operand offset inside a tile is a 32-bit byte offset from the
+    // tile's first row (buffer loads): up to 256 rows of the pitch must stay
+    // below 2^31 bytes.
+    if (s.lda > kMaxLd || s.ldb > kMaxLd)
+      return forge_set_error(FORGE_ERR_INVALID, "gemm: segment %d leading dimension above %lld elements", i,
+                             (long long)kMaxLd);
   }
   return FORGE_OK;
 }

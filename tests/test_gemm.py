@@ -259,6 +259,19 @@ def test_gemm_column_ranged_segments(M, r, split):
     torch.testing.assert_close(got / scale, ref / scale, atol=2e-2, rtol=0)
 
 
+def test_gemm_rejects_pitches_beyond_32bit_tile_offsets_without_gpu():
+    """Operand offsets inside a tile are 32-bit: a pitch whose 256 rows reach
+    2^31 bytes is refused before any launch instead of reading wrong rows."""
+    limit = (1 << 31) // (256 * 2) - 1
+    seg = (L.GemmSegment * 1)()
+    seg[0] = L.GemmSegment(16, limit - limit % 8 + 8, 16, 64, 64)  # lda just above the limit
+    rc = L.forge_gemm(64, 64, seg, 1, 0, 1, 16, 64, L.DTYPE_BF16, 1.0, 0.0, L.EPI_STORE, 1, None)
+    assert rc == 1 and b"leading dimension above" in L.forge_last_error()
+    seg[0] = L.GemmSegment(16, 64, 16, limit - limit % 8 + 8, 64)  # ldb
+    rc = L.forge_gemm(64, 64, seg, 1, 0, 1, 16, 64, L.DTYPE_BF16, 1.0, 0.0, L.EPI_STORE, 1, None)
+    assert rc == 1 and b"leading dimension above" in L.forge_last_error()
+
+
 def test_gemm_rejects_bad_column_ranges_without_gpu():
     seg = (L.GemmSegment * 1)()
     seg[0] = L.GemmSegment(16, 8, 16, 8, 8, 4, 40)  # [4, 40) outside N = 32
