@@ -38,8 +38,10 @@ def qkv_forward(X2, W_q, W_k, W_v, A_q, B_q, s_q, A_k, B_k, s_k, A_v, B_v, s_v,
                 rope=None, aux: Optional[dict] = None, a_packed=None):
     """Returns out [M, Hq + 2 Hkv] bf16.  rope = {cos, sin, positions, head_dim}
     (tables [P, D]; int64 positions [M], validated by the caller) applies
-    RoPE to Q and K: bf16 tables in the GEMM epilogue, fp32 tables by an
-    in-place forge_rope pass over the stored Q/K (the unfused composition).
+    RoPE to Q and K: in the GEMM epilogue when `rope_fusable` allows it
+    (bf16 tables, head_dim 64 / 128, Q and K widths multiples of 256), else
+    by an in-place forge_rope pass over the stored Q/K (the unfused
+    composition).
     rope may also be a callable that returns that dict (or None): it is
     called once the LoRA-A product is queued, so the host prepares the
     tables while the device already works.
