@@ -318,3 +318,33 @@ def test_rope_v1_non_divisible_gqa_and_gradcheck():
     assert torch.autograd.gradcheck(lambda a, b_: ForgeRoPEv2Function.apply(a, b_, c.cuda(), sn.cuda()), (qg, kg), **kw)
     oq2, _ = ForgeRoPEv2()(qg, kg, c.cuda(), sn.cuda())
     torch.testing.assert_close(oq2, apply_rope(qg, kg, c.cuda(), sn.cuda())[0], rtol=0, atol=0)
+
+
+@pytest.mark.gpu
+def test_rope_64bit_offsets_match_32bit():
+    """Index math is 32-bit when every element offset fits and 64-bit
+    otherwise: q as a view whose second batch lies 2^31 elements into a
+    4.3 GB buffer takes the 64-bit path (forward and backward), and gives
+    bit-identical results to the same values in a compact tensor."""
+    b, nq, nkv, s, d = 2, 2, 1, 16, 64
+    dtype = torch.bfloat16
+    g = torch.Generator().manual_seed(11)
+    q_small = torch.randn(b, nq, s, d, generator=g).to(dtype).cuda()
+    k = torch.randn(b, nkv, s, d, generator=g).to(dtype).cuda()
+    dq = torch.randn(b, nq, s, d, generator=g).to(dtype).cuda()
+    dk = torch.randn(b, nkv, s, d, generator=g).to(dtype).cuda()
+    c, sn = (t.unsqueeze(0).cuda() for t in cos_sin(torch.arange(s), d, 10000.0, dtype))
+    stride_b = 2 ** 31
+    big = torch.empty(stride_b + nq * s * d, dtype=dtype, device="cuda")
+    q_far = big.as_strided((b, nq, s, d), (stride_b, s * d, d, 1))
+    q_far.copy_(q_small)
+    results = []
+    for q in (q_small, q_far):
+        qg = q.detach().requires_grad_(True)
+        kg = k.clone().requires_grad_(True)
+        oq, ok = apply_rope(qg, kg, c, sn)
+        (oq * dq).sum().add((ok * dk).sum()).backward()
+        results.append([oq.contiguous(), ok, qg.grad.contiguous(), kg.grad])
+    del big, q_far
+    for a, bb in zip(*results):
+        assert torch.equal(a, bb)
