@@ -14,12 +14,16 @@
 // Layout: rows of H elements (row pitches ld*); every row is read from HBM
 // once.  Two engines, chosen by the row's width in 16-byte vectors:
 //  * workgroup per row block (256 .. 2048 vectors, aligned rows): the 256
-//    threads of a workgroup span the row, NVT vectors each, with R = 8/NVT
-//    rows in flight per chunk; a row sum is a wave shuffle reduction plus a
-//    fixed-order sum of the four wave totals in LDS (one barrier per chunk).
-//    Each thread owns its dw columns for the whole launch, so the backward
-//    writes its per-workgroup dw partial row straight from registers.  This
-//    is the engine of Llama-class hidden sizes (2048 .. 16384 bf16).
+//    threads of a workgroup span the row, NVT vectors each, with R rows per
+//    chunk (fwd_rows / bwd_rows below); a row sum is a wave shuffle
+//    reduction plus a fixed-order sum of the four wave totals in LDS (one
+//    barrier per chunk).  Each thread owns the same columns for the whole
+//    launch: it loads their weights once, and the backward writes its
+//    per-workgroup dw partial row straight from registers.  The backward's
+//    grid is capped (one partial row per workgroup), so each workgroup loops
+//    over chunks; up to NVT = 4 it loads the next chunk's rows while it
+//    reduces and writes the current one (two register sets).  This is the
+//    engine of Llama-class hidden sizes (2048 .. 16384 bf16).
 //  * wave per row (narrower or unaligned rows): one 64-lane wave per row,
 //    four rows per workgroup, reductions by shuffles only.  A lane's share
 //    is held in registers up to NV = 8 vectors; wider rows take a two-pass
@@ -27,8 +31,8 @@
 //    separate column-tiled pass.  The backward combines the four waves' dw
 //    accumulators in LDS in a fixed order into one partial row per
 //    workgroup.
-// dw = a two-level fixed-order column sum of the partial rows, rounded once
-// to the weight dtype: deterministic, no atomics.  dx may alias dy (in
+// dw = a fixed-order column sum of the partial rows (one launch), rounded
+// once to the weight dtype: deterministic, no atomics.  dx may alias dy (in
 // place): every thread reads its dy elements before it writes the dx
 // elements at the same addresses.
 #include <type_traits>
@@ -426,6 +430,12 @@ __global__ __launch_bounds__(256) void rms_fwd_wg_kernel(RmsArgs a) {
   const int64_t H = a.H;
   const A eps = (A)a.eps, off = (A)a.offset;
   const TW* w = (const TW*)a.w;
+  TW wr[NVT][VEC];  // this thread's weights, loaded once before the first row
+#pragma unroll
+  for (int j = 0; j < NVT; ++j) {
+    const uint32_t c = (uint32_t)(tid + 256 * j) * VEC;
+    if ((int64_t)c < H) load_w_raw<TW, VEC>(w, c, wr[j], a.wvec);
+  }
   const int64_t n_chunks = (a.rows + R - 1) / R;
   int buf = 0;
   for (int64_t ch = blockIdx.x; ch < n_chunks; ch += gridDim.x, buf ^= 1) {
@@ -457,8 +467,6 @@ __global__ __launch_bounds__(256) void rms_fwd_wg_kernel(RmsArgs a) {
     for (int j = 0; j < NVT; ++j) {
       const uint32_t c = (uint32_t)(tid + 256 * j) * VEC;
       if ((int64_t)c >= H) continue;
-      TW wr[VEC];
-      load_w_raw<TW, VEC>(w, c, wr, a.wvec);
 #pragma unroll
       for (int r = 0; r < R; ++r) {
         const int64_t row = ch * R + r;
@@ -467,7 +475,7 @@ __global__ __launch_bounds__(256) void rms_fwd_wg_kernel(RmsArgs a) {
         A o[VEC];
 #pragma unroll
         for (int q = 0; q < VEC; ++q)
-          o[q] = fwd_elem<T, TW, TY, A>(pk_get<A>(xv[r][j], q), rstd, cv<A, TW>(wr[q]), off, MODE);
+          o[q] = fwd_elem<T, TW, TY, A>(pk_get<A>(xv[r][j], q), rstd, cv<A, TW>(wr[j][q]), off, MODE);
         store_n<TY, VEC, A>((TY*)a.y + row * a.ldy + c, o);
       }
     }
@@ -479,25 +487,17 @@ __global__ __launch_bounds__(256) void rms_fwd_wg_kernel(RmsArgs a) {
   }
 }
 
+// One chunk (R rows) of the workgroup backward: load() queues the chunk's x,
+// dy and rstd loads into one register set; process() reduces the row dots,
+// writes dx and adds the dw terms.  Splitting the two lets the kernel queue
+// chunk i+1's loads before it processes chunk i.
 template <class T, class TW, int VEC, int NVT, int R, int VARIANT>
-__global__ __launch_bounds__(256) void rms_bwd_wg_kernel(RmsArgs a) {
+struct BwdChunk {
   using A = typename Acc<T>::type;
-  __shared__ A dots[2][kWaves][R];
-  const int tid = threadIdx.x, lane = tid % 64, wave = tid / 64;
-  const int64_t H = a.H;
-  const A off = (A)a.offset;
-  const A inv_h = (A)1 / (A)H;
-  const TW* w = (const TW*)a.w;
-  A dwacc[NVT][VEC];
-#pragma unroll
-  for (int j = 0; j < NVT; ++j)
-#pragma unroll
-    for (int q = 0; q < VEC; ++q) dwacc[j][q] = 0;
-  const int64_t n_chunks = (a.rows + R - 1) / R;
-  int buf = 0;
-  for (int64_t ch = blockIdx.x; ch < n_chunks; ch += gridDim.x, buf ^= 1) {
-    Pk<T, VEC> xv[R][NVT], dv[R][NVT];
-    A dot[R], rs[R];
+  using P = Pk<T, VEC>;
+
+  __device__ __forceinline__ static void load(const RmsArgs& a, int tid, int64_t ch, P (&xv)[R][NVT],
+                                              P (&dv)[R][NVT], A (&rs)[R]) {
 #pragma unroll
     for (int r = 0; r < R; ++r) {
       const int64_t row = ch * R + r;
@@ -505,30 +505,38 @@ __global__ __launch_bounds__(256) void rms_bwd_wg_kernel(RmsArgs a) {
 #pragma unroll
       for (int j = 0; j < NVT; ++j) {
         const uint32_t c = (uint32_t)(tid + 256 * j) * VEC;
-        if (row < a.rows && (int64_t)c < H) {
+        if (row < a.rows && (int64_t)c < a.H) {
           pk_load<T, VEC>((const T*)a.x + row * a.ldx + c, xv[r][j]);
           pk_load<T, VEC>((const T*)a.dy + row * a.lddy + c, dv[r][j]);
         }
       }
     }
+  }
+
+  __device__ __forceinline__ static void process(const RmsArgs& a, int tid, int lane, int wave, int64_t ch,
+                                                 P (&xv)[R][NVT], P (&dv)[R][NVT], const A (&rs)[R],
+                                                 const TW (&wr)[NVT][VEC], A (&dwacc)[NVT][VEC],
+                                                 A (*dbuf)[R]) {
+    const int64_t H = a.H;
+    const A off = (A)a.offset;
+    const A inv_h = (A)1 / (A)H;
+    A dot[R];
 #pragma unroll
     for (int r = 0; r < R; ++r) dot[r] = 0;
 #pragma unroll
     for (int j = 0; j < NVT; ++j) {
       const uint32_t c = (uint32_t)(tid + 256 * j) * VEC;
       if ((int64_t)c >= H) continue;
-      TW wr[VEC];
-      load_w_raw<TW, VEC>(w, c, wr, a.wvec);
 #pragma unroll
       for (int r = 0; r < R; ++r) {
         if (ch * R + r >= a.rows) continue;
 #pragma unroll
         for (int q = 0; q < VEC; ++q)
-          dot[r] += scaled_dy<T, TW, A>(pk_get<A>(dv[r][j], q), cv<A, TW>(wr[q]), off, VARIANT) *
+          dot[r] += scaled_dy<T, TW, A>(pk_get<A>(dv[r][j], q), cv<A, TW>(wr[j][q]), off, VARIANT) *
                     pk_get<A>(xv[r][j], q);
       }
     }
-    block_row_sums<A, R>(dot, dots[buf], lane, wave);
+    block_row_sums<A, R>(dot, dbuf, lane, wave);
 #pragma unroll
     for (int r = 0; r < R; ++r)
 #pragma unroll
@@ -540,8 +548,6 @@ __global__ __launch_bounds__(256) void rms_bwd_wg_kernel(RmsArgs a) {
     for (int j = 0; j < NVT; ++j) {
       const uint32_t c = (uint32_t)(tid + 256 * j) * VEC;
       if ((int64_t)c >= H) continue;
-      TW wr[VEC];
-      load_w_raw<TW, VEC>(w, c, wr, a.wvec);
 #pragma unroll
       for (int r = 0; r < R; ++r) {
         const int64_t row = ch * R + r;
@@ -551,11 +557,64 @@ __global__ __launch_bounds__(256) void rms_bwd_wg_kernel(RmsArgs a) {
 #pragma unroll
         for (int q = 0; q < VEC; ++q) {
           const A x = pk_get<A>(xv[r][j], q), d = pk_get<A>(dv[r][j], q);
-          o[q] = rs[r] * (scaled_dy<T, TW, A>(d, cv<A, TW>(wr[q]), off, VARIANT) - x * k);
+          o[q] = rs[r] * (scaled_dy<T, TW, A>(d, cv<A, TW>(wr[j][q]), off, VARIANT) - x * k);
           dwacc[j][q] += dw_term<T, A>(d, x, rs[r], VARIANT);
         }
         store_vec<T, VEC, A>((T*)a.dx + row * a.lddx + c, o);
       }
+    }
+  }
+};
+
+// Chunks ch = blockIdx.x + i * gridDim.x in order.  With PF (NVT <= 4) two
+// register sets alternate: the loads of the next chunk are queued before the
+// current chunk's reduction, so a workgroup keeps HBM reads in flight across
+// its barrier and its dx stores (measured on MI355X, bf16 [8192, 4096]:
+// backward 52 -> 44 us cold).  At NVT = 8 the second set would take the
+// kernel to 256 VGPRs and one wave per SIMD, so it runs one set.  dx may
+// alias dy: the prefetched chunk's rows are never the rows being written.
+template <class T, class TW, int VEC, int NVT, int R, int VARIANT>
+__global__ __launch_bounds__(256) void rms_bwd_wg_kernel(RmsArgs a) {
+  using K = BwdChunk<T, TW, VEC, NVT, R, VARIANT>;
+  using A = typename K::A;
+  using P = typename K::P;
+  constexpr bool PF = NVT <= 4;
+  __shared__ A dots[2][kWaves][R];
+  const int tid = threadIdx.x, lane = tid % 64, wave = tid / 64;
+  const int64_t H = a.H;
+  const TW* w = (const TW*)a.w;
+  TW wr[NVT][VEC];  // this thread's weights, loaded once
+#pragma unroll
+  for (int j = 0; j < NVT; ++j) {
+    const uint32_t c = (uint32_t)(tid + 256 * j) * VEC;
+    if ((int64_t)c < H) load_w_raw<TW, VEC>(w, c, wr[j], a.wvec);
+  }
+  A dwacc[NVT][VEC];
+#pragma unroll
+  for (int j = 0; j < NVT; ++j)
+#pragma unroll
+    for (int q = 0; q < VEC; ++q) dwacc[j][q] = 0;
+  const int64_t n_chunks = (a.rows + R - 1) / R;
+  const int64_t G = gridDim.x;
+  if constexpr (PF) {
+    P xa[R][NVT], da[R][NVT], xb[R][NVT], db[R][NVT];
+    A ra[R], rb[R];
+    int64_t ch = blockIdx.x;
+    if (ch < n_chunks) K::load(a, tid, ch, xa, da, ra);
+    for (; ch < n_chunks; ch += 2 * G) {
+      if (ch + G < n_chunks) K::load(a, tid, ch + G, xb, db, rb);
+      K::process(a, tid, lane, wave, ch, xa, da, ra, wr, dwacc, dots[0]);
+      if (ch + G >= n_chunks) break;
+      if (ch + 2 * G < n_chunks) K::load(a, tid, ch + 2 * G, xa, da, ra);
+      K::process(a, tid, lane, wave, ch + G, xb, db, rb, wr, dwacc, dots[1]);
+    }
+  } else {
+    int buf = 0;
+    for (int64_t ch = blockIdx.x; ch < n_chunks; ch += G, buf ^= 1) {
+      P xv[R][NVT], dv[R][NVT];
+      A rs[R];
+      K::load(a, tid, ch, xv, dv, rs);
+      K::process(a, tid, lane, wave, ch, xv, dv, rs, wr, dwacc, dots[buf]);
     }
   }
   if (a.part == nullptr) return;
@@ -593,36 +652,42 @@ __global__ __launch_bounds__(256) void rms_dw_kernel(RmsArgs a, int64_t rows_per
   for (int q = 0; q < VEC; ++q) part[q] = acc[q];
 }
 
-// The column sum of the partials in two fixed-order levels.  Level 1, in
-// place: group g of kGroup partial rows is summed into its first row
-// (part[g kGroup, c]); each (group, column) is one thread's, so the write
-// touches nothing another thread reads.  Level 2: dw[c] = sum over groups of
-// those rows, rounded once to the weight dtype.
-constexpr int kGroup = 16;
-
-template <class A>
-__global__ __launch_bounds__(256) void colsum_group_kernel(A* part, int64_t n_part, int64_t H) {
-  const int64_t c = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  if (c >= H) return;
-  const int64_t p0 = (int64_t)blockIdx.y * kGroup;
-  const int64_t n = n_part - p0 < kGroup ? n_part - p0 : kGroup;
-  A v[kGroup];
-#pragma unroll
-  for (int p = 0; p < kGroup; ++p) v[p] = p < n ? part[(p0 + p) * H + c] : (A)0;
-  A s = v[0];
-#pragma unroll
-  for (int p = 1; p < kGroup; ++p) s += v[p];
-  part[p0 * H + c] = s;
-}
+// The column sum of the n partial rows in one launch: 64 columns per
+// workgroup (one per lane); wave w of the 16 takes the consecutive block of
+// ceil(n/16) partial rows starting at w ceil(n/16), loads them NB at a time
+// (all in flight together) and adds them in row order; wave 0 then adds the
+// 16 wave totals in wave order and rounds once to the weight dtype.  Fixed
+// order throughout: deterministic.  (Replaced a two-launch version, a group
+// sum of 16 rows and then a sum of the groups: 8.8 -> 4.6 us for 512
+// partial rows of 4096 columns on MI355X.)
+constexpr int kColsumWaves = 16;
 
 template <class A, class TO>
-__global__ __launch_bounds__(256) void colsum_kernel(const A* part, int64_t n, int64_t stride, int64_t H, TO* out) {
-  const int64_t c = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  if (c >= H) return;
+__global__ __launch_bounds__(64 * kColsumWaves) void colsum_kernel(const A* part, int64_t n, int64_t H, TO* out) {
+  constexpr int NB = sizeof(A) == 8 ? 16 : 32;  // rows in flight per lane (no spills at 1024 threads)
+  __shared__ A red[kColsumWaves][64];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int64_t c = (int64_t)blockIdx.x * 64 + lane;
+  const int64_t per = (n + kColsumWaves - 1) / kColsumWaves;
+  const int64_t p0 = wave * per, p1 = p0 + per < n ? p0 + per : n;
   A s = 0;
-#pragma unroll 8
-  for (int64_t p = 0; p < n; ++p) s += part[p * stride + c];
-  out[c] = st<TO, A>(s);
+  if (c < H) {
+    for (int64_t p = p0; p < p1; p += NB) {
+      A v[NB];
+#pragma unroll
+      for (int k = 0; k < NB; ++k) v[k] = p + k < p1 ? part[(p + k) * H + c] : (A)0;
+#pragma unroll
+      for (int k = 0; k < NB; ++k) s += v[k];
+    }
+  }
+  red[wave][lane] = s;
+  __syncthreads();
+  if (wave == 0 && c < H) {
+    A t = red[0][lane];
+#pragma unroll
+    for (int k = 1; k < kColsumWaves; ++k) t += red[k][lane];
+    out[c] = st<TO, A>(t);
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -682,18 +747,30 @@ void fwd_wg(const RmsArgs& a, int grid, hipStream_t s) {
   }
 }
 
+// Rows per chunk of the workgroup engine, by vectors per thread (NVT 1, 2,
+// 4, 8), from a sweep of cold fwd+bwd steps on MI355X over bf16 widths 2048
+// .. 16384 at 2^25 elements (forward R in {8, 4, 2, 1}, backward R in
+// {8, 4, 2, 1}): small forward chunks on a grid of up to 8192 workgroups
+// (one or two rows each: fewer VGPRs, so all resident workgroups fit in one
+// round, and a short tail), and backward chunks of 4 / 2 / 1 / 1 rows behind
+// its 512-workgroup cap.  Steps against the previous 8 / 4 / 2 / 1 rows in
+// both directions: 76.8 -> 68.8 us (H 2048), 80.6 -> 69.2 (4096), 87.0 ->
+// 72.8 (8192), 96.2 -> 83.0 (16384).
+constexpr int fwd_rows(int nvt) { return nvt == 1 ? 2 : 1; }
+constexpr int bwd_rows_per_chunk(int nvt) { return nvt == 1 ? 4 : nvt == 2 ? 2 : 1; }
+
 template <class T, class TW, class TY, int VEC>
 int fwd_v(const RmsArgs& a, hipStream_t s) {
   const int nvt = VEC > 1 ? pick_nvt(a.H, VEC) : 0;
   if constexpr (VEC > 1) {
     if (nvt) {
-      const int r = 8 / nvt;
-      const int grid = grid_for((a.rows + r - 1) / r, 1, 256 * 8);
+      const int r = fwd_rows(nvt);
+      const int grid = grid_for((a.rows + r - 1) / r, 1, 256 * 32);
       switch (nvt) {
-        case 1: fwd_wg<T, TW, TY, VEC, 1, 8>(a, grid, s); break;
-        case 2: fwd_wg<T, TW, TY, VEC, 2, 4>(a, grid, s); break;
-        case 4: fwd_wg<T, TW, TY, VEC, 4, 2>(a, grid, s); break;
-        default: fwd_wg<T, TW, TY, VEC, 8, 1>(a, grid, s); break;
+        case 1: fwd_wg<T, TW, TY, VEC, 1, fwd_rows(1)>(a, grid, s); break;
+        case 2: fwd_wg<T, TW, TY, VEC, 2, fwd_rows(2)>(a, grid, s); break;
+        case 4: fwd_wg<T, TW, TY, VEC, 4, fwd_rows(4)>(a, grid, s); break;
+        default: fwd_wg<T, TW, TY, VEC, 8, fwd_rows(8)>(a, grid, s); break;
       }
       FORGE_CHECK_LAUNCH();
       return FORGE_OK;
@@ -734,13 +811,14 @@ int64_t bwd_rows(RmsArgs a, hipStream_t s) {
   const int nvt = VEC > 1 ? pick_nvt(a.H, VEC) : 0;
   if constexpr (VEC > 1) {
     if (nvt) {
-      const int64_t chunks = (a.rows + 8 / nvt - 1) / (8 / nvt);
+      const int br = bwd_rows_per_chunk(nvt);
+      const int64_t chunks = (a.rows + br - 1) / br;
       const int grid = (int)(chunks < npm ? chunks : npm);
       switch (nvt) {
-        case 1: bwd_wg<T, TW, VEC, 1, 8>(a, grid, s); break;
-        case 2: bwd_wg<T, TW, VEC, 2, 4>(a, grid, s); break;
-        case 4: bwd_wg<T, TW, VEC, 4, 2>(a, grid, s); break;
-        default: bwd_wg<T, TW, VEC, 8, 1>(a, grid, s); break;
+        case 1: bwd_wg<T, TW, VEC, 1, bwd_rows_per_chunk(1)>(a, grid, s); break;
+        case 2: bwd_wg<T, TW, VEC, 2, bwd_rows_per_chunk(2)>(a, grid, s); break;
+        case 4: bwd_wg<T, TW, VEC, 4, bwd_rows_per_chunk(4)>(a, grid, s); break;
+        default: bwd_wg<T, TW, VEC, 8, bwd_rows_per_chunk(8)>(a, grid, s); break;
       }
       return a.part ? grid : 0;
     }
@@ -767,15 +845,8 @@ int64_t bwd_rows(RmsArgs a, hipStream_t s) {
 }
 
 template <class A, class TO>
-void colsum(A* part, int64_t np, int64_t H, TO* dw, hipStream_t s) {
-  const unsigned gx = (unsigned)((H + 255) / 256);
-  if (np > kGroup) {
-    const int64_t groups = (np + kGroup - 1) / kGroup;
-    colsum_group_kernel<A><<<dim3(gx, (unsigned)groups), 256, 0, s>>>(part, np, H);
-    colsum_kernel<A, TO><<<gx, 256, 0, s>>>(part, groups, kGroup * H, H, dw);
-  } else {
-    colsum_kernel<A, TO><<<gx, 256, 0, s>>>(part, np, H, H, dw);
-  }
+void colsum(const A* part, int64_t np, int64_t H, TO* dw, hipStream_t s) {
+  colsum_kernel<A, TO><<<(unsigned)((H + 63) / 64), 64 * kColsumWaves, 0, s>>>(part, np, H, dw);
 }
 
 template <class T, class TW>

@@ -120,6 +120,36 @@ def test_backward_matches_oracle(shape, dtype, case, in_place):
     assert dw_diff <= atol + rtol * rdw.abs().max().item() * (1 if dtype == torch.float32 else 2), ("dw", dw_diff)
 
 
+@pytest.mark.parametrize("rows_per_chunk, h, dtype", [(4, 2048, torch.bfloat16), (2, 4096, torch.bfloat16),
+                                                      (1, 8192, torch.bfloat16), (1, 4096, torch.float32)])
+@pytest.mark.parametrize("in_place", [False, True])
+def test_backward_chunk_loop_ragged(rows_per_chunk, h, dtype, in_place):
+    """The workgroup backward runs at most 512 workgroups, each looping over
+    chunks b, b + 512, ... with the next chunk's loads queued before the
+    current one is processed.  1324 full chunks plus one single-row chunk:
+    workgroups 0..300 take three chunks (the loop's second half, then the
+    early exit), the rest two, and the last chunk is ragged.  The forward at
+    the same rows ends in a partial chunk too."""
+    from kernels.rmsnorm import apply_rmsnorm_v4
+
+    rows = rows_per_chunk * 1324 + 1
+    xd, wd = _inputs(1, rows, h, dtype, "ones_plus_noise", seed=4)
+    grad = torch.randn(1, rows, h, device="cuda", dtype=dtype)
+    x = xd.clone().requires_grad_(True)
+    w = wd.clone().requires_grad_(True)
+    y = apply_rmsnorm_v4(x, w, 1e-6, 0.0, "llama", in_place=in_place)
+    ref_y, _ = orms.rms_forward(xd, wd, 1e-6, 0.0, orms.LLAMA)
+    ok, diff = _passes(y, ref_y, dtype)
+    assert ok, ("y", diff)
+    y.backward(grad.clone())
+    rdx, rdw = orms.rms_backward(grad, xd, wd, 0.0, 1e-6)
+    ok, diff = _passes(x.grad, rdx, dtype)
+    assert ok, ("dx", diff)
+    atol, rtol = TOL[dtype]
+    dw_diff = (w.grad.double().cpu() - rdw).abs().max().item()
+    assert dw_diff <= atol + rtol * rdw.abs().max().item() * (1 if dtype == torch.float32 else 2), ("dw", dw_diff)
+
+
 def test_weight_gradient_is_deterministic():
     from kernels.rmsnorm import apply_rmsnorm_v4
 
