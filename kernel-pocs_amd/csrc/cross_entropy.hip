@@ -592,17 +592,30 @@ int launch_scale(void* x, int64_t ld, int64_t rows, int64_t cols, const void* g,
 // n_valid, min / max of target * (target != ignore) (ignored rows count as 0,
 // as the reference's masked max / min do), and whether that range is inside
 // [0, n_cols).  One workgroup; labels are a few thousand to a few million.
+// Both single-workgroup kernels here load kBatch elements per thread before
+// they combine any (thread i takes i, i + 1024, ... in order, so the sum's
+// order is that of a plain strided loop): one memory latency per 8192
+// elements instead of one per 1024.
+constexpr int kBatch = 8;
+
 __global__ __launch_bounds__(1024) void ce_target_stats_kernel(const int64_t* t, int64_t stride, int64_t n,
                                                                int64_t ignore, int64_t n_cols, int64_t* out) {
   __shared__ int64_t red[3][16];
   int64_t cnt = 0, mn = INT64_MAX, mx = INT64_MIN;
-  for (int64_t i = threadIdx.x; i < n; i += 1024) {
-    const int64_t v = t[i * stride];
-    const bool valid = v != ignore;
-    const int64_t m = valid ? v : 0;
-    cnt += valid;
-    mn = m < mn ? m : mn;
-    mx = m > mx ? m : mx;
+  for (int64_t i0 = threadIdx.x; i0 < n; i0 += 1024 * kBatch) {
+    int64_t v[kBatch];
+#pragma unroll
+    for (int k = 0; k < kBatch; ++k) v[k] = i0 + k * 1024 < n ? t[(i0 + k * 1024) * stride] : ignore;
+#pragma unroll
+    for (int k = 0; k < kBatch; ++k) {
+      const bool valid = v[k] != ignore;
+      const int64_t m = valid ? v[k] : 0;
+      cnt += valid;
+      if (i0 + k * 1024 < n) {  // a row past the end counts as nothing, not as an ignored 0
+        mn = m < mn ? m : mn;
+        mx = m > mx ? m : mx;
+      }
+    }
   }
 #pragma unroll
   for (int off = 32; off >= 1; off >>= 1) {
@@ -631,7 +644,14 @@ __global__ __launch_bounds__(1024) void sum_f32_kernel(const float* x, int64_t n
                                                        int cast_dtype) {
   __shared__ float red[16];
   float acc = 0.f;
-  for (int64_t i = threadIdx.x; i < n; i += 1024) acc += x[i];
+  for (int64_t i0 = threadIdx.x; i0 < n; i0 += 1024 * kBatch) {
+    float v[kBatch];
+#pragma unroll
+    for (int k = 0; k < kBatch; ++k) v[k] = i0 + k * 1024 < n ? x[i0 + k * 1024] : 0.f;
+#pragma unroll
+    for (int k = 0; k < kBatch; ++k)
+      if (i0 + k * 1024 < n) acc += v[k];
+  }
   acc = block_sum<16>(acc, red);
   if (threadIdx.x == 0) {
     out[0] = acc;
