@@ -19,11 +19,12 @@
 //    reduction plus a fixed-order sum of the four wave totals in LDS (one
 //    barrier per chunk).  Each thread owns the same columns for the whole
 //    launch: it loads their weights once, and the backward writes its
-//    per-workgroup dw partial row straight from registers.  The backward's
-//    grid is capped (one partial row per workgroup), so each workgroup loops
-//    over chunks; up to NVT = 4 it loads the next chunk's rows while it
-//    reduces and writes the current one (two register sets).  This is the
-//    engine of Llama-class hidden sizes (2048 .. 16384 bf16).
+//    per-workgroup dw partial row straight from registers.  Both directions
+//    run persistent grids (the backward's is capped at one dw partial row
+//    per workgroup), so each workgroup loops over chunks; up to NVT = 4 it
+//    loads the next chunk's rows while it reduces and writes the current
+//    one (two register sets).  This is the engine of Llama-class hidden
+//    sizes (2048 .. 16384 bf16).
 //  * wave per row (narrower or unaligned rows): one 64-lane wave per row,
 //    four rows per workgroup, reductions by shuffles only.  A lane's share
 //    is held in registers up to NV = 8 vectors; wider rows take a two-pass
@@ -422,24 +423,30 @@ __device__ __forceinline__ void block_row_sums(A (&v)[R], A (*buf)[R], int lane,
   }
 }
 
+// One chunk (R rows) of the workgroup forward: load() queues the rows' x
+// loads into one register set; process() sums the squares, reduces them
+// across the workgroup and writes y and rstd.
 template <class T, class TW, class TY, int VEC, int NVT, int R, int MODE>
-__global__ __launch_bounds__(256) void rms_fwd_wg_kernel(RmsArgs a) {
+struct FwdChunk {
   using A = typename Acc<T>::type;
-  __shared__ A sums[2][kWaves][R];
-  const int tid = threadIdx.x, lane = tid % 64, wave = tid / 64;
-  const int64_t H = a.H;
-  const A eps = (A)a.eps, off = (A)a.offset;
-  const TW* w = (const TW*)a.w;
-  TW wr[NVT][VEC];  // this thread's weights, loaded once before the first row
+  using P = Pk<T, VEC>;
+
+  __device__ __forceinline__ static void load(const RmsArgs& a, int tid, int64_t ch, P (&xv)[R][NVT]) {
 #pragma unroll
-  for (int j = 0; j < NVT; ++j) {
-    const uint32_t c = (uint32_t)(tid + 256 * j) * VEC;
-    if ((int64_t)c < H) load_w_raw<TW, VEC>(w, c, wr[j], a.wvec);
+    for (int r = 0; r < R; ++r) {
+      const int64_t row = ch * R + r;
+#pragma unroll
+      for (int j = 0; j < NVT; ++j) {
+        const uint32_t c = (uint32_t)(tid + 256 * j) * VEC;
+        if (row < a.rows && (int64_t)c < a.H) pk_load<T, VEC>((const T*)a.x + row * a.ldx + c, xv[r][j]);
+      }
+    }
   }
-  const int64_t n_chunks = (a.rows + R - 1) / R;
-  int buf = 0;
-  for (int64_t ch = blockIdx.x; ch < n_chunks; ch += gridDim.x, buf ^= 1) {
-    Pk<T, VEC> xv[R][NVT];
+
+  __device__ __forceinline__ static void process(const RmsArgs& a, int tid, int lane, int wave, int64_t ch,
+                                                 P (&xv)[R][NVT], const TW (&wr)[NVT][VEC], A (*sbuf)[R]) {
+    const int64_t H = a.H;
+    const A eps = (A)a.eps, off = (A)a.offset;
     A ss[R];
 #pragma unroll
     for (int r = 0; r < R; ++r) {
@@ -449,7 +456,6 @@ __global__ __launch_bounds__(256) void rms_fwd_wg_kernel(RmsArgs a) {
       for (int j = 0; j < NVT; ++j) {
         const uint32_t c = (uint32_t)(tid + 256 * j) * VEC;
         if (row < a.rows && (int64_t)c < H) {
-          pk_load<T, VEC>((const T*)a.x + row * a.ldx + c, xv[r][j]);
 #pragma unroll
           for (int q = 0; q < VEC; ++q) {
             const A x = pk_get<A>(xv[r][j], q);
@@ -458,7 +464,7 @@ __global__ __launch_bounds__(256) void rms_fwd_wg_kernel(RmsArgs a) {
         }
       }
     }
-    block_row_sums<A, R>(ss, sums[buf], lane, wave);
+    block_row_sums<A, R>(ss, sbuf, lane, wave);
 #pragma unroll
     for (int r = 0; r < R; ++r)
 #pragma unroll
@@ -483,6 +489,48 @@ __global__ __launch_bounds__(256) void rms_fwd_wg_kernel(RmsArgs a) {
     for (int r = 0; r < R; ++r) {
       const int64_t row = ch * R + r;
       if (tid == r && row < a.rows) ((A*)a.rstd)[row] = rsqrt_a(ss[r] / (A)H + eps);
+    }
+  }
+};
+
+// A persistent grid (fwd_grid below) over chunks blockIdx.x + i gridDim.x:
+// each workgroup loads its weights once and, up to NVT = 4, queues the next
+// chunk's x loads before it processes the current one (two register sets,
+// as the backward).  One row per workgroup on 8192 workgroups had read the
+// whole weight vector from L2 once per row.
+template <class T, class TW, class TY, int VEC, int NVT, int R, int MODE>
+__global__ __launch_bounds__(256) void rms_fwd_wg_kernel(RmsArgs a) {
+  using K = FwdChunk<T, TW, TY, VEC, NVT, R, MODE>;
+  using A = typename K::A;
+  using P = typename K::P;
+  __shared__ A sums[2][kWaves][R];
+  const int tid = threadIdx.x, lane = tid % 64, wave = tid / 64;
+  const TW* w = (const TW*)a.w;
+  TW wr[NVT][VEC];  // this thread's weights, loaded once before the first row
+#pragma unroll
+  for (int j = 0; j < NVT; ++j) {
+    const uint32_t c = (uint32_t)(tid + 256 * j) * VEC;
+    if ((int64_t)c < a.H) load_w_raw<TW, VEC>(w, c, wr[j], a.wvec);
+  }
+  const int64_t n_chunks = (a.rows + R - 1) / R;
+  const int64_t G = gridDim.x;
+  if constexpr (NVT <= 4) {
+    P xa[R][NVT], xb[R][NVT];
+    int64_t ch = blockIdx.x;
+    if (ch < n_chunks) K::load(a, tid, ch, xa);
+    for (; ch < n_chunks; ch += 2 * G) {
+      if (ch + G < n_chunks) K::load(a, tid, ch + G, xb);
+      K::process(a, tid, lane, wave, ch, xa, wr, sums[0]);
+      if (ch + G >= n_chunks) break;
+      if (ch + 2 * G < n_chunks) K::load(a, tid, ch + 2 * G, xa);
+      K::process(a, tid, lane, wave, ch + G, xb, wr, sums[1]);
+    }
+  } else {
+    int buf = 0;
+    for (int64_t ch = blockIdx.x; ch < n_chunks; ch += G, buf ^= 1) {
+      P xv[R][NVT];
+      K::load(a, tid, ch, xv);
+      K::process(a, tid, lane, wave, ch, xv, wr, sums[buf]);
     }
   }
 }
@@ -747,16 +795,21 @@ void fwd_wg(const RmsArgs& a, int grid, hipStream_t s) {
   }
 }
 
-// Rows per chunk of the workgroup engine, by vectors per thread (NVT 1, 2,
-// 4, 8), from a sweep of cold fwd+bwd steps on MI355X over bf16 widths 2048
-// .. 16384 at 2^25 elements (forward R in {8, 4, 2, 1}, backward R in
-// {8, 4, 2, 1}): small forward chunks on a grid of up to 8192 workgroups
-// (one or two rows each: fewer VGPRs, so all resident workgroups fit in one
-// round, and a short tail), and backward chunks of 4 / 2 / 1 / 1 rows behind
-// its 512-workgroup cap.  Steps against the previous 8 / 4 / 2 / 1 rows in
-// both directions: 76.8 -> 68.8 us (H 2048), 80.6 -> 69.2 (4096), 87.0 ->
-// 72.8 (8192), 96.2 -> 83.0 (16384).
+// Rows per chunk and forward grid of the workgroup engine, by vectors per
+// thread (NVT 1, 2, 4, 8), from sweeps of cold fwd+bwd steps on MI355X over
+// bf16 widths 2048 .. 16384 at 2^25 elements:
+//  * forward: 2 / 1 / 1 / 1 rows per chunk (fewer VGPRs than 8 / 4 / 2 / 1,
+//    whose 89 VGPRs at NVT = 2 left 1280 of 2048 workgroups resident) on a
+//    persistent grid of 2048 workgroups up to NVT = 2 and 1024 beyond
+//    (against 8192: forward 30.2 -> 27.0 us at H 2048, 29.1 -> 27.1 at
+//    4096, 30.8 -> 27.7 at 8192, 35.5 -> 31.5 at 16384; 512 was slower at
+//    the two narrow widths);
+//  * backward: 4 / 2 / 1 / 1 rows per chunk behind its 512-workgroup cap.
+// Steps against the previous kernels (8 / 4 / 2 / 1 rows both ways, one
+// chunk per forward workgroup): 76.8 -> 66.2 us (H 2048), 80.6 -> 67.7
+// (4096), 87.0 -> 70.4 (8192), 96.2 -> 79.8 (16384).
 constexpr int fwd_rows(int nvt) { return nvt == 1 ? 2 : 1; }
+constexpr int fwd_grid(int nvt) { return nvt <= 2 ? 2048 : 1024; }
 constexpr int bwd_rows_per_chunk(int nvt) { return nvt == 1 ? 4 : nvt == 2 ? 2 : 1; }
 
 template <class T, class TW, class TY, int VEC>
@@ -765,7 +818,7 @@ int fwd_v(const RmsArgs& a, hipStream_t s) {
   if constexpr (VEC > 1) {
     if (nvt) {
       const int r = fwd_rows(nvt);
-      const int grid = grid_for((a.rows + r - 1) / r, 1, 256 * 32);
+      const int grid = grid_for((a.rows + r - 1) / r, 1, fwd_grid(nvt));
       switch (nvt) {
         case 1: fwd_wg<T, TW, TY, VEC, 1, fwd_rows(1)>(a, grid, s); break;
         case 2: fwd_wg<T, TW, TY, VEC, 2, fwd_rows(2)>(a, grid, s); break;

@@ -150,6 +150,25 @@ def test_backward_chunk_loop_ragged(rows_per_chunk, h, dtype, in_place):
     assert dw_diff <= atol + rtol * rdw.abs().max().item() * (1 if dtype == torch.float32 else 2), ("dw", dw_diff)
 
 
+@pytest.mark.parametrize("rows, h, dtype", [(8793, 2048, torch.bfloat16), (4397, 4096, torch.bfloat16),
+                                            (2349, 8192, torch.bfloat16), (2349, 16384, torch.bfloat16),
+                                            (2349, 4096, torch.float32)])
+def test_forward_chunk_loop_ragged(rows, h, dtype):
+    """The workgroup forward runs a persistent grid (2048 workgroups up to two
+    vectors per thread, 1024 beyond; chunks of 2 rows at one vector per
+    thread, else 1) with the next chunk's loads queued before the current
+    one is processed.  These row counts give the first 301 workgroups three
+    chunks and the rest two, and leave a ragged last chunk where chunks
+    hold two rows; 16384 bf16 columns run the one-register-set loop."""
+    from kernels.rmsnorm import apply_rmsnorm_v4
+
+    xd, wd = _inputs(1, rows, h, dtype, "ones_plus_noise", seed=5)
+    y = apply_rmsnorm_v4(xd, wd, 1e-6, 0.0, "llama")
+    ref_y, _ = orms.rms_forward(xd, wd, 1e-6, 0.0, orms.LLAMA)
+    ok, diff = _passes(y, ref_y, dtype)
+    assert ok, ("y", diff)
+
+
 def test_weight_gradient_is_deterministic():
     from kernels.rmsnorm import apply_rmsnorm_v4
 
