@@ -368,6 +368,19 @@ int forge_lora_mlp_down_bwd(int64_t M, int64_t H, int64_t I, int64_t r,
                             const void* a_down, int64_t ld_ad, int w_layout,
                             void* h_out, void* e_df, void* g_de, int64_t ld, int activation, void* stream);
 
+/* The gated activation of forge_lora_mlp_gate_up on its own, for callers
+ * whose e and g (LoRA terms included) come from a library GEMM as bf16
+ * [M, I] (pitch ld_eg): h = glu(e, g) [M, I] (pitch ld_h) with that entry
+ * point's per-element formulas on the bf16 values.  I and the pitches
+ * multiples of 8, pointers 16-byte aligned (else FORGE_ERR_UNSUPPORTED).
+ * Replaces the activation stage of `_fused_lora_swiglu_kernel` after the
+ * reference's cuBLAS gate/up GEMMs
+ * (kernels/lora_mlp/experiments/v6/lora_mlp_kernel_v6.py:374-415,
+ * experiments/v3/lora_mlp_kernel_v3.py:45-138), or geglu(gate, up) on the
+ * Gemma path (kernels/geglu/geglu.py:126-148). */
+int forge_lora_mlp_glu_fwd(int64_t M, int64_t I, const void* e, const void* g, int64_t ld_eg, void* h,
+                           int64_t ld_h, int activation, void* stream);
+
 /* LoRA-QKV forward with GQA-asymmetric widths and optional fused RoPE:
  *   out[:, 0:hq]          = X Wq^T + xa[:, 0:r]   Bq^T   (rotated if apply_rope)
  *   out[:, hq:hq+hkv]     = X Wk^T + xa[:, r:2r]  Bk^T   (rotated if apply_rope)

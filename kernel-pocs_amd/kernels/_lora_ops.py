@@ -4,10 +4,19 @@ Thin wrappers over the MFMA GEMM entry points of libforge_hip.so
 (csrc/gemm.hip, csrc/lora.hip).  Operands are bf16 with unit stride in the
 last dimension and 16-byte aligned rows; every wrapper checks that and calls
 the library on torch's current stream.
+
+Plain products of the base weights (no epilogue: W_down in the LoRA-MLP
+forward, dX in the backwards) go to hipBLASLt through torch.matmul, as the
+reference sends every big matmul to cuBLAS
+(kernels/lora_mlp/experiments/v6/lora_mlp_kernel_v6.py:5, 374-443, 650-652).
+On MI355X its stream-K 256 x 256 kernel runs these shapes 22-28% faster than
+the library's LDS-DMA GEMM (8192 x 4096 x 14336: 609 against 782 us cold,
+same box).  FORGE_PLAIN_GEMM=forge keeps them on libforge_hip's GEMM.
 """
 from __future__ import annotations
 
 import ctypes
+import os
 import weakref
 from typing import Optional, Sequence, Tuple
 
@@ -16,6 +25,20 @@ import torch
 from forge_hip import _lib as L
 
 ROW, COL = L.LAYOUT_ROW, L.LAYOUT_COL
+
+# plain base-weight products on hipBLASLt (torch.matmul) unless FORGE_PLAIN_GEMM=forge
+BLAS_PLAIN = os.environ.get("FORGE_PLAIN_GEMM", "hipblaslt") != "forge"
+
+
+def blas_nt(a: torch.Tensor, b: torch.Tensor, lora: Sequence[Tuple[torch.Tensor, torch.Tensor]] = ()) -> torch.Tensor:
+    """a @ b^T (+ sum of xa @ xb^T over `lora`) with a [M, K] and b [N, K]
+    K-contiguous bf16 (a frozen weight in nn.Linear layout, or a cached W^T):
+    one hipBLASLt GEMM, then one rank-r addmm per LoRA pair on the output
+    (the reference's out.addmm_, lora_mlp_kernel_v6.py:428, 651-655)."""
+    out = torch.matmul(a, b.t())
+    for xa, xb in lora:
+        out.addmm_(xa, xb.t())
+    return out
 
 
 def as_operand(t: torch.Tensor) -> torch.Tensor:
@@ -159,6 +182,37 @@ def lora_a(x: torch.Tensor, mats: Sequence[torch.Tensor], scales: Sequence[float
         "forge_lora_a",
     )
     return out
+
+
+_EXT_CACHE = {}
+
+
+def lora_ext_weight(w: torch.Tensor, b: torch.Tensor, slot: int, n_slots: int) -> torch.Tensor:
+    """[W | B_0 | .. | B_{n-1}] [N, K + n r] for a library GEMM that takes a
+    LoRA product as extra K columns ([X | xa] @ ext^T = X W^T + xa_slot B^T
+    with xa = [xa_0 | .. | xa_{n-1}]): block `slot` holds b (bf16 [N, r]), the
+    others zero.  W is copied once per frozen weight (kept, like frozen_t,
+    until the weight is freed, changed in place or given new storage); b is
+    written into its block on every call, since it trains."""
+    N, K = w.shape
+    r = b.shape[1]
+    key = (id(w), slot, n_slots, r)
+    ent = _EXT_CACHE.get(key)
+    ext = None
+    if ent is not None:
+        ref, ver, ptr, cached = ent
+        if ref() is w and ver == w._version and ptr == w.data_ptr():
+            ext = cached
+    if ext is None:
+        ext = torch.zeros(N, K + n_slots * r, dtype=w.dtype, device=w.device)
+        ext[:, :K].copy_(w.detach())
+
+        def _drop(_ref, key=key):
+            _EXT_CACHE.pop(key, None)
+
+        _EXT_CACHE[key] = (weakref.ref(w, _drop), w._version, w.data_ptr(), ext)
+    ext[:, K + slot * r:K + (slot + 1) * r].copy_(b.detach())
+    return ext
 
 
 _T_CACHE = {}

@@ -3,11 +3,17 @@
 Forward  (reference v6 `_v6_forward_impl`,
 kernels/lora_mlp/experiments/v6/lora_mlp_kernel_v6.py:335-451):
   1. xa   = [sg X Ag^T | su X Au^T]                  forge_lora_a       [M, 2r]
-  2. e, g, h = gate/up GEMM + LoRA-B + SwiGLU        forge_lora_mlp_gate_up
-     (one MFMA GEMM: each tile computes gate and up columns together, h is
-      formed in registers, e and g (LoRA included) are saved for backward)
+  2. e = [X | xa] [Wg | Bg | 0]^T, g = [X | xa] [Wu | 0 | Bu]^T
+                                                     hipBLASLt (torch.matmul; the
+     LoRA-B products ride along as extra K columns of cached extended weights,
+     one rounding), then h = glu(e, g)               forge_lora_mlp_glu_fwd
   3. xd   = sd h Ad^T                                forge_lora_a       [M, r]
-  4. out  = h Wd^T + xd Bd^T                         forge_gemm (2 K segments)
+  4. out  = h Wd^T + xd Bd^T                         hipBLASLt GEMM + rank-r addmm
+  (the reference sends these products to cuBLAS, lora_mlp_kernel_v6.py:374-443.
+   With FORGE_PLAIN_GEMM=forge, steps 2 and 4 are the library's MFMA GEMMs
+   instead: forge_lora_mlp_gate_up, one GEMM with the LoRA-B K segments and the
+   GLU epilogue that forms h in registers, and forge_gemm with xd Bd^T as a K
+   segment.)
 
 Backward (reference `LoRAMLPv6.backward`, :592-672, Unsloth-style in place;
 math of kernels/lora_mlp/reference/lora_mlp_pytorch.py:145-225):
@@ -17,7 +23,8 @@ math of kernels/lora_mlp/reference/lora_mlp_pytorch.py:145-225):
   3. dAd = td^T h,  dBd = sd dY^T (h Ad^T)           split-K forge_gemm
   4. vu = su df Bu, vg = sg de Bg                    forge_gemm         [M, r]
      dAu = vu^T X, dAg = vg^T X, dBu = su df^T (X Au^T), dBg = sg de^T (X Ag^T)
-  5. dX = df Wu + de Wg + vu Au + vg Ag              forge_gemm (4 K segments)
+  5. dX = df Wu + de Wg + vu Au + vg Ag              hipBLASLt on the cached W^T, then
+     + de Wg and + [vu | vg] [Au; Ag] as addmm      (or forge_gemm with 4 K segments)
 The saved e/g buffers are overwritten by df/de in step 2 (the reference's
 in-place contract: backward is not re-entrant).
 
@@ -38,8 +45,8 @@ import torch.nn.functional as F
 
 from forge_hip import _lib as L
 from kernels import _generic_lora as G
-from kernels._lora_ops import (COL, ROW, as_operand, frozen_t, gemm, grad_at_b, grad_at_b_group, ld, lora_a,
-                               pad_rank, small_t_batch, times_b)
+from kernels._lora_ops import (BLAS_PLAIN, COL, ROW, as_operand, blas_nt, frozen_t, gemm, grad_at_b, grad_at_b_group,
+                               ld, lora_a, lora_ext_weight, pad_rank, small_t_batch, times_b)
 
 
 def _w(t):
@@ -86,20 +93,38 @@ def mlp_forward(X2, W_gate, A_gate, B_gate, s_gate, W_up, A_up, B_up, s_up,
     g = torch.empty(M, I, dtype=torch.bfloat16, device=dev)
     h = torch.empty(M, I, dtype=torch.bfloat16, device=dev)
     st = L.stream_of(X2)
-    L.check(
-        L.forge_lora_mlp_gate_up(
-            M, H, I, r, X2.data_ptr(), ld(X2), Wg.data_ptr(), Wu.data_ptr(), ld(Wg),
-            L.ptr(xa), 2 * r, L.ptr(Bg), L.ptr(Bu), r, e.data_ptr(), g.data_ptr(), h.data_ptr(), I, act, st),
-        "forge_lora_mlp_gate_up",
-    )
+    if BLAS_PLAIN:
+        # hipBLASLt: e = [X | xa] [Wg | Bg | 0]^T and g = [X | xa] [Wu | 0 | Bu]^T,
+        # the LoRA-B products as extra K columns (one rounding, as the fused
+        # GEMM); forge_lora_mlp_glu_fwd then forms h from the bf16 e, g
+        if has_lora:
+            xx = torch.cat([X2, xa], 1)
+            torch.matmul(xx, lora_ext_weight(W_gate, Bg, 0, 2).t(), out=e)
+            torch.matmul(xx, lora_ext_weight(W_up, Bu, 1, 2).t(), out=g)
+            del xx
+        else:
+            torch.matmul(X2, Wg.t(), out=e)
+            torch.matmul(X2, Wu.t(), out=g)
+        L.check(L.forge_lora_mlp_glu_fwd(M, I, e.data_ptr(), g.data_ptr(), I, h.data_ptr(), I, act, st),
+                "forge_lora_mlp_glu_fwd")
+    else:
+        L.check(
+            L.forge_lora_mlp_gate_up(
+                M, H, I, r, X2.data_ptr(), ld(X2), Wg.data_ptr(), Wu.data_ptr(), ld(Wg),
+                L.ptr(xa), 2 * r, L.ptr(Bg), L.ptr(Bu), r, e.data_ptr(), g.data_ptr(), h.data_ptr(), I, act, st),
+            "forge_lora_mlp_gate_up",
+        )
     segs = [(h, I, Wd, ld(Wd), I)]
+    lora_d = []
     if has_lora and A_down is not None and B_down is not None:
         xd = lora_a(h, [A_down], [s_down])
         Bd = _w(B_down)
         segs.append((xd, r, Bd, ld(Bd), r))
+        lora_d = [(xd, Bd)]
         if aux is not None:
             aux["xa"], aux["xd"] = xa, xd
-    out = gemm(M, Wd.shape[0], segs, ROW, COL)
+    # a plain product: hipBLASLt (h Wd^T, then + xd Bd^T), or the library's GEMM with xd Bd^T as a K segment
+    out = blas_nt(h, Wd, lora_d) if BLAS_PLAIN else gemm(M, Wd.shape[0], segs, ROW, COL)
     if not save_eg:
         e = g = None
     return out, e, g
@@ -191,7 +216,11 @@ def mlp_backward(dY2, X2, e, g, W_gate, A_gate, B_gate, s_gate, W_up, A_up, B_up
         dBg = grad_at_b(de, I, xa_ug[:, r:], 2 * r, I, r, M, alpha=s_gate, out_dtype=dt)
 
     # 5: dX
-    if kt:
+    if kt and BLAS_PLAIN:
+        # hipBLASLt on the cached W^T (both operands K-contiguous): df Wu, + de Wg, + v [Au; Ag]
+        WuT, WgT = frozen_t(W_up), frozen_t(W_gate)
+        dX = blas_nt(df, WuT, [(de, WgT), (v, torch.cat([Au, Ag]).t())])
+    elif kt:
         WuT, WgT = frozen_t(W_up), frozen_t(W_gate)
         dX = gemm(M, H, [(df, I, WuT, I, I), (de, I, WgT, I, I),
                          (v[:, :r], 2 * r, AuT, r, r), (v[:, r:], 2 * r, AgT, r, r)], ROW, COL)

@@ -56,6 +56,26 @@ def test_lora_mlp_matches_oracle(B, S, H, I, r, alpha, version):
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("blas_plain", [True, False])
+def test_lora_mlp_plain_gemm_backends_match_oracle(blas_plain, monkeypatch):
+    """The plain base-weight products (h Wd^T and dX) run on hipBLASLt by
+    default and on the library's GEMM with FORGE_PLAIN_GEMM=forge: both
+    backends against the oracle, forward and every gradient."""
+    import kernels.lora_mlp._impl as impl
+
+    monkeypatch.setattr(impl, "BLAS_PLAIN", blas_plain)
+    gen = torch.Generator().manual_seed(17)
+    params = orc.make_params(1024, 2816, 64, 128, gen)
+    X = torch.randn(2, 256, 1024, generator=gen).to(torch.bfloat16)
+    dY = torch.randn(2, 256, 1024, generator=gen).to(torch.bfloat16)
+    ref_out, ref_grads = orc.fwd_bwd(X, dY, params)
+    out, grads = _run(lambda x, *p: LoRAMLPv6.apply(x, *p), X, dY, params)
+    _close_bf16(out.reshape(-1, 1024), ref_out, "out")
+    for n, a, b in zip(NAMES, grads, ref_grads):
+        _close_bf16(a.reshape(b.shape), b, n)
+
+
+@pytest.mark.gpu
 def test_lora_mlp_saved_tensors_contract():
     """save_for_backward = (A_gate, B_gate, A_up, B_up, A_down, B_down, X, e, g)
     with e/g = pre-activations WITH LoRA added (v6 :586)."""
