@@ -215,6 +215,62 @@ def lora_ext_weight(w: torch.Tensor, b: torch.Tensor, slot: int, n_slots: int) -
     return ext
 
 
+def lora_ext_rows(ws: Sequence[torch.Tensor], bs: Sequence[Optional[torch.Tensor]], r: int,
+                  transpose: bool = False) -> torch.Tensor:
+    """Row blocks [W_i | 0 .. b_i .. 0] stacked: [sum N_i, K + n r] with b_i
+    (bf16 [N_i, r]) in column block i after K, for one library GEMM over
+    [X | x_0 | .. | x_{n-1}] that gives every projection its own rank-r
+    term (LoRA-QKV: [X | xa] ext^T = [X Wq^T + xa_q Bq^T | ..]).  With
+    transpose the base blocks are W_i^T (w_i [K_i, N] stacked along K:
+    ext = [W_0^T | .. | W_{n-1}^T | b_0 | .. ] [N, sum K_i + n r], for
+    [dY_0 | .. | dY_{n-1} | t] ext^T = sum dY_i W_i + t [b ..]^T).  The base
+    blocks are copied once per set of frozen weights (as frozen_t); the b
+    blocks are written on every call (they train).  r = 0: the bare stack."""
+    key = ("rows", tuple(id(w) for w in ws), r, transpose)
+    ent = _EXT_CACHE.get(key)
+    ext = None
+    if ent is not None:
+        refs, vers, ptrs, cached = ent
+        if all(rf() is w and v == w._version and p == w.data_ptr() for rf, v, p, w in zip(refs, vers, ptrs, ws)):
+            ext = cached
+    n = len(ws)
+    if transpose:
+        N, Ks = ws[0].shape[1], [w.shape[0] for w in ws]
+        base = sum(Ks)
+    else:
+        Ns, K = [w.shape[0] for w in ws], ws[0].shape[1]
+        base = K
+    if ext is None:
+        if transpose:
+            ext = torch.zeros(N, base + n * r, dtype=ws[0].dtype, device=ws[0].device)
+            k0 = 0
+            for w, k in zip(ws, Ks):
+                ext[:, k0:k0 + k].copy_(w.detach().t())
+                k0 += k
+        else:
+            ext = torch.zeros(sum(Ns), base + n * r, dtype=ws[0].dtype, device=ws[0].device)
+            n0 = 0
+            for w, nn in zip(ws, Ns):
+                ext[n0:n0 + nn, :K].copy_(w.detach())
+                n0 += nn
+
+        def _drop(_ref, key=key):
+            _EXT_CACHE.pop(key, None)
+
+        _EXT_CACHE[key] = ([weakref.ref(w, _drop) for w in ws], [w._version for w in ws], [w.data_ptr() for w in ws],
+                           ext)
+    if r:
+        if transpose:
+            for i, b in enumerate(bs):  # b_i [N, r]
+                ext[:, base + i * r:base + (i + 1) * r].copy_(b.detach())
+        else:
+            n0 = 0
+            for i, (w, b) in enumerate(zip(ws, bs)):
+                ext[n0:n0 + w.shape[0], base + i * r:base + (i + 1) * r].copy_(b.detach())
+                n0 += w.shape[0]
+    return ext
+
+
 _T_CACHE = {}
 
 
