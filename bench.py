@@ -545,26 +545,32 @@ def _gpu_params_mlp(H, I, r, alpha, gen):
     return (W(I, H), A(H), B(I), s, W(I, H), A(H), B(I), s, W(H, I), A(I), B(H), s)
 
 
-def _gate_up_roofline(args, X2, Wg, Wu, Bg, Bu, r, act=None, traffic_key="lora_mlp_gate_up"):
-    """(mean launch ms, roofline) of the LoRA-MLP's dominant kernel, the fused
-    gate/up GEMM + gated-activation epilogue (forge_lora_mlp_gate_up; SwiGLU
-    unless act names another FORGE_ACT_*), on X2 [M, H]."""
+def _down_bwd_roofline(args, M, H, I, r, Wd, act=None, traffic_key="lora_mlp_down_bwd"):
+    """(mean launch ms, roofline) of the LoRA-MLP step's largest launch, the
+    library's fused down-projection backward GEMM (forge_lora_mlp_down_bwd:
+    DW = dY Wd + td Ad on the cached Wd^T, then the in-place gated-activation
+    backward in the epilogue; SwiGLU unless act names another FORGE_ACT_*).
+    The step's other big products are hipBLASLt GEMMs of 0.6-0.65 ms each."""
     import torch
     from forge_hip import _lib as L
+    from kernels._lora_ops import COL, frozen_t
 
-    M, H = X2.shape
-    I = Wg.shape[0]
-    xa = torch.randn(M, 2 * r, device="cuda").to(torch.bfloat16)
-    e = torch.empty(M, I, device="cuda", dtype=torch.bfloat16)
-    gg, hh = torch.empty_like(e), torch.empty_like(e)
-    st = L.stream_of(X2)
+    bf = torch.bfloat16
+    g = torch.Generator(device="cuda").manual_seed(11)
+    dY = torch.randn(M, H, device="cuda", generator=g).to(bf)
+    WdT = frozen_t(Wd)
+    td = (torch.randn(M, r, device="cuda", generator=g) * 0.1).to(bf)
+    AdT = (torch.randn(I, r, device="cuda", generator=g) * 0.1).to(bf)
+    e = torch.randn(M, I, device="cuda", generator=g).to(bf)
+    gg = torch.randn(M, I, device="cuda", generator=g).to(bf)
+    hh = torch.empty_like(e)
+    st = L.stream_of(dY)
     act = L.ACT_SILU if act is None else act
-    launch_ms = time_launches(lambda i: L.forge_lora_mlp_gate_up(
-        M, H, I, r, X2.data_ptr(), X2.stride(0), Wg.data_ptr(), Wu.data_ptr(), Wg.stride(0), xa.data_ptr(), 2 * r,
-        Bg.data_ptr(), Bu.data_ptr(), Bg.stride(0), e.data_ptr(), gg.data_ptr(), hh.data_ptr(), I, act, st),
-        max(args.steps, 10))
-    gu_flops = 4 * M * H * I + 4 * M * r * I
-    return launch_ms, _roof("mfma", gu_flops / (launch_ms * 1e-3) / 1e12, BF16_PEAK_TFLOPS, "TFLOP/s",
+    launch_ms = time_launches(lambda i: L.forge_lora_mlp_down_bwd(
+        M, H, I, r, dY.data_ptr(), H, WdT.data_ptr(), H, td.data_ptr(), r, AdT.data_ptr(), r, COL, hh.data_ptr(),
+        e.data_ptr(), gg.data_ptr(), I, act, st), max(args.steps, 10))
+    db_flops = 2 * M * H * I + 2 * M * r * I
+    return launch_ms, _roof("mfma", db_flops / (launch_ms * 1e-3) / 1e12, BF16_PEAK_TFLOPS, "TFLOP/s",
                             _traffic(traffic_key))
 
 
@@ -596,18 +602,17 @@ def bench_lora_mlp(args, activation="silu"):
     ms, wall = run_steps(args, step)
     fl = flops(M, H, I, r)
     tf = rate(fl, ms, 1e12)
-    # dominant kernel: the fused gate/up GEMM + gated-activation epilogue
-    Wg, Ag, Bg, sg, Wu, Au, Bu, su = [t.detach() if isinstance(t, torch.Tensor) else t for t in params[:8]]
-    launch_ms, roof = _gate_up_roofline(args, X.detach().reshape(M, H), Wg, Wu, Bg, Bu, r,
-                                        act=L.ACT_GELU_TANH if geglu else L.ACT_SILU,
-                                        traffic_key="lora_mlp_geglu_gate_up" if geglu else "lora_mlp_gate_up")
+    # roofline kernel: the step's largest launch, the fused down-projection backward GEMM
+    launch_ms, roof = _down_bwd_roofline(args, M, H, I, r, params[8].detach(),
+                                         act=L.ACT_GELU_TANH if geglu else L.ACT_SILU,
+                                         traffic_key="lora_mlp_geglu_down_bwd" if geglu else "lora_mlp_down_bwd")
     res = {
         "config": {"workload": "lora_mlp_geglu_fwd_bwd" if geglu else "lora_mlp_fwd_bwd", "dtype": "bf16", "M": M,
                    "H": H, "I": I, "rank": r, "alpha": 32,
                    "api": "LoRAMLPGeGLU (tanh GELU)" if geglu else "LoRAMLPv6"},
         "value": tf, "unit": "TFLOP/s", "ms_per_step": rnd(ms, 4), "wall_ms_per_step": rnd(wall, 4),
         "frac_of_mfma_peak": rnd(tf and tf / BF16_PEAK_TFLOPS, 4), "algorithmic_flops_per_step": fl,
-        "launches_ms": {"forge_lora_mlp_gate_up": round(launch_ms, 4)},
+        "launches_ms": {"forge_lora_mlp_down_bwd": round(launch_ms, 4)},
         "roofline": roof,
         "dtype": "bf16",
     }
@@ -729,11 +734,9 @@ def bench_lora_patch(args, arch="llama"):
     ms_ref, _ = run_steps(args, stepper(ref))
     fl = flops(M, H, I, r)
     tf, tf_ref = rate(fl, ms, 1e12), rate(fl, ms_ref, 1e12)
-    w = [getattr(ref, n).base_layer.weight.detach() for n in ("gate_proj", "up_proj")]
-    b = [getattr(ref, n).lora_B["default"].weight.detach() for n in ("gate_proj", "up_proj")]
-    launch_ms, roof = _gate_up_roofline(args, X.detach().reshape(M, H), w[0], w[1], b[0], b[1], r,
-                                        act=L.ACT_GELU_TANH if gemma else L.ACT_SILU,
-                                        traffic_key="lora_patch_gemma_gate_up" if gemma else "lora_mlp_gate_up")
+    wd = ref.down_proj.base_layer.weight.detach()
+    launch_ms, roof = _down_bwd_roofline(args, M, H, I, r, wd, act=L.ACT_GELU_TANH if gemma else L.ACT_SILU,
+                                         traffic_key="lora_patch_gemma_down_bwd" if gemma else "lora_mlp_down_bwd")
     return {
         "config": {"workload": "lora_mlp_patch_gemma2_fwd_bwd" if gemma else "lora_mlp_patch_fwd_bwd", "dtype": "bf16",
                    "M": M, "H": H, "I": I, "rank": r, "alpha": 32,
@@ -744,7 +747,7 @@ def bench_lora_patch(args, arch="llama"):
         "frac_of_mfma_peak": rnd(tf and tf / BF16_PEAK_TFLOPS, 4), "algorithmic_flops_per_step": fl,
         "reference_submodule_path": {"value": tf_ref, "unit": "TFLOP/s", "ms_per_step": rnd(ms_ref, 4)},
         "speedup_vs_submodule_path": rnd(ms and ms_ref / ms, 3),
-        "launches_ms": {"forge_lora_mlp_gate_up": round(launch_ms, 4)},
+        "launches_ms": {"forge_lora_mlp_down_bwd": round(launch_ms, 4)},
         "roofline": roof,
         "dtype": "bf16",
     }
@@ -798,17 +801,17 @@ def bench_lora_qkv(args):
     ms, wall = run_steps(args, step)
     fl = T * flops_per_token(K, Hq, Hkv, r)
     tf = rate(fl, ms, 1e12)
-    # dominant kernel: the forward GEMM (X [Wq;Wk;Wv]^T + LoRA-B segment, RoPE
-    # epilogue), forge_lora_qkv_rope
-    from kernels._lora_ops import lora_a
-    from kernels.lora_qkv._impl import qkv_gemm
+    # dominant kernel: the forward product, a hipBLASLt GEMM [X | xa] [W | B]^T
+    # (X [Wq;Wk;Wv]^T with the LoRA-B products as extra K columns); the
+    # backward's dX product is the other one of the same size
+    from kernels._lora_ops import lora_a, lora_ext_rows
 
     Xd = X.detach()
     xa = lora_a(Xd, [Aq.detach(), Ak.detach(), Av.detach()], [s, s, s])  # the forward's LoRA-A product
+    xx = torch.cat([Xd, xa], 1)
+    ext = lora_ext_rows([Wq, Wk, Wv], [Bq.detach(), Bk.detach(), Bv.detach()], r)
     out = torch.empty(T, Hq + 2 * Hkv, device="cuda", dtype=bf)
-    rope = {"cos": c, "sin": sn, "positions": pos, "head_dim": D}
-    launch_ms = time_launches(lambda i: qkv_gemm(Xd, Wq, Wk, Wv, xa, Bq.detach(), Bk.detach(), Bv.detach(), r, rope,
-                                                 out), max(args.steps, 10))
+    launch_ms = time_launches(lambda i: torch.matmul(xx, ext.t(), out=out), max(args.steps, 10))
     fwd_flops = 2 * T * K * (Hq + 2 * Hkv) + 2 * T * r * (Hq + 2 * Hkv)
     res = {
         "config": {"workload": "lora_qkv_rope_fwd_bwd", "dtype": "bf16", "tokens": T, "seq_lens": lens,
@@ -816,7 +819,7 @@ def bench_lora_qkv(args):
                    "rope_base": 500000},
         "value": tf, "unit": "TFLOP/s", "ms_per_step": rnd(ms, 4), "wall_ms_per_step": rnd(wall, 4),
         "frac_of_mfma_peak": rnd(tf and tf / BF16_PEAK_TFLOPS, 4), "algorithmic_flops_per_step": fl,
-        "launches_ms": {"forge_lora_qkv_rope": round(launch_ms, 4)},
+        "launches_ms": {"hipBLASLt forward GEMM ([X | xa] [W | B]^T, 22954 x 6144 x 4288)": round(launch_ms, 4)},
         "roofline": _roof("mfma", fwd_flops / (launch_ms * 1e-3) / 1e12, BF16_PEAK_TFLOPS, "TFLOP/s",
                           _traffic("lora_qkv_fwd_gemm")),
         "dtype": "bf16",
@@ -875,7 +878,6 @@ def bench_flce(args):
     gradients."""
     import torch
     from forge_hip import _lib as L
-    from kernels._lora_ops import COL, ROW, gemm
     from kernels.cross_entropy.experiments.v2 import forge_fused_linear_cross_entropy
     from oracle.fused_linear_ce import flops
 
@@ -895,19 +897,19 @@ def bench_flce(args):
     ms, wall = run_steps(args, step)
     fl = flops(BT, H, V)
     tf = rate(fl, ms, 1e12)
-    # dominant kernel: the LDS-DMA GEMM that computes the logits of a
-    # 4096-token chunk (X_c W^T) and, with the same symbol, dX_c = dlogits W
+    # dominant kernel: the hipBLASLt GEMM that computes the logits of a
+    # 4096-token chunk (X_c W^T); dX_c = dlogits W is the same size
     n = 4096
     logits = torch.empty(n, V, device="cuda", dtype=bf)
     xc, wd = x.detach()[:n], W.detach()
-    launch_ms = time_launches(lambda i: gemm(n, V, [(xc, H, wd, H, H)], ROW, COL, out=logits), max(args.steps, 10))
+    launch_ms = time_launches(lambda i: torch.matmul(xc, wd.t(), out=logits), max(args.steps, 10))
     res = {
         "config": {"workload": "fused_linear_cross_entropy_fwd_bwd", "dtype": "bf16", "tokens": BT, "hidden": H,
                    "vocab": V, "ignored_rows": 410, "reduction": "mean", "chunk_tokens": 4096,
                    "api": "forge_fused_linear_cross_entropy"},
         "value": tf, "unit": "TFLOP/s", "ms_per_step": rnd(ms, 4), "wall_ms_per_step": rnd(wall, 4),
         "frac_of_mfma_peak": rnd(tf and tf / BF16_PEAK_TFLOPS, 4), "algorithmic_flops_per_step": fl,
-        "launches_ms": {"forge_gemm logits chunk (X_c W^T, 4096 x 128256 x 4096)": round(launch_ms, 4)},
+        "launches_ms": {"hipBLASLt logits GEMM (X_c W^T, 4096 x 128256 x 4096)": round(launch_ms, 4)},
         "roofline": _roof("mfma", 2 * n * H * V / (launch_ms * 1e-3) / 1e12, BF16_PEAK_TFLOPS, "TFLOP/s",
                           _traffic("flce_logits_gemm")),
         "dtype": "bf16",

@@ -37,7 +37,7 @@ from typing import Optional
 import torch
 
 from forge_hip import _lib as L
-from kernels._lora_ops import COL, ROW, frozen_t, gemm, ld
+from kernels._lora_ops import BLAS_PLAIN, COL, ROW, frozen_t, gemm, ld
 
 from .cross_entropy_kernel_v2 import CrossEntropyOutput, _check_targets, _sum_f32, _target_stats_async
 
@@ -213,6 +213,10 @@ def fused_linear_cross_entropy_forward(
         # transposed (one HBM pass each) it is a K-contiguous product for the
         # LDS-DMA GEMM instead of a transposing register-path GEMM
         dw_nt = fast and want_w and chunk % 8 == 0
+        # the three products on hipBLASLt, as the reference's torch matmuls
+        # (kernels/cross_entropy/experiments/v2/fused_linear_cross_entropy.py:142,
+        # 212-214), when the vocabulary needs no column padding
+        blas = fast and BLAS_PLAIN and v_pad == V and dtype == torch.bfloat16
         if dw_nt:
             dlT_buf = torch.empty(v_pad, chunk, dtype=dtype, device=dev)
             xT_buf = torch.empty(H, chunk, dtype=dtype, device=dev)
@@ -226,7 +230,12 @@ def fused_linear_cross_entropy_forward(
             t_c = target[c0:c0 + n]
             logits = logits_buf[:n]
 
-            if fast:
+            if blas:  # hipBLASLt (torch.matmul / addmm): the bias rides in its epilogue
+                if b is None:
+                    torch.matmul(x_c, w.t(), out=logits)
+                else:
+                    torch.addmm(b, x_c, w.t(), out=logits)
+            elif fast:
                 segs = [(x_c, ld(x_c), w, ld(w), H)]
                 if b is not None:
                     segs.append((ones8[:n], 8, bias8, 8, 8))
@@ -267,14 +276,21 @@ def fused_linear_cross_entropy_forward(
             beta = 0.0 if c0 == 0 else 1.0
             gi = grad_input[c0:c0 + n]
             if fast:
-                gemm(n, H, [(logits, v_pad, wt, v_pad, v_pad)], ROW, COL, out=gi)
+                if blas:
+                    torch.matmul(logits, wt.t(), out=gi)
+                else:
+                    gemm(n, H, [(logits, v_pad, wt, v_pad, v_pad)], ROW, COL, out=gi)
                 if dw_nt and n % 8 == 0:
                     L.check(L.forge_transpose_2b(logits.data_ptr(), v_pad, n, v_pad, dlT_buf.data_ptr(), chunk, st),
                             "forge_transpose_2b")
                     L.check(L.forge_transpose_2b(x_c.data_ptr(), ld(x_c), n, H, xT_buf.data_ptr(), chunk, st),
                             "forge_transpose_2b")
-                    gemm(v_pad, H, [(dlT_buf, chunk, xT_buf, chunk, n)], ROW, COL, out=gw32, beta=beta,
-                         out_dtype=torch.float32)
+                    if blas:  # fp32 accumulation across chunks (beta 0 ignores gw32 on the first)
+                        torch.addmm(gw32, dlT_buf[:, :n], xT_buf[:, :n].t(), out_dtype=torch.float32, beta=beta,
+                                    out=gw32)
+                    else:
+                        gemm(v_pad, H, [(dlT_buf, chunk, xT_buf, chunk, n)], ROW, COL, out=gw32, beta=beta,
+                             out_dtype=torch.float32)
                 elif want_w:
                     gemm(v_pad, H, [(logits, v_pad, x_c, ld(x_c), n)], COL, ROW, out=gw32, beta=beta,
                          out_dtype=torch.float32)
