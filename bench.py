@@ -804,11 +804,11 @@ def bench_lora_qkv(args):
     # dominant kernel: the forward product, a hipBLASLt GEMM [X | xa] [W | B]^T
     # (X [Wq;Wk;Wv]^T with the LoRA-B products as extra K columns); the
     # backward's dX product is the other one of the same size
-    from kernels._lora_ops import lora_a, lora_ext_rows
+    from kernels._lora_ops import lora_a, lora_ext_rows, lora_operand
 
     Xd = X.detach()
     xa = lora_a(Xd, [Aq.detach(), Ak.detach(), Av.detach()], [s, s, s])  # the forward's LoRA-A product
-    xx = torch.cat([Xd, xa], 1)
+    xx = lora_operand(Xd, xa)
     ext = lora_ext_rows([Wq, Wk, Wv], [Bq.detach(), Bk.detach(), Bv.detach()], r)
     out = torch.empty(T, Hq + 2 * Hkv, device="cuda", dtype=bf)
     launch_ms = time_launches(lambda i: torch.matmul(xx, ext.t(), out=out), max(args.steps, 10))

@@ -30,17 +30,6 @@ ROW, COL = L.LAYOUT_ROW, L.LAYOUT_COL
 BLAS_PLAIN = os.environ.get("FORGE_PLAIN_GEMM", "hipblaslt") != "forge"
 
 
-def blas_nt(a: torch.Tensor, b: torch.Tensor, lora: Sequence[Tuple[torch.Tensor, torch.Tensor]] = ()) -> torch.Tensor:
-    """a @ b^T (+ sum of xa @ xb^T over `lora`) with a [M, K] and b [N, K]
-    K-contiguous bf16 (a frozen weight in nn.Linear layout, or a cached W^T):
-    one hipBLASLt GEMM, then one rank-r addmm per LoRA pair on the output
-    (the reference's out.addmm_, lora_mlp_kernel_v6.py:428, 651-655)."""
-    out = torch.matmul(a, b.t())
-    for xa, xb in lora:
-        out.addmm_(xa, xb.t())
-    return out
-
-
 def as_operand(t: torch.Tensor) -> torch.Tensor:
     """A 2-D bf16 operand the kernels can read: unit last stride, row pitch a
     multiple of 8 elements, 16-byte aligned base.  Copies only if needed."""
@@ -187,8 +176,29 @@ def lora_a(x: torch.Tensor, mats: Sequence[torch.Tensor], scales: Sequence[float
 _EXT_CACHE = {}
 
 
+def k_pad(k: int) -> int:
+    """K of a K-stacked library GEMM, rounded up to a multiple of 64 with
+    zero columns: hipBLASLt's stream-K kernel for K-contiguous bf16 operands
+    runs only at K % 64 == 0 (measured on MI355X, M = 8192, N = 4096: K =
+    14352 781 us, K = 14400 611 us)."""
+    return (k + 63) // 64 * 64
+
+
+def lora_operand(x: torch.Tensor, xa: torch.Tensor) -> torch.Tensor:
+    """[x | xa | 0] [M, k_pad(K + c)]: the A operand of a K-stacked product
+    (its zero columns meet the zero columns of lora_ext_weight / lora_ext_rows)."""
+    M, K = x.shape
+    c = xa.shape[1]
+    out = torch.empty(M, k_pad(K + c), dtype=x.dtype, device=x.device)
+    out[:, :K].copy_(x)
+    out[:, K:K + c].copy_(xa)
+    if out.shape[1] > K + c:
+        out[:, K + c:].zero_()
+    return out
+
+
 def lora_ext_weight(w: torch.Tensor, b: torch.Tensor, slot: int, n_slots: int) -> torch.Tensor:
-    """[W | B_0 | .. | B_{n-1}] [N, K + n r] for a library GEMM that takes a
+    """[W | B_0 | .. | B_{n-1} | 0] [N, k_pad(K + n r)] for a library GEMM that takes a
     LoRA product as extra K columns ([X | xa] @ ext^T = X W^T + xa_slot B^T
     with xa = [xa_0 | .. | xa_{n-1}]): block `slot` holds b (bf16 [N, r]), the
     others zero.  W is copied once per frozen weight (kept, like frozen_t,
@@ -204,7 +214,7 @@ def lora_ext_weight(w: torch.Tensor, b: torch.Tensor, slot: int, n_slots: int) -
         if ref() is w and ver == w._version and ptr == w.data_ptr():
             ext = cached
     if ext is None:
-        ext = torch.zeros(N, K + n_slots * r, dtype=w.dtype, device=w.device)
+        ext = torch.zeros(N, k_pad(K + n_slots * r), dtype=w.dtype, device=w.device)
         ext[:, :K].copy_(w.detach())
 
         def _drop(_ref, key=key):
@@ -225,7 +235,8 @@ def lora_ext_rows(ws: Sequence[torch.Tensor], bs: Sequence[Optional[torch.Tensor
     ext = [W_0^T | .. | W_{n-1}^T | b_0 | .. ] [N, sum K_i + n r], for
     [dY_0 | .. | dY_{n-1} | t] ext^T = sum dY_i W_i + t [b ..]^T).  The base
     blocks are copied once per set of frozen weights (as frozen_t); the b
-    blocks are written on every call (they train).  r = 0: the bare stack."""
+    blocks are written on every call (they train).  With r > 0 zero columns
+    pad the width to k_pad(..); r = 0: the bare stack."""
     key = ("rows", tuple(id(w) for w in ws), r, transpose)
     ent = _EXT_CACHE.get(key)
     ext = None
@@ -242,13 +253,13 @@ def lora_ext_rows(ws: Sequence[torch.Tensor], bs: Sequence[Optional[torch.Tensor
         base = K
     if ext is None:
         if transpose:
-            ext = torch.zeros(N, base + n * r, dtype=ws[0].dtype, device=ws[0].device)
+            ext = torch.zeros(N, k_pad(base + n * r) if r else base, dtype=ws[0].dtype, device=ws[0].device)
             k0 = 0
             for w, k in zip(ws, Ks):
                 ext[:, k0:k0 + k].copy_(w.detach().t())
                 k0 += k
         else:
-            ext = torch.zeros(sum(Ns), base + n * r, dtype=ws[0].dtype, device=ws[0].device)
+            ext = torch.zeros(sum(Ns), k_pad(base + n * r) if r else base, dtype=ws[0].dtype, device=ws[0].device)
             n0 = 0
             for w, nn in zip(ws, Ns):
                 ext[n0:n0 + nn, :K].copy_(w.detach())

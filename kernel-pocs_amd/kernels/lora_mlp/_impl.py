@@ -45,8 +45,9 @@ import torch.nn.functional as F
 
 from forge_hip import _lib as L
 from kernels import _generic_lora as G
-from kernels._lora_ops import (BLAS_PLAIN, COL, ROW, as_operand, blas_nt, frozen_t, gemm, grad_at_b, grad_at_b_group,
-                               ld, lora_a, lora_ext_weight, pad_rank, small_t_batch, times_b)
+from kernels._lora_ops import (BLAS_PLAIN, COL, ROW, as_operand, frozen_t, gemm, grad_at_b, grad_at_b_group, ld,
+                               k_pad, lora_a, lora_ext_rows, lora_ext_weight, lora_operand, pad_rank, small_t_batch,
+                               times_b)
 
 
 def _w(t):
@@ -89,23 +90,38 @@ def mlp_forward(X2, W_gate, A_gate, B_gate, s_gate, W_up, A_up, B_up, s_up,
     if has_lora:  # the first launch; the gate/up GEMM needs its result
         xa = lora_a(X2, [A_gate, A_up], [s_gate, s_up])
         Bg, Bu = _w(B_gate), _w(B_up)
-    e = torch.empty(M, I, dtype=torch.bfloat16, device=dev)
-    g = torch.empty(M, I, dtype=torch.bfloat16, device=dev)
-    h = torch.empty(M, I, dtype=torch.bfloat16, device=dev)
+    # hipBLASLt path with LoRA: e, g and spare columns side by side in one
+    # [M, k_pad(2I + 2r)] buffer ([e | g | v | 0]): the gate/up products are
+    # one library GEMM, and the backward's dX one GEMM over [df | de | v | 0]
+    # (df, de overwrite e, g; v = [su df Bu | sg de Bg]).  h gets spare
+    # columns for xd = sd h Ad^T, so the down projection is one GEMM too.
+    # The zero columns keep K a multiple of 64 (k_pad).
+    packed = BLAS_PLAIN and has_lora
+    if packed:
+        egv = torch.empty(M, k_pad(2 * I + 2 * r), dtype=torch.bfloat16, device=dev)
+        if egv.shape[1] > 2 * I + 2 * r:
+            egv[:, 2 * I + 2 * r:].zero_()
+        e, g = egv[:, :I], egv[:, I:2 * I]
+        hx = torch.empty(M, k_pad(I + r), dtype=torch.bfloat16, device=dev)
+        if hx.shape[1] > I + r:
+            hx[:, I + r:].zero_()
+        h = hx[:, :I]
+    else:
+        e = torch.empty(M, I, dtype=torch.bfloat16, device=dev)
+        g = torch.empty(M, I, dtype=torch.bfloat16, device=dev)
+        h = torch.empty(M, I, dtype=torch.bfloat16, device=dev)
     st = L.stream_of(X2)
     if BLAS_PLAIN:
-        # hipBLASLt: e = [X | xa] [Wg | Bg | 0]^T and g = [X | xa] [Wu | 0 | Bu]^T,
-        # the LoRA-B products as extra K columns (one rounding, as the fused
-        # GEMM); forge_lora_mlp_glu_fwd then forms h from the bf16 e, g
-        if has_lora:
-            xx = torch.cat([X2, xa], 1)
-            torch.matmul(xx, lora_ext_weight(W_gate, Bg, 0, 2).t(), out=e)
-            torch.matmul(xx, lora_ext_weight(W_up, Bu, 1, 2).t(), out=g)
-            del xx
+        # hipBLASLt: [e | g] = [X | xa] [Wg | Bg | 0; Wu | 0 | Bu]^T, the LoRA-B
+        # products as extra K columns (one rounding, as the fused GEMM);
+        # forge_lora_mlp_glu_fwd then forms h from the bf16 e, g
+        if packed:
+            torch.matmul(lora_operand(X2, xa), lora_ext_rows([W_gate, W_up], [Bg, Bu], r).t(),
+                         out=egv[:, :2 * I])
         else:
             torch.matmul(X2, Wg.t(), out=e)
             torch.matmul(X2, Wu.t(), out=g)
-        L.check(L.forge_lora_mlp_glu_fwd(M, I, e.data_ptr(), g.data_ptr(), I, h.data_ptr(), I, act, st),
+        L.check(L.forge_lora_mlp_glu_fwd(M, I, e.data_ptr(), g.data_ptr(), ld(e), h.data_ptr(), ld(h), act, st),
                 "forge_lora_mlp_glu_fwd")
     else:
         L.check(
@@ -114,17 +130,25 @@ def mlp_forward(X2, W_gate, A_gate, B_gate, s_gate, W_up, A_up, B_up, s_up,
                 L.ptr(xa), 2 * r, L.ptr(Bg), L.ptr(Bu), r, e.data_ptr(), g.data_ptr(), h.data_ptr(), I, act, st),
             "forge_lora_mlp_gate_up",
         )
-    segs = [(h, I, Wd, ld(Wd), I)]
-    lora_d = []
+    segs = [(h, ld(h), Wd, ld(Wd), I)]
+    Bd = None
     if has_lora and A_down is not None and B_down is not None:
-        xd = lora_a(h, [A_down], [s_down])
+        xd = lora_a(h, [A_down], [s_down], out=hx[:, I:I + r] if packed else None)
         Bd = _w(B_down)
-        segs.append((xd, r, Bd, ld(Bd), r))
-        lora_d = [(xd, Bd)]
+        segs.append((xd, ld(xd), Bd, ld(Bd), r))
         if aux is not None:
-            aux["xa"], aux["xd"] = xa, xd
-    # a plain product: hipBLASLt (h Wd^T, then + xd Bd^T), or the library's GEMM with xd Bd^T as a K segment
-    out = blas_nt(h, Wd, lora_d) if BLAS_PLAIN else gemm(M, Wd.shape[0], segs, ROW, COL)
+            # a compact copy, so the backward does not keep the [M, I + r] buffer alive
+            aux["xa"], aux["xd"] = xa, (xd.contiguous() if packed else xd)
+    # a plain product: hipBLASLt over [h | xd] [Wd | Bd]^T (xd Bd^T as extra K
+    # columns), or the library's GEMM with xd Bd^T as a K segment
+    if not BLAS_PLAIN:
+        out = gemm(M, Wd.shape[0], segs, ROW, COL)
+    elif packed and Bd is not None:
+        out = torch.matmul(hx, lora_ext_weight(W_down, Bd, 0, 1).t())
+    else:
+        out = torch.matmul(h, Wd.t())
+        if Bd is not None:
+            out.addmm_(xd, Bd.t())
     if not save_eg:
         e = g = None
     return out, e, g
@@ -168,13 +192,21 @@ def mlp_backward(dY2, X2, e, g, W_gate, A_gate, B_gate, s_gate, W_up, A_up, B_up
     if kt:
         BdT, AdT, BuT, BgT, AuT, AgT = small_t_batch([Bd, Ad, Bu, Bg, Au, Ag])
 
+    # e, g as the forward left them: pitch I, or [e | g | spare 2r] (one buffer)
+    lde = e.stride(0) if M > 1 else I
+    if M > 1 and g.stride(0) != lde:  # h, e, g share one pitch
+        e, g, lde = e.contiguous(), g.contiguous(), I
+    packed = kt and BLAS_PLAIN and M > 1 and lde == k_pad(2 * I + 2 * r) and g.data_ptr() - e.data_ptr() == 2 * I
+
     # 1-2: DW = dY Wd + sd (dY Bd) Ad with the GLU backward fused in place
+    # (h, e, g share one pitch)
     td = times_b(dY2, ld(dY2), Bd, H, alpha=s_down, b_t=BdT)
-    h = torch.empty(M, I, dtype=torch.bfloat16, device=dev)
+    h = torch.empty(M, lde, dtype=torch.bfloat16, device=dev)[:, :I] if lde != I else \
+        torch.empty(M, I, dtype=torch.bfloat16, device=dev)
     WdB, AdB, wl = (frozen_t(W_down), AdT, COL) if kt else (Wd, Ad, ROW)
     L.check(
         L.forge_lora_mlp_down_bwd(M, H, I, r, dY2.data_ptr(), ld(dY2), WdB.data_ptr(), ld(WdB), td.data_ptr(), r,
-                                  AdB.data_ptr(), ld(AdB), wl, h.data_ptr(), e.data_ptr(), g.data_ptr(), I, act,
+                                  AdB.data_ptr(), ld(AdB), wl, h.data_ptr(), e.data_ptr(), g.data_ptr(), lde, act,
                                   L.stream_of(X2)),
         "forge_lora_mlp_down_bwd",
     )
@@ -182,51 +214,61 @@ def mlp_backward(dY2, X2, e, g, W_gate, A_gate, B_gate, s_gate, W_up, A_up, B_up
 
     # 3: down-projection LoRA grads
     dt = A_gate.dtype
-    dAd = grad_at_b(td, r, h, I, r, I, M, out_dtype=dt)          # [r, I] = (sd dY Bd)^T h
+    dAd = grad_at_b(td, r, h, lde, r, I, M, out_dtype=dt)          # [r, I] = (sd dY Bd)^T h
     # with the forward's scaled products the three B gradients are one
     # launch (step 4); otherwise each is its own
     grouped = aux is not None and "xd" in aux and "xa" in aux and dt == torch.bfloat16
     if grouped:
         dBd = None
     elif aux is not None and "xd" in aux:
-        dBd = grad_at_b(dY2, ld(dY2), aux["xd"], r, H, r, M, out_dtype=dt)  # [H, r] = dY^T (sd h Ad^T)
+        dBd = grad_at_b(dY2, ld(dY2), aux["xd"], ld(aux["xd"]), H, r, M, out_dtype=dt)  # [H, r] = dY^T (sd h Ad^T)
     else:
         u = lora_a(h, [Ad], [1.0])                                # h Ad^T [M, r]
         dBd = grad_at_b(dY2, ld(dY2), u, r, H, r, M, alpha=s_down, out_dtype=dt)
 
     # 4: up / gate LoRA grads
-    v = torch.empty(M, 2 * r, dtype=torch.bfloat16, device=dev)  # [su df Bu | sg de Bg]
-    if kt and s_up == s_gate:  # both products in one launch (column-ranged segments)
-        gemm(M, 2 * r, [(df, I, BuT, I, I, 0, r), (de, I, BgT, I, I, r, 2 * r)], ROW, COL, out=v, alpha=s_up)
+    if packed:  # the spare columns of [df | de | v]
+        egv = torch.as_strided(e, (M, lde), (lde, 1), e.storage_offset())
+        v = egv[:, 2 * I:2 * I + 2 * r]
     else:
-        times_b(df, I, Bu, I, out=v[:, :r], alpha=s_up, b_t=BuT)
-        times_b(de, I, Bg, I, out=v[:, r:], alpha=s_gate, b_t=BgT)
-    dA_ug = grad_at_b(v, 2 * r, X2, ld(X2), 2 * r, H, M, out_dtype=dt)  # [2r, H]: rows [dAu; dAg]
+        v = torch.empty(M, 2 * r, dtype=torch.bfloat16, device=dev)  # [su df Bu | sg de Bg]
+    if kt and s_up == s_gate:  # both products in one launch (column-ranged segments)
+        gemm(M, 2 * r, [(df, lde, BuT, I, I, 0, r), (de, lde, BgT, I, I, r, 2 * r)], ROW, COL, out=v, alpha=s_up)
+    else:
+        times_b(df, lde, Bu, I, out=v[:, :r], alpha=s_up, b_t=BuT)
+        times_b(de, lde, Bg, I, out=v[:, r:], alpha=s_gate, b_t=BgT)
+    dA_ug = grad_at_b(v, ld(v), X2, ld(X2), 2 * r, H, M, out_dtype=dt)  # [2r, H]: rows [dAu; dAg]
     if grouped:
         xa = aux["xa"]                                            # [sg X Ag^T | su X Au^T]
-        dBd, dBu, dBg = grad_at_b_group([(aux["xd"], r, dY2, ld(dY2), H), (xa[:, r:], 2 * r, df, I, I),
-                                         (xa[:, :r], 2 * r, de, I, I)], r, M)
+        dBd, dBu, dBg = grad_at_b_group([(aux["xd"], ld(aux["xd"]), dY2, ld(dY2), H), (xa[:, r:], 2 * r, df, lde, I),
+                                         (xa[:, :r], 2 * r, de, lde, I)], r, M)
     elif aux is not None and "xa" in aux:
         xa = aux["xa"]                                            # [sg X Ag^T | su X Au^T]
-        dBu = grad_at_b(df, I, xa[:, r:], 2 * r, I, r, M, out_dtype=dt)
-        dBg = grad_at_b(de, I, xa[:, :r], 2 * r, I, r, M, out_dtype=dt)
+        dBu = grad_at_b(df, lde, xa[:, r:], 2 * r, I, r, M, out_dtype=dt)
+        dBg = grad_at_b(de, lde, xa[:, :r], 2 * r, I, r, M, out_dtype=dt)
     else:
         xa_ug = lora_a(X2, [Au, Ag], [1.0, 1.0])                 # [X Au^T | X Ag^T]
-        dBu = grad_at_b(df, I, xa_ug[:, :r], 2 * r, I, r, M, alpha=s_up, out_dtype=dt)
-        dBg = grad_at_b(de, I, xa_ug[:, r:], 2 * r, I, r, M, alpha=s_gate, out_dtype=dt)
+        dBu = grad_at_b(df, lde, xa_ug[:, :r], 2 * r, I, r, M, alpha=s_up, out_dtype=dt)
+        dBg = grad_at_b(de, lde, xa_ug[:, r:], 2 * r, I, r, M, alpha=s_gate, out_dtype=dt)
 
     # 5: dX
     if kt and BLAS_PLAIN:
-        # hipBLASLt on the cached W^T (both operands K-contiguous): df Wu, + de Wg, + v [Au; Ag]
-        WuT, WgT = frozen_t(W_up), frozen_t(W_gate)
-        dX = blas_nt(df, WuT, [(de, WgT), (v, torch.cat([Au, Ag]).t())])
+        if packed:
+            # one hipBLASLt GEMM, K-contiguous operands, one rounding:
+            # [df | de | v] [Wu^T | Wg^T | Au^T | Ag^T]^T
+            dX = torch.matmul(egv, lora_ext_rows([W_up, W_gate], [AuT, AgT], r, transpose=True).t())
+        else:  # hipBLASLt on the cached W^T: df Wu, + de Wg, + v [Au; Ag]
+            WuT, WgT = frozen_t(W_up), frozen_t(W_gate)
+            dX = torch.matmul(df, WuT.t())
+            dX.addmm_(de, WgT.t())
+            dX.addmm_(v, torch.cat([Au, Ag]))
     elif kt:
         WuT, WgT = frozen_t(W_up), frozen_t(W_gate)
-        dX = gemm(M, H, [(df, I, WuT, I, I), (de, I, WgT, I, I),
-                         (v[:, :r], 2 * r, AuT, r, r), (v[:, r:], 2 * r, AgT, r, r)], ROW, COL)
+        dX = gemm(M, H, [(df, lde, WuT, I, I), (de, lde, WgT, I, I),
+                         (v[:, :r], ld(v), AuT, r, r), (v[:, r:], ld(v), AgT, r, r)], ROW, COL)
     else:
-        dX = gemm(M, H, [(df, I, Wu, ld(Wu), I), (de, I, Wg, ld(Wg), I),
-                         (v[:, :r], 2 * r, Au, ld(Au), r), (v[:, r:], 2 * r, Ag, ld(Ag), r)], ROW, ROW)
+        dX = gemm(M, H, [(df, lde, Wu, ld(Wu), I), (de, lde, Wg, ld(Wg), I),
+                         (v[:, :r], ld(v), Au, ld(Au), r), (v[:, r:], ld(v), Ag, ld(Ag), r)], ROW, ROW)
     return (dX, dA_ug[r:], dBg, dA_ug[:r], dBu, dAd, dBd)
 
 

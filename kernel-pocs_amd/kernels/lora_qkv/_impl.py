@@ -32,7 +32,7 @@ import torch
 from forge_hip import _lib as L
 from kernels import _generic_lora as G
 from kernels._lora_ops import (BLAS_PLAIN, COL, ROW, as_operand, frozen_t, gemm, grad_at_b, grad_at_b_group, ld,
-                               lora_a, lora_ext_rows, pad_rank, small_t_batch, times_b)
+                               k_pad, lora_a, lora_ext_rows, lora_operand, pad_rank, small_t_batch, times_b)
 
 
 def _w(t):
@@ -85,7 +85,7 @@ def qkv_forward(X2, W_q, W_k, W_v, A_q, B_q, s_q, A_k, B_k, s_k, A_v, B_v, s_v,
         # LoRA-B products as extra K columns of a cached extended weight (one
         # rounding); RoPE then rotates the stored Q/K with a forge_rope pass
         ext = lora_ext_rows([W_q, W_k, W_v], [Bq, Bk, Bv], r)
-        torch.matmul(torch.cat([X2, xa], 1) if has_lora else X2, ext.t(), out=out)
+        torch.matmul(lora_operand(X2, xa) if has_lora else X2, ext.t(), out=out)
         if rope is not None:
             rope_qk_inplace(out, Hq, Hkv, rope)
     elif rope is not None and not rope_fusable(rope, Hq, Hkv):
@@ -203,11 +203,12 @@ def qkv_backward(dQ, dK, dV, X2, W_q, W_k, W_v, A_q, B_q, s_q, A_k, B_k, s_k, A_
         # hipBLASLt: [dQ | dK | dV | t] [Wq^T | Wk^T | Wv^T | Aq^T | Ak^T | Av^T]^T,
         # one GEMM on a cached extended weight (one rounding)
         W3 = Hq + 2 * Hkv
-        P = packed if packed is not None and packed.shape[1] == W3 + 3 * r else packed_grad_buffer(M, Hq, Hkv, r, dev)
+        P = packed if packed is not None and packed.shape[1] == k_pad(W3 + 3 * r) else \
+            packed_grad_buffer(M, Hq, Hkv, r, dev)
         for blk, (c0, c1) in ((dQ, (0, Hq)), (dK, (Hq, Hq + Hkv)), (dV, (Hq + Hkv, W3))):
             if blk.data_ptr() != P[:, c0:c1].data_ptr() or ld(blk) != ld(P):
                 P[:, c0:c1].copy_(blk)
-        P[:, W3:].copy_(t)
+        P[:, W3:W3 + 3 * r].copy_(t)
         dX = torch.matmul(P, lora_ext_rows([W_q, W_k, W_v], [AqT, AkT, AvT], r, transpose=True).t())
     elif kt:
         dX = gemm(M, K, [(dQ, ld(dQ), frozen_t(W_q), Hq, Hq), (dK, ld(dK), frozen_t(W_k), Hkv, Hkv),
@@ -222,9 +223,14 @@ def qkv_backward(dQ, dK, dV, X2, W_q, W_k, W_v, A_q, B_q, s_q, A_k, B_k, s_k, A_
 
 
 def packed_grad_buffer(M: int, Hq: int, Hkv: int, r: int, device) -> torch.Tensor:
-    """[M, Hq + 2 Hkv + 3 r] bf16 for the backward's hipBLASLt dX product:
-    [dQ | dK | dV | t] (t = the scaled dY B products)."""
-    return torch.empty(M, Hq + 2 * Hkv + 3 * r, dtype=torch.bfloat16, device=device)
+    """[M, k_pad(Hq + 2 Hkv + 3 r)] bf16 for the backward's hipBLASLt dX
+    product: [dQ | dK | dV | t | 0] (t = the scaled dY B products; the zero
+    columns meet the extended weight's)."""
+    W = Hq + 2 * Hkv + 3 * r
+    P = torch.empty(M, k_pad(W), dtype=torch.bfloat16, device=device)
+    if P.shape[1] > W:
+        P[:, W:].zero_()
+    return P
 
 
 def torch_qkv_forward(X, W_q, W_k, W_v, A_q, B_q, s_q, A_k, B_k, s_k, A_v, B_v, s_v):
