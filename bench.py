@@ -545,33 +545,28 @@ def _gpu_params_mlp(H, I, r, alpha, gen):
     return (W(I, H), A(H), B(I), s, W(I, H), A(H), B(I), s, W(H, I), A(I), B(H), s)
 
 
-def _down_bwd_roofline(args, M, H, I, r, Wd, act=None, traffic_key="lora_mlp_down_bwd"):
-    """(mean launch ms, roofline) of the LoRA-MLP step's largest launch, the
-    library's fused down-projection backward GEMM (forge_lora_mlp_down_bwd:
-    DW = dY Wd + td Ad on the cached Wd^T, then the in-place gated-activation
-    backward in the epilogue; SwiGLU unless act names another FORGE_ACT_*).
-    The step's other big products are hipBLASLt GEMMs of 0.6-0.65 ms each."""
+def _gate_up_roofline(args, M, H, I, r, Wg, Wu, traffic_key="lora_mlp_gate_up"):
+    """(label, mean launch ms, roofline) of the LoRA-MLP step's largest
+    launch: the hipBLASLt gate/up product [X | xa | 0] [Wg | Bg | 0; Wu | 0 |
+    Bu | 0]^T into the packed [e | g | v] buffer, as the step issues it (the
+    backward's dX product over [df | de | v] has the same FLOPs)."""
     import torch
-    from forge_hip import _lib as L
-    from kernels._lora_ops import COL, frozen_t
+    from kernels._lora_ops import k_pad, lora_ext_rows, lora_operand
 
     bf = torch.bfloat16
     g = torch.Generator(device="cuda").manual_seed(11)
-    dY = torch.randn(M, H, device="cuda", generator=g).to(bf)
-    WdT = frozen_t(Wd)
-    td = (torch.randn(M, r, device="cuda", generator=g) * 0.1).to(bf)
-    AdT = (torch.randn(I, r, device="cuda", generator=g) * 0.1).to(bf)
-    e = torch.randn(M, I, device="cuda", generator=g).to(bf)
-    gg = torch.randn(M, I, device="cuda", generator=g).to(bf)
-    hh = torch.empty_like(e)
-    st = L.stream_of(dY)
-    act = L.ACT_SILU if act is None else act
-    launch_ms = time_launches(lambda i: L.forge_lora_mlp_down_bwd(
-        M, H, I, r, dY.data_ptr(), H, WdT.data_ptr(), H, td.data_ptr(), r, AdT.data_ptr(), r, COL, hh.data_ptr(),
-        e.data_ptr(), gg.data_ptr(), I, act, st), max(args.steps, 10))
-    db_flops = 2 * M * H * I + 2 * M * r * I
-    return launch_ms, _roof("mfma", db_flops / (launch_ms * 1e-3) / 1e12, BF16_PEAK_TFLOPS, "TFLOP/s",
-                            _traffic(traffic_key))
+    X = torch.randn(M, H, device="cuda", generator=g).to(bf)
+    xa = (torch.randn(M, 2 * r, device="cuda", generator=g) * 0.1).to(bf)
+    Bg = (torch.randn(I, r, device="cuda", generator=g) * 0.01).to(bf)
+    Bu = (torch.randn(I, r, device="cuda", generator=g) * 0.01).to(bf)
+    xx = lora_operand(X, xa)
+    ext = lora_ext_rows([Wg, Wu], [Bg, Bu], r)
+    egv = torch.empty(M, k_pad(2 * I + 2 * r), dtype=bf, device="cuda")
+    launch_ms = time_launches(lambda i: torch.matmul(xx, ext.t(), out=egv[:, :2 * I]), max(args.steps, 10))
+    fl = 4 * M * H * I + 4 * M * r * I
+    label = f"hipBLASLt gate/up GEMM ([X | xa] [Wg | Bg; Wu | Bu]^T, {M} x {2 * I} x {xx.shape[1]})"
+    return label, launch_ms, _roof("mfma", fl / (launch_ms * 1e-3) / 1e12, BF16_PEAK_TFLOPS, "TFLOP/s",
+                                   _traffic(traffic_key))
 
 
 def bench_lora_mlp(args, activation="silu"):
@@ -602,17 +597,16 @@ def bench_lora_mlp(args, activation="silu"):
     ms, wall = run_steps(args, step)
     fl = flops(M, H, I, r)
     tf = rate(fl, ms, 1e12)
-    # roofline kernel: the step's largest launch, the fused down-projection backward GEMM
-    launch_ms, roof = _down_bwd_roofline(args, M, H, I, r, params[8].detach(),
-                                         act=L.ACT_GELU_TANH if geglu else L.ACT_SILU,
-                                         traffic_key="lora_mlp_geglu_down_bwd" if geglu else "lora_mlp_down_bwd")
+    # roofline kernel: the step's largest launch, the hipBLASLt gate/up product
+    label, launch_ms, roof = _gate_up_roofline(args, M, H, I, r, params[0].detach(), params[4].detach(),
+                                               traffic_key="lora_mlp_geglu_gate_up" if geglu else "lora_mlp_gate_up")
     res = {
         "config": {"workload": "lora_mlp_geglu_fwd_bwd" if geglu else "lora_mlp_fwd_bwd", "dtype": "bf16", "M": M,
                    "H": H, "I": I, "rank": r, "alpha": 32,
                    "api": "LoRAMLPGeGLU (tanh GELU)" if geglu else "LoRAMLPv6"},
         "value": tf, "unit": "TFLOP/s", "ms_per_step": rnd(ms, 4), "wall_ms_per_step": rnd(wall, 4),
         "frac_of_mfma_peak": rnd(tf and tf / BF16_PEAK_TFLOPS, 4), "algorithmic_flops_per_step": fl,
-        "launches_ms": {"forge_lora_mlp_down_bwd": round(launch_ms, 4)},
+        "launches_ms": {label: round(launch_ms, 4)},
         "roofline": roof,
         "dtype": "bf16",
     }
@@ -734,9 +728,9 @@ def bench_lora_patch(args, arch="llama"):
     ms_ref, _ = run_steps(args, stepper(ref))
     fl = flops(M, H, I, r)
     tf, tf_ref = rate(fl, ms, 1e12), rate(fl, ms_ref, 1e12)
-    wd = ref.down_proj.base_layer.weight.detach()
-    launch_ms, roof = _down_bwd_roofline(args, M, H, I, r, wd, act=L.ACT_GELU_TANH if gemma else L.ACT_SILU,
-                                         traffic_key="lora_patch_gemma_down_bwd" if gemma else "lora_mlp_down_bwd")
+    label, launch_ms, roof = _gate_up_roofline(args, M, H, I, r, ref.gate_proj.base_layer.weight.detach(),
+                                               ref.up_proj.base_layer.weight.detach(),
+                                               traffic_key="lora_patch_gemma_gate_up" if gemma else "lora_mlp_gate_up")
     return {
         "config": {"workload": "lora_mlp_patch_gemma2_fwd_bwd" if gemma else "lora_mlp_patch_fwd_bwd", "dtype": "bf16",
                    "M": M, "H": H, "I": I, "rank": r, "alpha": 32,
@@ -747,7 +741,7 @@ def bench_lora_patch(args, arch="llama"):
         "frac_of_mfma_peak": rnd(tf and tf / BF16_PEAK_TFLOPS, 4), "algorithmic_flops_per_step": fl,
         "reference_submodule_path": {"value": tf_ref, "unit": "TFLOP/s", "ms_per_step": rnd(ms_ref, 4)},
         "speedup_vs_submodule_path": rnd(ms and ms_ref / ms, 3),
-        "launches_ms": {"forge_lora_mlp_down_bwd": round(launch_ms, 4)},
+        "launches_ms": {label: round(launch_ms, 4)},
         "roofline": roof,
         "dtype": "bf16",
     }

@@ -381,6 +381,18 @@ int forge_lora_mlp_down_bwd(int64_t M, int64_t H, int64_t I, int64_t r,
 int forge_lora_mlp_glu_fwd(int64_t M, int64_t I, const void* e, const void* g, int64_t ld_eg, void* h,
                            int64_t ld_h, int activation, void* stream);
 
+/* The gated-activation backward of forge_lora_mlp_down_bwd on its own, for
+ * callers whose D = dY Wd + t Ad comes from a library GEMM as bf16 [M, I]
+ * (pitch ld_d): (D, e, g) -> h [M, I] (pitch ld_h), df over e and de over g
+ * (pitch ld_eg), with that entry point's per-element formulas.  Same layout
+ * contract as forge_lora_mlp_glu_fwd.  Replaces `_DWf_DW_dfg_kernel` after
+ * the reference's cuBLAS `matmul_lora(dY, W_down^T, ...)`
+ * (kernels/lora_mlp/experiments/v6/lora_mlp_kernel_v6.py:632-640,
+ * kernels/lora_mlp/reference/unsloth_baseline.py:34-55), or the GeGLU
+ * backward on the Gemma path (kernels/geglu/geglu.py:151-182). */
+int forge_lora_mlp_glu_bwd(int64_t M, int64_t I, const void* d, int64_t ld_d, void* e_df, void* g_de,
+                           int64_t ld_eg, void* h, int64_t ld_h, int activation, void* stream);
+
 /* LoRA-QKV forward with GQA-asymmetric widths and optional fused RoPE:
  *   out[:, 0:hq]          = X Wq^T + xa[:, 0:r]   Bq^T   (rotated if apply_rope)
  *   out[:, hq:hq+hkv]     = X Wk^T + xa[:, r:2r]  Bk^T   (rotated if apply_rope)

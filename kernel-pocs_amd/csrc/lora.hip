@@ -57,6 +57,34 @@ __global__ __launch_bounds__(kGluBlock) void lora_glu_fwd_kernel(const __bf16* e
   }
 }
 
+// The gated-activation backward of the down-projection epilogue as a kernel
+// of its own, for the path whose D = round(dY Wd + t Ad) comes from a library
+// GEMM as bf16: (D, e, g) -> (h, df, de), df and de over e and g, with the
+// epilogue's per-element formula (glu_bwd_vals; its rounding of D to bf16 is
+// exact on a bf16 input, so the results equal the fused epilogue's for equal D).
+template <int EPI>
+__global__ __launch_bounds__(kGluBlock) void lora_glu_bwd_kernel(const __bf16* d, int64_t ld_d, __bf16* e, __bf16* g,
+                                                                 int64_t ld_eg, __bf16* h, int64_t ld_h, int64_t rows,
+                                                                 int64_t cols) {
+  const int64_t cpr = cols / 8, n = rows * cpr;
+  for (int64_t i = (int64_t)blockIdx.x * kGluBlock + threadIdx.x; i < n; i += (int64_t)gridDim.x * kGluBlock) {
+    const int64_t r = i / cpr, c = (i - r * cpr) * 8;
+    const Vec16<__bf16> dv = load16(d + r * ld_d + c), ev = load16(e + r * ld_eg + c), gv = load16(g + r * ld_eg + c);
+    Vec16<__bf16> hv, dfv, dev;
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+      float hh, du, dg;
+      glu_bwd_vals<EPI>((float)dv.v[q], (float)ev.v[q], (float)gv.v[q], hh, du, dg);
+      hv.v[q] = (__bf16)hh;
+      dfv.v[q] = (__bf16)du;
+      dev.v[q] = (__bf16)dg;
+    }
+    store16(h + r * ld_h + c, hv);
+    store16(e + r * ld_eg + c, dfv);
+    store16(g + r * ld_eg + c, dev);
+  }
+}
+
 }  // namespace
 
 extern "C" int forge_lora_mlp_gate_up(int64_t M, int64_t H, int64_t I, int64_t r,
@@ -145,6 +173,35 @@ extern "C" int forge_lora_mlp_glu_fwd(int64_t M, int64_t I, const void* e, const
       lora_glu_fwd_kernel<EPI_GEGLU_ERF_FWD><<<grid, kGluBlock, 0, s>>>(ep, gp, ld_eg, hp, ld_h, M, I);
       break;
     default: return forge_set_error(FORGE_ERR_INVALID, "lora_mlp_glu_fwd: activation %d", activation);
+  }
+  FORGE_CHECK_LAUNCH();
+  return FORGE_OK;
+}
+
+extern "C" int forge_lora_mlp_glu_bwd(int64_t M, int64_t I, const void* d, int64_t ld_d, void* e_df, void* g_de,
+                                      int64_t ld_eg, void* h, int64_t ld_h, int activation, void* stream) {
+  if (M < 0 || I < 0) return forge_set_error(FORGE_ERR_INVALID, "lora_mlp_glu_bwd: shape");
+  if (M == 0 || I == 0) return FORGE_OK;
+  if (!d || !e_df || !g_de || !h) return forge_set_error(FORGE_ERR_INVALID, "lora_mlp_glu_bwd: null pointer");
+  if (I % 8 || ld_d % 8 || ld_eg % 8 || ld_h % 8 || ld_d < I || ld_eg < I || ld_h < I || !aligned16(d) ||
+      !aligned16(e_df) || !aligned16(g_de) || !aligned16(h))
+    return forge_set_error(FORGE_ERR_UNSUPPORTED,
+                           "lora_mlp_glu_bwd: I and the pitches must be multiples of 8, pointers 16-byte aligned");
+  const int grid = grid_for(M * (I / 8), kGluBlock, kGluMaxBlocks);
+  hipStream_t s = (hipStream_t)stream;
+  const __bf16* dp = (const __bf16*)d;
+  __bf16 *ep = (__bf16*)e_df, *gp = (__bf16*)g_de, *hp = (__bf16*)h;
+  switch (glu_epi(activation, true)) {
+    case EPI_SWIGLU_BWD:
+      lora_glu_bwd_kernel<EPI_SWIGLU_BWD><<<grid, kGluBlock, 0, s>>>(dp, ld_d, ep, gp, ld_eg, hp, ld_h, M, I);
+      break;
+    case EPI_GEGLU_TANH_BWD:
+      lora_glu_bwd_kernel<EPI_GEGLU_TANH_BWD><<<grid, kGluBlock, 0, s>>>(dp, ld_d, ep, gp, ld_eg, hp, ld_h, M, I);
+      break;
+    case EPI_GEGLU_ERF_BWD:
+      lora_glu_bwd_kernel<EPI_GEGLU_ERF_BWD><<<grid, kGluBlock, 0, s>>>(dp, ld_d, ep, gp, ld_eg, hp, ld_h, M, I);
+      break;
+    default: return forge_set_error(FORGE_ERR_INVALID, "lora_mlp_glu_bwd: activation %d", activation);
   }
   FORGE_CHECK_LAUNCH();
   return FORGE_OK;

@@ -203,13 +203,21 @@ def mlp_backward(dY2, X2, e, g, W_gate, A_gate, B_gate, s_gate, W_up, A_up, B_up
     td = times_b(dY2, ld(dY2), Bd, H, alpha=s_down, b_t=BdT)
     h = torch.empty(M, lde, dtype=torch.bfloat16, device=dev)[:, :I] if lde != I else \
         torch.empty(M, I, dtype=torch.bfloat16, device=dev)
-    WdB, AdB, wl = (frozen_t(W_down), AdT, COL) if kt else (Wd, Ad, ROW)
-    L.check(
-        L.forge_lora_mlp_down_bwd(M, H, I, r, dY2.data_ptr(), ld(dY2), WdB.data_ptr(), ld(WdB), td.data_ptr(), r,
-                                  AdB.data_ptr(), ld(AdB), wl, h.data_ptr(), e.data_ptr(), g.data_ptr(), lde, act,
-                                  L.stream_of(X2)),
-        "forge_lora_mlp_down_bwd",
-    )
+    if packed:
+        # hipBLASLt: D = [dY | td | 0] [Wd^T | Ad^T | 0]^T (one rounding), then
+        # the GLU backward as its own pass (the fused epilogue's formulas)
+        D = torch.matmul(lora_operand(dY2, td), lora_ext_rows([W_down], [AdT], r, transpose=True).t())
+        L.check(L.forge_lora_mlp_glu_bwd(M, I, D.data_ptr(), ld(D), e.data_ptr(), g.data_ptr(), lde, h.data_ptr(),
+                                         lde, act, L.stream_of(X2)), "forge_lora_mlp_glu_bwd")
+        del D
+    else:
+        WdB, AdB, wl = (frozen_t(W_down), AdT, COL) if kt else (Wd, Ad, ROW)
+        L.check(
+            L.forge_lora_mlp_down_bwd(M, H, I, r, dY2.data_ptr(), ld(dY2), WdB.data_ptr(), ld(WdB), td.data_ptr(),
+                                      r, AdB.data_ptr(), ld(AdB), wl, h.data_ptr(), e.data_ptr(), g.data_ptr(), lde,
+                                      act, L.stream_of(X2)),
+            "forge_lora_mlp_down_bwd",
+        )
     df, de = e, g
 
     # 3: down-projection LoRA grads

@@ -200,3 +200,42 @@ def test_lora_mlp_rank_not_multiple_of_8(r, version):
         if n != "dX":  # the LoRA gradients keep the caller's rank
             assert a.shape == b.shape, n
         _close_bf16(a.reshape(b.shape), b, n)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("act", ["silu", "gelu_tanh", "gelu_exact"])
+def test_glu_bwd_pass_equals_fused_down_bwd_epilogue(act):
+    """forge_lora_mlp_glu_bwd on D equals forge_lora_mlp_down_bwd's in-place
+    epilogue bit for bit when the GEMM's DW is exact: W_down = identity and
+    a zero LoRA term make DW = dY, so both see the same D."""
+    import torch
+    from forge_hip import _lib as L
+    from kernels.lora_mlp._impl import ACTIVATIONS
+
+    torch.manual_seed(5)
+    M, I, r = 1000, 512, 8
+    bf = torch.bfloat16
+    dY = torch.randn(M, I, device="cuda").to(bf)
+    eye = torch.eye(I, device="cuda", dtype=bf)
+    td = torch.zeros(M, r, device="cuda", dtype=bf)
+    AdT = torch.zeros(I, r, device="cuda", dtype=bf)
+    e0 = (torch.randn(M, I, device="cuda") * 2).to(bf)
+    g0 = torch.randn(M, I, device="cuda").to(bf)
+    code = ACTIVATIONS[act]
+    st = L.stream_of(dY)
+    e1, g1, h1 = e0.clone(), g0.clone(), torch.empty_like(e0)
+    L.check(L.forge_lora_mlp_down_bwd(M, I, I, r, dY.data_ptr(), I, eye.data_ptr(), I, td.data_ptr(), r,
+                                      AdT.data_ptr(), r, L.LAYOUT_COL, h1.data_ptr(), e1.data_ptr(), g1.data_ptr(), I,
+                                      code, st), "down_bwd")
+    # the standalone pass on a padded pitch, e and g side by side as the packed path stores them
+    P = 2 * I + 64
+    egv = torch.zeros(M, P, device="cuda", dtype=bf)
+    egv[:, :I], egv[:, I:2 * I] = e0, g0
+    h2 = torch.empty(M, P, device="cuda", dtype=bf)
+    L.check(L.forge_lora_mlp_glu_bwd(M, I, dY.data_ptr(), I, egv.data_ptr(), egv[:, I:].data_ptr(), P,
+                                     h2.data_ptr(), P, code, st), "glu_bwd")
+    torch.cuda.synchronize()
+    assert torch.equal(h2[:, :I], h1)
+    assert torch.equal(egv[:, :I], e1)
+    assert torch.equal(egv[:, I:2 * I], g1)
+    assert torch.count_nonzero(egv[:, 2 * I:]) == 0
