@@ -891,19 +891,21 @@ def bench_flce(args):
     ms, wall = run_steps(args, step)
     fl = flops(BT, H, V)
     tf = rate(fl, ms, 1e12)
-    # dominant kernel: the hipBLASLt GEMM that computes the logits of a
-    # 4096-token chunk (X_c W^T); dX_c = dlogits W is the same size
-    n = 4096
+    # dominant kernel: the hipBLASLt GEMM that computes the logits of one
+    # chunk (X_c W^T; at this shape the whole batch is one 2 GiB chunk);
+    # dX_c = dlogits W and dW are the same size
+    from kernels.cross_entropy.experiments.v2.fused_linear_cross_entropy import _chunk_rows
+    n = _chunk_rows(BT, V * 2)
     logits = torch.empty(n, V, device="cuda", dtype=bf)
     xc, wd = x.detach()[:n], W.detach()
     launch_ms = time_launches(lambda i: torch.matmul(xc, wd.t(), out=logits), max(args.steps, 10))
     res = {
         "config": {"workload": "fused_linear_cross_entropy_fwd_bwd", "dtype": "bf16", "tokens": BT, "hidden": H,
-                   "vocab": V, "ignored_rows": 410, "reduction": "mean", "chunk_tokens": 4096,
+                   "vocab": V, "ignored_rows": 410, "reduction": "mean", "chunk_tokens": n,
                    "api": "forge_fused_linear_cross_entropy"},
         "value": tf, "unit": "TFLOP/s", "ms_per_step": rnd(ms, 4), "wall_ms_per_step": rnd(wall, 4),
         "frac_of_mfma_peak": rnd(tf and tf / BF16_PEAK_TFLOPS, 4), "algorithmic_flops_per_step": fl,
-        "launches_ms": {"hipBLASLt logits GEMM (X_c W^T, 4096 x 128256 x 4096)": round(launch_ms, 4)},
+        "launches_ms": {f"hipBLASLt logits GEMM (X_c W^T, {n} x {V} x {H})": round(launch_ms, 4)},
         "roofline": _roof("mfma", 2 * n * H * V / (launch_ms * 1e-3) / 1e12, BF16_PEAK_TFLOPS, "TFLOP/s",
                           _traffic("flce_logits_gemm")),
         "dtype": "bf16",

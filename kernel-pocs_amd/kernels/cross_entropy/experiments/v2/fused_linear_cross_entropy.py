@@ -49,7 +49,7 @@ __all__ = [
     "forge_fused_linear_cross_entropy",
 ]
 
-_LOGITS_CHUNK_BYTES = 1 << 30
+_LOGITS_CHUNK_BYTES = 1 << 31
 
 
 def _chunk_rows(bt: int, row_bytes: int) -> int:
@@ -172,7 +172,13 @@ def fused_linear_cross_entropy_forward(
                   else torch.zeros_like(_input))
     want_w = input_requires_grad and weight.requires_grad
     want_b = input_requires_grad and bias is not None
-    gw32 = torch.empty(v_pad, H, dtype=torch.float32, device=dev) if want_w else None
+    # one bf16 chunk (the common case at 2 GiB of logits): dW is one library
+    # GEMM with bf16 output (fp32 accumulation inside, one rounding), so no
+    # fp32 accumulator and no final cast
+    dw_direct = (want_w and fast and BLAS_PLAIN and chunk >= BT and chunk % 8 == 0 and v_pad == V
+                 and dtype == torch.bfloat16 and weight.dtype == torch.bfloat16)
+    gw_out = torch.empty(V, H, dtype=weight.dtype, device=dev) if dw_direct else None
+    gw32 = torch.empty(v_pad, H, dtype=torch.float32, device=dev) if want_w and not dw_direct else None
     gb32 = torch.empty(1, V, dtype=torch.float32, device=dev) if want_b else None
 
     loss_1d = torch.zeros(BT, dtype=torch.float32, device=dev)
@@ -285,7 +291,9 @@ def fused_linear_cross_entropy_forward(
                             "forge_transpose_2b")
                     L.check(L.forge_transpose_2b(x_c.data_ptr(), ld(x_c), n, H, xT_buf.data_ptr(), chunk, st),
                             "forge_transpose_2b")
-                    if blas:  # fp32 accumulation across chunks (beta 0 ignores gw32 on the first)
+                    if dw_direct:
+                        torch.matmul(dlT_buf[:, :n], xT_buf[:, :n].t(), out=gw_out)
+                    elif blas:  # fp32 accumulation across chunks (beta 0 ignores gw32 on the first)
                         torch.addmm(gw32, dlT_buf[:, :n], xT_buf[:, :n].t(), out_dtype=torch.float32, beta=beta,
                                     out=gw32)
                     else:
@@ -312,7 +320,8 @@ def fused_linear_cross_entropy_forward(
         token_accuracy = torch.sum(token_accuracy_1d) / n_non_ignore if return_token_accuracy else None
     predicted_tokens = predicted_tokens_1d if return_predicted_tokens else None
 
-    grad_weight = _cast_into(gw32, torch.empty(V, H, dtype=weight.dtype, device=dev)) if want_w else None
+    grad_weight = gw_out if dw_direct else (
+        _cast_into(gw32, torch.empty(V, H, dtype=weight.dtype, device=dev)) if want_w else None)
     grad_bias = _cast_into(gb32, torch.empty(1, V, dtype=bias.dtype, device=dev)).view(V) if want_b else None
     return loss, z_loss, token_accuracy, predicted_tokens, grad_input, grad_weight, grad_bias
 
