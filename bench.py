@@ -545,28 +545,56 @@ def _gpu_params_mlp(H, I, r, alpha, gen):
     return (W(I, H), A(H), B(I), s, W(I, H), A(H), B(I), s, W(H, I), A(I), B(H), s)
 
 
-def _gate_up_roofline(args, M, H, I, r, Wg, Wu, traffic_key="lora_mlp_gate_up"):
-    """(label, mean launch ms, roofline) of the LoRA-MLP step's largest
-    launch: the hipBLASLt gate/up product [X | xa | 0] [Wg | Bg | 0; Wu | 0 |
-    Bu | 0]^T into the packed [e | g | v] buffer, as the step issues it (the
-    backward's dX product over [df | de | v] has the same FLOPs)."""
+def _hipblaslt_leg(args, M, N, K, flops_, seed=12):
+    """Comparison leg, not the product: hipBLASLt (torch.matmul) on a plain
+    bf16 product of the same FLOPs as the step's dominant library launch,
+    timed the same way (cold launches), so the library GEMM can be judged
+    against the vendor library on this box."""
     import torch
-    from kernels._lora_ops import k_pad, lora_ext_rows, lora_operand
 
     bf = torch.bfloat16
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    A = torch.randn(M, K, device="cuda", generator=g).to(bf)
+    B = (torch.randn(N, K, device="cuda", generator=g) * 0.02).to(bf)
+    C = torch.empty(M, N, device="cuda", dtype=bf)
+    ms = time_launches(lambda i: torch.matmul(A, B.t(), out=C), max(args.steps, 10))
+    del A, B, C
+    return {"what": f"hipBLASLt torch.matmul {M} x {N} x {K} (plain, no epilogue)", "ms": round(ms, 4),
+            "tflops": round(flops_ / (ms * 1e-3) / 1e12, 1)}
+
+
+def _gate_up_roofline(args, M, H, I, r, Wg, Wu, traffic_key="lora_mlp_gate_up", activation=None):
+    """(label, mean launch ms, roofline, hipBLASLt comparison) of the LoRA-MLP
+    step's largest launch: forge_lora_mlp_gate_up, the dual gate/up GEMM with
+    the LoRA-B products as K segments and the gated activation in its
+    epilogue (e, g, h stored), as the step issues it."""
+    import torch
+    from forge_hip import _lib as L
+
+    bf = torch.bfloat16
+    act = L.ACT_SILU if activation is None else activation
     g = torch.Generator(device="cuda").manual_seed(11)
     X = torch.randn(M, H, device="cuda", generator=g).to(bf)
     xa = (torch.randn(M, 2 * r, device="cuda", generator=g) * 0.1).to(bf)
     Bg = (torch.randn(I, r, device="cuda", generator=g) * 0.01).to(bf)
     Bu = (torch.randn(I, r, device="cuda", generator=g) * 0.01).to(bf)
-    xx = lora_operand(X, xa)
-    ext = lora_ext_rows([Wg, Wu], [Bg, Bu], r)
-    egv = torch.empty(M, k_pad(2 * I + 2 * r), dtype=bf, device="cuda")
-    launch_ms = time_launches(lambda i: torch.matmul(xx, ext.t(), out=egv[:, :2 * I]), max(args.steps, 10))
+    e = torch.empty(M, I, dtype=bf, device="cuda")
+    gg = torch.empty_like(e)
+    h = torch.empty_like(e)
+    st = L.stream_of(X)
+
+    def launch(i):
+        L.check(L.forge_lora_mlp_gate_up(M, H, I, r, X.data_ptr(), H, Wg.data_ptr(), Wu.data_ptr(), Wg.stride(0),
+                                         xa.data_ptr(), 2 * r, Bg.data_ptr(), Bu.data_ptr(), r, e.data_ptr(),
+                                         gg.data_ptr(), h.data_ptr(), I, act, st), "forge_lora_mlp_gate_up")
+
+    launch_ms = time_launches(launch, max(args.steps, 10))
+    del X, xa, e, gg, h
     fl = 4 * M * H * I + 4 * M * r * I
-    label = f"hipBLASLt gate/up GEMM ([X | xa] [Wg | Bg; Wu | Bu]^T, {M} x {2 * I} x {xx.shape[1]})"
+    label = f"forge_lora_mlp_gate_up (dual gate/up GEMM + GLU epilogue, {M} x {2 * I} x {H} + LoRA-B segments)"
+    cmp_ = _hipblaslt_leg(args, M, 2 * I, H, 4 * M * H * I)
     return label, launch_ms, _roof("mfma", fl / (launch_ms * 1e-3) / 1e12, BF16_PEAK_TFLOPS, "TFLOP/s",
-                                   _traffic(traffic_key))
+                                   _traffic(traffic_key)), cmp_
 
 
 def bench_lora_mlp(args, activation="silu"):
@@ -597,9 +625,11 @@ def bench_lora_mlp(args, activation="silu"):
     ms, wall = run_steps(args, step)
     fl = flops(M, H, I, r)
     tf = rate(fl, ms, 1e12)
-    # roofline kernel: the step's largest launch, the hipBLASLt gate/up product
-    label, launch_ms, roof = _gate_up_roofline(args, M, H, I, r, params[0].detach(), params[4].detach(),
-                                               traffic_key="lora_mlp_geglu_gate_up" if geglu else "lora_mlp_gate_up")
+    # roofline kernel: the step's largest launch, the fused gate/up GEMM
+    label, launch_ms, roof, cmp_ = _gate_up_roofline(
+        args, M, H, I, r, params[0].detach(), params[4].detach(),
+        traffic_key="lora_mlp_geglu_gate_up" if geglu else "lora_mlp_gate_up",
+        activation=L.ACT_GELU_TANH if geglu else L.ACT_SILU)
     res = {
         "config": {"workload": "lora_mlp_geglu_fwd_bwd" if geglu else "lora_mlp_fwd_bwd", "dtype": "bf16", "M": M,
                    "H": H, "I": I, "rank": r, "alpha": 32,
@@ -608,6 +638,7 @@ def bench_lora_mlp(args, activation="silu"):
         "frac_of_mfma_peak": rnd(tf and tf / BF16_PEAK_TFLOPS, 4), "algorithmic_flops_per_step": fl,
         "launches_ms": {label: round(launch_ms, 4)},
         "roofline": roof,
+        "comparison_hipblaslt": cmp_,
         "dtype": "bf16",
     }
     if not (args.no_cpu_baseline or args.only_launches):
@@ -728,9 +759,10 @@ def bench_lora_patch(args, arch="llama"):
     ms_ref, _ = run_steps(args, stepper(ref))
     fl = flops(M, H, I, r)
     tf, tf_ref = rate(fl, ms, 1e12), rate(fl, ms_ref, 1e12)
-    label, launch_ms, roof = _gate_up_roofline(args, M, H, I, r, ref.gate_proj.base_layer.weight.detach(),
-                                               ref.up_proj.base_layer.weight.detach(),
-                                               traffic_key="lora_patch_gemma_gate_up" if gemma else "lora_mlp_gate_up")
+    label, launch_ms, roof, cmp_ = _gate_up_roofline(
+        args, M, H, I, r, ref.gate_proj.base_layer.weight.detach(), ref.up_proj.base_layer.weight.detach(),
+        traffic_key="lora_patch_gemma_gate_up" if gemma else "lora_mlp_gate_up",
+        activation=L.ACT_GELU_TANH if gemma else L.ACT_SILU)
     return {
         "config": {"workload": "lora_mlp_patch_gemma2_fwd_bwd" if gemma else "lora_mlp_patch_fwd_bwd", "dtype": "bf16",
                    "M": M, "H": H, "I": I, "rank": r, "alpha": 32,
@@ -743,6 +775,7 @@ def bench_lora_patch(args, arch="llama"):
         "speedup_vs_submodule_path": rnd(ms and ms_ref / ms, 3),
         "launches_ms": {label: round(launch_ms, 4)},
         "roofline": roof,
+        "comparison_hipblaslt": cmp_,
         "dtype": "bf16",
     }
 
@@ -795,17 +828,19 @@ def bench_lora_qkv(args):
     ms, wall = run_steps(args, step)
     fl = T * flops_per_token(K, Hq, Hkv, r)
     tf = rate(fl, ms, 1e12)
-    # dominant kernel: the forward product, a hipBLASLt GEMM [X | xa] [W | B]^T
-    # (X [Wq;Wk;Wv]^T with the LoRA-B products as extra K columns); the
-    # backward's dX product is the other one of the same size
-    from kernels._lora_ops import lora_a, lora_ext_rows, lora_operand
+    # dominant kernel: the forward product, forge_lora_qkv_rope (X [Wq;Wk;Wv]^T
+    # with the LoRA-B products as K segments and RoPE on Q/K in the
+    # epilogue); the backward's dX product is the other one of its size
+    from kernels._lora_ops import lora_a
+    from kernels.lora_qkv._impl import qkv_gemm
 
     Xd = X.detach()
     xa = lora_a(Xd, [Aq.detach(), Ak.detach(), Av.detach()], [s, s, s])  # the forward's LoRA-A product
-    xx = lora_operand(Xd, xa)
-    ext = lora_ext_rows([Wq, Wk, Wv], [Bq.detach(), Bk.detach(), Bv.detach()], r)
     out = torch.empty(T, Hq + 2 * Hkv, device="cuda", dtype=bf)
-    launch_ms = time_launches(lambda i: torch.matmul(xx, ext.t(), out=out), max(args.steps, 10))
+    rope = {"cos": c, "sin": sn, "positions": pos, "head_dim": D}
+    launch_ms = time_launches(lambda i: qkv_gemm(Xd, Wq, Wk, Wv, xa, Bq.detach(), Bk.detach(), Bv.detach(), r,
+                                                 rope, out), max(args.steps, 10))
+    del out
     fwd_flops = 2 * T * K * (Hq + 2 * Hkv) + 2 * T * r * (Hq + 2 * Hkv)
     res = {
         "config": {"workload": "lora_qkv_rope_fwd_bwd", "dtype": "bf16", "tokens": T, "seq_lens": lens,
@@ -813,9 +848,11 @@ def bench_lora_qkv(args):
                    "rope_base": 500000},
         "value": tf, "unit": "TFLOP/s", "ms_per_step": rnd(ms, 4), "wall_ms_per_step": rnd(wall, 4),
         "frac_of_mfma_peak": rnd(tf and tf / BF16_PEAK_TFLOPS, 4), "algorithmic_flops_per_step": fl,
-        "launches_ms": {"hipBLASLt forward GEMM ([X | xa] [W | B]^T, 22954 x 6144 x 4288)": round(launch_ms, 4)},
+        "launches_ms": {f"forge_lora_qkv_rope (QKV GEMM + LoRA-B segments + RoPE epilogue, {T} x "
+                        f"{Hq + 2 * Hkv} x {K})": round(launch_ms, 4)},
         "roofline": _roof("mfma", fwd_flops / (launch_ms * 1e-3) / 1e12, BF16_PEAK_TFLOPS, "TFLOP/s",
                           _traffic("lora_qkv_fwd_gemm")),
+        "comparison_hipblaslt": _hipblaslt_leg(args, T, Hq + 2 * Hkv, K, 2 * T * K * (Hq + 2 * Hkv)),
         "dtype": "bf16",
     }
     if not (args.no_cpu_baseline or args.only_launches):
@@ -891,23 +928,26 @@ def bench_flce(args):
     ms, wall = run_steps(args, step)
     fl = flops(BT, H, V)
     tf = rate(fl, ms, 1e12)
-    # dominant kernel: the hipBLASLt GEMM that computes the logits of one
-    # chunk (X_c W^T; at this shape the whole batch is one 2 GiB chunk);
-    # dX_c = dlogits W and dW are the same size
+    # dominant kernel: the library GEMM that computes the logits of one chunk
+    # (X_c W^T; at this shape the whole batch is one 2 GiB chunk); dX_c =
+    # dlogits W and dW are the same size
+    from kernels._lora_ops import COL, ROW, gemm
     from kernels.cross_entropy.experiments.v2.fused_linear_cross_entropy import _chunk_rows
     n = _chunk_rows(BT, V * 2)
     logits = torch.empty(n, V, device="cuda", dtype=bf)
     xc, wd = x.detach()[:n], W.detach()
-    launch_ms = time_launches(lambda i: torch.matmul(xc, wd.t(), out=logits), max(args.steps, 10))
+    launch_ms = time_launches(lambda i: gemm(n, V, [(xc, H, wd, H, H)], ROW, COL, out=logits), max(args.steps, 10))
+    del logits
     res = {
         "config": {"workload": "fused_linear_cross_entropy_fwd_bwd", "dtype": "bf16", "tokens": BT, "hidden": H,
                    "vocab": V, "ignored_rows": 410, "reduction": "mean", "chunk_tokens": n,
                    "api": "forge_fused_linear_cross_entropy"},
         "value": tf, "unit": "TFLOP/s", "ms_per_step": rnd(ms, 4), "wall_ms_per_step": rnd(wall, 4),
         "frac_of_mfma_peak": rnd(tf and tf / BF16_PEAK_TFLOPS, 4), "algorithmic_flops_per_step": fl,
-        "launches_ms": {f"hipBLASLt logits GEMM (X_c W^T, {n} x {V} x {H})": round(launch_ms, 4)},
+        "launches_ms": {f"forge_gemm logits GEMM (X_c W^T, {n} x {V} x {H})": round(launch_ms, 4)},
         "roofline": _roof("mfma", 2 * n * H * V / (launch_ms * 1e-3) / 1e12, BF16_PEAK_TFLOPS, "TFLOP/s",
                           _traffic("flce_logits_gemm")),
+        "comparison_hipblaslt": _hipblaslt_leg(args, n, V, H, 2 * n * H * V),
         "dtype": "bf16",
     }
     if not (args.no_cpu_baseline or args.only_launches):

@@ -368,28 +368,15 @@ int forge_lora_mlp_down_bwd(int64_t M, int64_t H, int64_t I, int64_t r,
                             const void* a_down, int64_t ld_ad, int w_layout,
                             void* h_out, void* e_df, void* g_de, int64_t ld, int activation, void* stream);
 
-/* The gated activation of forge_lora_mlp_gate_up on its own, for callers
- * whose e and g (LoRA terms included) come from a library GEMM as bf16
- * [M, I] (pitch ld_eg): h = glu(e, g) [M, I] (pitch ld_h) with that entry
- * point's per-element formulas on the bf16 values.  I and the pitches
- * multiples of 8, pointers 16-byte aligned (else FORGE_ERR_UNSUPPORTED).
- * Replaces the activation stage of `_fused_lora_swiglu_kernel` after the
- * reference's cuBLAS gate/up GEMMs
- * (kernels/lora_mlp/experiments/v6/lora_mlp_kernel_v6.py:374-415,
- * experiments/v3/lora_mlp_kernel_v3.py:45-138), or geglu(gate, up) on the
- * Gemma path (kernels/geglu/geglu.py:126-148). */
-int forge_lora_mlp_glu_fwd(int64_t M, int64_t I, const void* e, const void* g, int64_t ld_eg, void* h,
-                           int64_t ld_h, int activation, void* stream);
-
-/* The gated-activation backward of forge_lora_mlp_down_bwd on its own, for
- * callers whose D = dY Wd + t Ad comes from a library GEMM as bf16 [M, I]
- * (pitch ld_d): (D, e, g) -> h [M, I] (pitch ld_h), df over e and de over g
- * (pitch ld_eg), with that entry point's per-element formulas.  Same layout
- * contract as forge_lora_mlp_glu_fwd.  Replaces `_DWf_DW_dfg_kernel` after
- * the reference's cuBLAS `matmul_lora(dY, W_down^T, ...)`
- * (kernels/lora_mlp/experiments/v6/lora_mlp_kernel_v6.py:632-640,
- * kernels/lora_mlp/reference/unsloth_baseline.py:34-55), or the GeGLU
- * backward on the Gemma path (kernels/geglu/geglu.py:151-182). */
+/* The gated-activation backward of forge_lora_mlp_down_bwd on its own:
+ * (D, e, g) -> h [M, I] (pitch ld_h), df over e and de over g (pitch ld_eg)
+ * for a bf16 D = dY Wd + t Ad [M, I] (pitch ld_d) that the caller computed,
+ * with that entry point's per-element formulas.  I and the pitches multiples
+ * of 8, pointers 16-byte aligned (else FORGE_ERR_UNSUPPORTED).  With
+ * FORGE_ACT_SILU it replaces Unsloth's in-place `_DWf_DW_dfg_kernel`
+ * (`swiglu_DWf_DW_dfg_kernel`, kernels/lora_mlp/reference/unsloth_baseline.py
+ * :118-168, called by experiments/v6/lora_mlp_kernel_v6.py:632-640); the
+ * GELU activations give the GeGLU backward (kernels/geglu/geglu.py:151-182). */
 int forge_lora_mlp_glu_bwd(int64_t M, int64_t I, const void* d, int64_t ld_d, void* e_df, void* g_de,
                            int64_t ld_eg, void* h, int64_t ld_h, int activation, void* stream);
 

@@ -2,12 +2,13 @@
 // and the fused LoRA entry points (LoRA-MLP gate/up + SwiGLU / GeGLU, LoRA-MLP
 // down-projection backward + SwiGLU / GeGLU backward, LoRA-QKV + RoPE).
 #include "gemm_core.h"
+#include "gemm_w4.h"
 
 namespace fgemm {
 
 // Tile configurations.
 enum Cfg {
-  CFG_BIG = 0,       // 256 x 256: 2 x 2 waves (128 x 128 per wave); 4 x 2 on the LDS-DMA path
+  CFG_BIG = 0,       // 256 x 256: 2 x 2 waves (128 x 128 per wave); 4 x 2 on the token-major LDS-DMA path
   CFG_SKINNY_N = 1,  // N <= 32-ish (rank-r outputs): 64 x 64 tiles (2 x 2 waves) for a K-contiguous
                      // A, else 256 x 32 (4 x 1 waves)
   CFG_SKINNY_M = 2,  // 32 x 256, 1 x 4 waves: M <= 32-ish (LoRA A gradients)
@@ -71,14 +72,13 @@ static int launch_cfg(GemmArgs a, hipStream_t s) {
   constexpr bool CAN_STAGE = staged_ok(BM, BN, WM, WN, EPI);
   const bool staged = CAN_STAGE && a.ep.vec_ok;
   if constexpr (BM == 256 && BN == 256 && AL == ROW && BL == COL) {
-    // both operands K-contiguous: the LDS-DMA engine (64-deep tiles, 2 stages),
-    // 8 waves so that two share each SIMD
-    constexpr int DWM = 4, DWN = 2;
-    constexpr bool DMA_STAGE = staged_ok(BM, BN, DWM, DWN, EPI);
-    if (DMA_STAGE && a.ep.vec_ok)
-      gemm_dma_kernel<BM, BN, DWM, DWN, BMODE, EPI, 64, 2, DMA_STAGE, 2><<<grid, DWM * DWN * 64, 0, s>>>(a);
+    // both operands K-contiguous: the 4-wave engine (128 x 128 per wave,
+    // accumulators in AGPRs, a ring of five LDS half-slots fed by LDS-DMA)
+    constexpr bool W4_STAGE = staged_ok(BM, BN, 2, 2, EPI);
+    if (W4_STAGE && a.ep.vec_ok)
+      gemm_w4_kernel<BMODE, EPI, W4_STAGE><<<grid, 256, 0, s>>>(a);
     else
-      gemm_dma_kernel<BM, BN, DWM, DWN, BMODE, EPI, 64, 2, false, 2><<<grid, DWM * DWN * 64, 0, s>>>(a);
+      gemm_w4_kernel<BMODE, EPI, false><<<grid, 256, 0, s>>>(a);
   } else if constexpr (BM == 64 && (BN == 64 || BN == 128 || BN == 256) && AL == ROW &&
                        (BL == COL || BL == ROW) && BMODE == B_SINGLE) {
     // narrow outputs (N <= 256: X A^T, dY B) with A K-contiguous: 64-row

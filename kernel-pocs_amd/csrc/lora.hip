@@ -35,33 +35,16 @@ int glu_epi(int activation, bool backward) {
   return -1;
 }
 
-// The gated activation of the gate/up epilogue as a kernel of its own, for
-// the path whose e = [X | xa] [Wg | Bg]^T and g come from a library GEMM
-// (hipBLASLt) as bf16 tensors: h = glu(e, g) with the epilogue's
-// per-element formula (glu_fwd_h), one 16-byte vector (8 elements) per
-// thread per step of a grid-stride loop.
 constexpr int kGluBlock = 256;
 constexpr int kGluMaxBlocks = 256 * 64;
 
-template <int EPI>
-__global__ __launch_bounds__(kGluBlock) void lora_glu_fwd_kernel(const __bf16* e, const __bf16* g, int64_t ld_eg,
-                                                                 __bf16* h, int64_t ld_h, int64_t rows, int64_t cols) {
-  const int64_t cpr = cols / 8, n = rows * cpr;
-  for (int64_t i = (int64_t)blockIdx.x * kGluBlock + threadIdx.x; i < n; i += (int64_t)gridDim.x * kGluBlock) {
-    const int64_t r = i / cpr, c = (i - r * cpr) * 8;
-    const Vec16<__bf16> ev = load16(e + r * ld_eg + c), gv = load16(g + r * ld_eg + c);
-    Vec16<__bf16> hv;
-#pragma unroll
-    for (int q = 0; q < 8; ++q) hv.v[q] = (__bf16)glu_fwd_h<EPI>((float)ev.v[q], (float)gv.v[q]);
-    store16(h + r * ld_h + c, hv);
-  }
-}
-
 // The gated-activation backward of the down-projection epilogue as a kernel
-// of its own, for the path whose D = round(dY Wd + t Ad) comes from a library
-// GEMM as bf16: (D, e, g) -> (h, df, de), df and de over e and g, with the
+// of its own: (D, e, g) -> (h, df, de), df and de over e and g, with the
 // epilogue's per-element formula (glu_bwd_vals; its rounding of D to bf16 is
-// exact on a bf16 input, so the results equal the fused epilogue's for equal D).
+// exact on a bf16 input, so the results equal the fused epilogue's for equal
+// D).  For SiLU this is Unsloth's in-place `_DWf_DW_dfg_kernel`
+// (kernels/lora_mlp/reference/unsloth_baseline.py:118-168) on a D that the
+// caller computed.
 template <int EPI>
 __global__ __launch_bounds__(kGluBlock) void lora_glu_bwd_kernel(const __bf16* d, int64_t ld_d, __bf16* e, __bf16* g,
                                                                  int64_t ld_eg, __bf16* h, int64_t ld_h, int64_t rows,
@@ -150,32 +133,6 @@ extern "C" int forge_lora_mlp_down_bwd(int64_t M, int64_t H, int64_t I, int64_t 
   a.ep.g = (__bf16*)g_de;
   a.ep.ld_eg = ld;
   return run(-1, ROW, w_layout, epi, a, (hipStream_t)stream);
-}
-
-extern "C" int forge_lora_mlp_glu_fwd(int64_t M, int64_t I, const void* e, const void* g, int64_t ld_eg, void* h,
-                                      int64_t ld_h, int activation, void* stream) {
-  if (M < 0 || I < 0) return forge_set_error(FORGE_ERR_INVALID, "lora_mlp_glu_fwd: shape");
-  if (M == 0 || I == 0) return FORGE_OK;
-  if (!e || !g || !h) return forge_set_error(FORGE_ERR_INVALID, "lora_mlp_glu_fwd: null pointer");
-  if (I % 8 || ld_eg % 8 || ld_h % 8 || ld_eg < I || ld_h < I || !aligned16(e) || !aligned16(g) || !aligned16(h))
-    return forge_set_error(FORGE_ERR_UNSUPPORTED,
-                           "lora_mlp_glu_fwd: I and the pitches must be multiples of 8, pointers 16-byte aligned");
-  const int grid = grid_for(M * (I / 8), kGluBlock, kGluMaxBlocks);
-  hipStream_t s = (hipStream_t)stream;
-  const __bf16 *ep = (const __bf16*)e, *gp = (const __bf16*)g;
-  __bf16* hp = (__bf16*)h;
-  switch (glu_epi(activation, false)) {
-    case EPI_SWIGLU_FWD: lora_glu_fwd_kernel<EPI_SWIGLU_FWD><<<grid, kGluBlock, 0, s>>>(ep, gp, ld_eg, hp, ld_h, M, I); break;
-    case EPI_GEGLU_TANH_FWD:
-      lora_glu_fwd_kernel<EPI_GEGLU_TANH_FWD><<<grid, kGluBlock, 0, s>>>(ep, gp, ld_eg, hp, ld_h, M, I);
-      break;
-    case EPI_GEGLU_ERF_FWD:
-      lora_glu_fwd_kernel<EPI_GEGLU_ERF_FWD><<<grid, kGluBlock, 0, s>>>(ep, gp, ld_eg, hp, ld_h, M, I);
-      break;
-    default: return forge_set_error(FORGE_ERR_INVALID, "lora_mlp_glu_fwd: activation %d", activation);
-  }
-  FORGE_CHECK_LAUNCH();
-  return FORGE_OK;
 }
 
 extern "C" int forge_lora_mlp_glu_bwd(int64_t M, int64_t I, const void* d, int64_t ld_d, void* e_df, void* g_de,

@@ -3,20 +3,21 @@
 Thin wrappers over the MFMA GEMM entry points of libforge_hip.so
 (csrc/gemm.hip, csrc/lora.hip).  Operands are bf16 with unit stride in the
 last dimension and 16-byte aligned rows; every wrapper checks that and calls
-the library on torch's current stream.
+the library on torch's current stream.  Every product, the plain base-weight
+ones included (which the reference sends to cuBLAS,
+kernels/lora_mlp/experiments/v6/lora_mlp_kernel_v6.py:374-443, 650-652), is
+the library's own gfx950 GEMM.
 
-Plain products of the base weights (no epilogue: W_down in the LoRA-MLP
-forward, dX in the backwards) go to hipBLASLt through torch.matmul, as the
-reference sends every big matmul to cuBLAS
-(kernels/lora_mlp/experiments/v6/lora_mlp_kernel_v6.py:5, 374-443, 650-652).
-On MI355X its stream-K 256 x 256 kernel runs these shapes 22-28% faster than
-the library's LDS-DMA GEMM (8192 x 4096 x 14336: 609 against 782 us cold,
-same box).  FORGE_PLAIN_GEMM=forge keeps them on libforge_hip's GEMM.
+Caches: frozen_t keeps one W^T per frozen base weight and frozen_cat one
+stacked copy per weight triple (the LoRA-QKV v4 save contract).  An entry is
+rebuilt when its weight is freed, modified through autograd-visible
+in-place ops (tensor._version) or given new storage (data_ptr).  Writes
+that bypass both (``w.data.copy_(...)``, ``w.data += delta``) are invisible
+to that check: call clear_caches() after them.
 """
 from __future__ import annotations
 
 import ctypes
-import os
 import weakref
 from typing import Optional, Sequence, Tuple
 
@@ -25,9 +26,6 @@ import torch
 from forge_hip import _lib as L
 
 ROW, COL = L.LAYOUT_ROW, L.LAYOUT_COL
-
-# plain base-weight products on hipBLASLt (torch.matmul) unless FORGE_PLAIN_GEMM=forge
-BLAS_PLAIN = os.environ.get("FORGE_PLAIN_GEMM", "hipblaslt") != "forge"
 
 
 def as_operand(t: torch.Tensor) -> torch.Tensor:
@@ -173,115 +171,6 @@ def lora_a(x: torch.Tensor, mats: Sequence[torch.Tensor], scales: Sequence[float
     return out
 
 
-_EXT_CACHE = {}
-
-
-def k_pad(k: int) -> int:
-    """K of a K-stacked library GEMM, rounded up to a multiple of 64 with
-    zero columns: hipBLASLt's stream-K kernel for K-contiguous bf16 operands
-    runs only at K % 64 == 0 (measured on MI355X, M = 8192, N = 4096: K =
-    14352 781 us, K = 14400 611 us)."""
-    return (k + 63) // 64 * 64
-
-
-def lora_operand(x: torch.Tensor, xa: torch.Tensor) -> torch.Tensor:
-    """[x | xa | 0] [M, k_pad(K + c)]: the A operand of a K-stacked product
-    (its zero columns meet the zero columns of lora_ext_weight / lora_ext_rows)."""
-    M, K = x.shape
-    c = xa.shape[1]
-    out = torch.empty(M, k_pad(K + c), dtype=x.dtype, device=x.device)
-    out[:, :K].copy_(x)
-    out[:, K:K + c].copy_(xa)
-    if out.shape[1] > K + c:
-        out[:, K + c:].zero_()
-    return out
-
-
-def lora_ext_weight(w: torch.Tensor, b: torch.Tensor, slot: int, n_slots: int) -> torch.Tensor:
-    """[W | B_0 | .. | B_{n-1} | 0] [N, k_pad(K + n r)] for a library GEMM that takes a
-    LoRA product as extra K columns ([X | xa] @ ext^T = X W^T + xa_slot B^T
-    with xa = [xa_0 | .. | xa_{n-1}]): block `slot` holds b (bf16 [N, r]), the
-    others zero.  W is copied once per frozen weight (kept, like frozen_t,
-    until the weight is freed, changed in place or given new storage); b is
-    written into its block on every call, since it trains."""
-    N, K = w.shape
-    r = b.shape[1]
-    key = (id(w), slot, n_slots, r)
-    ent = _EXT_CACHE.get(key)
-    ext = None
-    if ent is not None:
-        ref, ver, ptr, cached = ent
-        if ref() is w and ver == w._version and ptr == w.data_ptr():
-            ext = cached
-    if ext is None:
-        ext = torch.zeros(N, k_pad(K + n_slots * r), dtype=w.dtype, device=w.device)
-        ext[:, :K].copy_(w.detach())
-
-        def _drop(_ref, key=key):
-            _EXT_CACHE.pop(key, None)
-
-        _EXT_CACHE[key] = (weakref.ref(w, _drop), w._version, w.data_ptr(), ext)
-    ext[:, K + slot * r:K + (slot + 1) * r].copy_(b.detach())
-    return ext
-
-
-def lora_ext_rows(ws: Sequence[torch.Tensor], bs: Sequence[Optional[torch.Tensor]], r: int,
-                  transpose: bool = False) -> torch.Tensor:
-    """Row blocks [W_i | 0 .. b_i .. 0] stacked: [sum N_i, K + n r] with b_i
-    (bf16 [N_i, r]) in column block i after K, for one library GEMM over
-    [X | x_0 | .. | x_{n-1}] that gives every projection its own rank-r
-    term (LoRA-QKV: [X | xa] ext^T = [X Wq^T + xa_q Bq^T | ..]).  With
-    transpose the base blocks are W_i^T (w_i [K_i, N] stacked along K:
-    ext = [W_0^T | .. | W_{n-1}^T | b_0 | .. ] [N, sum K_i + n r], for
-    [dY_0 | .. | dY_{n-1} | t] ext^T = sum dY_i W_i + t [b ..]^T).  The base
-    blocks are copied once per set of frozen weights (as frozen_t); the b
-    blocks are written on every call (they train).  With r > 0 zero columns
-    pad the width to k_pad(..); r = 0: the bare stack."""
-    key = ("rows", tuple(id(w) for w in ws), r, transpose)
-    ent = _EXT_CACHE.get(key)
-    ext = None
-    if ent is not None:
-        refs, vers, ptrs, cached = ent
-        if all(rf() is w and v == w._version and p == w.data_ptr() for rf, v, p, w in zip(refs, vers, ptrs, ws)):
-            ext = cached
-    n = len(ws)
-    if transpose:
-        N, Ks = ws[0].shape[1], [w.shape[0] for w in ws]
-        base = sum(Ks)
-    else:
-        Ns, K = [w.shape[0] for w in ws], ws[0].shape[1]
-        base = K
-    if ext is None:
-        if transpose:
-            ext = torch.zeros(N, k_pad(base + n * r) if r else base, dtype=ws[0].dtype, device=ws[0].device)
-            k0 = 0
-            for w, k in zip(ws, Ks):
-                ext[:, k0:k0 + k].copy_(w.detach().t())
-                k0 += k
-        else:
-            ext = torch.zeros(sum(Ns), k_pad(base + n * r) if r else base, dtype=ws[0].dtype, device=ws[0].device)
-            n0 = 0
-            for w, nn in zip(ws, Ns):
-                ext[n0:n0 + nn, :K].copy_(w.detach())
-                n0 += nn
-
-        def _drop(_ref, key=key):
-            _EXT_CACHE.pop(key, None)
-
-        _EXT_CACHE[key] = ([weakref.ref(w, _drop) for w in ws], [w._version for w in ws], [w.data_ptr() for w in ws],
-                           ext)
-    if r:
-        if transpose:
-            for i, b in enumerate(bs):  # b_i [N, r]
-                ext[:, base + i * r:base + (i + 1) * r].copy_(b.detach())
-        else:
-            n0 = 0
-            for i, (w, b) in enumerate(zip(ws, bs)):
-                ext[n0:n0 + w.shape[0], base + i * r:base + (i + 1) * r].copy_(b.detach())
-                n0 += w.shape[0]
-    return ext
-
-
 _T_CACHE = {}
 
 
@@ -318,6 +207,15 @@ def frozen_t(w: torch.Tensor, pitch_multiple: int = 1) -> torch.Tensor:
 
 
 _CAT_CACHE = {}
+
+
+def clear_caches() -> None:
+    """Drops every cached W^T (frozen_t) and stacked weight copy
+    (frozen_cat).  Needed after a write to a frozen base weight that
+    autograd does not see (through ``.data``: checkpoint loads, PEFT-style
+    merges); the next call rebuilds the copies from the current weights."""
+    _T_CACHE.clear()
+    _CAT_CACHE.clear()
 
 
 def frozen_cat(ws: Sequence[torch.Tensor]) -> torch.Tensor:

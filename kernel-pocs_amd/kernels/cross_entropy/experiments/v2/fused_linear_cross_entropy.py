@@ -12,7 +12,7 @@ target)` without materialising the whole [BT, V] logits at once.
 
 Per token chunk (all device work in libforge_hip.so):
   1. logits = X_c W^T (+ b)
-       bf16 with H % 8 == 0: the MFMA GEMM (LDS-DMA engine); the bias is one
+       bf16 with H % 8 == 0: the MFMA GEMM (4-wave engine); the bias is one
        more 8-wide K segment ([X_c | 1] [W | b]^T), so it is added to the fp32
        accumulator.  Otherwise forge_gemm_generic (fp32 accumulation, any
        dtype / shape).
@@ -23,12 +23,16 @@ Per token chunk (all device work in libforge_hip.so):
   4. dX_c = dlogits W (MFMA on a cached, row-padded W^T, or generic),
      dW += dlogits^T X_c (fp32, beta accumulation over chunks; on the MFMA
      path both operands are first transposed by forge_transpose_2b so the
-     product is K-contiguous for the LDS-DMA GEMM), db += colsum(dlogits)
-     (generic GEMM with a ones row)
-Chunks are sized to ~1 GiB of logits (MI355X has 288 GB of HBM): the
+     product is K-contiguous for the 4-wave GEMM; a batch that is one chunk
+     writes bf16 dW straight from the fp32 accumulators, one rounding),
+     db += colsum(dlogits) (generic GEMM with a ones row)
+Chunks are sized to ~2 GiB of logits (MI355X has 288 GB of HBM): the
 reference's ~V/H-fold split (256-token chunks at the Llama-3 shape) would
 re-read and re-write the fp32 weight gradient 32 times.  Chunking changes
-only the fp32 summation order of dW and db.
+only the fp32 summation order of dW and db.  Every product is the
+library's own GEMM (the reference's three torch matmuls per chunk,
+kernels/cross_entropy/experiments/v2/fused_linear_cross_entropy.py:142,
+212-214).
 """
 from __future__ import annotations
 
@@ -37,7 +41,7 @@ from typing import Optional
 import torch
 
 from forge_hip import _lib as L
-from kernels._lora_ops import BLAS_PLAIN, COL, ROW, frozen_t, gemm, ld
+from kernels._lora_ops import COL, ROW, frozen_t, gemm, ld
 
 from .cross_entropy_kernel_v2 import CrossEntropyOutput, _check_targets, _sum_f32, _target_stats_async
 
@@ -172,10 +176,10 @@ def fused_linear_cross_entropy_forward(
                   else torch.zeros_like(_input))
     want_w = input_requires_grad and weight.requires_grad
     want_b = input_requires_grad and bias is not None
-    # one bf16 chunk (the common case at 2 GiB of logits): dW is one library
-    # GEMM with bf16 output (fp32 accumulation inside, one rounding), so no
-    # fp32 accumulator and no final cast
-    dw_direct = (want_w and fast and BLAS_PLAIN and chunk >= BT and chunk % 8 == 0 and v_pad == V
+    # one bf16 chunk (the common case at 2 GiB of logits): dW is one GEMM
+    # with bf16 output (fp32 accumulation inside, one rounding), so no fp32
+    # accumulator and no final cast
+    dw_direct = (want_w and fast and chunk >= BT and chunk % 8 == 0 and v_pad == V
                  and dtype == torch.bfloat16 and weight.dtype == torch.bfloat16)
     gw_out = torch.empty(V, H, dtype=weight.dtype, device=dev) if dw_direct else None
     gw32 = torch.empty(v_pad, H, dtype=torch.float32, device=dev) if want_w and not dw_direct else None
@@ -217,12 +221,8 @@ def fused_linear_cross_entropy_forward(
                 bias8[:, 0] = b
         # dW = dlogits^T X_c reduces over tokens; with both operands
         # transposed (one HBM pass each) it is a K-contiguous product for the
-        # LDS-DMA GEMM instead of a transposing register-path GEMM
+        # 4-wave GEMM instead of a transposing token-major GEMM
         dw_nt = fast and want_w and chunk % 8 == 0
-        # the three products on hipBLASLt, as the reference's torch matmuls
-        # (kernels/cross_entropy/experiments/v2/fused_linear_cross_entropy.py:142,
-        # 212-214), when the vocabulary needs no column padding
-        blas = fast and BLAS_PLAIN and v_pad == V and dtype == torch.bfloat16
         if dw_nt:
             dlT_buf = torch.empty(v_pad, chunk, dtype=dtype, device=dev)
             xT_buf = torch.empty(H, chunk, dtype=dtype, device=dev)
@@ -236,12 +236,7 @@ def fused_linear_cross_entropy_forward(
             t_c = target[c0:c0 + n]
             logits = logits_buf[:n]
 
-            if blas:  # hipBLASLt (torch.matmul / addmm): the bias rides in its epilogue
-                if b is None:
-                    torch.matmul(x_c, w.t(), out=logits)
-                else:
-                    torch.addmm(b, x_c, w.t(), out=logits)
-            elif fast:
+            if fast:
                 segs = [(x_c, ld(x_c), w, ld(w), H)]
                 if b is not None:
                     segs.append((ones8[:n], 8, bias8, 8, 8))
@@ -282,20 +277,14 @@ def fused_linear_cross_entropy_forward(
             beta = 0.0 if c0 == 0 else 1.0
             gi = grad_input[c0:c0 + n]
             if fast:
-                if blas:
-                    torch.matmul(logits, wt.t(), out=gi)
-                else:
-                    gemm(n, H, [(logits, v_pad, wt, v_pad, v_pad)], ROW, COL, out=gi)
+                gemm(n, H, [(logits, v_pad, wt, v_pad, v_pad)], ROW, COL, out=gi)
                 if dw_nt and n % 8 == 0:
                     L.check(L.forge_transpose_2b(logits.data_ptr(), v_pad, n, v_pad, dlT_buf.data_ptr(), chunk, st),
                             "forge_transpose_2b")
                     L.check(L.forge_transpose_2b(x_c.data_ptr(), ld(x_c), n, H, xT_buf.data_ptr(), chunk, st),
                             "forge_transpose_2b")
                     if dw_direct:
-                        torch.matmul(dlT_buf[:, :n], xT_buf[:, :n].t(), out=gw_out)
-                    elif blas:  # fp32 accumulation across chunks (beta 0 ignores gw32 on the first)
-                        torch.addmm(gw32, dlT_buf[:, :n], xT_buf[:, :n].t(), out_dtype=torch.float32, beta=beta,
-                                    out=gw32)
+                        gemm(V, H, [(dlT_buf, chunk, xT_buf, chunk, n)], ROW, COL, out=gw_out)
                     else:
                         gemm(v_pad, H, [(dlT_buf, chunk, xT_buf, chunk, n)], ROW, COL, out=gw32, beta=beta,
                              out_dtype=torch.float32)

@@ -3,17 +3,15 @@
 Forward  (reference v6 `_v6_forward_impl`,
 kernels/lora_mlp/experiments/v6/lora_mlp_kernel_v6.py:335-451):
   1. xa   = [sg X Ag^T | su X Au^T]                  forge_lora_a       [M, 2r]
-  2. e = [X | xa] [Wg | Bg | 0]^T, g = [X | xa] [Wu | 0 | Bu]^T
-                                                     hipBLASLt (torch.matmul; the
-     LoRA-B products ride along as extra K columns of cached extended weights,
-     one rounding), then h = glu(e, g)               forge_lora_mlp_glu_fwd
+  2. e = X Wg^T + xa_g Bg^T, g = X Wu^T + xa_u Bu^T, h = glu(e, g)
+                                                     forge_lora_mlp_gate_up: one
+     MFMA GEMM over the dual gate/up B with the LoRA-B products as K segments
+     (one rounding) and the gated activation in its epilogue (h forms in
+     registers; e, g are stored for the backward)
   3. xd   = sd h Ad^T                                forge_lora_a       [M, r]
-  4. out  = h Wd^T + xd Bd^T                         hipBLASLt GEMM + rank-r addmm
-  (the reference sends these products to cuBLAS, lora_mlp_kernel_v6.py:374-443.
-   With FORGE_PLAIN_GEMM=forge, steps 2 and 4 are the library's MFMA GEMMs
-   instead: forge_lora_mlp_gate_up, one GEMM with the LoRA-B K segments and the
-   GLU epilogue that forms h in registers, and forge_gemm with xd Bd^T as a K
-   segment.)
+  4. out  = h Wd^T + xd Bd^T                         forge_gemm, xd Bd^T a K segment
+  (the reference sends the base products to cuBLAS, lora_mlp_kernel_v6.py:374-443;
+   here every product is the library's own gfx950 GEMM.)
 
 Backward (reference `LoRAMLPv6.backward`, :592-672, Unsloth-style in place;
 math of kernels/lora_mlp/reference/lora_mlp_pytorch.py:145-225):
@@ -23,8 +21,8 @@ math of kernels/lora_mlp/reference/lora_mlp_pytorch.py:145-225):
   3. dAd = td^T h,  dBd = sd dY^T (h Ad^T)           split-K forge_gemm
   4. vu = su df Bu, vg = sg de Bg                    forge_gemm         [M, r]
      dAu = vu^T X, dAg = vg^T X, dBu = su df^T (X Au^T), dBg = sg de^T (X Ag^T)
-  5. dX = df Wu + de Wg + vu Au + vg Ag              hipBLASLt on the cached W^T, then
-     + de Wg and + [vu | vg] [Au; Ag] as addmm      (or forge_gemm with 4 K segments)
+  5. dX = df Wu + de Wg + vu Au + vg Ag              forge_gemm, 4 K segments over the
+                                                     cached W^T and the small A^T
 The saved e/g buffers are overwritten by df/de in step 2 (the reference's
 in-place contract: backward is not re-entrant).
 
@@ -45,9 +43,8 @@ import torch.nn.functional as F
 
 from forge_hip import _lib as L
 from kernels import _generic_lora as G
-from kernels._lora_ops import (BLAS_PLAIN, COL, ROW, as_operand, frozen_t, gemm, grad_at_b, grad_at_b_group, ld,
-                               k_pad, lora_a, lora_ext_rows, lora_ext_weight, lora_operand, pad_rank, small_t_batch,
-                               times_b)
+from kernels._lora_ops import (COL, ROW, as_operand, frozen_t, gemm, grad_at_b, grad_at_b_group, ld, lora_a,
+                               pad_rank, small_t_batch, times_b)
 
 
 def _w(t):
@@ -90,65 +87,24 @@ def mlp_forward(X2, W_gate, A_gate, B_gate, s_gate, W_up, A_up, B_up, s_up,
     if has_lora:  # the first launch; the gate/up GEMM needs its result
         xa = lora_a(X2, [A_gate, A_up], [s_gate, s_up])
         Bg, Bu = _w(B_gate), _w(B_up)
-    # hipBLASLt path with LoRA: e, g and spare columns side by side in one
-    # [M, k_pad(2I + 2r)] buffer ([e | g | v | 0]): the gate/up products are
-    # one library GEMM, and the backward's dX one GEMM over [df | de | v | 0]
-    # (df, de overwrite e, g; v = [su df Bu | sg de Bg]).  h gets spare
-    # columns for xd = sd h Ad^T, so the down projection is one GEMM too.
-    # The zero columns keep K a multiple of 64 (k_pad).
-    packed = BLAS_PLAIN and has_lora
-    if packed:
-        egv = torch.empty(M, k_pad(2 * I + 2 * r), dtype=torch.bfloat16, device=dev)
-        if egv.shape[1] > 2 * I + 2 * r:
-            egv[:, 2 * I + 2 * r:].zero_()
-        e, g = egv[:, :I], egv[:, I:2 * I]
-        hx = torch.empty(M, k_pad(I + r), dtype=torch.bfloat16, device=dev)
-        if hx.shape[1] > I + r:
-            hx[:, I + r:].zero_()
-        h = hx[:, :I]
-    else:
-        e = torch.empty(M, I, dtype=torch.bfloat16, device=dev)
-        g = torch.empty(M, I, dtype=torch.bfloat16, device=dev)
-        h = torch.empty(M, I, dtype=torch.bfloat16, device=dev)
+    e = torch.empty(M, I, dtype=torch.bfloat16, device=dev)
+    g = torch.empty(M, I, dtype=torch.bfloat16, device=dev)
+    h = torch.empty(M, I, dtype=torch.bfloat16, device=dev)
     st = L.stream_of(X2)
-    if BLAS_PLAIN:
-        # hipBLASLt: [e | g] = [X | xa] [Wg | Bg | 0; Wu | 0 | Bu]^T, the LoRA-B
-        # products as extra K columns (one rounding, as the fused GEMM);
-        # forge_lora_mlp_glu_fwd then forms h from the bf16 e, g
-        if packed:
-            torch.matmul(lora_operand(X2, xa), lora_ext_rows([W_gate, W_up], [Bg, Bu], r).t(),
-                         out=egv[:, :2 * I])
-        else:
-            torch.matmul(X2, Wg.t(), out=e)
-            torch.matmul(X2, Wu.t(), out=g)
-        L.check(L.forge_lora_mlp_glu_fwd(M, I, e.data_ptr(), g.data_ptr(), ld(e), h.data_ptr(), ld(h), act, st),
-                "forge_lora_mlp_glu_fwd")
-    else:
-        L.check(
-            L.forge_lora_mlp_gate_up(
-                M, H, I, r, X2.data_ptr(), ld(X2), Wg.data_ptr(), Wu.data_ptr(), ld(Wg),
-                L.ptr(xa), 2 * r, L.ptr(Bg), L.ptr(Bu), r, e.data_ptr(), g.data_ptr(), h.data_ptr(), I, act, st),
-            "forge_lora_mlp_gate_up",
-        )
+    L.check(
+        L.forge_lora_mlp_gate_up(
+            M, H, I, r, X2.data_ptr(), ld(X2), Wg.data_ptr(), Wu.data_ptr(), ld(Wg),
+            L.ptr(xa), 2 * r, L.ptr(Bg), L.ptr(Bu), r, e.data_ptr(), g.data_ptr(), h.data_ptr(), I, act, st),
+        "forge_lora_mlp_gate_up",
+    )
     segs = [(h, ld(h), Wd, ld(Wd), I)]
-    Bd = None
     if has_lora and A_down is not None and B_down is not None:
-        xd = lora_a(h, [A_down], [s_down], out=hx[:, I:I + r] if packed else None)
+        xd = lora_a(h, [A_down], [s_down])
         Bd = _w(B_down)
         segs.append((xd, ld(xd), Bd, ld(Bd), r))
         if aux is not None:
-            # a compact copy, so the backward does not keep the [M, I + r] buffer alive
-            aux["xa"], aux["xd"] = xa, (xd.contiguous() if packed else xd)
-    # a plain product: hipBLASLt over [h | xd] [Wd | Bd]^T (xd Bd^T as extra K
-    # columns), or the library's GEMM with xd Bd^T as a K segment
-    if not BLAS_PLAIN:
-        out = gemm(M, Wd.shape[0], segs, ROW, COL)
-    elif packed and Bd is not None:
-        out = torch.matmul(hx, lora_ext_weight(W_down, Bd, 0, 1).t())
-    else:
-        out = torch.matmul(h, Wd.t())
-        if Bd is not None:
-            out.addmm_(xd, Bd.t())
+            aux["xa"], aux["xd"] = xa, xd
+    out = gemm(M, Wd.shape[0], segs, ROW, COL)
     if not save_eg:
         e = g = None
     return out, e, g
@@ -183,41 +139,29 @@ def mlp_backward(dY2, X2, e, g, W_gate, A_gate, B_gate, s_gate, W_up, A_up, B_up
     dev = X2.device
     Ag, Bg, Au, Bu, Ad, Bd = (_w(t) for t in (A_gate, B_gate, A_up, B_up, A_down, B_down))
 
-    # K-contiguous weights (cached W^T, small A^T) put the three big GEMMs of
-    # the backward on the LDS-DMA engine; a rank that is not a multiple of 8
-    # keeps the [K][N] layout.  The six small transposes (B^T for the dY B
-    # products, A^T for the LoRA segments) are one launch.
-    kt = r % 8 == 0
-    BdT = BuT = BgT = None
-    if kt:
-        BdT, AdT, BuT, BgT, AuT, AgT = small_t_batch([Bd, Ad, Bu, Bg, Au, Ag])
+    # K-contiguous weights (cached W^T, small A^T: the rank is a multiple of
+    # 8 here) put the three big GEMMs of the backward on the 4-wave engine.
+    # The six small transposes (B^T for the dY B products, A^T for the LoRA
+    # segments) are one launch.
+    BdT, AdT, BuT, BgT, AuT, AgT = small_t_batch([Bd, Ad, Bu, Bg, Au, Ag])
 
-    # e, g as the forward left them: pitch I, or [e | g | spare 2r] (one buffer)
-    lde = e.stride(0) if M > 1 else I
-    if M > 1 and g.stride(0) != lde:  # h, e, g share one pitch
+    # h, e, g share one pitch
+    e, g = as_operand(e), as_operand(g)
+    lde = ld(e)
+    if ld(g) != lde:
         e, g, lde = e.contiguous(), g.contiguous(), I
-    packed = kt and BLAS_PLAIN and M > 1 and lde == k_pad(2 * I + 2 * r) and g.data_ptr() - e.data_ptr() == 2 * I
 
     # 1-2: DW = dY Wd + sd (dY Bd) Ad with the GLU backward fused in place
-    # (h, e, g share one pitch)
     td = times_b(dY2, ld(dY2), Bd, H, alpha=s_down, b_t=BdT)
     h = torch.empty(M, lde, dtype=torch.bfloat16, device=dev)[:, :I] if lde != I else \
         torch.empty(M, I, dtype=torch.bfloat16, device=dev)
-    if packed:
-        # hipBLASLt: D = [dY | td | 0] [Wd^T | Ad^T | 0]^T (one rounding), then
-        # the GLU backward as its own pass (the fused epilogue's formulas)
-        D = torch.matmul(lora_operand(dY2, td), lora_ext_rows([W_down], [AdT], r, transpose=True).t())
-        L.check(L.forge_lora_mlp_glu_bwd(M, I, D.data_ptr(), ld(D), e.data_ptr(), g.data_ptr(), lde, h.data_ptr(),
-                                         lde, act, L.stream_of(X2)), "forge_lora_mlp_glu_bwd")
-        del D
-    else:
-        WdB, AdB, wl = (frozen_t(W_down), AdT, COL) if kt else (Wd, Ad, ROW)
-        L.check(
-            L.forge_lora_mlp_down_bwd(M, H, I, r, dY2.data_ptr(), ld(dY2), WdB.data_ptr(), ld(WdB), td.data_ptr(),
-                                      r, AdB.data_ptr(), ld(AdB), wl, h.data_ptr(), e.data_ptr(), g.data_ptr(), lde,
-                                      act, L.stream_of(X2)),
-            "forge_lora_mlp_down_bwd",
-        )
+    WdT = frozen_t(W_down)
+    L.check(
+        L.forge_lora_mlp_down_bwd(M, H, I, r, dY2.data_ptr(), ld(dY2), WdT.data_ptr(), ld(WdT), td.data_ptr(),
+                                  r, AdT.data_ptr(), ld(AdT), COL, h.data_ptr(), e.data_ptr(), g.data_ptr(), lde,
+                                  act, L.stream_of(X2)),
+        "forge_lora_mlp_down_bwd",
+    )
     df, de = e, g
 
     # 3: down-projection LoRA grads
@@ -235,12 +179,8 @@ def mlp_backward(dY2, X2, e, g, W_gate, A_gate, B_gate, s_gate, W_up, A_up, B_up
         dBd = grad_at_b(dY2, ld(dY2), u, r, H, r, M, alpha=s_down, out_dtype=dt)
 
     # 4: up / gate LoRA grads
-    if packed:  # the spare columns of [df | de | v]
-        egv = torch.as_strided(e, (M, lde), (lde, 1), e.storage_offset())
-        v = egv[:, 2 * I:2 * I + 2 * r]
-    else:
-        v = torch.empty(M, 2 * r, dtype=torch.bfloat16, device=dev)  # [su df Bu | sg de Bg]
-    if kt and s_up == s_gate:  # both products in one launch (column-ranged segments)
+    v = torch.empty(M, 2 * r, dtype=torch.bfloat16, device=dev)  # [su df Bu | sg de Bg]
+    if s_up == s_gate:  # both products in one launch (column-ranged segments)
         gemm(M, 2 * r, [(df, lde, BuT, I, I, 0, r), (de, lde, BgT, I, I, r, 2 * r)], ROW, COL, out=v, alpha=s_up)
     else:
         times_b(df, lde, Bu, I, out=v[:, :r], alpha=s_up, b_t=BuT)
@@ -259,24 +199,10 @@ def mlp_backward(dY2, X2, e, g, W_gate, A_gate, B_gate, s_gate, W_up, A_up, B_up
         dBu = grad_at_b(df, lde, xa_ug[:, :r], 2 * r, I, r, M, alpha=s_up, out_dtype=dt)
         dBg = grad_at_b(de, lde, xa_ug[:, r:], 2 * r, I, r, M, alpha=s_gate, out_dtype=dt)
 
-    # 5: dX
-    if kt and BLAS_PLAIN:
-        if packed:
-            # one hipBLASLt GEMM, K-contiguous operands, one rounding:
-            # [df | de | v] [Wu^T | Wg^T | Au^T | Ag^T]^T
-            dX = torch.matmul(egv, lora_ext_rows([W_up, W_gate], [AuT, AgT], r, transpose=True).t())
-        else:  # hipBLASLt on the cached W^T: df Wu, + de Wg, + v [Au; Ag]
-            WuT, WgT = frozen_t(W_up), frozen_t(W_gate)
-            dX = torch.matmul(df, WuT.t())
-            dX.addmm_(de, WgT.t())
-            dX.addmm_(v, torch.cat([Au, Ag]))
-    elif kt:
-        WuT, WgT = frozen_t(W_up), frozen_t(W_gate)
-        dX = gemm(M, H, [(df, lde, WuT, I, I), (de, lde, WgT, I, I),
-                         (v[:, :r], ld(v), AuT, r, r), (v[:, r:], ld(v), AgT, r, r)], ROW, COL)
-    else:
-        dX = gemm(M, H, [(df, lde, Wu, ld(Wu), I), (de, lde, Wg, ld(Wg), I),
-                         (v[:, :r], ld(v), Au, ld(Au), r), (v[:, r:], ld(v), Ag, ld(Ag), r)], ROW, ROW)
+    # 5: dX = df Wu + de Wg + v [Au; Ag]: one GEMM over four K segments
+    WuT, WgT = frozen_t(W_up), frozen_t(W_gate)
+    dX = gemm(M, H, [(df, lde, WuT, I, I), (de, lde, WgT, I, I),
+                     (v[:, :r], ld(v), AuT, r, r), (v[:, r:], ld(v), AgT, r, r)], ROW, COL)
     return (dX, dA_ug[r:], dBg, dA_ug[:r], dBu, dAd, dBd)
 
 

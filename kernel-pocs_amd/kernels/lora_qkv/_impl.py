@@ -3,12 +3,11 @@
 Forward (reference `lora_qkv_v2_3`,
 kernels/lora_qkv/experiments/v2/lora_qkv_kernel_v2_3.py:177-267):
   1. xa = [sq X Aq^T | sk X Ak^T | sv X Av^T]            forge_lora_a [M, 3r]
-  2. out = [Q | K | V] = X [Wq; Wk; Wv]^T + LoRA-B terms: one hipBLASLt GEMM
-     [X | xa] [Wq | Bq . . ; Wk | . Bk . ; Wv | . . Bv]^T on a cached extended
-     weight (the LoRA-B products as extra K columns, one rounding), then RoPE
-     as a forge_rope pass over the stored Q and K.  With FORGE_PLAIN_GEMM=forge:
-     one MFMA GEMM with per-projection K segments whose epilogue rotates the
-     Q and K heads in registers                        forge_lora_qkv_rope
+  2. out = [Q | K | V] = X [Wq; Wk; Wv]^T + LoRA-B terms: one MFMA GEMM whose
+     per-projection K segments carry xa_p B_p^T (one rounding) and whose
+     epilogue rotates the Q and K heads in registers   forge_lora_qkv_rope
+     (tables or head widths the epilogue cannot take: Q/K stored unrotated,
+     then a forge_rope pass over them)
   Q, K, V are returned as column views of `out` (row pitch Hq + 2 Hkv), the
   reference's "strided views of one packed buffer" contract.
 Backward (reference `LoRAQKVv4Function.backward`,
@@ -16,10 +15,9 @@ kernels/lora_qkv/experiments/v4/lora_qkv_kernel_v4.py:221-336):
   t  = [sq dQ Bq | sk dK Bk | sv dV Bv]                   forge_gemm x3 [M, 3r]
   dA = t^T X (rows split per projection)                 split-K forge_gemm
   dB_p = s_p dY_p^T (X A_p^T)                            split-K forge_gemm
-  dX = dQ Wq + dK Wk + dV Wv + sum_p t_p A_p             one hipBLASLt GEMM over a
-     packed [dQ | dK | dV | t] (the RoPE backward writes dQ / dK into it) and the
-     cached [Wq^T | Wk^T | Wv^T | Aq^T | Ak^T | Av^T]; with FORGE_PLAIN_GEMM=forge
-     forge_gemm with 6 K segments
+  dX = dQ Wq + dK Wk + dV Wv + sum_p t_p A_p             forge_gemm, 6 K segments
+     over the cached W^T and the small A^T (the dX epilogue of the reference,
+     lora_qkv_kernel_v4.py:79-163, as K segments: no pass re-reads dX)
 With fused RoPE the incoming dQ/dK are first rotated back by -theta
 (forge_rope backward) — the chain rule through the rotation.
 """
@@ -31,8 +29,8 @@ import torch
 
 from forge_hip import _lib as L
 from kernels import _generic_lora as G
-from kernels._lora_ops import (BLAS_PLAIN, COL, ROW, as_operand, frozen_t, gemm, grad_at_b, grad_at_b_group, ld,
-                               k_pad, lora_a, lora_ext_rows, lora_operand, pad_rank, small_t_batch, times_b)
+from kernels._lora_ops import (COL, ROW, as_operand, frozen_t, gemm, grad_at_b, grad_at_b_group, ld, lora_a,
+                               pad_rank, small_t_batch, times_b)
 
 
 def _w(t):
@@ -80,15 +78,7 @@ def qkv_forward(X2, W_q, W_k, W_v, A_q, B_q, s_q, A_k, B_k, s_k, A_v, B_v, s_v,
     Bq = Bk = Bv = None
     if has_lora:
         Bq, Bk, Bv = _w(B_q), _w(B_k), _w(B_v)
-    if BLAS_PLAIN:
-        # hipBLASLt: [X | xa] [Wq | Bq . . ; Wk | . Bk . ; Wv | . . Bv]^T, the
-        # LoRA-B products as extra K columns of a cached extended weight (one
-        # rounding); RoPE then rotates the stored Q/K with a forge_rope pass
-        ext = lora_ext_rows([W_q, W_k, W_v], [Bq, Bk, Bv], r)
-        torch.matmul(lora_operand(X2, xa) if has_lora else X2, ext.t(), out=out)
-        if rope is not None:
-            rope_qk_inplace(out, Hq, Hkv, rope)
-    elif rope is not None and not rope_fusable(rope, Hq, Hkv):
+    if rope is not None and not rope_fusable(rope, Hq, Hkv):
         # the unfused composition: a forge_rope pass over the stored Q/K
         qkv_gemm(X2, Wq, Wk, Wv, xa, Bq, Bk, Bv, r, None, out)
         rope_qk_inplace(out, Hq, Hkv, rope)
@@ -152,18 +142,16 @@ def rope_qk_inplace(out, Hq, Hkv, rope, backward=False):
 
 
 def qkv_backward(dQ, dK, dV, X2, W_q, W_k, W_v, A_q, B_q, s_q, A_k, B_k, s_k, A_v, B_v, s_v,
-                 aux: Optional[dict] = None, packed: Optional[torch.Tensor] = None):
+                 aux: Optional[dict] = None):
     """Returns (dX, dA_q, dB_q, dA_k, dB_k, dA_v, dB_v).  With the forward's
-    aux the B gradients reuse its scaled xa instead of re-reading X.  packed
-    (optional, from packed_grad_buffer): the [M, Hq + 2 Hkv + 3r] buffer of
-    the hipBLASLt dX product, whose Q / K blocks dQ / dK already are."""
+    aux the B gradients reuse its scaled xa instead of re-reading X."""
     if X2.dtype in G.GENERIC_DTYPES:
         return G.qkv_backward(dQ, dK, dV, X2, W_q, W_k, W_v, A_q, B_q, s_q, A_k, B_k, s_k, A_v, B_v, s_v, aux=aux)
     if A_q.shape[0] % 8:  # rank padded to a multiple of 8 (exact); the padding's gradients are dropped
         r0 = A_q.shape[0]
         (Aq8, Bq8), (Ak8, Bk8), (Av8, Bv8) = (pad_rank(a, b) for a, b in ((A_q, B_q), (A_k, B_k), (A_v, B_v)))
         dX, dAq, dBq, dAk, dBk, dAv, dBv = qkv_backward(dQ, dK, dV, X2, W_q, W_k, W_v, Aq8, Bq8, s_q, Ak8, Bk8, s_k,
-                                                        Av8, Bv8, s_v, aux=aux)  # (a packed buffer has r0 columns)
+                                                        Av8, Bv8, s_v, aux=aux)
         return (dX, dAq[:r0].contiguous(), dBq[:, :r0].contiguous(), dAk[:r0].contiguous(),
                 dBk[:, :r0].contiguous(), dAv[:r0].contiguous(), dBv[:, :r0].contiguous())
     X2 = as_operand(X2)
@@ -174,12 +162,11 @@ def qkv_backward(dQ, dK, dV, X2, W_q, W_k, W_v, A_q, B_q, s_q, A_k, B_k, s_k, A_
     r = A_q.shape[0]
     dev = X2.device
     Aq, Bq, Ak, Bk, Av, Bv = (_w(t) for t in (A_q, B_q, A_k, B_k, A_v, B_v))
-    kt = r % 8 == 0  # K-contiguous operands for the LDS-DMA engine (cached W^T, small A^T / B^T)
-    BqT = BkT = BvT = None
-    if kt:  # the six small transposes in one launch
-        BqT, BkT, BvT, AqT, AkT, AvT = small_t_batch([Bq, Bk, Bv, Aq, Ak, Av])
+    # K-contiguous operands for the 4-wave engine (cached W^T, small A^T / B^T;
+    # the rank is a multiple of 8 here): the six small transposes in one launch
+    BqT, BkT, BvT, AqT, AkT, AvT = small_t_batch([Bq, Bk, Bv, Aq, Ak, Av])
     t = torch.empty(M, 3 * r, dtype=torch.bfloat16, device=dev)
-    if kt and s_q == s_k == s_v:  # [dQ Bq | dK Bk | dV Bv] in one launch (column-ranged segments)
+    if s_q == s_k == s_v:  # [dQ Bq | dK Bk | dV Bv] in one launch (column-ranged segments)
         gemm(M, 3 * r, [(dQ, ld(dQ), BqT, Hq, Hq, 0, r), (dK, ld(dK), BkT, Hkv, Hkv, r, 2 * r),
                         (dV, ld(dV), BvT, Hkv, Hkv, 2 * r, 3 * r)], ROW, COL, out=t, alpha=s_q)
     else:
@@ -199,38 +186,11 @@ def qkv_backward(dQ, dK, dV, X2, W_q, W_k, W_v, A_q, B_q, s_q, A_k, B_k, s_k, A_
         dBq = grad_at_b(dQ, ld(dQ), xa[:, :r], 3 * r, Hq, r, M, alpha=sc[0], out_dtype=dt)
         dBk = grad_at_b(dK, ld(dK), xa[:, r:2 * r], 3 * r, Hkv, r, M, alpha=sc[1], out_dtype=dt)
         dBv = grad_at_b(dV, ld(dV), xa[:, 2 * r:], 3 * r, Hkv, r, M, alpha=sc[2], out_dtype=dt)
-    if kt and BLAS_PLAIN:
-        # hipBLASLt: [dQ | dK | dV | t] [Wq^T | Wk^T | Wv^T | Aq^T | Ak^T | Av^T]^T,
-        # one GEMM on a cached extended weight (one rounding)
-        W3 = Hq + 2 * Hkv
-        P = packed if packed is not None and packed.shape[1] == k_pad(W3 + 3 * r) else \
-            packed_grad_buffer(M, Hq, Hkv, r, dev)
-        for blk, (c0, c1) in ((dQ, (0, Hq)), (dK, (Hq, Hq + Hkv)), (dV, (Hq + Hkv, W3))):
-            if blk.data_ptr() != P[:, c0:c1].data_ptr() or ld(blk) != ld(P):
-                P[:, c0:c1].copy_(blk)
-        P[:, W3:W3 + 3 * r].copy_(t)
-        dX = torch.matmul(P, lora_ext_rows([W_q, W_k, W_v], [AqT, AkT, AvT], r, transpose=True).t())
-    elif kt:
-        dX = gemm(M, K, [(dQ, ld(dQ), frozen_t(W_q), Hq, Hq), (dK, ld(dK), frozen_t(W_k), Hkv, Hkv),
-                         (dV, ld(dV), frozen_t(W_v), Hkv, Hkv), (t[:, :r], 3 * r, AqT, r, r),
-                         (t[:, r:2 * r], 3 * r, AkT, r, r), (t[:, 2 * r:], 3 * r, AvT, r, r)],
-                  ROW, COL)
-    else:
-        dX = gemm(M, K, [(dQ, ld(dQ), Wq, ld(Wq), Hq), (dK, ld(dK), Wk, ld(Wk), Hkv),
-                         (dV, ld(dV), Wv, ld(Wv), Hkv), (t[:, :r], 3 * r, Aq, ld(Aq), r),
-                         (t[:, r:2 * r], 3 * r, Ak, ld(Ak), r), (t[:, 2 * r:], 3 * r, Av, ld(Av), r)], ROW, ROW)
+    dX = gemm(M, K, [(dQ, ld(dQ), frozen_t(W_q), Hq, Hq), (dK, ld(dK), frozen_t(W_k), Hkv, Hkv),
+                     (dV, ld(dV), frozen_t(W_v), Hkv, Hkv), (t[:, :r], 3 * r, AqT, r, r),
+                     (t[:, r:2 * r], 3 * r, AkT, r, r), (t[:, 2 * r:], 3 * r, AvT, r, r)],
+              ROW, COL)
     return (dX, dA[:r], dBq, dA[r:2 * r], dBk, dA[2 * r:], dBv)
-
-
-def packed_grad_buffer(M: int, Hq: int, Hkv: int, r: int, device) -> torch.Tensor:
-    """[M, k_pad(Hq + 2 Hkv + 3 r)] bf16 for the backward's hipBLASLt dX
-    product: [dQ | dK | dV | t | 0] (t = the scaled dY B products; the zero
-    columns meet the extended weight's)."""
-    W = Hq + 2 * Hkv + 3 * r
-    P = torch.empty(M, k_pad(W), dtype=torch.bfloat16, device=device)
-    if P.shape[1] > W:
-        P[:, W:].zero_()
-    return P
 
 
 def torch_qkv_forward(X, W_q, W_k, W_v, A_q, B_q, s_q, A_k, B_k, s_k, A_v, B_v, s_v):

@@ -21,12 +21,11 @@ from __future__ import annotations
 import torch
 
 from forge_hip import _lib as L
-from kernels._lora_ops import BLAS_PLAIN, frozen_cat
+from kernels._lora_ops import frozen_cat
 from kernels._positions import check_positions
 from kernels.lora_qkv._impl import (  # noqa: F401
     pack_lora_a,
     pack_weights_backward,
-    packed_grad_buffer,
     qkv_backward,
     qkv_forward,
     split_views,
@@ -115,21 +114,17 @@ def _rope_rows_backward(d, n_heads, head_dim, cos, sin, positions):
     return out
 
 
-def _rope_qk_backward(dQ, dK, head_dim, cos, sin, positions, out=None):
+def _rope_qk_backward(dQ, dK, head_dim, cos, sin, positions):
     """Rotates the [M, Hq] and [M, Hkv] gradients (any row pitches) by -theta
-    per token in one forge_rope launch (GQA: Hq/D a multiple of Hkv/D);
-    returns new tensors: contiguous ones, or the first Hq and next Hkv
-    columns of `out` (a packed dX-product buffer) when given."""
+    per token in one forge_rope launch (GQA: Hq/D a multiple of Hkv/D) into
+    new contiguous tensors."""
     nq, nk = dQ.shape[1] // head_dim, dK.shape[1] // head_dim
     if nk == 0 or nq % nk != 0:
         return (_rope_rows_backward(dQ, nq, head_dim, cos, sin, positions),
                 _rope_rows_backward(dK, nk, head_dim, cos, sin, positions))
     M = dQ.shape[0]
-    if out is not None:
-        oq, ok = out[:, :nq * head_dim], out[:, nq * head_dim:(nq + nk) * head_dim]
-    else:
-        oq = torch.empty(M, nq * head_dim, dtype=dQ.dtype, device=dQ.device)
-        ok = torch.empty(M, nk * head_dim, dtype=dK.dtype, device=dK.device)
+    oq = torch.empty(M, nq * head_dim, dtype=dQ.dtype, device=dQ.device)
+    ok = torch.empty(M, nk * head_dim, dtype=dK.dtype, device=dK.device)
     L.check(
         L.forge_rope(L.dtype_code(dQ.dtype),
                      dQ.data_ptr(), 0, head_dim, dQ.stride(0),
@@ -203,15 +198,10 @@ class LoRAQKVRoPEFunction(torch.autograd.Function):
         dQ2, dK2 = _flat(dQ), _flat(dK)
         dQ2 = dQ2 if dQ2.stride(-1) == 1 else dQ2.contiguous()
         dK2 = dK2 if dK2.stride(-1) == 1 else dK2.contiguous()
-        # bf16 with a rank that needs no padding: dQ / dK rotate straight into the
-        # hipBLASLt dX product's packed buffer
-        P = None
-        if BLAS_PLAIN and dQ2.dtype == torch.bfloat16 and A_q is not None and A_q.shape[0] % 8 == 0:
-            P = packed_grad_buffer(dQ2.shape[0], dQ2.shape[1], dK2.shape[1], A_q.shape[0], dQ2.device)
-        dQu, dKu = _rope_qk_backward(dQ2, dK2, D, cos2, sin2, pos, out=P)
+        dQu, dKu = _rope_qk_backward(dQ2, dK2, D, cos2, sin2, pos)
         dX, dAq, dBq, dAk, dBk, dAv, dBv = qkv_backward(dQu, dKu, _flat(dV), _flat(X), W_q, W_k, W_v,
                                                         A_q, B_q, s_q, A_k, B_k, s_k, A_v, B_v, s_v,
-                                                        aux=ctx.lora_aux, packed=P)
+                                                        aux=ctx.lora_aux)
         if X.dim() == 3:
             dX = dX.reshape(X.shape)
         return (dX, None, None, None, dAq, dBq, None, dAk, dBk, None, dAv, dBv, None, None, None, None, None)

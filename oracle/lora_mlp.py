@@ -70,6 +70,32 @@ def backward(dY, X, e, g, W_gate, A_gate, B_gate, s_gate, W_up, A_up, B_up, s_up
     return dX, d_gateA, d_gateB, d_upA, d_upB, d_downA, d_downB
 
 
+def lora_grads(dY, X, W_gate, A_gate, B_gate, s_gate, W_up, A_up, B_up, s_up, W_down, A_down, B_down, s_down):
+    """The LoRA-parameter part of `forward` + `backward` alone (SiLU,
+    lora_mlp_pytorch.py:100-104, 153-211): (dA_gate, dB_gate, dA_up, dB_up,
+    dA_down, dB_down).  It skips the output and dX products (two of the five
+    [M, H] x [H, I]-sized products), so it runs over the BASELINE token count
+    on the CPU."""
+    e = matmul_lora(X, W_gate, A_gate, B_gate, s_gate)
+    g = matmul_lora(X, W_up, A_up, B_up, s_up)
+    sig_e = torch.sigmoid(e.float()).to(e.dtype)
+    act_e = e * sig_e
+    h = act_e * g
+    dYB = dY @ B_down
+    DW = dY @ W_down + s_down * (dYB @ A_down)
+    d_downA = s_down * (dYB.t() @ h)
+    d_downB = s_down * (dY.t() @ (h @ A_down.t()))
+    del h
+    df = DW * act_e
+    de = DW * g * (sig_e * (1.0 + e * (1.0 - sig_e)))
+    del DW, e, g, act_e, sig_e
+    d_upA = s_up * ((df @ B_up).t() @ X)
+    d_upB = s_up * (df.t() @ (X @ A_up.t()))
+    d_gateA = s_gate * ((de @ B_gate).t() @ X)
+    d_gateB = s_gate * (de.t() @ (X @ A_gate.t()))
+    return d_gateA, d_gateB, d_upA, d_upB, d_downA, d_downB
+
+
 def fwd_bwd(X, dY, params, compute_dtype=torch.float32, activation="silu"):
     """CPU forward + backward; params = (W_gate, A_gate, B_gate, s_gate, ...)."""
     c = lambda t: t.detach().cpu().to(compute_dtype) if isinstance(t, torch.Tensor) else t  # noqa: E731

@@ -13,6 +13,7 @@ from kernels.lora_qkv.experiments.v4.lora_qkv_kernel_v4 import (
     pack_lora_a,
     pack_weights_backward,
 )
+from kernels.lora_qkv._impl import qkv_forward, rope_fusable, rope_qk_inplace
 from oracle import lora_qkv as orc
 from oracle.rope import cos_sin
 from _parity import close_bf16 as _close_bf16
@@ -92,10 +93,22 @@ def test_lora_qkv_rope_fused_matches_composition(head_dim):
     (Qr, Kr, Vr), ref_grads = orc.qkv_rope_fwd_bwd(X, dQ, dK, dV, params, c[pos], s[pos], head_dim)
     p = _cuda(params)
     x = X.cuda().requires_grad_(True)
+    rope = {"cos": c.cuda(), "sin": s.cuda(), "positions": pos.cuda(), "head_dim": head_dim}
+    assert rope_fusable(rope, Hq, Hkv)  # this shape takes the GEMM's RoPE epilogue
     Q, K_, V = lora_qkv_rope(x, p[0], p[3], p[4], p[5], p[1], p[6], p[7], p[8], p[2], p[9], p[10], p[11],
                              c.cuda(), s.cuda(), pos.cuda(), head_dim)
     for a, b, n in ((Q, Qr, "Q"), (K_, Kr, "K"), (V, Vr, "V")):
         _close_bf16(a, b, n)
+    # the unfused composition on the device: the same GEMM storing Q/K, then
+    # a forge_rope pass; both round the projection to bf16 before rotating,
+    # so they differ by at most one bf16 rounding of the rotated value
+    args = (x.detach(), p[0], p[1], p[2], p[3].detach(), p[4].detach(), p[5], p[6].detach(), p[7].detach(), p[8],
+            p[9].detach(), p[10].detach(), p[11])
+    plain = qkv_forward(*args)
+    rope_qk_inplace(plain, Hq, Hkv, rope)
+    fused = torch.cat([Q, K_, V], 1)
+    assert torch.equal(fused[:, Hq + Hkv:], plain[:, Hq + Hkv:])  # V is not rotated
+    torch.testing.assert_close(fused.float(), plain.float(), rtol=2 ** -7, atol=1e-5)
     torch.autograd.backward((Q, K_, V), (dQ.cuda(), dK.cuda(), dV.cuda()))
     got = [x.grad, p[3].grad, p[4].grad, p[6].grad, p[7].grad, p[9].grad, p[10].grad]
     for n, a, b in zip(NAMES, got, ref_grads):
@@ -105,11 +118,9 @@ def test_lora_qkv_rope_fused_matches_composition(head_dim):
 @pytest.mark.gpu
 @pytest.mark.parametrize("head_dim", [128, 64])
 def test_qkv_rope_epilogue_paths_agree(head_dim):
-    """The fused RoPE epilogue has a 16-byte staged path and a per-element
-    path (taken when the cos/sin rows are not 8-element aligned); both must
-    give bit-identical Q/K/V."""
-    from kernels.lora_qkv._impl import qkv_forward
-
+    """The fused RoPE epilogue of forge_lora_qkv_rope has a 16-byte staged
+    path and a per-element path (taken when the cos/sin rows are not
+    8-element aligned); both must give bit-identical Q/K/V."""
     gen = torch.Generator().manual_seed(100 + head_dim)
     T, K, Hq, Hkv, r = 300, 512, 512, 256, 16
     p = _cuda(orc.make_params(K, Hq, Hkv, r, 32, gen))

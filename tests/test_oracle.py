@@ -409,6 +409,26 @@ def test_lora_mlp_flops_known_answer():
     assert omlp.flops(8192, 4096, 14336, 16) == 5_821_828_169_728
 
 
+def test_lora_mlp_lora_grads_match_autograd_float64():
+    """lora_grads (the LoRA-parameter gradients without the out / dX
+    products, used at the BASELINE token count) against autograd of the
+    forward: every gradient, O(1) LoRA terms so a dropped term or a swapped
+    gate / up slot is visible."""
+    p = _mlp_params(seed=8)
+    g = torch.Generator().manual_seed(9)
+    X = torch.randn(9, 12, generator=g, dtype=torch.float64)
+    dY = torch.randn(9, 12, generator=g, dtype=torch.float64)
+    got = omlp.lora_grads(dY, X, *p)
+    leaves = [X.clone().requires_grad_(True)] + [t.clone().requires_grad_(True) if isinstance(t, torch.Tensor) else t
+                                                 for t in p]
+    o2, _, _ = omlp.forward(*leaves)
+    (o2 * dY).sum().backward()
+    expect = [leaves[2].grad, leaves[3].grad, leaves[6].grad, leaves[7].grad, leaves[10].grad, leaves[11].grad]
+    for a, b in zip(got, expect):
+        torch.testing.assert_close(a, b, rtol=2e-5, atol=2e-6)
+    assert not torch.allclose(got[0], got[2], rtol=1e-3)  # gate and up differ
+
+
 # ---------------------------------------------------------------------------
 # LoRA-QKV
 # ---------------------------------------------------------------------------
