@@ -74,8 +74,9 @@ static int launch_cfg(GemmArgs a, hipStream_t s) {
   if constexpr (BM == 256 && BN == 256 && AL == ROW && BL == COL) {
     // both operands K-contiguous: the 4-wave engine (128 x 128 per wave,
     // accumulators in AGPRs, a ring of five LDS half-slots fed by LDS-DMA)
-    constexpr bool W4_STAGE = staged_ok(BM, BN, 2, 2, EPI);
-    if (W4_STAGE && a.ep.vec_ok)
+    constexpr bool W4_STAGE = w4_staged_epi(EPI);
+    const bool plain = a.ep.beta == 0.f && a.ep.act == ACT_NONE && a.ep.alpha_group == 0;
+    if (W4_STAGE && a.ep.vec_ok && (EPI != EPI_STORE_BF16 || plain))
       gemm_w4_kernel<BMODE, EPI, W4_STAGE><<<grid, 256, 0, s>>>(a);
     else
       gemm_w4_kernel<BMODE, EPI, false><<<grid, 256, 0, s>>>(a);

@@ -24,6 +24,7 @@
 #pragma once
 
 #include "gemm_core.h"
+#include "gemm_w4_epi.h"
 
 namespace fgemm {
 
@@ -62,9 +63,13 @@ struct W4Loader {
   int64_t ld_bytes;
   int kch[2];          // first k of this lane's chunk, by instruction parity
 
-  static __device__ __forceinline__ int sel_of(int wave, int j) {
-    return DUAL ? (((wave * IPW + j) * RPI) / 32) % 2 : 0;  // 32-row groups alternate gate / up
-  }
+  // 32-row groups alternate gate / up.  A wave's rows are a whole number of
+  // 64-row pairs, so the pointer an instruction reads depends on j alone:
+  // a compile-time choice (computed from the wave index, the compiler kept
+  // both descriptors in a scratch array and issued every DMA through a
+  // waterfall loop with vmcnt(0): the dual GEMM ran 2.6x slower).
+  static_assert((IPW * RPI) % 64 == 0, "wave slab = whole gate/up group pairs");
+  static __device__ __forceinline__ constexpr int sel_of(int j) { return DUAL ? ((j * RPI) / 32) % 2 : 0; }
 
   template <class RowSrc>
   __device__ __forceinline__ void setup(const void* p0, const void* p1, int64_t ld, int64_t panel_off,
@@ -82,7 +87,7 @@ struct W4Loader {
     for (int j = 0; j < IPW; ++j) {
       const int q = (wave * IPW + j) * RPI + lane / CPR;   // tile row
       const int chunk = (lane % CPR) ^ swz<BKT>(q);        // source chunk of LDS slot lane % CPR
-      const int sel = sel_of(wave, j);
+      const int sel = sel_of(j);
       const int64_t row = base[sel] ? row_src(q, sel) : -1;
       voff[j] = row < 0 ? OOB : (uint32_t)(row * ld_bytes + chunk * 16);
       if (j < 2) kch[j] = chunk * 8;
@@ -109,7 +114,7 @@ struct W4Loader {
     // (the resource goes through a local: passed to the builtin as a
     // conditional of two struct members, hipcc's host pass emitted the
     // launch stub of the first instantiation of the kernel only)
-    const __amdgpu_buffer_rsrc_t r = sel_of(wave, j) ? p.r1 : p.r0;
+    const __amdgpu_buffer_rsrc_t r = sel_of(j) ? p.r1 : p.r0;
     __builtin_amdgcn_raw_ptr_buffer_load_lds(r,
                                              (__attribute__((address_space(3))) void*)(dst + (wave * IPW + j) * 1024),
                                              16, off, 0, 0, 0);
@@ -138,7 +143,8 @@ void gemm_w4_kernel(GemmArgs args) {
   constexpr int NH = W4_NHALF;
   static_assert(KS % 2 == 0, "an even number of k-steps per tile keeps the fragment slots static");
   constexpr int RING = NH * W4_HALF;
-  constexpr int SMEM = RING > (STAGED ? STAGED_BYTES : 0) ? RING : STAGED_BYTES;
+  static_assert(RING >= W4_STAGE_BYTES && RING >= W4_DUAL_BYTES, "the staged epilogue reuses the ring");
+  constexpr int SMEM = RING;
   __shared__ __attribute__((aligned(1024))) char smem[SMEM];
 
   const int64_t M = args.M;
@@ -259,12 +265,15 @@ void gemm_w4_kernel(GemmArgs args) {
     else if (idx <= FN) bfr[sl][idx - 1] = *reinterpret_cast<const bf16x8*>(pb + b_row + (idx - 1) * 32 * RB + ko);
     else af[sl][idx - FN] = *reinterpret_cast<const bf16x8*>(pa + a_row + (idx - FN) * 32 * RB + ko);
   };
-  // MFMAs 2p and 2p+1 of a k-step, (i, j) row-major
+  // MFMAs 2p and 2p+1 of a k-step, (i, j) row-major.  The operands are
+  // swapped (block (i, j) is computed as B_j A_i^T), so a lane accumulates
+  // four consecutive output columns of one row (the layout gemm_w4_epi.h
+  // stages with 8-byte writes).
   auto mfma_pair = [&](int sl, int p) {
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
       const int m = 2 * p + u, i = m / FN, j = m % FN;
-      acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[sl][i], bfr[sl][j], acc[i][j], 0, 0, 0);
+      acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bfr[sl][j], af[sl][i], acc[i][j], 0, 0, 0);
     }
   };
   constexpr int NPAIR = FM * FN / 2;  // 8 MFMA pairs per k-step ...
@@ -361,10 +370,14 @@ void gemm_w4_kernel(GemmArgs args) {
     wait_vmcnt<0>();  // no zero-fill DMA may land in the staged epilogue's LDS
   }
   if constexpr (STAGED) {
-    static_assert(staged_ok(BM, BN, WAVES_M, WAVES_N, EPI), "staged epilogue: 256 x 256 tile, wave tiles of <= 128 rows");
-    epilogue_staged<WAVES_M, WAVES_N, BMODE, EPI>(args, acc, m0, n0, lane, wm, wn, reinterpret_cast<float*>(smem));
+    static_assert(w4_staged_epi(EPI), "staged epilogue: bf16 outputs");
+    __bf16* lds = reinterpret_cast<__bf16*>(smem);
+    if constexpr (BMODE == B_DUAL)
+      w4_epilogue_staged_dual<EPI>(args, acc, m0, n0, lane, wm, wn, lds);
+    else  // (STORE_BF16 is launched staged at beta = 0 only)
+      w4_epilogue_staged<EPI>(args, acc, m0, n0, lane, wm, wn, lds);
   } else {
-    epilogue<BM, BN, WAVES_M, WAVES_N, BMODE, EPI>(args, acc, m0, n0, lane, wm, wn);
+    w4_epilogue_direct<BMODE, EPI>(args, acc, m0, n0, lane, wm, wn);
   }
 }
 

@@ -1,0 +1,397 @@
+// Epilogues of the 4-wave GEMM engine (gemm_w4.h).
+//
+// The engine issues its MFMAs with the operands swapped (each 32 x 32 block
+// is computed as B_tile A_tile^T, i.e. C^T), so that a lane's accumulators
+// hold runs of four consecutive output COLUMNS of one row:
+//   acc[i][j][r] of lane l = C[m][n],  m = m0 + 128 wm + 32 i + l % 32,
+//   n = colbase(j) + 8 (r / 4) + 4 (l / 32) + r % 4
+// with colbase(j) = n0 + 128 wn + 32 j for a single B, and for the dual
+// gate / up B (wave tile j = gate for even j, up for odd j) the output
+// columns n0 + 64 wn + 32 (j / 2) + ...
+// (With A and B in the usual order a lane holds four consecutive ROWS of one
+// column, so staging a tile took 256 scattered 4-byte LDS writes per lane.)
+//
+// Staged epilogues (bf16 outputs; the hot path): the tile goes through LDS
+// as bf16, 8 bytes per lane per write, all four waves at once, so that every
+// thread then reads side inputs and writes outputs as 16-byte vectors.
+// Staging in bf16 loses nothing: each of them rounds its GEMM result to bf16
+// before any further arithmetic (STORE, RoPE, the GLU backward's DW) or
+// computes its fp32 result in registers before staging (the GLU forward's h,
+// the STORE activation and alpha).  Measured on MI355X, epilogue alone over a
+// whole 8192 x 14336 output (K = 0 launches): fp32 staging of 128-row halves
+// 16.2 us per round of 256 tiles.
+//
+// The direct epilogue (fp32 and atomic outputs, beta != 0, and buffers whose
+// alignment rules out 16-byte vectors) works per element from registers.
+#pragma once
+
+#include "gemm_core.h"
+
+namespace fgemm {
+
+constexpr int W4_SP = 256 + 8;  // staged bf16 row, single B: 528 bytes (rows 4 banks apart)
+constexpr int W4_DP = 128 + 8;  // staged bf16 row of one dual-B output (e, g or h)
+constexpr int W4_STAGE_BYTES = 256 * W4_SP * 2;       // single B: the whole tile
+constexpr int W4_DUAL_BYTES = 3 * 128 * W4_DP * 2;    // dual B: e, g, h of 128 rows
+
+// Epilogues staged through LDS (with ep.vec_ok; STORE_BF16 only with a plain
+// alpha: no beta, no activation, no per-column alpha groups).
+constexpr bool w4_staged_epi(int epi) {
+  return epi == EPI_STORE_BF16 || epi == EPI_ROPE || glu_fwd_epi(epi) || glu_bwd_epi(epi);
+}
+
+__device__ __forceinline__ uint2 pack4(const float (&f)[4]) {
+  uint32_t w[2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const __bf16 lo = (__bf16)f[2 * i], hi = (__bf16)f[2 * i + 1];
+    w[i] = (uint32_t)__builtin_bit_cast(uint16_t, lo) | ((uint32_t)__builtin_bit_cast(uint16_t, hi) << 16);
+  }
+  return make_uint2(w[0], w[1]);
+}
+
+__device__ __forceinline__ float col_alpha(const EpiArgs& ep, int64_t n) {
+  if (ep.alpha_group > 0) {
+    const int64_t grp = n / ep.alpha_group;
+    return ep.alphas[grp < 4 ? grp : 3];
+  }
+  return ep.alpha;
+}
+
+// ---------------------------------------------------------------------------
+// Direct epilogue: every element from registers, bounds-checked.
+// ---------------------------------------------------------------------------
+template <int BMODE, int EPI>
+__device__ __forceinline__ void w4_epilogue_direct(const GemmArgs& args, f32x16 (&acc)[4][4], int64_t m0, int64_t n0,
+                                                   int lane, int wm, int wn) {
+  const EpiArgs& ep = args.ep;
+  const int64_t M = args.M, N = args.N;
+  const int cl = 4 * (lane / 32);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int64_t m = m0 + wm * 128 + i * 32 + lane % 32;
+    if (m >= M) continue;
+    if constexpr (glu_fwd_epi(EPI)) {
+#pragma unroll
+      for (int jp = 0; jp < 2; ++jp)
+#pragma unroll
+        for (int g = 0; g < 4; ++g)
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            const int64_t n = n0 + wn * 64 + 32 * jp + 8 * g + cl + q;
+            if (n >= N) continue;
+            const float e = acc[i][2 * jp][4 * g + q], gg = acc[i][2 * jp + 1][4 * g + q];
+            const int64_t off = m * ep.ld_eg + n;
+            if (ep.e) {
+              ep.e[off] = (__bf16)e;
+              ep.g[off] = (__bf16)gg;
+            }
+            ((__bf16*)ep.c)[m * ep.ldc + n] = (__bf16)glu_fwd_h<EPI>(e, gg);
+          }
+    } else if constexpr (EPI == EPI_ROPE) {
+      const int64_t pos = ep.positions ? ep.positions[m] : m;
+      const bool pos_ok = pos >= 0 && pos < ep.cs_rows;
+      const int half_tiles = ep.head_dim / 64;  // partner distance in 32-column tiles
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int g = 0; g < 4; ++g)
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            const int64_t n = n0 + wn * 128 + 32 * j + 8 * g + cl + q;
+            if (n >= N) continue;
+            float v = acc[i][j][4 * g + q];
+            if (n < ep.rope_cols) {
+              const bool lo = (j % (2 * half_tiles)) < half_tiles;
+              const int partner = lo ? j + half_tiles : j - half_tiles;
+              float pv = 0.f;
+#pragma unroll
+              for (int t = 0; t < 4; ++t)
+                if (t == partner) pv = acc[i][t][4 * g + q];
+              const int d = (int)(n % ep.head_dim) % (ep.head_dim / 2);
+              const float c = pos_ok ? (float)ep.cos[pos * ep.cs_ld + d] : __builtin_nanf("");
+              const float s = pos_ok ? (float)ep.sin[pos * ep.cs_ld + d] : __builtin_nanf("");
+              // the projection is rounded to bf16 first: RoPE is applied to the
+              // materialised Q/K in the unfused reference path
+              const float x = bf16r(v), xp = bf16r(pv);
+              v = lo ? x * c - xp * s : x * c + xp * s;
+            }
+            ((__bf16*)ep.c)[m * ep.ldc + n] = (__bf16)v;
+          }
+    } else {
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const int64_t nb = n0 + wn * 128 + 32 * j + 8 * g + cl;
+          if (nb >= N) continue;
+          if constexpr (EPI == EPI_STORE_F32) {
+            float* cp = (float*)ep.c + (int64_t)blockIdx.z * ep.split_stride + m * ep.ldc + nb;
+            float v[4];
+#pragma unroll
+            for (int q = 0; q < 4; ++q) v[q] = col_alpha(ep, nb + q) * acc[i][j][4 * g + q];
+            if (ep.vec_ok && nb + 4 <= N) {  // 16-byte aligned: ldc % 8 == 0, nb % 4 == 0
+              float4* c4 = reinterpret_cast<float4*>(cp);
+              if (ep.beta != 0.f) {
+                const float4 o = *c4;
+                v[0] += ep.beta * o.x; v[1] += ep.beta * o.y; v[2] += ep.beta * o.z; v[3] += ep.beta * o.w;
+              }
+              if (ep.act)
+#pragma unroll
+                for (int q = 0; q < 4; ++q) v[q] = epi_act(ep.act, v[q]);
+              *c4 = make_float4(v[0], v[1], v[2], v[3]);
+            } else {
+              for (int q = 0; q < 4 && nb + q < N; ++q) {
+                float o = v[q];
+                if (ep.beta != 0.f) o += ep.beta * cp[q];
+                cp[q] = ep.act ? epi_act(ep.act, o) : o;
+              }
+            }
+          } else if constexpr (EPI == EPI_ATOMIC_F32) {
+            for (int q = 0; q < 4 && nb + q < N; ++q)
+              atomicAdd((float*)ep.c + m * ep.ldc + nb + q, col_alpha(ep, nb + q) * acc[i][j][4 * g + q]);
+          } else if constexpr (EPI == EPI_STORE_BF16) {
+            __bf16* cp = (__bf16*)ep.c + m * ep.ldc + nb;
+            for (int q = 0; q < 4 && nb + q < N; ++q) {
+              float o = col_alpha(ep, nb + q) * acc[i][j][4 * g + q];
+              if (ep.beta != 0.f) o += ep.beta * (float)cp[q];
+              if (ep.act) o = epi_act(ep.act, o);
+              cp[q] = (__bf16)o;
+            }
+          } else if constexpr (glu_bwd_epi(EPI)) {
+            for (int q = 0; q < 4 && nb + q < N; ++q) {
+              const int64_t off = m * ep.ld_eg + nb + q;
+              float h, df, de;
+              glu_bwd_vals<EPI>(acc[i][j][4 * g + q], (float)ep.e[off], (float)ep.g[off], h, df, de);
+              ((__bf16*)ep.c)[m * ep.ldc + nb + q] = (__bf16)h;
+              ep.e[off] = (__bf16)df;
+              ep.g[off] = (__bf16)de;
+            }
+          }
+        }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Staged epilogue, single B (STORE_BF16 at beta = 0, ROPE, GLU backward):
+// the whole 256 x 256 tile in LDS as bf16, then each thread owns column chunk
+// c = 8 (tid % 32) and walks rows tid / 32 + 8 it.
+// ---------------------------------------------------------------------------
+template <int EPI>
+__device__ __forceinline__ void w4_epilogue_staged(const GemmArgs& args, f32x16 (&acc)[4][4], int64_t m0, int64_t n0,
+                                                   int lane, int wm, int wn, __bf16* lds) {
+  const EpiArgs& ep = args.ep;
+  const int64_t M = args.M, N = args.N;
+  const int tid = threadIdx.x;
+  const int cl = 4 * (lane / 32);
+  lds_barrier();  // the main loop's LDS reads are done (its DMAs drained before)
+  // STORE_BF16 scales by alpha (the host launches per-column alpha groups,
+  // activations and beta != 0 on the direct epilogue)
+  const float alpha = EPI == EPI_STORE_BF16 ? ep.alpha : 1.f;
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        float v[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) v[q] = alpha * acc[i][j][4 * g + q];
+        *reinterpret_cast<uint2*>(lds + (wm * 128 + i * 32 + lane % 32) * W4_SP + wn * 128 + 32 * j + 8 * g + cl) =
+            pack4(v);
+      }
+  lds_barrier();
+  constexpr int IT = 256 / 8, GRP = 4;  // rows per thread; side inputs of 4 rows in flight
+  const int c = (tid % 32) * 8;
+  const int64_t n = n0 + c;
+  const bool full = n + 8 <= N;
+  if constexpr (EPI == EPI_STORE_BF16) {
+#pragma unroll 4
+    for (int it = 0; it < IT; ++it) {
+      const int rr = it * 8 + tid / 32;
+      const int64_t m = m0 + rr;
+      if (m >= M || n >= N) continue;
+      const uint4 v = *reinterpret_cast<const uint4*>(lds + rr * W4_SP + c);
+      __bf16* cp = (__bf16*)ep.c + m * ep.ldc + n;
+      if (full) {
+        st16(cp, v);
+      } else {
+        const __bf16* pv = lds + rr * W4_SP + c;
+        for (int q = 0; q < 8 && n + q < N; ++q) cp[q] = pv[q];
+      }
+    }
+  } else if constexpr (glu_bwd_epi(EPI)) {
+    // the saved e / g chunks of four rows are read before any of them is used
+#pragma unroll
+    for (int g0 = 0; g0 < IT; g0 += GRP) {
+      uint4 ew[GRP], gw[GRP];
+#pragma unroll
+      for (int q = 0; q < GRP; ++q) {
+        const int64_t m = m0 + (g0 + q) * 8 + tid / 32;
+        if (m < M && full) {
+          const int64_t off = m * ep.ld_eg + n;
+          ew[q] = ld16(ep.e + off);
+          gw[q] = ld16(ep.g + off);
+        }
+      }
+#pragma unroll
+      for (int q = 0; q < GRP; ++q) {
+        const int rr = (g0 + q) * 8 + tid / 32;
+        const int64_t m = m0 + rr;
+        if (m >= M || n >= N) continue;
+        const int64_t off = m * ep.ld_eg + n;
+        float dw[8], ev[8], gv[8], hv[8], dfv[8], dev[8];
+        unpack8(*reinterpret_cast<const uint4*>(lds + rr * W4_SP + c), dw);
+        if (full) {
+          unpack8(ew[q], ev);
+          unpack8(gw[q], gv);
+        } else {
+          for (int t = 0; t < 8; ++t) {
+            ev[t] = n + t < N ? (float)ep.e[off + t] : 0.f;
+            gv[t] = n + t < N ? (float)ep.g[off + t] : 0.f;
+          }
+        }
+#pragma unroll
+        for (int t = 0; t < 8; ++t) glu_bwd_vals<EPI>(dw[t], ev[t], gv[t], hv[t], dfv[t], dev[t]);
+        if (full) {
+          st16((__bf16*)ep.c + m * ep.ldc + n, pack8(hv));
+          st16(ep.e + off, pack8(dfv));
+          st16(ep.g + off, pack8(dev));
+        } else {
+          for (int t = 0; t < 8 && n + t < N; ++t) {
+            ((__bf16*)ep.c)[m * ep.ldc + n + t] = (__bf16)hv[t];
+            ep.e[off + t] = (__bf16)dfv[t];
+            ep.g[off + t] = (__bf16)dev[t];
+          }
+        }
+      }
+    }
+  } else {  // EPI_ROPE
+    // d and the lo / hi half are fixed per thread: the positions of all its
+    // rows first, then the cos / sin chunks of four rows at a time
+    const bool rot = n < N && n < ep.rope_cols;
+    const int half = ep.head_dim / 2;
+    const int in_head = (int)(n % ep.head_dim);
+    const bool lo = in_head < half;
+    const int d = in_head % half;
+    const int pc = lo ? c + half : c - half;  // partner chunk (the 256-column tile holds whole heads)
+    int64_t posv[IT];
+#pragma unroll
+    for (int it = 0; it < IT; ++it) {
+      const int64_t m = m0 + it * 8 + tid / 32;
+      posv[it] = (rot && m < M) ? (ep.positions ? ep.positions[m] : m) : -1;
+    }
+#pragma unroll
+    for (int g0 = 0; g0 < IT; g0 += GRP) {
+      uint4 cv[GRP], sv[GRP];
+#pragma unroll
+      for (int q = 0; q < GRP; ++q) {
+        const int64_t pos = posv[g0 + q];
+        if (pos >= 0 && pos < ep.cs_rows) {
+          cv[q] = ld16(ep.cos + pos * ep.cs_ld + d);
+          sv[q] = ld16(ep.sin + pos * ep.cs_ld + d);
+        }
+      }
+#pragma unroll
+      for (int q = 0; q < GRP; ++q) {
+        const int rr = (g0 + q) * 8 + tid / 32;
+        const int64_t m = m0 + rr;
+        if (m >= M || n >= N) continue;
+        float v[8];
+        unpack8(*reinterpret_cast<const uint4*>(lds + rr * W4_SP + c), v);
+        if (rot) {
+          float pv[8], cs[8], sn[8];
+          unpack8(*reinterpret_cast<const uint4*>(lds + rr * W4_SP + pc), pv);
+          const int64_t pos = posv[g0 + q];
+          if (pos >= 0 && pos < ep.cs_rows) {
+            unpack8(cv[q], cs);
+            unpack8(sv[q], sn);
+          } else {
+#pragma unroll
+            for (int t = 0; t < 8; ++t) cs[t] = sn[t] = __builtin_nanf("");
+          }
+#pragma unroll
+          for (int t = 0; t < 8; ++t) v[t] = lo ? v[t] * cs[t] - pv[t] * sn[t] : v[t] * cs[t] + pv[t] * sn[t];
+        }
+        __bf16* cp = (__bf16*)ep.c + m * ep.ldc + n;
+        if (full) st16(cp, pack8(v));
+        else
+          for (int t = 0; t < 8 && n + t < N; ++t) cp[t] = (__bf16)v[t];
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Staged epilogue, dual B (GLU forward): e, g and h = glu(e, g) of one
+// 128-row half at a time (three [128][128] bf16 buffers); h is formed in
+// registers from the fp32 accumulators before anything is rounded.
+// ---------------------------------------------------------------------------
+template <int EPI>
+__device__ __forceinline__ void w4_epilogue_staged_dual(const GemmArgs& args, f32x16 (&acc)[4][4], int64_t m0,
+                                                        int64_t n0, int lane, int wm, int wn, __bf16* lds) {
+  const EpiArgs& ep = args.ep;
+  const int64_t M = args.M, N = args.N;
+  const int tid = threadIdx.x;
+  const int cl = 4 * (lane / 32);
+  __bf16* le = lds;
+  __bf16* lg = lds + 128 * W4_DP;
+  __bf16* lh = lds + 2 * 128 * W4_DP;
+  lds_barrier();  // the main loop's LDS reads are done
+#pragma unroll 1
+  for (int pass = 0; pass < 2; ++pass) {
+    if (pass) lds_barrier();  // pass 0's readers are done with the buffers
+    if (wm == pass) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int row = i * 32 + lane % 32;
+#pragma unroll
+        for (int jp = 0; jp < 2; ++jp)
+#pragma unroll
+          for (int g = 0; g < 4; ++g) {
+            const int col = wn * 64 + 32 * jp + 8 * g + cl;
+            float e[4], gg[4], h[4];
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+              e[q] = acc[i][2 * jp][4 * g + q];
+              gg[q] = acc[i][2 * jp + 1][4 * g + q];
+              h[q] = glu_fwd_h<EPI>(e[q], gg[q]);
+            }
+            *reinterpret_cast<uint2*>(le + row * W4_DP + col) = pack4(e);
+            *reinterpret_cast<uint2*>(lg + row * W4_DP + col) = pack4(gg);
+            *reinterpret_cast<uint2*>(lh + row * W4_DP + col) = pack4(h);
+          }
+      }
+    }
+    lds_barrier();
+    const int64_t mrow0 = m0 + pass * 128;
+#pragma unroll 2
+    for (int it = 0; it < 128 * 16 / 256; ++it) {
+      const int id = it * 256 + tid;
+      const int rr = id / 16, c = (id % 16) * 8;
+      const int64_t m = mrow0 + rr, n = n0 + c;
+      if (m >= M || n >= N) continue;
+      const int o = rr * W4_DP + c;
+      const int64_t off = m * ep.ld_eg + n;
+      __bf16* hp = (__bf16*)ep.c + m * ep.ldc + n;
+      if (n + 8 <= N) {
+        if (ep.e) {  // training saves e and g; inference (e = g = null) stores h only
+          st16(ep.e + off, *reinterpret_cast<const uint4*>(le + o));
+          st16(ep.g + off, *reinterpret_cast<const uint4*>(lg + o));
+        }
+        st16(hp, *reinterpret_cast<const uint4*>(lh + o));
+      } else {
+        for (int q = 0; q < 8 && n + q < N; ++q) {
+          if (ep.e) {
+            ep.e[off + q] = le[o + q];
+            ep.g[off + q] = lg[o + q];
+          }
+          hp[q] = lh[o + q];
+        }
+      }
+    }
+  }
+}
+
+}  // namespace fgemm
