@@ -42,6 +42,7 @@ work per kernel, median per call), scaled to the metric.
 from __future__ import annotations
 
 import argparse
+import ctypes
 import json
 import os
 import statistics
@@ -479,17 +480,21 @@ def bench_ce(args):
     ms, wall = run_steps(args, step, restore)
     bytes_step = V * 2 * (2 * n_valid + n_ign) + 8 * BT
     gbs = rate(bytes_step, ms, 1e9)
-    # sustained over two 2.1 GB logits buffers (the steps' buffer and one more)
+    # sustained over two 2.1 GB logits buffers (the steps' buffer and one
+    # more): the forward's one launch, forge_ce_fwd_reduce (statistics, rows,
+    # dlogits and the reduced loss)
     xbuf.copy_(logits0)
     xb = logits0.clone()
     sets = [xbuf, xb]
     loss1d = torch.empty(BT, device="cuda")
+    lsum = torch.empty((), device="cuda")
     st = L.stream_of(xb)
     flags = L.CE_HAS_GRADIENTS | L.CE_REDUCTION_MEAN
+    ticket = ctypes.c_uint64()
     launch_ms = time_sustained(
-        lambda i: L.forge_ce_fwd(2, sets[i % 2].data_ptr(), V, BT, V, target.data_ptr(), 1, None, loss1d.data_ptr(),
-                                 None, None, None, -100, float(n_valid), float(n_valid), 0.0, 0.0, 0.0, 0.0, flags,
-                                 None, st),
+        lambda i: L.forge_ce_fwd_reduce(2, sets[i % 2].data_ptr(), V, BT, V, target.data_ptr(), 1, loss1d.data_ptr(),
+                                        None, None, None, -100, 0.0, 0.0, 0.0, flags, lsum.data_ptr(), None, None,
+                                        None, L.DTYPE_F32, ctypes.byref(ticket), st),
         max(args.steps, 20))
     del sets
     res = {
@@ -499,7 +504,9 @@ def bench_ce(args):
         "frac_of_hbm_peak": rnd(gbs and gbs / HBM_PEAK_GBS, 4), "algorithmic_bytes_per_step": bytes_step,
         "timing": "cold: each step alone after its logits are restored and a 512 MB read",
         "launch_timing": SUSTAINED_LABEL,
-        "launches_ms": {"forge_ce_fwd": round(launch_ms, 5)},
+        "launches_ms": {"forge_ce_fwd_reduce": round(launch_ms, 5)},
+        "launches_per_step": "forward: forge_ce_fwd_reduce (1); backward: forge_ce_scale, a no-op on the device "
+                             "for grad_output == 1 (1), after torch's implicit ones_like for loss.backward()",
         "roofline": _roof("hbm", bytes_step / (launch_ms * 1e-3) / 1e9, HBM_PEAK_GBS, "GB/s", _traffic("ce_fwd")),
         "copy_ceiling": None,
         "dtype": "bf16",

@@ -170,6 +170,36 @@ int forge_ce_fwd(int dtype, void* logits, int64_t ld, int64_t n_rows, int64_t n_
 int forge_ce_target_stats(const int64_t* target, int64_t target_stride, int64_t n_rows,
                           int64_t ignore_index, int64_t n_cols, int64_t* stats, void* stream);
 
+/* forge_ce_fwd in one launch with the target statistics and the loss
+ * reduction inside it (no class weights: FORGE_CE_HAS_WEIGHT is rejected).
+ * The launch computes the statistics of forge_ce_target_stats itself (n_valid
+ * for the mean; nothing but the per-row losses is written when they are out
+ * of range) and copies them to pinned host memory, tagged with the call's
+ * *ticket; forge_ce_stats_wait(ticket) returns them on the host (for the
+ * reference's bounds asserts) as soon as the launch has computed them,
+ * without waiting for the rest of it.  loss (and z_loss) [n_rows] receive the
+ * per-row values.  With loss_sum non-NULL the launch also stores their fp32
+ * sum there (and z_loss's in z_sum), summed in a fixed order (deterministic),
+ * and, when loss_cast / z_cast are given, the sums rounded to cast_dtype.
+ * The library keeps 64 call slots per device (allocated on the first call):
+ * at most 64 calls may be between launch and forge_ce_stats_wait at once.
+ * Replaces `forge_cross_entropy_kernel` with the `.item()` reads and bounds
+ * asserts before it and the `torch.sum` after it
+ * (kernels/cross_entropy/experiments/v2/cross_entropy_kernel_v2.py:374-387,
+ * 414-441, 451). */
+int forge_ce_fwd_reduce(int dtype, void* logits, int64_t ld, int64_t n_rows, int64_t n_cols,
+                        const int64_t* target, int64_t target_stride,
+                        float* loss, float* z_loss, float* token_accuracy, int64_t* predicted_tokens,
+                        int64_t ignore_index, float lse_square_scale, float label_smoothing, float softcap,
+                        int flags, float* loss_sum, float* z_sum, void* loss_cast, void* z_cast, int cast_dtype,
+                        uint64_t* ticket, void* stream);
+
+/* Host: waits until the launch of `ticket` (forge_ce_fwd_reduce on a stream of
+ * the same device as `stream`) has computed its target statistics, then
+ * stores them in stats[4] (host memory), laid out as forge_ce_target_stats'.
+ * Returns an error if the stream finishes without them. */
+int forge_ce_stats_wait(uint64_t ticket, int64_t* stats, void* stream);
+
 /* x[r, :] *= *grad_output (device scalar of grad_dtype: fp32, bf16 or fp16),
  * in place; a no-op when *grad_output == 1 (the reference's torch.equal
  * skip, :465-467, decided on the device so the host does not wait).

@@ -104,6 +104,13 @@ forge_ce_fwd = _decl(
     + [c_int, c_vp, c_vp],
 )
 forge_ce_target_stats = _decl("forge_ce_target_stats", [c_vp, c_i64, c_i64, c_i64, c_i64, c_vp, c_vp])
+forge_ce_fwd_reduce = _decl(
+    "forge_ce_fwd_reduce",
+    [c_int, c_vp, c_i64, c_i64, c_i64, c_vp, c_i64, c_vp, c_vp, c_vp, c_vp, c_i64]
+    + [c_f32] * 3
+    + [c_int, c_vp, c_vp, c_vp, c_vp, c_int, ctypes.POINTER(ctypes.c_uint64), c_vp],
+)
+forge_ce_stats_wait = _decl("forge_ce_stats_wait", [ctypes.c_uint64, ctypes.POINTER(c_i64), c_vp])
 forge_splitk_reduce = _decl("forge_splitk_reduce", [c_vp, c_i64, c_int, c_i64, c_i64, c_i64, c_vp, c_i64, c_int, c_f32, c_vp])
 forge_ce_scale = _decl("forge_ce_scale", [c_int, c_vp, c_i64, c_i64, c_i64, c_vp, c_int, c_vp])
 forge_sum_f32 = _decl("forge_sum_f32", [c_vp, c_i64, c_vp, c_vp, c_int, c_vp])
@@ -173,7 +180,8 @@ forge_cast_f32_bf16 = _decl("forge_cast_f32_bf16", [c_vp, c_i64, c_vp, c_i64, c_
 EXPORTED = [
     "forge_version", "forge_last_error", "forge_arch_ok",
     "forge_swiglu_fwd", "forge_swiglu_bwd", "forge_geglu_fwd", "forge_geglu_bwd", "forge_rope",
-    "forge_ce_fwd", "forge_ce_target_stats", "forge_ce_scale", "forge_sum_f32",
+    "forge_ce_fwd", "forge_ce_target_stats", "forge_ce_fwd_reduce", "forge_ce_stats_wait", "forge_ce_scale",
+    "forge_sum_f32",
     "forge_gemm", "forge_lora_mlp_gate_up", "forge_lora_mlp_down_bwd", "forge_lora_mlp_glu_bwd",
     "forge_lora_qkv_rope",
     "forge_lora_a", "forge_lora_a_noalloc", "forge_zero", "forge_copy", "forge_cast_f32_bf16", "forge_splitk_reduce",

@@ -9,15 +9,17 @@ writes dloss/dlogits over the logits buffer, which is what backward returns.
 Features: class weights, ignore_index, label smoothing, z-loss, softcap,
 token accuracy, predicted tokens, mean/sum/none reductions.
 
-Device work: `forge_ce_target_stats` (target count and range), `forge_ce_fwd`
-(row kernel, reading the count from the statistics on the device),
-`forge_sum_f32` (loss reduction) and `forge_ce_scale` (grad_output != 1) in
-libforge_hip.so (csrc/cross_entropy.hip).  The host queues the statistics
-kernel and the row kernel back to back, and only then copies the four
-statistics to pinned host memory on a side stream (for the reference's
-bounds assert), so the device does not wait for host work between the two.
-With class weights the host needs the validated count before the launch (as
-the reference), so there it waits for the copy first.
+Device work (libforge_hip.so, csrc/cross_entropy.hip): without class
+weights the forward is ONE launch, `forge_ce_fwd_reduce`: it computes the
+target statistics (count and range), the per-row losses, dlogits in place and
+the reduced loss (fixed-order sum, cast to the logits dtype); the host reads
+the statistics for the reference's bounds asserts with `forge_ce_stats_wait`
+as soon as the launch has them (the launch copies them to pinned host memory
+itself; no event or copy sits between kernels).  With class weights the host
+needs the validated count before the launch, as the reference does:
+`forge_ce_target_stats`, the host check, `forge_ce_fwd`, `forge_sum_f32`.
+The backward is `forge_ce_scale` (a no-op on the device when grad_output is
+1).
 
 Numerics: per-row losses are kept in fp32 and summed in fp32, then cast to the
 logits dtype once (the reference rounds every row to the logits dtype before
@@ -25,6 +27,7 @@ logits dtype once (the reference rounds every row to the logits dtype before
 """
 from __future__ import annotations
 
+import ctypes
 from dataclasses import dataclass
 from typing import Optional
 
@@ -119,8 +122,8 @@ def _cross_entropy_forward_impl(
     out_dtype=None,
 ):
     """Returns (loss, z_loss, token_accuracy, predicted_tokens, _input); loss
-    and z_loss are fp32 unless out_dtype is given (then already cast to it,
-    the cast of a reduced loss fused into the sum kernel)."""
+    and z_loss are fp32 unless out_dtype is given (then a reduced loss is
+    already cast to it, by the launch that sums it)."""
     assert isinstance(return_z_loss, bool), f"return_z_loss must be True or False. Got: {return_z_loss}"
     assert isinstance(return_token_accuracy, bool), (
         f"return_token_accuracy must be True or False. Got: {return_token_accuracy}"
@@ -144,26 +147,6 @@ def _cross_entropy_forward_impl(
     if _input.stride(-1) != 1:
         _input = _input.contiguous()
 
-    stats = ready = None
-    n_non_ignore = 0
-    if BT > 0:
-        stats, ready = _target_stats_launch(target, ignore_index, V)
-    sum_non_ignore_weight = 0.0
-    weight_sum = 0.0
-    if weight is not None:
-        # the weighted sums need validated targets: check first, as the reference does
-        if BT > 0:
-            stats_host, stats_ev = _target_stats_to_host(stats, ready)
-            n_non_ignore = _check_targets(stats_host, stats_ev, V)
-        assert weight.shape[0] == V, f"If given, weight has to be a Tensor of size V. Got: {weight.shape}"
-        assert torch.is_floating_point(weight), (
-            f"If given, weight has to be a Tensor of floating point dtype. Got: {weight.dtype}"
-        )
-        target_mask = target != ignore_index
-        sum_non_ignore_weight = torch.gather(weight, dim=0, index=target.masked_select(target_mask)).sum().item()
-        weight_sum = weight.sum().item()
-        weight = weight.to(torch.float32).contiguous()
-
     flags = 0
     if _input.requires_grad:
         flags |= L.CE_HAS_GRADIENTS
@@ -179,10 +162,53 @@ def _cross_entropy_forward_impl(
         flags |= L.CE_RETURN_PREDICTED
     if reduction == "mean":
         flags |= L.CE_REDUCTION_MEAN
+    reduce = reduction != "none"
+    st = L.stream_of(_input)
+    n_non_ignore = 0
+    loss = z_loss = None
 
-    if BT > 0:
-        # n_non_ignore (unweighted) is read by the kernel from `stats`
-        st = L.stream_of(_input)
+    if BT > 0 and weight is None:
+        # one launch: target statistics, row losses, dlogits and the reduced
+        # loss; the host reads the statistics (for the bounds asserts) as soon
+        # as the launch has them, while the rest of it runs
+        cast = None if out_dtype in (None, torch.float32) else out_dtype
+        if reduce:
+            loss = torch.empty((), dtype=torch.float32, device=dev)
+            loss_c = torch.empty((), dtype=cast, device=dev) if cast is not None else None
+            if return_z_loss:
+                z_loss = torch.empty((), dtype=torch.float32, device=dev)
+                z_c = torch.empty((), dtype=cast, device=dev) if cast is not None else None
+        ticket = ctypes.c_uint64()
+        L.check(
+            L.forge_ce_fwd_reduce(
+                L.dtype_code(_input.dtype), _input.data_ptr(), _input.stride(-2), BT, V,
+                target.data_ptr(), target.stride(-1),
+                loss_1d.data_ptr(), L.ptr(z_loss_1d), L.ptr(token_accuracy_1d), L.ptr(predicted_tokens_1d),
+                int(ignore_index), float(lse_square_scale), float(label_smoothing), float(softcap or 0.0), flags,
+                L.ptr(loss), L.ptr(z_loss), L.ptr(loss_c) if reduce else None,
+                L.ptr(z_c) if reduce and return_z_loss else None,
+                L.dtype_code(cast) if cast is not None else L.DTYPE_F32, ctypes.byref(ticket), st,
+            ),
+            "forge_ce_fwd_reduce",
+        )
+        n_non_ignore = _wait_targets(ticket.value, V, st)
+        if reduce and cast is not None:
+            loss = loss_c
+            z_loss = z_c if return_z_loss else None
+    elif BT > 0:
+        # class weights: the weighted sums need validated targets first, as in
+        # the reference
+        stats, ready = _target_stats_launch(target, ignore_index, V)
+        stats_host, stats_ev = _target_stats_to_host(stats, ready)
+        n_non_ignore = _check_targets(stats_host, stats_ev, V)
+        assert weight.shape[0] == V, f"If given, weight has to be a Tensor of size V. Got: {weight.shape}"
+        assert torch.is_floating_point(weight), (
+            f"If given, weight has to be a Tensor of floating point dtype. Got: {weight.dtype}"
+        )
+        target_mask = target != ignore_index
+        sum_non_ignore_weight = torch.gather(weight, dim=0, index=target.masked_select(target_mask)).sum().item()
+        weight_sum = weight.sum().item()
+        weight = weight.to(torch.float32).contiguous()
         L.check(
             L.forge_ce_fwd(
                 L.dtype_code(_input.dtype), _input.data_ptr(), _input.stride(-2), BT, V,
@@ -194,21 +220,34 @@ def _cross_entropy_forward_impl(
             ),
             "forge_ce_fwd",
         )
-        if weight is None:
-            # the kernel is already queued (and writes nothing if this fails)
-            stats_host, stats_ev = _target_stats_to_host(stats, ready)
-            n_non_ignore = _check_targets(stats_host, stats_ev, V)
+    elif weight is not None:
+        assert weight.shape[0] == V, f"If given, weight has to be a Tensor of size V. Got: {weight.shape}"
+        assert torch.is_floating_point(weight), (
+            f"If given, weight has to be a Tensor of floating point dtype. Got: {weight.dtype}"
+        )
 
-    if reduction == "none":
+    if not reduce:
         loss = loss_1d
         z_loss = z_loss_1d if return_z_loss else None
         token_accuracy = token_accuracy_1d if return_token_accuracy else None
     else:
-        loss = _sum_f32(loss_1d, out_dtype)
-        z_loss = _sum_f32(z_loss_1d, out_dtype) if return_z_loss else None
+        if loss is None:  # weighted path, or no rows
+            loss = _sum_f32(loss_1d, out_dtype)
+            z_loss = _sum_f32(z_loss_1d, out_dtype) if return_z_loss else None
         token_accuracy = torch.sum(token_accuracy_1d) / n_non_ignore if return_token_accuracy else None
     predicted_tokens = predicted_tokens_1d if return_predicted_tokens else None
     return loss, z_loss, token_accuracy, predicted_tokens, _input
+
+
+def _wait_targets(ticket: int, n_cols: int, stream) -> int:
+    """The reference's bounds asserts (:382-387) on the statistics the
+    forge_ce_fwd_reduce launch of `ticket` computed; returns n_non_ignore."""
+    host = (ctypes.c_int64 * 4)()
+    L.check(L.forge_ce_stats_wait(ticket, host, stream), "forge_ce_stats_wait")
+    n, tmin, tmax, _ = host
+    assert tmax < n_cols, f"Target {tmax} is out of bounds. Expected < {n_cols}"
+    assert tmin >= 0, f"Target {tmin} is out of bounds. Expected >= 0"
+    return int(n)
 
 
 def _sum_f32(x: torch.Tensor, out_dtype=None) -> torch.Tensor:

@@ -10,6 +10,8 @@ Tolerances: loss within 1e-3 relative (fp32 internal value) and exact
 rounding to the logits dtype; gradients fp32 1e-5, bf16/fp16 2e-2; labels,
 ignore rows, predicted tokens and accuracy bit-exact.
 """
+import ctypes
+
 import pytest
 import torch
 
@@ -180,6 +182,120 @@ def test_c_abi_skips_rows_with_out_of_range_targets():
     _, _, rows, _, _, g = ce_reference(ref_x[[0, 3]].cpu(), t[[0, 3]].cpu(), reduction="none")
     torch.testing.assert_close(loss[[0, 3]].cpu(), rows, rtol=1e-5, atol=1e-6)
     torch.testing.assert_close(x[[0, 3]].cpu(), g, rtol=1e-5, atol=1e-6)
+
+
+def _reduce_call(x, t, flags, loss1d, loss_sum, z1d=None, z_sum=None, cast=None, z_cast=None, ignore=-100):
+    """forge_ce_fwd_reduce through the C-ABI, then forge_ce_stats_wait;
+    returns the host statistics [n_valid, min, max, in_range]."""
+    BT, V = x.shape
+    ticket = ctypes.c_uint64()
+    st = L.stream_of(x)
+    L.check(L.forge_ce_fwd_reduce(L.dtype_code(x.dtype), x.data_ptr(), x.stride(0), BT, V, t.data_ptr(), 1,
+                                  loss1d.data_ptr(), L.ptr(z1d), None, None, ignore, 1e-4 if z1d is not None else 0.0,
+                                  0.0, 0.0, flags, L.ptr(loss_sum), L.ptr(z_sum), L.ptr(cast), L.ptr(z_cast),
+                                  L.dtype_code(cast.dtype) if cast is not None else L.DTYPE_F32,
+                                  ctypes.byref(ticket), st), "forge_ce_fwd_reduce")
+    stats = (ctypes.c_int64 * 4)()
+    L.check(L.forge_ce_stats_wait(ticket.value, stats, st), "forge_ce_stats_wait")
+    return list(stats)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("dtype,vocab", [(torch.bfloat16, 4096), (torch.float32, 300)])
+def test_fwd_reduce_sum_statistics_and_slot_reuse(dtype, vocab):
+    """forge_ce_fwd_reduce (one launch: statistics, rows, dlogits, reduced
+    loss).  The host statistics are the targets' count and masked range; the
+    reduced loss is the fixed-order fp32 sum of the per-row losses the launch
+    also writes (checked against a float64 sum of them, and against the
+    oracle), and it is bit-identical over 70 calls: more than the library's 64
+    call slots, so every slot is reused and its done count must have been
+    reset by the previous launch on it.  bf16 [*, 4096] runs the resident
+    engine, fp32 the streaming one."""
+    BT = 301
+    logits, target = _case(BT, vocab, dtype, scalar=2.0, seed=7)
+    target[::9] = -100
+    n_valid = int((target != -100).sum())
+    masked = torch.where(target != -100, target, torch.zeros_like(target))
+    ref_loss, ref_z, ref_rows, _, _, ref_grad = ce_reference(logits, target, reduction="mean", lse_square_scale=1e-4)
+    t = target.cuda()
+    flags = L.CE_HAS_GRADIENTS | L.CE_REDUCTION_MEAN | L.CE_RETURN_Z_LOSS
+    sums = set()
+    for i in range(70):
+        x = logits.cuda()
+        loss1d = torch.empty(BT, device="cuda")
+        z1d = torch.empty(BT, device="cuda")
+        s, zs = torch.empty((), device="cuda"), torch.empty((), device="cuda")
+        cast = torch.empty((), dtype=torch.bfloat16, device="cuda")
+        stats = _reduce_call(x, t, flags, loss1d, s, z1d, zs, cast)
+        assert stats == [n_valid, int(masked.min()), int(masked.max()), 1]
+        torch.cuda.synchronize()
+        sums.add((s.item(), zs.item(), cast.float().item()))
+        if i == 0:
+            torch.testing.assert_close(s.double().cpu(), loss1d.double().sum().cpu(), rtol=1e-6, atol=0)
+            torch.testing.assert_close(zs.double().cpu(), z1d.double().sum().cpu(), rtol=1e-6, atol=0)
+            assert cast.item() == s.to(torch.bfloat16).item()
+            torch.testing.assert_close(loss1d.cpu(), ref_rows.float(), rtol=1e-4, atol=1e-6)
+            torch.testing.assert_close(s.cpu(), ref_loss.float(), rtol=1e-4, atol=0)
+            torch.testing.assert_close(x.float().cpu(), ref_grad.float(), rtol=GTOL[dtype], atol=GTOL[dtype])
+    assert len(sums) == 1
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("dtype,vocab", [(torch.bfloat16, 4096), (torch.float32, 300)])
+def test_fwd_reduce_out_of_range_touches_nothing_and_next_call_is_clean(dtype, vocab):
+    """A target out of range: the launch reports in_range = 0 and a masked
+    min / max that names it, leaves the logits untouched, and still resets
+    its slot: the following calls (all 64 slots, then this one's again) give
+    the correct loss."""
+    BT = 64
+    logits, target = _case(BT, vocab, dtype, seed=3)
+    bad = target.clone()
+    bad[5] = vocab + 3
+    x = logits.cuda()
+    loss1d, s = torch.empty(BT, device="cuda"), torch.empty((), device="cuda")
+    stats = _reduce_call(x, bad.cuda(), L.CE_HAS_GRADIENTS | L.CE_REDUCTION_MEAN, loss1d, s)
+    assert stats[0] == BT and stats[2] == vocab + 3 and stats[3] == 0
+    torch.cuda.synchronize()
+    assert torch.equal(x.cpu(), logits)
+    ref_loss = ce_reference(logits, target, reduction="sum")[0]
+    for _ in range(65):
+        x = logits.cuda()
+        stats = _reduce_call(x, target.cuda(), 0, loss1d, s)
+        assert stats[3] == 1
+        torch.testing.assert_close(s.cpu(), ref_loss.float(), rtol=1e-4, atol=0)
+
+
+@pytest.mark.gpu
+def test_fwd_reduce_concurrent_streams():
+    """Calls on two streams at once use different call slots: both sums are
+    right."""
+    BT, V = 2048, 4096
+    la, ta = _case(BT, V, torch.bfloat16, seed=11)
+    lb, tb = _case(BT, V, torch.bfloat16, seed=12)
+    ra = ce_reference(la, ta, reduction="sum")[0]
+    rb = ce_reference(lb, tb, reduction="sum")[0]
+    s1, s2 = torch.cuda.Stream(), torch.cuda.Stream()
+    xa, xb, tga, tgb = la.cuda(), lb.cuda(), ta.cuda(), tb.cuda()
+    out = []
+    torch.cuda.synchronize()
+    for _ in range(4):
+        res = []
+        for x, t, s in ((xa.clone(), tga, s1), (xb.clone(), tgb, s2)):
+            with torch.cuda.stream(s):
+                l1, sm = torch.empty(BT, device="cuda"), torch.empty((), device="cuda")
+                ticket = ctypes.c_uint64()
+                L.check(L.forge_ce_fwd_reduce(2, x.data_ptr(), V, BT, V, t.data_ptr(), 1, l1.data_ptr(), None, None,
+                                              None, -100, 0.0, 0.0, 0.0, 0, sm.data_ptr(), None, None, None,
+                                              L.DTYPE_F32, ctypes.byref(ticket), L.stream_of(x)), "reduce")
+                res.append((ticket.value, sm, s))
+        for ticket, sm, s in res:
+            st = (ctypes.c_int64 * 4)()
+            L.check(L.forge_ce_stats_wait(ticket, st, s.cuda_stream), "wait")
+        torch.cuda.synchronize()
+        out.append((res[0][1].cpu(), res[1][1].cpu()))
+    for a, b in out:
+        torch.testing.assert_close(a, ra.float(), rtol=1e-4, atol=0)
+        torch.testing.assert_close(b, rb.float(), rtol=1e-4, atol=0)
 
 
 @pytest.mark.gpu
