@@ -4,19 +4,25 @@
                     [--no-cpu-baseline] [--only-launches]
 
 A step is one fwd+bwd pass of a kernel's drop-in autograd path over one batch
-of synthetic input already resident in HBM.  Every
-step is timed cold and alone: a read of a 512 MB buffer (twice the 256 MB
-Infinity Cache) precedes it outside the timed interval, so no input of the
-step is cached when it starts, and HIP events bracket the step (the
-reference's RoPE benchmark flushes a 256 MB buffer before every rep,
-kernels/rope/benchmarks/bench_v3.py:310, 371; its CE benchmark times a rep
-alone, kernels/cross_entropy/benchmarks/bench_cross_entropy.py:197-210).
-Reuse inside a step (the backward re-reading what the forward just touched)
-is part of the step.  Inputs a step overwrites (SwiGLU's fast backward,
-RMSNorm's in-place backward) are cloned per step beforehand; the 2.1 GB CE
-logits are restored into one buffer before each step.  The HBM-bound legs
-also report `warm`: the same steps back to back in one event bracket, with
-inputs reused from step to step (partly served by the Infinity Cache).
+of synthetic input already resident in HBM.  The
+HBM-bound legs (RoPE, SwiGLU, GeGLU, RMSNorm) time their steps sustained:
+steps back to back, step i on input set i % K where the K sets exceed 1.2 GB
+(several times the 256 MB Infinity Cache), so no input is cached when a step
+reads it and each step's writes drain to HBM during the next one; one pair of
+HIP events brackets all the steps, which the host queues behind a GPU delay
+sized to its own enqueue time, so the device runs them without host gaps
+(the host-inclusive `wall_ms_per_step` is reported beside).  Inputs a step
+overwrites (the in-place
+backwards) become that set's next inputs (finite values; the kernels' cost
+does not depend on them).  These legs also report `cold`: each step alone
+after a read of a 512 MB buffer (the reference's RoPE benchmark flushes a
+256 MB buffer before every rep, kernels/rope/benchmarks/bench_v3.py:310,
+371), whose writes can still sit in the Infinity Cache when its end event
+fires.  The cross-entropy and MFMA-bound legs time each step cold and alone
+(the reference's CE benchmark times a rep alone,
+kernels/cross_entropy/benchmarks/bench_cross_entropy.py:197-210); the 2.1 GB
+CE logits are restored into one buffer before each step, outside the timed
+interval.
 
 The launch loops behind `roofline` time one launch of the dominant kernel.
 For the HBM-bound legs they are sustained: launches back to back over
@@ -244,14 +250,55 @@ def run_steps(args, step_fn, restore=None):
     return time_steps_cold(step_fn, args.steps, args.warmup, restore)
 
 
-def warm_steps(args, step_fn, bytes_step):
-    """The HBM legs' warm figure: steps back to back with inputs reused
-    across steps (labelled, not the claim)."""
+STEP_SUSTAINED_LABEL = ("sustained steps: back to back, step i on input set i % K, the K sets over 1.2 GB "
+                        "(nothing cached; each step's writes drain during the next)")
+
+
+def sustained_steps(args, step_fn):
+    """The HBM legs' step figure: steps back to back, step_fn(i) on its
+    input set i % K (the K sets exceed 1.2 GB, several times the 256 MB
+    Infinity Cache, so no input is cached and the writes of each step drain
+    to HBM during the next), one event pair around all of them.  The host
+    queues the steps behind a GPU delay (torch.cuda._sleep) sized to its own
+    measured enqueue time, so the device runs them without host gaps, as in
+    a training loop whose host runs ahead; wall ms per step (host-inclusive,
+    steps enqueued one after another) is reported beside.  Returns (ms per
+    step, wall ms per step), or (None, None) with --only-launches."""
+    import torch
+
+    if args.only_launches:
+        return None, None
+    for i in range(args.warmup):
+        step_fn(i)
+    _sync()
+    t0 = time.perf_counter()
+    for i in range(args.warmup, 2 * args.warmup):
+        step_fn(i)
+    _sync()
+    wall = (time.perf_counter() - t0) * 1e3 / args.warmup
+    base = 2 * args.warmup
+    # GPU delay covering the enqueue of all steps (1.5x the measured host
+    # time per step, at most 200 ms; the sleep counts shader clocks)
+    delay_s = min(0.2, 1.5 * wall * 1e-3 * args.steps + 1e-3)
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    torch.cuda._sleep(int(delay_s * 2.5e9))
+    start.record()
+    for j in range(args.steps):
+        step_fn(base + j)
+    end.record()
+    _sync()
+    return start.elapsed_time(end) / args.steps, wall
+
+
+def cold_figure(args, step_fn, bytes_step, restore=None):
+    """Each step alone after a 512 MB read (labelled, not the claim): its
+    writes can still sit in the Infinity Cache when its end event fires."""
     if args.only_launches:
         return None
-    ms, _ = time_steps(step_fn, args.steps, args.warmup)
+    ms, _ = time_steps_cold(step_fn, args.steps, args.warmup, restore)
     return {"value": rate(bytes_step, ms, 1e9), "unit": "GB/s", "ms_per_step": rnd(ms, 5),
-            "timing": "steps back to back, inputs reused across steps (partly cached)"}
+            "timing": "cold: each step alone after a 512 MB read"}
 
 
 def rate(amount, ms, scale):
@@ -305,28 +352,24 @@ def bench_swiglu(args):
     gate0 = torch.randn(R, C, device="cuda", generator=g)
     up0 = torch.randn(R, C, device="cuda", generator=g)
     dout = torch.randn(R, C, device="cuda", generator=g)
-    total = args.warmup + args.steps
-    gates, ups = [], []
-
-    def fresh():  # the backward overwrites its inputs: one clone pair per step
-        gates[:] = [gate0.clone() for _ in range(total)]
-        ups[:] = [up0.clone() for _ in range(total)]
+    bytes_step = 8 * n * 4  # fwd 3 tensors + bwd 5 tensors, fp32
+    # input sets (gate, up, dout) for the steps; the backward writes the
+    # gradients over gate / up (the reference's in-place contract), which the
+    # set's next step then takes as its input (finite values; the kernels'
+    # cost does not depend on them)
+    ks = n_sets(4 * n * 4)  # gate, up, dout read + out written per step
+    ssets = [(gate0.clone().requires_grad_(True), up0.clone().requires_grad_(True), dout.clone())
+             for _ in range(ks)]
 
     def step(i):
-        gi = gates[i].requires_grad_(True)
-        ui = ups[i].requires_grad_(True)
-        out = swiglu(gi, ui)
-        out.backward(dout)
-        gates[i] = ups[i] = None
+        gi, ui, di = ssets[i % ks]
+        gi.grad = ui.grad = None
+        swiglu(gi, ui).backward(di)
 
-    bytes_step = 8 * n * 4  # fwd 3 tensors + bwd 5 tensors, fp32
-    fresh()
-    ms, wall = run_steps(args, step)
+    ms, wall = sustained_steps(args, step)
     gbs = rate(bytes_step, ms, 1e9)
-    fresh()
-    warm = warm_steps(args, step, bytes_step)
-    gates.clear()
-    ups.clear()
+    cold = cold_figure(args, step, bytes_step)
+    del ssets
     # dominant kernel: backward (5 tensor passes), sustained over rotating
     # sets of (gate, up, dout, out)
     bwd_bytes = 5 * n * 4
@@ -351,7 +394,7 @@ def bench_swiglu(args):
                    "down_multiplier": 1.0, "preserve_inputs": False},
         "value": gbs, "unit": "GB/s", "ms_per_step": rnd(ms, 5), "wall_ms_per_step": rnd(wall, 5),
         "frac_of_hbm_peak": rnd(gbs and gbs / HBM_PEAK_GBS, 4), "algorithmic_bytes_per_step": bytes_step,
-        "timing": "cold: each step alone after a 512 MB read", "warm": warm, "launch_timing": SUSTAINED_LABEL,
+        "timing": STEP_SUSTAINED_LABEL, "cold": cold, "launch_timing": SUSTAINED_LABEL,
         "launches_ms": {"forge_swiglu_fwd": round(fwd_ms, 5), "forge_swiglu_bwd": round(bwd_ms, 5)},
         "roofline": _roof("hbm", bwd_bytes / (bwd_ms * 1e-3) / 1e9, HBM_PEAK_GBS, "GB/s", _traffic("swiglu_bwd")),
         "copy_ceiling": copy_ceiling(args, bwd_bytes),
@@ -397,19 +440,26 @@ def bench_rope(args):
     qv, kv = q.transpose(1, 2), k.transpose(1, 2)
     dqv, dkv = dq.transpose(1, 2), dk.transpose(1, 2)
 
-    def step(i):
-        c, s = tabs[i % 2]
-        qi = qv.detach().requires_grad_(True)
-        ki = kv.detach().requires_grad_(True)
-        oq, ok = apply_rope(qi, ki, c, s)
-        torch.autograd.backward((oq, ok), (dqv, dkv))
-
-    ms, wall = run_steps(args, step)
     elems = q.numel() + k.numel()
     bytes_dir = 2 * elems * 2 + 2 * S * D * 2  # read+write Q,K + cos/sin (the reference's formula)
     bytes_step = 2 * bytes_dir
+    # input sets (q, k, dq, dk) for the steps, HF transpose(1, 2) views of
+    # BSHD memory; the base alternates
+    ks = n_sets(bytes_step)
+    ssets = [tuple(t.clone().transpose(1, 2) for t in (q, k, dq, dk)) for _ in range(ks)]
+
+    def step(i):
+        c, s = tabs[i % 2]
+        qs, kss, dqs, dks = ssets[i % ks]
+        qi = qs.detach().requires_grad_(True)
+        ki = kss.detach().requires_grad_(True)
+        oq, ok = apply_rope(qi, ki, c, s)
+        torch.autograd.backward((oq, ok), (dqs, dks))
+
+    ms, wall = sustained_steps(args, step)
     gbs = rate(bytes_step, ms, 1e9)
-    warm = warm_steps(args, step, bytes_step)
+    cold = cold_figure(args, step, bytes_step)
+    del ssets
     # one direction, sustained over rotating sets of (q, k, q_out, k_out),
     # each a fresh HF transpose(1, 2) view of BSHD memory; the base and the
     # direction alternate as in the steps
@@ -430,7 +480,7 @@ def bench_rope(args):
                    "layout": "BSHD memory, HF transpose(1,2) view", "bases": [10000, 500000]},
         "value": gbs, "unit": "GB/s", "ms_per_step": rnd(ms, 5), "wall_ms_per_step": rnd(wall, 5),
         "frac_of_hbm_peak": rnd(gbs and gbs / HBM_PEAK_GBS, 4), "algorithmic_bytes_per_step": bytes_step,
-        "timing": "cold: each step alone after a 512 MB read", "warm": warm, "launch_timing": SUSTAINED_LABEL,
+        "timing": STEP_SUSTAINED_LABEL, "cold": cold, "launch_timing": SUSTAINED_LABEL,
         "launches_ms": {"forge_rope": round(launch_ms, 5)},
         "roofline": _roof("hbm", bytes_dir / (launch_ms * 1e-3) / 1e9, HBM_PEAK_GBS, "GB/s", _traffic("rope")),
         "copy_ceiling": copy_ceiling(args, bytes_dir),
@@ -983,27 +1033,22 @@ def bench_geglu(args):
     gate0 = torch.randn(R, C, device="cuda", generator=g).to(bf)
     up0 = torch.randn(R, C, device="cuda", generator=g).to(bf)
     dout = torch.randn(R, C, device="cuda", generator=g).to(bf)
-    total = args.warmup + args.steps
-    gates, ups = [], []
-
-    def fresh():  # the backward overwrites its inputs: one clone pair per step
-        gates[:] = [gate0.clone() for _ in range(total)]
-        ups[:] = [up0.clone() for _ in range(total)]
+    bytes_step = 8 * n * 2  # fwd 3 tensors + bwd 5 tensors, bf16
+    # input sets (gate, up, dout); the backward's in-place gradients become
+    # the set's next inputs (finite; the cost does not depend on the values)
+    ks = n_sets(4 * n * 2)
+    ssets = [(gate0.clone().requires_grad_(True), up0.clone().requires_grad_(True), dout.clone())
+             for _ in range(ks)]
 
     def step(i):
-        gi = gates[i].requires_grad_(True)
-        ui = ups[i].requires_grad_(True)
-        geglu(gi, ui, "tanh").backward(dout)
-        gates[i] = ups[i] = None
+        gi, ui, di = ssets[i % ks]
+        gi.grad = ui.grad = None
+        geglu(gi, ui, "tanh").backward(di)
 
-    bytes_step = 8 * n * 2  # fwd 3 tensors + bwd 5 tensors, bf16
-    fresh()
-    ms, wall = run_steps(args, step)
+    ms, wall = sustained_steps(args, step)
     gbs = rate(bytes_step, ms, 1e9)
-    fresh()
-    warm = warm_steps(args, step, bytes_step)
-    gates.clear()
-    ups.clear()
+    cold = cold_figure(args, step, bytes_step)
+    del ssets
     # the backward, sustained over rotating sets of (gate, up, dout)
     k = n_sets(5 * n * 2)
     sets = [(gate0.clone(), up0.clone(), dout.clone()) for _ in range(k)]
@@ -1020,7 +1065,7 @@ def bench_geglu(args):
         "config": {"workload": "geglu_fwd_bwd", "dtype": "bf16", "shape": [R, C], "approximate": "tanh"},
         "value": gbs, "unit": "GB/s", "ms_per_step": rnd(ms, 5), "wall_ms_per_step": rnd(wall, 5),
         "frac_of_hbm_peak": rnd(gbs and gbs / HBM_PEAK_GBS, 4), "algorithmic_bytes_per_step": bytes_step,
-        "timing": "cold: each step alone after a 512 MB read", "warm": warm, "launch_timing": SUSTAINED_LABEL,
+        "timing": STEP_SUSTAINED_LABEL, "cold": cold, "launch_timing": SUSTAINED_LABEL,
         "launches_ms": {"forge_geglu_bwd": round(bwd_ms, 5)},
         "roofline": _roof("hbm", 5 * n * 2 / (bwd_ms * 1e-3) / 1e9, HBM_PEAK_GBS, "GB/s", _traffic("geglu_bwd")),
         "copy_ceiling": copy_ceiling(args, 5 * n * 2),
@@ -1053,25 +1098,22 @@ def bench_rmsnorm(args):
     x = torch.randn(R, H, device="cuda", generator=g).to(bf).requires_grad_(True)
     w = (1 + 0.1 * torch.randn(H, device="cuda", generator=g)).to(bf).requires_grad_(True)
     dy0 = torch.randn(R, H, device="cuda", generator=g).to(bf)
-    total = args.warmup + args.steps
-    dys = []
-
-    def fresh():  # the in-place backward overwrites dy with dx: one clone per step
-        dys[:] = [dy0.clone() for _ in range(total)]
+    bytes_step = bytes_fwd_bwd(R, H)
+    # input sets (x, dy); the in-place backward writes dx over dy, which the
+    # set's next step takes as its upstream gradient
+    ks = n_sets(3 * R * H * 2)  # x, dy read + y written per step
+    ssets = [(x.detach().clone().requires_grad_(True), dy0.clone()) for _ in range(ks)]
 
     def step(i):
-        x.grad = None  # a training step after zero_grad(set_to_none=True)
+        xs, dys = ssets[i % ks]
+        xs.grad = None  # a training step after zero_grad(set_to_none=True)
         w.grad = None
-        apply_rmsnorm_v4(x, w, 1e-6, 0.0, "llama", in_place=True).backward(dys[i])
-        dys[i] = None
+        apply_rmsnorm_v4(xs, w, 1e-6, 0.0, "llama", in_place=True).backward(dys)
 
-    bytes_step = bytes_fwd_bwd(R, H)
-    fresh()
-    ms, wall = run_steps(args, step)
+    ms, wall = sustained_steps(args, step)
     gbs = rate(bytes_step, ms, 1e9)
-    fresh()
-    warm = warm_steps(args, step, bytes_step)
-    dys.clear()
+    cold = cold_figure(args, step, bytes_step)
+    del ssets
     # dominant kernel: the backward (reads x and dy, writes dx over dy, dw partials)
     xd, wd = x.detach(), w.detach()
     rstd = torch.empty(R, device="cuda")
@@ -1098,7 +1140,7 @@ def bench_rmsnorm(args):
                    "offset": 0.0, "in_place": True, "weight_grad": True},
         "value": gbs, "unit": "GB/s", "ms_per_step": rnd(ms, 5), "wall_ms_per_step": rnd(wall, 5),
         "frac_of_hbm_peak": rnd(gbs and gbs / HBM_PEAK_GBS, 4), "algorithmic_bytes_per_step": bytes_step,
-        "timing": "cold: each step alone after a 512 MB read", "warm": warm, "launch_timing": SUSTAINED_LABEL,
+        "timing": STEP_SUSTAINED_LABEL, "cold": cold, "launch_timing": SUSTAINED_LABEL,
         "launches_ms": {"forge_rmsnorm_bwd": round(bwd_ms, 5)},
         "roofline": _roof("hbm", bwd_bytes / (bwd_ms * 1e-3) / 1e9, HBM_PEAK_GBS, "GB/s", _traffic("rmsnorm_bwd")),
         "copy_ceiling": copy_ceiling(args, bwd_bytes),
@@ -1171,7 +1213,7 @@ def main():
         "data": "synthetic",
         "config": head["config"],
         "timing": head.get("timing"),
-        "warm": head.get("warm"),
+        "cold": head.get("cold"),
         "roofline": head["roofline"],
         "copy_ceiling": head.get("copy_ceiling"),
         "cpu_baseline": head.get("cpu_baseline"),

@@ -10,11 +10,12 @@
 // [2048, 11008] 5.65 -> 5.82 TB/s with 2 vectors per thread and no grid cap
 // (was 4 vectors, 8192 workgroups); GeGLU bf16 [4096, 24576] 4.9 -> 5.65
 // TB/s with 1 vector (its GELU math holds more registers per vector).
-// Loads are ordinary (the backward re-reads gate/up right after the forward,
-// largely from the Infinity Cache); stores are nontemporal, so the outputs do
-// not displace those lines and the next kernel does not pay their write-back
-// (measured on MI355X in a SwiGLU fwd+bwd loop at [2048, 11008] fp32:
-// 142 -> 135 us per step).
+// Loads and stores are nontemporal: every operand is touched once per
+// launch.  In a training step the backward runs long after the forward, so
+// nothing it reads is still cached; measured on MI355X over rotating buffer
+// sets (nothing cached, as in training) at SwiGLU [2048, 11008] fp32,
+// nontemporal loads take the backward from 84.9 to 73.0 us (5.31 -> 6.18
+// TB/s) and the forward from 47.4 to 43.0 us.
 //
 // An activation policy Act provides, in fp32 registers with rounding to the
 // storage type T exactly where its reference materialises a tensor:
@@ -63,7 +64,7 @@ __global__ __launch_bounds__(kBlock) void glu_fwd_kernel(
         const T* gp = gate + ri[u] * ld_in + ci[u];
         const T* up_ = up + ri[u] * ld_in + ci[u];
         if constexpr (VEC * sizeof(T) == 16) {
-          Vec16<T> a = load16(gp), b = load16(up_);
+          Vec16<T> a = load16_nt(gp), b = load16_nt(up_);
 #pragma unroll
           for (int j = 0; j < VEC; ++j) { gv[u][j] = a.v[j]; uv[u][j] = b.v[j]; }
         } else {
@@ -114,7 +115,7 @@ __global__ __launch_bounds__(kBlock) void glu_bwd_kernel(
         const T* gp = gate + ri[u] * ld_in + ci[u];
         const T* up_ = up + ri[u] * ld_in + ci[u];
         if constexpr (VEC * sizeof(T) == 16) {
-          Vec16<T> a = load16(dp), b = load16(gp), c = load16(up_);
+          Vec16<T> a = load16_nt(dp), b = load16_nt(gp), c = load16_nt(up_);
 #pragma unroll
           for (int j = 0; j < VEC; ++j) { dv[u][j] = a.v[j]; gv[u][j] = b.v[j]; uv[u][j] = c.v[j]; }
         } else {
