@@ -35,7 +35,10 @@
 // dw = a fixed-order column sum of the partial rows (one launch), rounded
 // once to the weight dtype: deterministic, no atomics.  dx may alias dy (in
 // place): every thread reads its dy elements before it writes the dx
-// elements at the same addresses.
+// elements at the same addresses.  The 16-byte row loads and stores are
+// nontemporal (each row is touched once per launch): backward bf16
+// [8192, 4096] over rotating buffers (nothing cached) 46.0 -> 43.3 us on
+// MI355X.
 #include <type_traits>
 
 #include "common.h"
@@ -91,7 +94,7 @@ __device__ __forceinline__ void store_vec(T* p, const A (&o)[VEC]) {
     Vec16<T> v;
 #pragma unroll
     for (int q = 0; q < VEC; ++q) v.v[q] = st<T, A>(o[q]);
-    *reinterpret_cast<uint4*>(p) = v.raw;
+    store16_nt(p, v);
   } else {
     p[0] = st<T, A>(o[0]);
   }
@@ -350,7 +353,7 @@ __device__ __forceinline__ void store_n(TY* p, const A (&o)[VEC]) {
       Vec16<TY> v;
 #pragma unroll
       for (int q = 0; q < PER; ++q) v.v[q] = st<TY, A>(o[k * PER + q]);
-      *reinterpret_cast<uint4*>(p + k * PER) = v.raw;
+      store16_nt(p + k * PER, v);
     }
   } else {
 #pragma unroll
@@ -369,7 +372,7 @@ struct Pk {
 template <class T, int VEC>
 __device__ __forceinline__ void pk_load(const T* p, Pk<T, VEC>& o) {
   if constexpr (VEC * sizeof(T) == 16) {
-    const uint4 v = *reinterpret_cast<const uint4*>(p);
+    const u32x4_t v = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(p));
     o.w[0] = v.x; o.w[1] = v.y; o.w[2] = v.z; o.w[3] = v.w;
   } else if constexpr (sizeof(T) == 2) {
     o.w[0] = *reinterpret_cast<const uint16_t*>(p);
@@ -738,6 +741,45 @@ __global__ __launch_bounds__(64 * kColsumWaves) void colsum_kernel(const A* part
   }
 }
 
+// fp32 partials, H a multiple of 16 with 16-byte aligned rows: 16 columns
+// per workgroup, so a 4096-column sum spreads over 256 workgroups (one per
+// CU) instead of 64.  Thread (ty, tx) (64 row groups x 4 float4 columns)
+// adds the consecutive partial rows ty ceil(n/64) .. in row order, 8 loads
+// in flight; the 64 group totals are then added in group order.  Fixed
+// order: deterministic.
+template <class TO>
+__global__ __launch_bounds__(256) void colsum16_kernel(const float* part, int64_t n, int64_t H, TO* out) {
+  __shared__ float red[64][17];
+  const int tx = threadIdx.x & 3, ty = threadIdx.x >> 2;
+  const int64_t c = (int64_t)blockIdx.x * 16 + tx * 4;
+  const int64_t per = (n + 63) / 64;
+  const int64_t p0 = ty * per, p1 = p0 + per < n ? p0 + per : n;
+  float4 s = make_float4(0.f, 0.f, 0.f, 0.f);
+  for (int64_t p = p0; p < p1; p += 8) {
+    float4 v[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k)
+      v[k] = p + k < p1 ? *reinterpret_cast<const float4*>(part + (p + k) * H + c) : make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      s.x += v[k].x;
+      s.y += v[k].y;
+      s.z += v[k].z;
+      s.w += v[k].w;
+    }
+  }
+  red[ty][tx * 4 + 0] = s.x;
+  red[ty][tx * 4 + 1] = s.y;
+  red[ty][tx * 4 + 2] = s.z;
+  red[ty][tx * 4 + 3] = s.w;
+  __syncthreads();
+  if (threadIdx.x < 16) {
+    float t = red[0][threadIdx.x];
+    for (int k = 1; k < 64; ++k) t += red[k][threadIdx.x];
+    out[(int64_t)blockIdx.x * 16 + threadIdx.x] = st<TO, float>(t);
+  }
+}
+
 // ---------------------------------------------------------------------------
 // host side
 // ---------------------------------------------------------------------------
@@ -899,6 +941,12 @@ int64_t bwd_rows(RmsArgs a, hipStream_t s) {
 
 template <class A, class TO>
 void colsum(const A* part, int64_t np, int64_t H, TO* dw, hipStream_t s) {
+  if constexpr (std::is_same<A, float>::value) {
+    if (H % 16 == 0 && aligned16(part)) {
+      colsum16_kernel<TO><<<(unsigned)(H / 16), 256, 0, s>>>(part, np, H, dw);
+      return;
+    }
+  }
   colsum_kernel<A, TO><<<(unsigned)((H + 63) / 64), 64 * kColsumWaves, 0, s>>>(part, np, H, dw);
 }
 
