@@ -6,8 +6,10 @@
  * Conventions (all entry points):
  *   - Plain device pointers, element counts and element strides; no framework
  *     types.  The caller (PyTorch's caching allocator on the Python side) owns
- *     every buffer; the library never allocates, frees or retains a pointer
- *     past the call.
+ *     every buffer; the library retains no caller pointer past the call.  Its
+ *     own memory: forge_ce_fwd_reduce's call slots (device memory and pinned
+ *     host memory, allocated on a device's first call and kept until the
+ *     process ends) and forge_lora_a_noalloc's static scratch array.
  *   - Every launch is asynchronous on the caller's `stream` (a hipStream_t
  *     passed as void*; NULL = the legacy default stream).  No host syncs.
  *   - Return value: FORGE_OK (0) or a FORGE_ERR_* code; forge_last_error()
@@ -270,7 +272,7 @@ int64_t forge_rmsnorm_bwd_workspace(int dtype, int64_t rows, int64_t cols);
 
 /* C[m, n] = act(alpha * sum_k A[m*a_sm + k*a_sk] * B[k*b_sk + n*b_sn]
  *               + beta * C[m, n] + bias[n])   (bias of the operand dtype,
- * optional; act = FORGE_GEMM_ACT_NONE, _SILU or _RELU)
+ * optional; act = FORGE_GEMM_ACT_NONE, _SILU, _RELU or _GELU, the tanh form)
  * with one fp32 fmaf per k in increasing k order (deterministic).  Operands
  * of `dtype` (fp32, fp16 or bf16); C of c_dtype = fp32 or dtype, row stride
  * ldc.  Any shape and stride: the path for fp32 / fp16 models and for K or
@@ -321,6 +323,7 @@ enum {
   FORGE_GEMM_ACT_NONE = 0,
   FORGE_GEMM_ACT_SILU = 1,
   FORGE_GEMM_ACT_RELU = 2,
+  FORGE_GEMM_ACT_GELU = 3,
 };
 
 /* C[M, N] = alpha * sum_s A_s @ B_s + beta * C.  A and B layouts are shared by

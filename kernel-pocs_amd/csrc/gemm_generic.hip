@@ -11,6 +11,7 @@
 // 256 threads with 4 x 4 outputs each.  Operand loads are coalesced along
 // whichever of the two strides is unit (checked once per launch).
 #include "common.h"
+#include "gelu.h"
 
 namespace {
 
@@ -30,6 +31,11 @@ struct GenArgs {
 __device__ __forceinline__ float gen_act(int act, float v) {
   if (act == FORGE_GEMM_ACT_SILU) return v * __builtin_amdgcn_rcpf(1.0f + __expf(-v));
   if (act == FORGE_GEMM_ACT_RELU) return v > 0.f ? v : 0.f;
+  if (act == FORGE_GEMM_ACT_GELU) {  // tanh form, as the MFMA core's GELU epilogue
+    float a, d;
+    fgelu::gelu_and_grad<true>(v, a, d);
+    return a;
+  }
   return v;
 }
 
@@ -124,7 +130,8 @@ extern "C" int forge_gemm_generic(int64_t M, int64_t N, int64_t K, int dtype, co
     return forge_set_error(FORGE_ERR_UNSUPPORTED, "gemm_generic: dtype %d", dtype);
   if (c_dtype != FORGE_DTYPE_F32 && c_dtype != dtype)
     return forge_set_error(FORGE_ERR_UNSUPPORTED, "gemm_generic: C dtype %d with operands %d", c_dtype, dtype);
-  if (act != FORGE_GEMM_ACT_NONE && act != FORGE_GEMM_ACT_SILU && act != FORGE_GEMM_ACT_RELU)
+  if (act != FORGE_GEMM_ACT_NONE && act != FORGE_GEMM_ACT_SILU && act != FORGE_GEMM_ACT_RELU &&
+      act != FORGE_GEMM_ACT_GELU)
     return forge_set_error(FORGE_ERR_UNSUPPORTED, "gemm_generic: activation %d", act);
   if (M == 0 || N == 0) return FORGE_OK;
   if (!c || (K > 0 && (!a || !b))) return forge_set_error(FORGE_ERR_INVALID, "gemm_generic: null operand");

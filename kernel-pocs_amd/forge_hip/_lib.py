@@ -35,7 +35,7 @@ c_vp = ctypes.c_void_p
 DTYPE_F32, DTYPE_F16, DTYPE_BF16, DTYPE_F64 = 0, 1, 2, 3
 LAYOUT_ROW, LAYOUT_COL = 0, 1
 EPI_STORE, EPI_ATOMIC_F32, EPI_SILU, EPI_RELU, EPI_GELU = 0, 1, 2, 3, 4
-GEMM_ACT_NONE, GEMM_ACT_SILU, GEMM_ACT_RELU = 0, 1, 2
+GEMM_ACT_NONE, GEMM_ACT_SILU, GEMM_ACT_RELU, GEMM_ACT_GELU = 0, 1, 2, 3
 ACT_SILU, ACT_GELU_TANH, ACT_GELU_ERF = 0, 1, 2
 
 CE_HAS_GRADIENTS = 1

@@ -9,7 +9,8 @@ wrapper cublaslt_wrapper.py:97-261): bf16 operands run on the MFMA GEMM
 (`forge_gemm` with FORGE_EPI_SILU / _RELU / _GELU: the activation is applied
 to the fp32 accumulator before the single bf16 rounding); fp32 / fp16
 operands, or bf16 shapes the MFMA core does not take (K or N not a multiple
-of 8), run on `forge_gemm_generic` with its SiLU / ReLU activation.
+of 8), run on `forge_gemm_generic` with the same activation (its GELU is
+the tanh form too).
 """
 from __future__ import annotations
 
@@ -20,7 +21,8 @@ import torch
 from forge_hip import _lib as L
 
 _EPI = {"none": L.EPI_STORE, "relu": L.EPI_RELU, "gelu": L.EPI_GELU, "swish": L.EPI_SILU, "silu": L.EPI_SILU}
-_GEN_ACT = {"none": L.GEMM_ACT_NONE, "relu": L.GEMM_ACT_RELU, "swish": L.GEMM_ACT_SILU, "silu": L.GEMM_ACT_SILU}
+_GEN_ACT = {"none": L.GEMM_ACT_NONE, "relu": L.GEMM_ACT_RELU, "gelu": L.GEMM_ACT_GELU, "swish": L.GEMM_ACT_SILU,
+            "silu": L.GEMM_ACT_SILU}
 
 
 def matmul_epilogue(A: torch.Tensor, B: torch.Tensor, epilogue: str = "none", alpha: float = 1.0,
@@ -46,8 +48,6 @@ def matmul_epilogue(A: torch.Tensor, B: torch.Tensor, epilogue: str = "none", al
         L.check(L.forge_gemm(M, N, seg, 1, L.LAYOUT_ROW, L.LAYOUT_ROW, D.data_ptr(), N, L.DTYPE_BF16,
                              float(alpha), float(beta), _EPI[epilogue], 1, st), "forge_gemm")
         return D
-    if epilogue not in _GEN_ACT:
-        raise NotImplementedError(f"epilogue {epilogue!r} is served for bf16 operands only")
     L.check(L.forge_gemm_generic(M, N, K, L.dtype_code(A.dtype), A.data_ptr(), K, 1, B.data_ptr(), N, 1,
                                  D.data_ptr(), N, L.dtype_code(D.dtype), float(alpha), float(beta), None,
                                  _GEN_ACT[epilogue], st), "forge_gemm_generic")
