@@ -79,7 +79,9 @@ def test_lora_qkv_v2_3_and_packed_helpers():
 @pytest.mark.gpu
 @pytest.mark.parametrize("head_dim", [128, 64])
 def test_lora_qkv_rope_fused_matches_composition(head_dim):
-    """Fused QKV+RoPE == LoRA-QKV then RoPE with per-token (varlen) positions."""
+    """LoRA-QKV+RoPE (the product path: the QKV GEMM, then an in-place
+    forge_rope pass) against the oracle with per-token (varlen) positions;
+    the GEMM's RoPE epilogue (fuse_rope=True) against that composition."""
     gen = torch.Generator().manual_seed(head_dim)
     lens = [37, 120, 99]
     pos = orc.positions_for(lens)
@@ -94,19 +96,20 @@ def test_lora_qkv_rope_fused_matches_composition(head_dim):
     p = _cuda(params)
     x = X.cuda().requires_grad_(True)
     rope = {"cos": c.cuda(), "sin": s.cuda(), "positions": pos.cuda(), "head_dim": head_dim}
-    assert rope_fusable(rope, Hq, Hkv)  # this shape takes the GEMM's RoPE epilogue
+    assert rope_fusable(rope, Hq, Hkv)  # this shape can take the GEMM's RoPE epilogue
     Q, K_, V = lora_qkv_rope(x, p[0], p[3], p[4], p[5], p[1], p[6], p[7], p[8], p[2], p[9], p[10], p[11],
                              c.cuda(), s.cuda(), pos.cuda(), head_dim)
     for a, b, n in ((Q, Qr, "Q"), (K_, Kr, "K"), (V, Vr, "V")):
         _close_bf16(a, b, n)
-    # the unfused composition on the device: the same GEMM storing Q/K, then
-    # a forge_rope pass; both round the projection to bf16 before rotating,
-    # so they differ by at most one bf16 rounding of the rotated value
+    # the GEMM's RoPE epilogue against the composition (the same GEMM storing
+    # Q/K, then a forge_rope pass); both round the projection to bf16 before
+    # rotating, so they differ by at most one bf16 rounding of the rotated value
     args = (x.detach(), p[0], p[1], p[2], p[3].detach(), p[4].detach(), p[5], p[6].detach(), p[7].detach(), p[8],
             p[9].detach(), p[10].detach(), p[11])
     plain = qkv_forward(*args)
     rope_qk_inplace(plain, Hq, Hkv, rope)
-    fused = torch.cat([Q, K_, V], 1)
+    assert torch.equal(torch.cat([Q, K_, V], 1), plain)  # the product path is the composition itself
+    fused = qkv_forward(*args, rope=rope, fuse_rope=True)
     assert torch.equal(fused[:, Hq + Hkv:], plain[:, Hq + Hkv:])  # V is not rotated
     torch.testing.assert_close(fused.float(), plain.float(), rtol=2 ** -7, atol=1e-5)
     torch.autograd.backward((Q, K_, V), (dQ.cuda(), dK.cuda(), dV.cuda()))
@@ -131,8 +134,9 @@ def test_qkv_rope_epilogue_paths_agree(head_dim):
     s_odd = torch.zeros(200, head_dim + 2, dtype=torch.bfloat16, device="cuda")[:, :head_dim].copy_(s)
     args = (X, p[0], p[1], p[2], p[3].detach(), p[4].detach(), p[5], p[6].detach(), p[7].detach(), p[8],
             p[9].detach(), p[10].detach(), p[11])
-    vec = qkv_forward(*args, rope={"cos": c, "sin": s, "positions": pos, "head_dim": head_dim})
-    per_elem = qkv_forward(*args, rope={"cos": c_odd, "sin": s_odd, "positions": pos, "head_dim": head_dim})
+    vec = qkv_forward(*args, rope={"cos": c, "sin": s, "positions": pos, "head_dim": head_dim}, fuse_rope=True)
+    per_elem = qkv_forward(*args, rope={"cos": c_odd, "sin": s_odd, "positions": pos, "head_dim": head_dim},
+                           fuse_rope=True)
     assert torch.equal(vec, per_elem)
 
 
