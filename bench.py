@@ -886,17 +886,17 @@ def bench_lora_qkv(args):
     fl = T * flops_per_token(K, Hq, Hkv, r)
     tf = rate(fl, ms, 1e12)
     # dominant kernel: the forward product, forge_lora_qkv_rope (X [Wq;Wk;Wv]^T
-    # with the LoRA-B products as K segments; the forward then rotates Q/K
-    # with a forge_rope pass); the backward's dX product is the other one of
-    # its size
+    # with the LoRA-B products as K segments and RoPE in its epilogue); the
+    # backward's dX product is the other one of its size
     from kernels._lora_ops import lora_a
     from kernels.lora_qkv._impl import qkv_gemm
 
     Xd = X.detach()
     xa = lora_a(Xd, [Aq.detach(), Ak.detach(), Av.detach()], [s, s, s])  # the forward's LoRA-A product
     out = torch.empty(T, Hq + 2 * Hkv, device="cuda", dtype=bf)
+    rope = {"cos": c, "sin": sn, "positions": pos, "head_dim": D}
     launch_ms = time_launches(lambda i: qkv_gemm(Xd, Wq, Wk, Wv, xa, Bq.detach(), Bk.detach(), Bv.detach(), r,
-                                                 None, out), max(args.steps, 10))
+                                                 rope, out), max(args.steps, 10))
     del out
     fwd_flops = 2 * T * K * (Hq + 2 * Hkv) + 2 * T * r * (Hq + 2 * Hkv)
     res = {
@@ -905,7 +905,7 @@ def bench_lora_qkv(args):
                    "rope_base": 500000},
         "value": tf, "unit": "TFLOP/s", "ms_per_step": rnd(ms, 4), "wall_ms_per_step": rnd(wall, 4),
         "frac_of_mfma_peak": rnd(tf and tf / BF16_PEAK_TFLOPS, 4), "algorithmic_flops_per_step": fl,
-        "launches_ms": {f"forge_lora_qkv_rope (QKV GEMM + LoRA-B segments, {T} x "
+        "launches_ms": {f"forge_lora_qkv_rope (QKV GEMM + LoRA-B segments + RoPE epilogue, {T} x "
                         f"{Hq + 2 * Hkv} x {K})": round(launch_ms, 4)},
         "roofline": _roof("mfma", fwd_flops / (launch_ms * 1e-3) / 1e12, BF16_PEAK_TFLOPS, "TFLOP/s",
                           _traffic("lora_qkv_fwd_gemm")),

@@ -174,6 +174,71 @@ __device__ __forceinline__ void w4_epilogue_direct(const GemmArgs& args, f32x16 
 }
 
 // ---------------------------------------------------------------------------
+// RoPE over a staged Q/K tile (256 rows x 256 columns = 256 / HD whole heads):
+// thread tid takes head-dimension chunk d = 8 (tid % DC) of the lo half and
+// rows tid / DC + RS k.  One cos / sin load pair then serves the 2 * 256 / HD
+// chunks of its row that share d (lo and hi of every head in the tile), and
+// a thread's few rows are loaded at once, so the tables' latency is paid
+// once per tile instead of once per group of rows (measured on MI355X at
+// the LoRA-QKV BASELINE shape: a thread per 8-column chunk walking all 32
+// of its rows, four rows' tables in flight, cost 125 us over a plain store).
+// ---------------------------------------------------------------------------
+template <int HD>
+__device__ __forceinline__ void w4_rope_tile(const EpiArgs& ep, int64_t M, int64_t m0, int64_t n0,
+                                             const __bf16* lds) {
+  constexpr int HALF = HD / 2, DC = HALF / 8;  // 16-byte d-chunks per half
+  constexpr int HPT = 256 / HD;                // heads per tile
+  constexpr int RS = 256 / DC;                 // row sets
+  constexpr int RPT = 256 / RS;                // rows per thread
+  const int tid = threadIdx.x;
+  const int d = (tid % DC) * 8;
+  const int r0 = tid / DC;
+  int pos[RPT];
+#pragma unroll
+  for (int k = 0; k < RPT; ++k) {
+    const int64_t m = m0 + r0 + RS * k;
+    const int64_t p = m < M ? (ep.positions ? ep.positions[m] : m) : -1;
+    pos[k] = (p >= 0 && p < ep.cs_rows) ? (int)p : -1;
+  }
+  uint4 cv[RPT], sv[RPT];
+#pragma unroll
+  for (int k = 0; k < RPT; ++k)
+    if (pos[k] >= 0) {
+      cv[k] = ld16(ep.cos + (int64_t)pos[k] * ep.cs_ld + d);
+      sv[k] = ld16(ep.sin + (int64_t)pos[k] * ep.cs_ld + d);
+    }
+#pragma unroll
+  for (int k = 0; k < RPT; ++k) {
+    const int rr = r0 + RS * k;
+    const int64_t m = m0 + rr;
+    if (m >= M) continue;
+    float cs[8], sn[8];
+    if (pos[k] >= 0) {
+      unpack8(cv[k], cs);
+      unpack8(sv[k], sn);
+    } else {
+#pragma unroll
+      for (int t = 0; t < 8; ++t) cs[t] = sn[t] = __builtin_nanf("");
+    }
+    __bf16* crow = (__bf16*)ep.c + m * ep.ldc + n0;
+#pragma unroll
+    for (int h = 0; h < HPT; ++h) {
+      const int cl = h * HD + d, ch = cl + HALF;
+      float xl[8], xh[8], yl[8], yh[8];
+      unpack8(*reinterpret_cast<const uint4*>(lds + rr * W4_SP + cl), xl);
+      unpack8(*reinterpret_cast<const uint4*>(lds + rr * W4_SP + ch), xh);
+#pragma unroll
+      for (int t = 0; t < 8; ++t) {
+        yl[t] = xl[t] * cs[t] - xh[t] * sn[t];
+        yh[t] = xh[t] * cs[t] + xl[t] * sn[t];
+      }
+      st16(crow + cl, pack8(yl));
+      st16(crow + ch, pack8(yh));
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
 // Staged epilogue, single B (STORE_BF16 at beta = 0, ROPE, GLU backward):
 // the whole 256 x 256 tile in LDS as bf16, then each thread owns column chunk
 // c = 8 (tid % 32) and walks rows tid / 32 + 8 it.
@@ -268,8 +333,14 @@ __device__ __forceinline__ void w4_epilogue_staged(const GemmArgs& args, f32x16 
       }
     }
   } else {  // EPI_ROPE
-    // d and the lo / hi half are fixed per thread: the positions of all its
-    // rows first, then the cos / sin chunks of four rows at a time
+    // Q / K tiles (the host launches the RoPE epilogue only when Q and K are
+    // whole 256-column tiles and head_dim is 64 or 128)
+    if (n0 < ep.rope_cols && n0 + 256 <= N) {
+      if (ep.head_dim == 128) w4_rope_tile<128>(ep, M, m0, n0, lds);
+      else w4_rope_tile<64>(ep, M, m0, n0, lds);
+      return;
+    }
+    // V tiles (and any other shape): a thread per 8-column chunk
     const bool rot = n < N && n < ep.rope_cols;
     const int half = ep.head_dim / 2;
     const int in_head = (int)(n % ep.head_dim);

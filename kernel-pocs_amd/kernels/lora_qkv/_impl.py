@@ -37,24 +37,22 @@ def _w(t):
     return None if t is None else as_operand(t)
 
 
-# RoPE of the bf16 forward: an in-place forge_rope pass over the stored Q/K
-# (False) or the QKV GEMM's RoPE epilogue (True, where rope_fusable allows).
-# Measured cold on MI355X at the BASELINE shape (22954 tokens, Q 4096, K/V
-# 1024): GEMM + forge_rope pass 1065 us, GEMM with the RoPE epilogue 1122 us
-# (the GEMM storing plain Q/K: 998 us).  The epilogue's per-element rotation
-# runs while the matrix cores of its CU idle (one wave per SIMD), where the
-# separate pass streams Q/K at HBM speed.
-ROPE_IN_EPILOGUE = False
+# RoPE of the bf16 forward: the QKV GEMM's RoPE epilogue (True, where
+# rope_fusable allows) or an in-place forge_rope pass over the stored Q/K
+# (False).  Measured cold on MI355X at the BASELINE shape (22954 tokens, Q
+# 4096, K/V 1024, same box): GEMM with the RoPE epilogue 994 us, GEMM +
+# forge_rope pass 1033 us (the GEMM storing plain Q/K: 952 us).
+ROPE_IN_EPILOGUE = True
 
 
 def qkv_forward(X2, W_q, W_k, W_v, A_q, B_q, s_q, A_k, B_k, s_k, A_v, B_v, s_v,
                 rope=None, aux: Optional[dict] = None, a_packed=None, fuse_rope: Optional[bool] = None):
     """Returns out [M, Hq + 2 Hkv] bf16.  rope = {cos, sin, positions, head_dim}
     (tables [P, D]; int64 positions [M], validated by the caller) applies
-    RoPE to Q and K: by an in-place forge_rope pass over the stored Q/K, or
-    in the GEMM epilogue when fuse_rope (default ROPE_IN_EPILOGUE) is set and
-    `rope_fusable` allows it (bf16 tables, head_dim 64 / 128, Q and K widths
-    multiples of 256).
+    RoPE to Q and K: in the GEMM epilogue when fuse_rope (default
+    ROPE_IN_EPILOGUE) is set and `rope_fusable` allows it (bf16 tables,
+    head_dim 64 / 128, Q and K widths multiples of 256), else by an in-place
+    forge_rope pass over the stored Q/K.
     rope may also be a callable that returns that dict (or None): it is
     called once the LoRA-A product is queued, so the host prepares the
     tables while the device already works.

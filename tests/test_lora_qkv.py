@@ -79,9 +79,10 @@ def test_lora_qkv_v2_3_and_packed_helpers():
 @pytest.mark.gpu
 @pytest.mark.parametrize("head_dim", [128, 64])
 def test_lora_qkv_rope_fused_matches_composition(head_dim):
-    """LoRA-QKV+RoPE (the product path: the QKV GEMM, then an in-place
-    forge_rope pass) against the oracle with per-token (varlen) positions;
-    the GEMM's RoPE epilogue (fuse_rope=True) against that composition."""
+    """LoRA-QKV+RoPE (the product path: the QKV GEMM with its RoPE epilogue)
+    against the oracle with per-token (varlen) positions, and against the
+    composition (the same GEMM storing Q/K, then an in-place forge_rope
+    pass), which fuse_rope=False selects."""
     gen = torch.Generator().manual_seed(head_dim)
     lens = [37, 120, 99]
     pos = orc.positions_for(lens)
@@ -108,8 +109,9 @@ def test_lora_qkv_rope_fused_matches_composition(head_dim):
             p[9].detach(), p[10].detach(), p[11])
     plain = qkv_forward(*args)
     rope_qk_inplace(plain, Hq, Hkv, rope)
-    assert torch.equal(torch.cat([Q, K_, V], 1), plain)  # the product path is the composition itself
-    fused = qkv_forward(*args, rope=rope, fuse_rope=True)
+    assert torch.equal(qkv_forward(*args, rope=rope, fuse_rope=False), plain)
+    fused = qkv_forward(*args, rope=rope)
+    assert torch.equal(torch.cat([Q, K_, V], 1), fused)  # the product path is the fused epilogue
     assert torch.equal(fused[:, Hq + Hkv:], plain[:, Hq + Hkv:])  # V is not rotated
     torch.testing.assert_close(fused.float(), plain.float(), rtol=2 ** -7, atol=1e-5)
     torch.autograd.backward((Q, K_, V), (dQ.cuda(), dK.cuda(), dV.cuda()))
