@@ -64,6 +64,10 @@ struct Seg {
   int64_t ldb;
   int64_t k;         // K extent of the segment
   int64_t n_lo, n_hi;  // output columns this segment applies to (B row = n - n_lo)
+  // dual mode only (the 4-wave engine): gate rows read k < k_split, up rows
+  // read k >= k_split from column k - k_split of b2; 0 = both read every k.
+  // Two rank-r LoRA-B products of a gate/up GEMM then share one K tile.
+  int64_t k_split;
 };
 
 constexpr int MAX_SEGS = 6;

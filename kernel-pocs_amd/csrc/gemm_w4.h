@@ -62,6 +62,7 @@ struct W4Loader {
   const char* base[2];
   int64_t ld_bytes;
   int kch[2];          // first k of this lane's chunk, by instruction parity
+  int64_t k_split;     // dual: gate rows k < k_split, up rows k >= k_split (0: none)
 
   // 32-row groups alternate gate / up.  A wave's rows are a whole number of
   // 64-row pairs, so the pointer an instruction reads depends on j alone:
@@ -73,11 +74,14 @@ struct W4Loader {
 
   template <class RowSrc>
   __device__ __forceinline__ void setup(const void* p0, const void* p1, int64_t ld, int64_t panel_off,
-                                        RowSrc row_src) {
+                                        RowSrc row_src, int64_t ksplit = 0) {
     ld_bytes = ld * 2;
+    k_split = DUAL ? ksplit : 0;
     const int64_t pan = panel_off * ld_bytes;
     base[0] = p0 ? (const char*)p0 + pan : nullptr;
-    base[1] = DUAL ? (p1 ? (const char*)p1 + pan : nullptr) : base[0];
+    // (up rows: k is counted from the segment start, their column is k - k_split;
+    // every lane that reads them has k >= k_split, so no address before p1 is read)
+    base[1] = DUAL ? (p1 ? (const char*)p1 + pan - k_split * 2 : nullptr) : base[0];
     const int lane = threadIdx.x % 64, wave = threadIdx.x / 64;
     // A lane's chunk depends on its instruction only through the parity of
     // the instruction's first row / RPI (BKT 64: swz = (row >> 1) & 7 with 8
@@ -98,19 +102,23 @@ struct W4Loader {
   // k; <= 0: every chunk reads zeros); load_one issues instruction j of it.
   struct Prep {
     __amdgpu_buffer_rsrc_t r0, r1;
-    bool kin0, kin1;
+    bool kin[2][2];  // [gate / up rows][instruction parity]
   };
   __device__ __forceinline__ Prep prep(int64_t k0, int64_t kvalid) const {
     Prep p;
     p.r0 = make_rsrc(base[0] + k0 * 2);
     p.r1 = make_rsrc(base[1] + k0 * 2);
-    p.kin0 = kch[0] < kvalid;
-    p.kin1 = kch[1] < kvalid;
+    const int64_t ks = k_split - k0;  // the split in tile coordinates
+#pragma unroll
+    for (int par = 0; par < 2; ++par) {
+      p.kin[0][par] = kch[par] < kvalid && (k_split == 0 || kch[par] < ks);
+      p.kin[1][par] = kch[par] < kvalid && kch[par] >= ks;
+    }
     return p;
   }
   __device__ __forceinline__ void load_one(const Prep& p, int j, char* dst) const {
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / 64);
-    const uint32_t off = (j % 2 ? p.kin1 : p.kin0) ? voff[j] : OOB;
+    const uint32_t off = p.kin[sel_of(j)][j % 2] ? voff[j] : OOB;
     // (the resource goes through a local: passed to the builtin as a
     // conditional of two struct members, hipcc's host pass emitted the
     // launch stub of the first instantiation of the kernel only)
@@ -199,7 +207,7 @@ void gemm_w4_kernel(GemmArgs args) {
         const int t4 = (q % 128) / 32;
         const int rel = (q / 128) * 64 + (t4 / 2) * 32 + q % 32;
         return n0 + rel < args.N ? rel : -1;
-      });
+      }, sg.k_split);
     } else {
       const int64_t off = n0 - sg.n_lo;
       lb.setup(sg.b, sg.b, sg.ldb, off, [&](int q, int) -> int64_t {

@@ -88,9 +88,10 @@ extern "C" int forge_lora_mlp_gate_up(int64_t M, int64_t H, int64_t I, int64_t r
   int ns = 0;
   a.segs[ns++] = Seg{(const __bf16*)x, ldx, (const __bf16*)w_gate, (const __bf16*)w_up, ldw, H, 0, I};
   if (r > 0 && xa) {
-    // gate rows take xa[:, :r] Bg^T, up rows take xa[:, r:2r] Bu^T
-    a.segs[ns++] = Seg{(const __bf16*)xa, ld_xa, (const __bf16*)b_gate, nullptr, ldb, r, 0, I};
-    a.segs[ns++] = Seg{(const __bf16*)xa + r, ld_xa, nullptr, (const __bf16*)b_up, ldb, r, 0, I};
+    // one K segment of 2r: gate rows take xa[:, :r] Bg^T, up rows xa[:, r:2r]
+    // Bu^T (k_split = r), so both rank-r products share one K tile of the
+    // 4-wave engine (which every dual-B launch runs on) instead of two
+    a.segs[ns++] = Seg{(const __bf16*)xa, ld_xa, (const __bf16*)b_gate, (const __bf16*)b_up, ldb, 2 * r, 0, I, r};
   }
   a.n_segs = ns;
   a.ep.c = h;
