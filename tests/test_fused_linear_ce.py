@@ -9,7 +9,8 @@ the Module, forward-only without grad, an fp32/bf16 dtype smoke test and the
 2e-2).  Added here: the bf16 MFMA path (H % 8 == 0) with a vocabulary that
 is and is not a multiple of 8, several token chunks (the weight gradient
 accumulated over chunks), token scaling, a grad_output != 1, and the generic
-GEMM / token-scaling entry points through the C ABI.
+GEMM / token-scaling entry points through the C ABI, and the benchmarked
+configuration at its full size against an fp32 torch reference on the GPU.
 """
 import pytest
 import torch
@@ -290,3 +291,37 @@ def test_target_prob_and_row_scale(dtype):
             "forge_row_scale")
     torch.testing.assert_close(xd.cpu().double(), x.double() * prob.cpu().double().unsqueeze(1),
                                rtol=tol, atol=tol)
+
+
+def test_bench_shape_one_chunk():
+    """The benchmarked configuration at its full size: BT = 8192, H = 4096,
+    V = 128256 (Llama-3-8B's lm_head), bf16, 410 ignored targets, mean.  The
+    batch is one 2 GiB logits chunk, so dW is the one bf16-output product
+    (no fp32 accumulator).  Reference: the same formula in fp32 on the GPU
+    (F.linear + F.cross_entropy + autograd on fp32 copies of the bf16
+    inputs; too large for the CPU oracle).  Loss within 1e-3 relative;
+    gradients within the bf16 tolerance scaled by each gradient's RMS."""
+    BT, H, V = 8192, 4096, 128256
+    g = torch.Generator(device=DEV).manual_seed(5)
+    x = torch.randn(BT, H, device=DEV, generator=g).to(torch.bfloat16).requires_grad_(True)
+    W = (torch.randn(V, H, device=DEV, generator=g) / H ** 0.5).to(torch.bfloat16).requires_grad_(True)
+    t = torch.randint(0, V, (BT,), device=DEV, generator=g)
+    t[torch.randperm(BT, device=DEV, generator=g)[:410]] = -100
+    assert flce_mod._chunk_rows(BT, V * 2) == BT  # one chunk
+    loss = forge_fused_linear_cross_entropy(x, W, t)
+    loss.backward()
+    dx, dw = x.grad, W.grad
+
+    xr = x.detach().float().requires_grad_(True)
+    Wr = W.detach().float().requires_grad_(True)
+    ref = torch.nn.functional.cross_entropy(torch.nn.functional.linear(xr, Wr), t, ignore_index=-100)
+    ref.backward()
+    assert abs(loss.item() - ref.item()) <= 1e-3 * abs(ref.item())
+    for got, want, name in ((dx, xr.grad, "dX"), (dw, Wr.grad, "dW")):
+        err = (got.float() - want).abs()
+        scale = want.pow(2).mean().sqrt().item()
+        assert err.max().item() <= 2e-2 * scale + 2e-2 * want.abs().max().item(), name
+        assert err.mean().item() <= 1e-2 * scale, name
+        cos = torch.nn.functional.cosine_similarity(got.float().flatten(), want.flatten(), dim=0).item()
+        assert cos > 0.9999, (name, cos)
+    assert dx[t == -100].abs().max().item() == 0  # ignored rows: dlogits zero-filled, so their dX rows are zero
