@@ -175,8 +175,9 @@ int forge_ce_target_stats(const int64_t* target, int64_t target_stride, int64_t 
 /* forge_ce_fwd in one launch with the target statistics and the loss
  * reduction inside it (no class weights: FORGE_CE_HAS_WEIGHT is rejected).
  * The launch computes the statistics of forge_ce_target_stats itself (n_valid
- * for the mean; nothing but the per-row losses is written when they are out
- * of range) and copies them to pinned host memory, tagged with the call's
+ * for the mean; when the targets are out of range it writes no per-row output
+ * and no gradient, and the sums, if requested, as 0) and copies them to
+ * pinned host memory, tagged with the call's
  * *ticket; forge_ce_stats_wait(ticket) returns them on the host (for the
  * reference's bounds asserts) as soon as the launch has computed them,
  * without waiting for the rest of it.  loss (and z_loss) [n_rows] receive the
@@ -184,7 +185,10 @@ int forge_ce_target_stats(const int64_t* target, int64_t target_stride, int64_t 
  * sum there (and z_loss's in z_sum), summed in a fixed order (deterministic),
  * and, when loss_cast / z_cast are given, the sums rounded to cast_dtype.
  * The library keeps 64 call slots per device (allocated on the first call):
- * at most 64 calls may be between launch and forge_ce_stats_wait at once.
+ * call t uses slot t % 64, so at most 64 calls per device may be in flight
+ * at once (launched and not yet finished on the device; calls on one stream
+ * never overlap), and forge_ce_stats_wait must be called before 64 later
+ * calls on the device have been made.
  * Replaces `forge_cross_entropy_kernel` with the `.item()` reads and bounds
  * asserts before it and the `torch.sum` after it
  * (kernels/cross_entropy/experiments/v2/cross_entropy_kernel_v2.py:374-387,

@@ -244,7 +244,8 @@ def test_fwd_reduce_sum_statistics_and_slot_reuse(dtype, vocab):
 @pytest.mark.parametrize("dtype,vocab", [(torch.bfloat16, 4096), (torch.float32, 300)])
 def test_fwd_reduce_out_of_range_touches_nothing_and_next_call_is_clean(dtype, vocab):
     """A target out of range: the launch reports in_range = 0 and a masked
-    min / max that names it, leaves the logits untouched, and still resets
+    min / max that names it, leaves the logits untouched, writes its sum as 0,
+    and still resets
     its slot: the following calls (all 64 slots, then this one's again) give
     the correct loss."""
     BT = 64
@@ -257,6 +258,7 @@ def test_fwd_reduce_out_of_range_touches_nothing_and_next_call_is_clean(dtype, v
     assert stats[0] == BT and stats[2] == vocab + 3 and stats[3] == 0
     torch.cuda.synchronize()
     assert torch.equal(x.cpu(), logits)
+    assert s.item() == 0.0  # the sum of a refused launch is written as 0
     ref_loss = ce_reference(logits, target, reduction="sum")[0]
     for _ in range(65):
         x = logits.cuda()
