@@ -405,6 +405,28 @@ int forge_lora_mlp_down_bwd(int64_t M, int64_t H, int64_t I, int64_t r,
                             const void* a_down, int64_t ld_ad, int w_layout,
                             void* h_out, void* e_df, void* g_de, int64_t ld, int activation, void* stream);
 
+/* forge_lora_mlp_down_bwd (W_down given as W^T [I][H], A_down as A^T [I][r])
+ * that also forms the up / gate rank-rv products of the LoRA backward from
+ * df and de while its epilogue holds them:
+ *   v_part[t][m][j]      = sum over the columns i of column tile t (256 wide)
+ *                          of df[m, i] B_u[i, j]          (j < rv)
+ *   v_part[t][m][rv + j] = the same of de[m, i] B_g[i, j]
+ * with b_up_t = B_u^T, b_gate_t = B_g^T ([rv][I], pitch ld_bt).  v_part is
+ * fp32 [ceil(I / 256)][M][2 rv]; forge_splitk_reduce over its ceil(I / 256)
+ * slices (fixed order) gives [df B_u | de B_g], scaled and rounded once.
+ * rv: 8..64, a multiple of 8; I a multiple of 8; every buffer 16-byte aligned
+ * and ld a multiple of 8 (else an error, no launch).
+ * Replaces the rank-r products of the LoRA up / gate backward that re-read df
+ * and de (kernels/lora_mlp/experiments/v6/lora_mlp_kernel_v6.py:643-653). */
+int forge_lora_mlp_down_bwd_v(int64_t M, int64_t H, int64_t I, int64_t r,
+                              const void* dy, int64_t lddy,
+                              const void* w_down_t, int64_t ldwd,
+                              const void* t_d, int64_t ld_t,
+                              const void* a_down_t, int64_t ld_ad,
+                              void* h_out, void* e_df, void* g_de, int64_t ld, int activation,
+                              const void* b_up_t, const void* b_gate_t, int64_t ld_bt, int64_t rv,
+                              float* v_part, void* stream);
+
 /* The gated-activation backward of forge_lora_mlp_down_bwd on its own:
  * (D, e, g) -> h [M, I] (pitch ld_h), df over e and de over g (pitch ld_eg)
  * for a bf16 D = dY Wd + t Ad [M, I] (pitch ld_d) that the caller computed,

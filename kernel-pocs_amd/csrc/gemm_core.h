@@ -115,6 +115,16 @@ struct EpiArgs {
   int vec_ok;                // every output / side buffer 16-byte aligned with pitches % 8 == 0
   int64_t split_stride;      // STORE_F32 with split-K: split z writes its partial sums at c + z * split_stride
   int act;                   // STORE epilogues: activation of the result (ACT_NONE / ACT_SILU / ACT_RELU / ACT_GELU)
+  // GLU backward (4-wave engine): the rank-r products [df B_u | de B_g] of
+  // the tile's columns as fp32 partial sums, one slice per column tile:
+  // vpart[(n0 / 256) * vpart_stride + m * 2 vr + j], j < vr from df B_u,
+  // vr <= j < 2 vr from de B_g; vbt = {B_u^T, B_g^T}, each [vr][N] with pitch
+  // vbt_ld.  vpart == nullptr: off.
+  float* vpart;
+  int64_t vpart_stride;
+  const __bf16* vbt[2];
+  int64_t vbt_ld;
+  int vr;
 };
 
 // Activations of the STORE epilogues, applied to alpha * acc + beta * C.

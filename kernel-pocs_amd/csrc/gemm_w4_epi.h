@@ -239,6 +239,69 @@ __device__ __forceinline__ void w4_rope_tile(const EpiArgs& ep, int64_t M, int64
 }
 
 // ---------------------------------------------------------------------------
+// Rank-r partial product of a staged 256 x 256 bf16 tile (GLU backward):
+// vp[m][col0 + j] = sum over the tile's columns k of lds[m][k] bt[j][n0 + k]
+// for j < r, with v_mfma_f32_16x16x32_bf16 (wave w takes the 16-row blocks
+// 4w .. 4w + 3; each lane then holds four consecutive j of one row, stored
+// as one 16-byte vector).  Columns at or past N read zeros from bt; rows at
+// or past M are not stored.
+// ---------------------------------------------------------------------------
+typedef float w4_f32x4 __attribute__((ext_vector_type(4)));
+
+template <int RB>
+__device__ __forceinline__ void w4_rank_partial(const __bf16* lds, const __bf16* bt, int64_t ldbt, int r,
+                                                int64_t N, int64_t n0, int64_t M, int64_t m0, float* vp,
+                                                int64_t ldv, int col0) {
+  const int lane = threadIdx.x % 64, wave = threadIdx.x / 64;
+  w4_f32x4 acc[4][RB];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb) acc[i][rb] = w4_f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int ks = 0; ks < 8; ++ks) {  // the tile's 256 columns: 8 k-steps of 32
+    const int k = ks * 32 + (lane / 16) * 8;
+    bf16x8 b[RB];
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb) {
+      const int j = rb * 16 + lane % 16;
+      if (j < r && n0 + k + 8 <= N) {
+        b[rb] = *reinterpret_cast<const bf16x8*>(bt + (int64_t)j * ldbt + n0 + k);
+      } else {
+#pragma unroll
+        for (int t = 0; t < 8; ++t) b[rb][t] = (__bf16)0.f;
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int row = (wave * 4 + i) * 16 + lane % 16;
+      const bf16x8 a = *reinterpret_cast<const bf16x8*>(lds + row * W4_SP + k);
+#pragma unroll
+      for (int rb = 0; rb < RB; ++rb)
+        acc[i][rb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(b[rb], a, acc[i][rb], 0, 0, 0);
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int64_t m = m0 + (wave * 4 + i) * 16 + lane % 16;
+    if (m >= M) continue;
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb) {
+      const int j0 = rb * 16 + 4 * (lane / 16);
+      if (j0 < r) *reinterpret_cast<w4_f32x4*>(vp + m * ldv + col0 + j0) = acc[i][rb];
+    }
+  }
+}
+
+__device__ __forceinline__ void w4_rank_partial_any(const __bf16* lds, const __bf16* bt, int64_t ldbt, int r,
+                                                    int64_t N, int64_t n0, int64_t M, int64_t m0, float* vp,
+                                                    int64_t ldv, int col0) {
+  if (r <= 16) w4_rank_partial<1>(lds, bt, ldbt, r, N, n0, M, m0, vp, ldv, col0);
+  else if (r <= 32) w4_rank_partial<2>(lds, bt, ldbt, r, N, n0, M, m0, vp, ldv, col0);
+  else w4_rank_partial<4>(lds, bt, ldbt, r, N, n0, M, m0, vp, ldv, col0);
+}
+
+// ---------------------------------------------------------------------------
 // Staged epilogue, single B (STORE_BF16 at beta = 0, ROPE, GLU backward):
 // the whole 256 x 256 tile in LDS as bf16, then each thread owns column chunk
 // c = 8 (tid % 32) and walks rows tid / 32 + 8 it.
@@ -287,6 +350,14 @@ __device__ __forceinline__ void w4_epilogue_staged(const GemmArgs& args, f32x16 
       }
     }
   } else if constexpr (glu_bwd_epi(EPI)) {
+    // With ep.vpart the rank-r products [df B_u | de B_g] of this tile's
+    // columns are formed here from df and de as they are produced, instead of
+    // by a later pass that streams both [M, I] tensors again: df goes into
+    // the staged tile in place of DW (each thread overwrites only the chunk it
+    // read), de stays in registers until the df product is done and then
+    // replaces df.
+    const bool vp = ep.vpart != nullptr;
+    uint4 de_keep[IT];
     // the saved e / g chunks of four rows are read before any of them is used
 #pragma unroll
     for (int g0 = 0; g0 < IT; g0 += GRP) {
@@ -319,10 +390,11 @@ __device__ __forceinline__ void w4_epilogue_staged(const GemmArgs& args, f32x16 
         }
 #pragma unroll
         for (int t = 0; t < 8; ++t) glu_bwd_vals<EPI>(dw[t], ev[t], gv[t], hv[t], dfv[t], dev[t]);
+        const uint4 dfp = pack8(dfv), dep = pack8(dev);
         if (full) {
           st16((__bf16*)ep.c + m * ep.ldc + n, pack8(hv));
-          st16(ep.e + off, pack8(dfv));
-          st16(ep.g + off, pack8(dev));
+          st16(ep.e + off, dfp);
+          st16(ep.g + off, dep);
         } else {
           for (int t = 0; t < 8 && n + t < N; ++t) {
             ((__bf16*)ep.c)[m * ep.ldc + n + t] = (__bf16)hv[t];
@@ -330,7 +402,27 @@ __device__ __forceinline__ void w4_epilogue_staged(const GemmArgs& args, f32x16 
             ep.g[off + t] = (__bf16)dev[t];
           }
         }
+        if (vp) {
+          *reinterpret_cast<uint4*>(lds + rr * W4_SP + c) = dfp;
+          de_keep[g0 + q] = dep;
+        }
       }
+    }
+    if (vp) {
+      // (rows and columns outside the output hold the staged zeros of DW:
+      // their operand rows and columns were read as zeros)
+      float* part = ep.vpart + (n0 / 256) * ep.vpart_stride;
+      const int r = ep.vr;
+      lds_barrier();  // df of the whole tile staged
+      w4_rank_partial_any(lds, ep.vbt[0], ep.vbt_ld, r, N, n0, M, m0, part, 2 * r, 0);
+      lds_barrier();  // every wave is done reading df
+#pragma unroll
+      for (int it = 0; it < IT; ++it) {
+        const int rr = it * 8 + tid / 32;
+        if (m0 + rr < M && n < N) *reinterpret_cast<uint4*>(lds + rr * W4_SP + c) = de_keep[it];
+      }
+      lds_barrier();
+      w4_rank_partial_any(lds, ep.vbt[1], ep.vbt_ld, r, N, n0, M, m0, part, 2 * r, r);
     }
   } else {  // EPI_ROPE
     // Q / K tiles (the host launches the RoPE epilogue only when Q and K are

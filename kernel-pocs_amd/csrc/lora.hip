@@ -105,13 +105,10 @@ extern "C" int forge_lora_mlp_gate_up(int64_t M, int64_t H, int64_t I, int64_t r
   return run(-1, ROW, COL, epi, a, (hipStream_t)stream);
 }
 
-extern "C" int forge_lora_mlp_down_bwd(int64_t M, int64_t H, int64_t I, int64_t r,
-                                       const void* dy, int64_t lddy,
-                                       const void* w_down, int64_t ldwd,
-                                       const void* t_d, int64_t ld_t,
-                                       const void* a_down, int64_t ld_ad, int w_layout,
-                                       void* h_out, void* e_df, void* g_de, int64_t ld, int activation,
-                                       void* stream) {
+static int down_bwd(int64_t M, int64_t H, int64_t I, int64_t r, const void* dy, int64_t lddy, const void* w_down,
+                    int64_t ldwd, const void* t_d, int64_t ld_t, const void* a_down, int64_t ld_ad, int w_layout,
+                    void* h_out, void* e_df, void* g_de, int64_t ld, int activation, const void* bu_t,
+                    const void* bg_t, int64_t ld_bt, int64_t rv, float* v_part, void* stream) {
   if (M < 0 || H < 0 || I < 0 || r < 0) return forge_set_error(FORGE_ERR_INVALID, "lora_mlp_down_bwd: shape");
   const int epi = glu_epi(activation, true);
   if (epi < 0) return forge_set_error(FORGE_ERR_INVALID, "lora_mlp_down_bwd: activation %d", activation);
@@ -133,7 +130,49 @@ extern "C" int forge_lora_mlp_down_bwd(int64_t M, int64_t H, int64_t I, int64_t 
   a.ep.e = (__bf16*)e_df;
   a.ep.g = (__bf16*)g_de;
   a.ep.ld_eg = ld;
+  if (v_part) {
+    // the rank-r partials are formed by the staged epilogue of the 4-wave
+    // engine: K-contiguous W (COL) and 16-byte vectors everywhere
+    if (w_layout != COL)
+      return forge_set_error(FORGE_ERR_UNSUPPORTED, "lora_mlp_down_bwd_v: W_down must be given as W^T (layout COL)");
+    if (rv <= 0 || rv > 64 || rv % 8 != 0 || I % 8 != 0 || ld_bt % 8 != 0 || ld_bt < I)
+      return forge_set_error(FORGE_ERR_INVALID, "lora_mlp_down_bwd_v: rank %lld (8..64, a multiple of 8), I %lld, "
+                             "ld_bt %lld", (long long)rv, (long long)I, (long long)ld_bt);
+    if (!bu_t || !bg_t || !aligned16(bu_t) || !aligned16(bg_t) || !aligned16(v_part) || !aligned16(h_out) ||
+        !aligned16(e_df) || !aligned16(g_de) || ld % 8 != 0)
+      return forge_set_error(FORGE_ERR_INVALID, "lora_mlp_down_bwd_v: operands must be 16-byte aligned, ld %% 8 == 0");
+    a.ep.vpart = v_part;
+    a.ep.vpart_stride = M * 2 * rv;
+    a.ep.vbt[0] = (const __bf16*)bu_t;
+    a.ep.vbt[1] = (const __bf16*)bg_t;
+    a.ep.vbt_ld = ld_bt;
+    a.ep.vr = (int)rv;
+  }
   return run(-1, ROW, w_layout, epi, a, (hipStream_t)stream);
+}
+
+extern "C" int forge_lora_mlp_down_bwd(int64_t M, int64_t H, int64_t I, int64_t r,
+                                       const void* dy, int64_t lddy,
+                                       const void* w_down, int64_t ldwd,
+                                       const void* t_d, int64_t ld_t,
+                                       const void* a_down, int64_t ld_ad, int w_layout,
+                                       void* h_out, void* e_df, void* g_de, int64_t ld, int activation,
+                                       void* stream) {
+  return down_bwd(M, H, I, r, dy, lddy, w_down, ldwd, t_d, ld_t, a_down, ld_ad, w_layout, h_out, e_df, g_de, ld,
+                  activation, nullptr, nullptr, 0, 0, nullptr, stream);
+}
+
+extern "C" int forge_lora_mlp_down_bwd_v(int64_t M, int64_t H, int64_t I, int64_t r,
+                                         const void* dy, int64_t lddy,
+                                         const void* w_down_t, int64_t ldwd,
+                                         const void* t_d, int64_t ld_t,
+                                         const void* a_down_t, int64_t ld_ad,
+                                         void* h_out, void* e_df, void* g_de, int64_t ld, int activation,
+                                         const void* b_up_t, const void* b_gate_t, int64_t ld_bt, int64_t rv,
+                                         float* v_part, void* stream) {
+  if (!v_part) return forge_set_error(FORGE_ERR_INVALID, "lora_mlp_down_bwd_v: v_part is NULL");
+  return down_bwd(M, H, I, r, dy, lddy, w_down_t, ldwd, t_d, ld_t, a_down_t, ld_ad, COL, h_out, e_df, g_de, ld,
+                  activation, b_up_t, b_gate_t, ld_bt, rv, v_part, stream);
 }
 
 extern "C" int forge_lora_mlp_glu_bwd(int64_t M, int64_t I, const void* d, int64_t ld_d, void* e_df, void* g_de,

@@ -17,9 +17,12 @@ Backward (reference `LoRAMLPv6.backward`, :592-672, Unsloth-style in place;
 math of kernels/lora_mlp/reference/lora_mlp_pytorch.py:145-225):
   1. td   = sd dY Bd                                 forge_gemm         [M, r]
   2. DW = dY Wd + td Ad, fused in-place SwiGLU backward:
-     (DW, e, g) -> (h, df, de)                       forge_lora_mlp_down_bwd
+     (DW, e, g) -> (h, df, de)                       forge_lora_mlp_down_bwd_v
+     (ranks up to 64: its epilogue also forms step 4's [df Bu | de Bg] as fp32
+     partial sums per 256-column tile from the df, de it holds)
   3. dAd = td^T h,  dBd = sd dY^T (h Ad^T)           split-K forge_gemm
-  4. vu = su df Bu, vg = sg de Bg                    forge_gemm         [M, r]
+  4. vu = su df Bu, vg = sg de Bg                    forge_splitk_reduce of those
+                                                     partials (else forge_gemm)  [M, r]
      dAu = vu^T X, dAg = vg^T X, dBu = su df^T (X Au^T), dBg = sg de^T (X Ag^T)
   5. dX = df Wu + de Wg + vu Au + vg Ag              forge_gemm, 4 K segments over the
                                                      cached W^T and the small A^T
@@ -50,6 +53,14 @@ from kernels._lora_ops import (COL, ROW, as_operand, frozen_t, gemm, grad_at_b, 
 def _w(t):
     return None if t is None else as_operand(t)
 
+
+# [df Bu | de Bg] of the backward: formed in the down-projection backward's
+# epilogue from the df, de it holds (True: SiLU, ranks up to 64), or by a GEMM
+# that reads df and de back (False, and the GELU activations).  Measured on
+# MI355X at M = 8192, H = 4096, I = 14336, r = 16 (A/B on one box): SiLU step
+# 5.32 -> 5.27 ms; GeGLU 5.22 -> 5.27 ms, its epilogue's GELU derivative
+# holding enough registers that de's stay spills to scratch.
+RANK_IN_EPILOGUE = True
 
 ACTIVATIONS = {"silu": L.ACT_SILU, "gelu_tanh": L.ACT_GELU_TANH, "gelu_exact": L.ACT_GELU_ERF}
 
@@ -156,12 +167,26 @@ def mlp_backward(dY2, X2, e, g, W_gate, A_gate, B_gate, s_gate, W_up, A_up, B_up
     h = torch.empty(M, lde, dtype=torch.bfloat16, device=dev)[:, :I] if lde != I else \
         torch.empty(M, I, dtype=torch.bfloat16, device=dev)
     WdT = frozen_t(W_down)
-    L.check(
-        L.forge_lora_mlp_down_bwd(M, H, I, r, dY2.data_ptr(), ld(dY2), WdT.data_ptr(), ld(WdT), td.data_ptr(),
-                                  r, AdT.data_ptr(), ld(AdT), COL, h.data_ptr(), e.data_ptr(), g.data_ptr(), lde,
-                                  act, L.stream_of(X2)),
-        "forge_lora_mlp_down_bwd",
-    )
+    # with ranks up to 64 the epilogue also forms [df Bu | de Bg] (step 4) as
+    # fp32 partial sums per 256-column tile, from df and de in its registers
+    in_epi = RANK_IN_EPILOGUE and act == L.ACT_SILU and r <= 64 and I % 8 == 0 and lde % 8 == 0
+    if in_epi:
+        n_ct = (I + 255) // 256
+        vpart = torch.empty(n_ct, M, 2 * r, dtype=torch.float32, device=dev)
+        L.check(
+            L.forge_lora_mlp_down_bwd_v(M, H, I, r, dY2.data_ptr(), ld(dY2), WdT.data_ptr(), ld(WdT), td.data_ptr(),
+                                        r, AdT.data_ptr(), ld(AdT), h.data_ptr(), e.data_ptr(), g.data_ptr(), lde,
+                                        act, BuT.data_ptr(), BgT.data_ptr(), ld(BuT), r, vpart.data_ptr(),
+                                        L.stream_of(X2)),
+            "forge_lora_mlp_down_bwd_v",
+        )
+    else:
+        L.check(
+            L.forge_lora_mlp_down_bwd(M, H, I, r, dY2.data_ptr(), ld(dY2), WdT.data_ptr(), ld(WdT), td.data_ptr(),
+                                      r, AdT.data_ptr(), ld(AdT), COL, h.data_ptr(), e.data_ptr(), g.data_ptr(), lde,
+                                      act, L.stream_of(X2)),
+            "forge_lora_mlp_down_bwd",
+        )
     df, de = e, g
 
     # 3: down-projection LoRA grads
@@ -180,7 +205,14 @@ def mlp_backward(dY2, X2, e, g, W_gate, A_gate, B_gate, s_gate, W_up, A_up, B_up
 
     # 4: up / gate LoRA grads
     v = torch.empty(M, 2 * r, dtype=torch.bfloat16, device=dev)  # [su df Bu | sg de Bg]
-    if s_up == s_gate:  # both products in one launch (column-ranged segments)
+    if in_epi:  # the column tiles' partial sums, in a fixed order, scaled and rounded once
+        st = L.stream_of(X2)
+        halves = [(0, 2 * r, s_up)] if s_up == s_gate else [(0, r, s_up), (r, r, s_gate)]
+        for c0, nc, sc in halves:
+            L.check(L.forge_splitk_reduce(vpart.data_ptr() + 4 * c0, M * 2 * r, n_ct, M, nc, 2 * r,
+                                          v.data_ptr() + 2 * c0, 2 * r, L.DTYPE_BF16, float(sc), st),
+                    "forge_splitk_reduce")
+    elif s_up == s_gate:  # both products in one launch (column-ranged segments)
         gemm(M, 2 * r, [(df, lde, BuT, I, I, 0, r), (de, lde, BgT, I, I, r, 2 * r)], ROW, COL, out=v, alpha=s_up)
     else:
         times_b(df, lde, Bu, I, out=v[:, :r], alpha=s_up, b_t=BuT)

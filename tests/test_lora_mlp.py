@@ -266,3 +266,57 @@ def test_unsloth_helpers_match_oracle():
     for name, a, b in zip(("h", "df", "de"), (dw2, e2, g2), exp):
         torch.testing.assert_close(a.cpu().double(), b.to(torch.bfloat16).double(), rtol=2 ** -6, atol=1e-6,
                                    msg=lambda m: f"{name}: {m}")
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("M,I,r,act", [(256, 512, 16, "silu"), (300, 776, 8, "silu"), (512, 1280, 64, "silu"),
+                                       (130, 264, 24, "silu"), (256, 512, 16, "gelu_tanh"), (130, 264, 24, "gelu_exact")])
+def test_down_bwd_rank_partials(M, I, r, act):
+    """forge_lora_mlp_down_bwd_v: the same h, df, de as forge_lora_mlp_down_bwd
+    (bit for bit), and partial sums over its column tiles that add up to
+    [df B_u | de B_g] (fp32 reference on the GPU from the df, de it wrote;
+    ragged M, I not a multiple of 256, ranks 8..64, SiLU and both GELU
+    forms)."""
+    from forge_hip import _lib as L
+    from kernels.lora_mlp._impl import ACTIVATIONS
+
+    code = ACTIVATIONS[act]
+    torch.manual_seed(M + I + r)
+    H = 256
+    dev = "cuda"
+    bf = torch.bfloat16
+    dY = torch.randn(M, H, device=dev).to(bf)
+    WdT = (torch.randn(I, H, device=dev) * 0.05).to(bf)       # W_down^T [I][H]
+    td = (torch.randn(M, r, device=dev) * 0.1).to(bf)
+    AdT = (torch.randn(I, r, device=dev) * 0.1).to(bf)        # A_down^T [I][r]
+    e0 = torch.randn(M, I, device=dev).to(bf)
+    g0 = torch.randn(M, I, device=dev).to(bf)
+    BuT = (torch.randn(r, I, device=dev) * 0.1).to(bf)
+    BgT = (torch.randn(r, I, device=dev) * 0.1).to(bf)
+    st = L.stream_of(dY)
+    outs = []
+    for with_v in (False, True):
+        e, g = e0.clone(), g0.clone()
+        h = torch.empty(M, I, device=dev, dtype=bf)
+        n_ct = (I + 255) // 256
+        vpart = torch.full((n_ct, M, 2 * r), float("nan"), device=dev)
+        if with_v:
+            L.check(L.forge_lora_mlp_down_bwd_v(M, H, I, r, dY.data_ptr(), H, WdT.data_ptr(), H, td.data_ptr(), r,
+                                                AdT.data_ptr(), r, h.data_ptr(), e.data_ptr(), g.data_ptr(), I,
+                                                code, BuT.data_ptr(), BgT.data_ptr(), I, r, vpart.data_ptr(),
+                                                st), "forge_lora_mlp_down_bwd_v")
+        else:
+            L.check(L.forge_lora_mlp_down_bwd(M, H, I, r, dY.data_ptr(), H, WdT.data_ptr(), H, td.data_ptr(), r,
+                                              AdT.data_ptr(), r, L.LAYOUT_COL, h.data_ptr(), e.data_ptr(),
+                                              g.data_ptr(), I, code, st), "forge_lora_mlp_down_bwd")
+        outs.append((h, e, g, vpart))
+    (h0, df0, de0, _), (h1, df1, de1, vpart) = outs
+    assert torch.equal(h0, h1) and torch.equal(df0, df1) and torch.equal(de0, de1)
+    assert not torch.isnan(vpart).any()
+    got = vpart.sum(0)
+    want = torch.cat([df1.float() @ BuT.float().t(), de1.float() @ BgT.float().t()], 1)
+    torch.testing.assert_close(got, want, rtol=1e-4, atol=1e-3 * want.abs().max().item())
+    v = torch.empty(M, 2 * r, device=dev, dtype=bf)
+    L.check(L.forge_splitk_reduce(vpart.data_ptr(), M * 2 * r, vpart.shape[0], M, 2 * r, 2 * r, v.data_ptr(), 2 * r,
+                                  L.DTYPE_BF16, 1.0, st), "forge_splitk_reduce")
+    torch.testing.assert_close(v.float(), want, rtol=1e-2, atol=1e-2 * want.abs().max().item())
