@@ -383,6 +383,25 @@ int forge_lora_mlp_gate_up(int64_t M, int64_t H, int64_t I, int64_t r,
                            const void* b_gate, const void* b_up, int64_t ldb,
                            void* e, void* g, void* h, int64_t ld_out, int activation, void* stream);
 
+/* forge_lora_mlp_gate_up that also forms the forward's down-projection
+ * LoRA-A product h A_down^T while its epilogue holds h:
+ *   v_part[t][m][j] = sum over the h columns i of column tile t (128 wide)
+ *                     of h[m, i] A_down[j, i]          (j < rd)
+ * with a_down = A_down [rd][I] (pitch ld_ad).  v_part is fp32
+ * [ceil(I / 128)][M][rd]; forge_splitk_reduce over its ceil(I / 128) slices
+ * (fixed order) gives s_down h A_down^T, scaled and rounded once.  e and g
+ * must be given (training); rd: 8..64, a multiple of 8; I a multiple of 8;
+ * every buffer 16-byte aligned and ld_out a multiple of 8 (else an error, no
+ * launch).  Replaces the LoRA-A product of the down projection that re-reads
+ * h (kernels/lora_mlp/experiments/v6/lora_mlp_kernel_v6.py:423-442). */
+int forge_lora_mlp_gate_up_v(int64_t M, int64_t H, int64_t I, int64_t r,
+                             const void* x, int64_t ldx,
+                             const void* w_gate, const void* w_up, int64_t ldw,
+                             const void* xa, int64_t ld_xa,
+                             const void* b_gate, const void* b_up, int64_t ldb,
+                             void* e, void* g, void* h, int64_t ld_out, int activation,
+                             const void* a_down, int64_t ld_ad, int64_t rd, float* v_part, void* stream);
+
 /* LoRA-MLP backward through the down projection and the gated activation:
  *   DW = dY Wd + t Ad   (dY [M, H], Wd [H, I], t = sd dY Bd [M, r], Ad [r, I])
  *   then in place, with D = round(DW):

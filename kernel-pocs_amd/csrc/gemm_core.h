@@ -115,11 +115,14 @@ struct EpiArgs {
   int vec_ok;                // every output / side buffer 16-byte aligned with pitches % 8 == 0
   int64_t split_stride;      // STORE_F32 with split-K: split z writes its partial sums at c + z * split_stride
   int act;                   // STORE epilogues: activation of the result (ACT_NONE / ACT_SILU / ACT_RELU / ACT_GELU)
-  // GLU backward (4-wave engine): the rank-r products [df B_u | de B_g] of
-  // the tile's columns as fp32 partial sums, one slice per column tile:
-  // vpart[(n0 / 256) * vpart_stride + m * 2 vr + j], j < vr from df B_u,
-  // vr <= j < 2 vr from de B_g; vbt = {B_u^T, B_g^T}, each [vr][N] with pitch
-  // vbt_ld.  vpart == nullptr: off.
+  // Rank-r LoRA products formed by the gated-activation epilogues of the
+  // 4-wave engine, as fp32 partial sums with one slice per column tile
+  // (vpart == nullptr: off):
+  //  * GLU backward: [df B_u | de B_g], vpart[(n0 / 256) * vpart_stride +
+  //    m * 2 vr + j], j < vr from df B_u, vr <= j < 2 vr from de B_g;
+  //    vbt = {B_u^T, B_g^T}, each [vr][N] with pitch vbt_ld;
+  //  * GLU forward (dual B): h A_d^T, vpart[(n0 / 128) * vpart_stride +
+  //    m * vr + j]; vbt[0] = A_d [vr][N] with pitch vbt_ld.
   float* vpart;
   int64_t vpart_stride;
   const __bf16* vbt[2];

@@ -239,27 +239,31 @@ __device__ __forceinline__ void w4_rope_tile(const EpiArgs& ep, int64_t M, int64
 }
 
 // ---------------------------------------------------------------------------
-// Rank-r partial product of a staged 256 x 256 bf16 tile (GLU backward):
-// vp[m][col0 + j] = sum over the tile's columns k of lds[m][k] bt[j][n0 + k]
-// for j < r, with v_mfma_f32_16x16x32_bf16 (wave w takes the 16-row blocks
-// 4w .. 4w + 3; each lane then holds four consecutive j of one row, stored
-// as one 16-byte vector).  Columns at or past N read zeros from bt; rows at
-// or past M are not stored.
+// Rank-r partial product of a staged bf16 tile of ROWS x KCOLS (row pitch
+// PITCH elements): vp[m][col0 + j] = sum over the tile's columns k of
+// lds[m][k] bt[j][n0 + k] for j < r, with v_mfma_f32_16x16x32_bf16 (the
+// ROWS / 16 row blocks split evenly over the 4 waves; each lane then holds
+// four consecutive j of one row, stored as one 16-byte vector).  Columns at
+// or past N read zeros from bt; rows at or past M are not stored.  Used for
+// the LoRA rank-r products of the GEMMs' gated-activation epilogues: [df B_u |
+// de B_g] in the backward (256 x 256 staged tiles), h A_d^T in the forward
+// (128-row halves of 128 columns).
 // ---------------------------------------------------------------------------
 typedef float w4_f32x4 __attribute__((ext_vector_type(4)));
 
-template <int RB>
+template <int RB, int ROWS, int KCOLS, int PITCH>
 __device__ __forceinline__ void w4_rank_partial(const __bf16* lds, const __bf16* bt, int64_t ldbt, int r,
                                                 int64_t N, int64_t n0, int64_t M, int64_t m0, float* vp,
                                                 int64_t ldv, int col0) {
+  constexpr int BPW = ROWS / 16 / 4;  // row blocks per wave
   const int lane = threadIdx.x % 64, wave = threadIdx.x / 64;
-  w4_f32x4 acc[4][RB];
+  w4_f32x4 acc[BPW][RB];
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+  for (int i = 0; i < BPW; ++i)
 #pragma unroll
     for (int rb = 0; rb < RB; ++rb) acc[i][rb] = w4_f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-  for (int ks = 0; ks < 8; ++ks) {  // the tile's 256 columns: 8 k-steps of 32
+  for (int ks = 0; ks < KCOLS / 32; ++ks) {
     const int k = ks * 32 + (lane / 16) * 8;
     bf16x8 b[RB];
 #pragma unroll
@@ -273,17 +277,17 @@ __device__ __forceinline__ void w4_rank_partial(const __bf16* lds, const __bf16*
       }
     }
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int row = (wave * 4 + i) * 16 + lane % 16;
-      const bf16x8 a = *reinterpret_cast<const bf16x8*>(lds + row * W4_SP + k);
+    for (int i = 0; i < BPW; ++i) {
+      const int row = (wave * BPW + i) * 16 + lane % 16;
+      const bf16x8 a = *reinterpret_cast<const bf16x8*>(lds + row * PITCH + k);
 #pragma unroll
       for (int rb = 0; rb < RB; ++rb)
         acc[i][rb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(b[rb], a, acc[i][rb], 0, 0, 0);
     }
   }
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int64_t m = m0 + (wave * 4 + i) * 16 + lane % 16;
+  for (int i = 0; i < BPW; ++i) {
+    const int64_t m = m0 + (wave * BPW + i) * 16 + lane % 16;
     if (m >= M) continue;
 #pragma unroll
     for (int rb = 0; rb < RB; ++rb) {
@@ -293,12 +297,13 @@ __device__ __forceinline__ void w4_rank_partial(const __bf16* lds, const __bf16*
   }
 }
 
+template <int ROWS, int KCOLS, int PITCH>
 __device__ __forceinline__ void w4_rank_partial_any(const __bf16* lds, const __bf16* bt, int64_t ldbt, int r,
                                                     int64_t N, int64_t n0, int64_t M, int64_t m0, float* vp,
                                                     int64_t ldv, int col0) {
-  if (r <= 16) w4_rank_partial<1>(lds, bt, ldbt, r, N, n0, M, m0, vp, ldv, col0);
-  else if (r <= 32) w4_rank_partial<2>(lds, bt, ldbt, r, N, n0, M, m0, vp, ldv, col0);
-  else w4_rank_partial<4>(lds, bt, ldbt, r, N, n0, M, m0, vp, ldv, col0);
+  if (r <= 16) w4_rank_partial<1, ROWS, KCOLS, PITCH>(lds, bt, ldbt, r, N, n0, M, m0, vp, ldv, col0);
+  else if (r <= 32) w4_rank_partial<2, ROWS, KCOLS, PITCH>(lds, bt, ldbt, r, N, n0, M, m0, vp, ldv, col0);
+  else w4_rank_partial<4, ROWS, KCOLS, PITCH>(lds, bt, ldbt, r, N, n0, M, m0, vp, ldv, col0);
 }
 
 // ---------------------------------------------------------------------------
@@ -414,7 +419,7 @@ __device__ __forceinline__ void w4_epilogue_staged(const GemmArgs& args, f32x16 
       float* part = ep.vpart + (n0 / 256) * ep.vpart_stride;
       const int r = ep.vr;
       lds_barrier();  // df of the whole tile staged
-      w4_rank_partial_any(lds, ep.vbt[0], ep.vbt_ld, r, N, n0, M, m0, part, 2 * r, 0);
+      w4_rank_partial_any<256, 256, W4_SP>(lds, ep.vbt[0], ep.vbt_ld, r, N, n0, M, m0, part, 2 * r, 0);
       lds_barrier();  // every wave is done reading df
 #pragma unroll
       for (int it = 0; it < IT; ++it) {
@@ -422,7 +427,7 @@ __device__ __forceinline__ void w4_epilogue_staged(const GemmArgs& args, f32x16 
         if (m0 + rr < M && n < N) *reinterpret_cast<uint4*>(lds + rr * W4_SP + c) = de_keep[it];
       }
       lds_barrier();
-      w4_rank_partial_any(lds, ep.vbt[1], ep.vbt_ld, r, N, n0, M, m0, part, 2 * r, r);
+      w4_rank_partial_any<256, 256, W4_SP>(lds, ep.vbt[1], ep.vbt_ld, r, N, n0, M, m0, part, 2 * r, r);
     }
   } else {  // EPI_ROPE
     // Q / K tiles (the host launches the RoPE epilogue only when Q and K are
@@ -529,6 +534,11 @@ __device__ __forceinline__ void w4_epilogue_staged_dual(const GemmArgs& args, f3
     }
     lds_barrier();
     const int64_t mrow0 = m0 + pass * 128;
+    // forward LoRA: this half's partial of h A_d^T over the tile's 128 h
+    // columns (one slice per column tile), read from the staged h
+    if (ep.vpart)
+      w4_rank_partial_any<128, 128, W4_DP>(lh, ep.vbt[0], ep.vbt_ld, ep.vr, N, n0, M, mrow0,
+                                           ep.vpart + (n0 / 128) * ep.vpart_stride, ep.vr, 0);
 #pragma unroll 2
     for (int it = 0; it < 128 * 16 / 256; ++it) {
       const int id = it * 256 + tid;

@@ -70,12 +70,10 @@ __global__ __launch_bounds__(kGluBlock) void lora_glu_bwd_kernel(const __bf16* d
 
 }  // namespace
 
-extern "C" int forge_lora_mlp_gate_up(int64_t M, int64_t H, int64_t I, int64_t r,
-                                      const void* x, int64_t ldx,
-                                      const void* w_gate, const void* w_up, int64_t ldw,
-                                      const void* xa, int64_t ld_xa,
-                                      const void* b_gate, const void* b_up, int64_t ldb,
-                                      void* e, void* g, void* h, int64_t ld_out, int activation, void* stream) {
+static int gate_up(int64_t M, int64_t H, int64_t I, int64_t r, const void* x, int64_t ldx, const void* w_gate,
+                   const void* w_up, int64_t ldw, const void* xa, int64_t ld_xa, const void* b_gate, const void* b_up,
+                   int64_t ldb, void* e, void* g, void* h, int64_t ld_out, int activation, const void* a_down,
+                   int64_t ld_ad, int64_t rd, float* v_part, void* stream) {
   if (M < 0 || H < 0 || I < 0 || r < 0) return forge_set_error(FORGE_ERR_INVALID, "lora_mlp_gate_up: shape");
   const int epi = glu_epi(activation, false);
   if (epi < 0) return forge_set_error(FORGE_ERR_INVALID, "lora_mlp_gate_up: activation %d", activation);
@@ -102,7 +100,43 @@ extern "C" int forge_lora_mlp_gate_up(int64_t M, int64_t H, int64_t I, int64_t r
   a.ep.ld_eg = ld_out;
   if (r > 0 && xa && (ld_xa % 8 != 0 || r % 8 != 0))
     return forge_set_error(FORGE_ERR_INVALID, "lora_mlp_gate_up: rank and ld_xa must be multiples of 8");
+  if (v_part) {
+    // formed by the staged dual epilogue: 16-byte vectors everywhere
+    if (!e || rd <= 0 || rd > 64 || rd % 8 != 0 || I % 8 != 0 || ld_ad % 8 != 0 || ld_ad < I)
+      return forge_set_error(FORGE_ERR_INVALID, "lora_mlp_gate_up_v: e, g given, rank %lld (8..64, a multiple of 8), "
+                             "I %lld, ld_ad %lld", (long long)rd, (long long)I, (long long)ld_ad);
+    if (!a_down || !aligned16(a_down) || !aligned16(v_part) || !aligned16(e) || !aligned16(g) || !aligned16(h) ||
+        ld_out % 8 != 0)
+      return forge_set_error(FORGE_ERR_INVALID, "lora_mlp_gate_up_v: operands must be 16-byte aligned, ld %% 8 == 0");
+    a.ep.vpart = v_part;
+    a.ep.vpart_stride = M * rd;
+    a.ep.vbt[0] = (const __bf16*)a_down;
+    a.ep.vbt_ld = ld_ad;
+    a.ep.vr = (int)rd;
+  }
   return run(-1, ROW, COL, epi, a, (hipStream_t)stream);
+}
+
+extern "C" int forge_lora_mlp_gate_up(int64_t M, int64_t H, int64_t I, int64_t r,
+                                      const void* x, int64_t ldx,
+                                      const void* w_gate, const void* w_up, int64_t ldw,
+                                      const void* xa, int64_t ld_xa,
+                                      const void* b_gate, const void* b_up, int64_t ldb,
+                                      void* e, void* g, void* h, int64_t ld_out, int activation, void* stream) {
+  return gate_up(M, H, I, r, x, ldx, w_gate, w_up, ldw, xa, ld_xa, b_gate, b_up, ldb, e, g, h, ld_out, activation,
+                 nullptr, 0, 0, nullptr, stream);
+}
+
+extern "C" int forge_lora_mlp_gate_up_v(int64_t M, int64_t H, int64_t I, int64_t r,
+                                        const void* x, int64_t ldx,
+                                        const void* w_gate, const void* w_up, int64_t ldw,
+                                        const void* xa, int64_t ld_xa,
+                                        const void* b_gate, const void* b_up, int64_t ldb,
+                                        void* e, void* g, void* h, int64_t ld_out, int activation,
+                                        const void* a_down, int64_t ld_ad, int64_t rd, float* v_part, void* stream) {
+  if (!v_part) return forge_set_error(FORGE_ERR_INVALID, "lora_mlp_gate_up_v: v_part is NULL");
+  return gate_up(M, H, I, r, x, ldx, w_gate, w_up, ldw, xa, ld_xa, b_gate, b_up, ldb, e, g, h, ld_out, activation,
+                 a_down, ld_ad, rd, v_part, stream);
 }
 
 static int down_bwd(int64_t M, int64_t H, int64_t I, int64_t r, const void* dy, int64_t lddy, const void* w_down,

@@ -8,7 +8,9 @@ kernels/lora_mlp/experiments/v6/lora_mlp_kernel_v6.py:335-451):
      MFMA GEMM over the dual gate/up B with the LoRA-B products as K segments
      (one rounding) and the gated activation in its epilogue (h forms in
      registers; e, g are stored for the backward)
-  3. xd   = sd h Ad^T                                forge_lora_a       [M, r]
+  3. xd   = sd h Ad^T                                (ranks up to 64) fp32 partials
+     per 128-column tile from forge_lora_mlp_gate_up_v's epilogue, summed by
+     forge_splitk_reduce; else forge_lora_a   [M, r]
   4. out  = h Wd^T + xd Bd^T                         forge_gemm, xd Bd^T a K segment
   (the reference sends the base products to cuBLAS, lora_mlp_kernel_v6.py:374-443;
    here every product is the library's own gfx950 GEMM.)
@@ -54,12 +56,14 @@ def _w(t):
     return None if t is None else as_operand(t)
 
 
-# [df Bu | de Bg] of the backward: formed in the down-projection backward's
-# epilogue from the df, de it holds (True: SiLU, ranks up to 64), or by a GEMM
-# that reads df and de back (False, and the GELU activations).  Measured on
-# MI355X at M = 8192, H = 4096, I = 14336, r = 16 (A/B on one box): SiLU step
-# 5.32 -> 5.27 ms; GeGLU 5.22 -> 5.27 ms, its epilogue's GELU derivative
-# holding enough registers that de's stay spills to scratch.
+# Rank-r LoRA products formed by the gated-activation epilogues from the
+# tensors they hold (True, ranks up to 64), or by GEMMs that read those
+# tensors back (False): h Ad^T of the forward in the gate/up epilogue, and
+# [df Bu | de Bg] of the backward in the down-projection backward's epilogue
+# (SiLU only).  Measured on MI355X at M = 8192, H = 4096, I = 14336, r = 16
+# (A/B on one box), the backward's alone: SiLU step 5.32 -> 5.27 ms; GeGLU
+# 5.22 -> 5.27 ms, its epilogue's GELU derivative holding enough registers
+# that de's stay spills to scratch, so GeGLU keeps the GEMM there.
 RANK_IN_EPILOGUE = True
 
 ACTIVATIONS = {"silu": L.ACT_SILU, "gelu_tanh": L.ACT_GELU_TANH, "gelu_exact": L.ACT_GELU_ERF}
@@ -102,15 +106,36 @@ def mlp_forward(X2, W_gate, A_gate, B_gate, s_gate, W_up, A_up, B_up, s_up,
     g = torch.empty(M, I, dtype=torch.bfloat16, device=dev)
     h = torch.empty(M, I, dtype=torch.bfloat16, device=dev)
     st = L.stream_of(X2)
-    L.check(
-        L.forge_lora_mlp_gate_up(
-            M, H, I, r, X2.data_ptr(), ld(X2), Wg.data_ptr(), Wu.data_ptr(), ld(Wg),
-            L.ptr(xa), 2 * r, L.ptr(Bg), L.ptr(Bu), r, e.data_ptr(), g.data_ptr(), h.data_ptr(), I, act, st),
-        "forge_lora_mlp_gate_up",
-    )
+    down_lora = has_lora and A_down is not None and B_down is not None
+    # with ranks up to 64 the gate/up epilogue also forms h Ad^T (step 3) as
+    # fp32 partial sums per 128-column tile, from the h it holds
+    xd_in_epi = RANK_IN_EPILOGUE and down_lora and r <= 64 and I % 8 == 0
+    if xd_in_epi:
+        Ad = _w(A_down)
+        n_ct = (I + 127) // 128
+        xpart = torch.empty(n_ct, M, r, dtype=torch.float32, device=dev)
+        L.check(
+            L.forge_lora_mlp_gate_up_v(
+                M, H, I, r, X2.data_ptr(), ld(X2), Wg.data_ptr(), Wu.data_ptr(), ld(Wg),
+                L.ptr(xa), 2 * r, L.ptr(Bg), L.ptr(Bu), r, e.data_ptr(), g.data_ptr(), h.data_ptr(), I, act,
+                Ad.data_ptr(), ld(Ad), r, xpart.data_ptr(), st),
+            "forge_lora_mlp_gate_up_v",
+        )
+    else:
+        L.check(
+            L.forge_lora_mlp_gate_up(
+                M, H, I, r, X2.data_ptr(), ld(X2), Wg.data_ptr(), Wu.data_ptr(), ld(Wg),
+                L.ptr(xa), 2 * r, L.ptr(Bg), L.ptr(Bu), r, e.data_ptr(), g.data_ptr(), h.data_ptr(), I, act, st),
+            "forge_lora_mlp_gate_up",
+        )
     segs = [(h, ld(h), Wd, ld(Wd), I)]
-    if has_lora and A_down is not None and B_down is not None:
-        xd = lora_a(h, [A_down], [s_down])
+    if down_lora:
+        if xd_in_epi:  # the column tiles' partial sums, in a fixed order, scaled and rounded once
+            xd = torch.empty(M, r, dtype=torch.bfloat16, device=dev)
+            L.check(L.forge_splitk_reduce(xpart.data_ptr(), M * r, n_ct, M, r, r, xd.data_ptr(), r, L.DTYPE_BF16,
+                                          float(s_down), st), "forge_splitk_reduce")
+        else:
+            xd = lora_a(h, [A_down], [s_down])
         Bd = _w(B_down)
         segs.append((xd, ld(xd), Bd, ld(Bd), r))
         if aux is not None:

@@ -320,3 +320,47 @@ def test_down_bwd_rank_partials(M, I, r, act):
     L.check(L.forge_splitk_reduce(vpart.data_ptr(), M * 2 * r, vpart.shape[0], M, 2 * r, 2 * r, v.data_ptr(), 2 * r,
                                   L.DTYPE_BF16, 1.0, st), "forge_splitk_reduce")
     torch.testing.assert_close(v.float(), want, rtol=1e-2, atol=1e-2 * want.abs().max().item())
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("M,I,r,act", [(256, 512, 16, "silu"), (300, 776, 8, "silu"), (512, 1280, 64, "silu"),
+                                       (130, 392, 24, "gelu_tanh"), (256, 512, 16, "gelu_exact")])
+def test_gate_up_rank_partials(M, I, r, act):
+    """forge_lora_mlp_gate_up_v: the same e, g, h as forge_lora_mlp_gate_up
+    (bit for bit), and partial sums over its 128-column tiles that add up to
+    h A_down^T (fp32 reference on the GPU from the h it wrote; ragged M, I not
+    a multiple of 128, ranks 8..64, SiLU and both GELU forms)."""
+    from forge_hip import _lib as L
+    from kernels.lora_mlp._impl import ACTIVATIONS
+
+    code = ACTIVATIONS[act]
+    torch.manual_seed(M + I + r + 1)
+    H = 256
+    dev = "cuda"
+    bf = torch.bfloat16
+    X = torch.randn(M, H, device=dev).to(bf)
+    Wg = (torch.randn(I, H, device=dev) * 0.05).to(bf)
+    Wu = (torch.randn(I, H, device=dev) * 0.05).to(bf)
+    xa = (torch.randn(M, 2 * r, device=dev) * 0.1).to(bf)
+    Bg = (torch.randn(I, r, device=dev) * 0.1).to(bf)
+    Bu = (torch.randn(I, r, device=dev) * 0.1).to(bf)
+    Ad = (torch.randn(r, I, device=dev) * 0.1).to(bf)
+    st = L.stream_of(X)
+    outs = []
+    for with_v in (False, True):
+        e, g, h = (torch.empty(M, I, device=dev, dtype=bf) for _ in range(3))
+        n_ct = (I + 127) // 128
+        xpart = torch.full((n_ct, M, r), float("nan"), device=dev)
+        common = (M, H, I, r, X.data_ptr(), H, Wg.data_ptr(), Wu.data_ptr(), H, xa.data_ptr(), 2 * r,
+                  Bg.data_ptr(), Bu.data_ptr(), r, e.data_ptr(), g.data_ptr(), h.data_ptr(), I, code)
+        if with_v:
+            L.check(L.forge_lora_mlp_gate_up_v(*common, Ad.data_ptr(), I, r, xpart.data_ptr(), st),
+                    "forge_lora_mlp_gate_up_v")
+        else:
+            L.check(L.forge_lora_mlp_gate_up(*common, st), "forge_lora_mlp_gate_up")
+        outs.append((e, g, h, xpart))
+    (e0, g0, h0, _), (e1, g1, h1, xpart) = outs
+    assert torch.equal(e0, e1) and torch.equal(g0, g1) and torch.equal(h0, h1)
+    assert not torch.isnan(xpart).any()
+    want = h1.float() @ Ad.float().t()
+    torch.testing.assert_close(xpart.sum(0), want, rtol=1e-4, atol=1e-3 * want.abs().max().item())
