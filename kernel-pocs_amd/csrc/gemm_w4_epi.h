@@ -256,6 +256,11 @@ __device__ __forceinline__ void w4_rank_partial(const __bf16* lds, const __bf16*
                                                 int64_t N, int64_t n0, int64_t M, int64_t m0, float* vp,
                                                 int64_t ldv, int col0) {
   constexpr int BPW = ROWS / 16 / 4;  // row blocks per wave
+  constexpr int KS = KCOLS / 32;      // k-steps
+  // bt fragments of KB k-steps are loaded before any of them is used, so the
+  // L2 latency is paid once per batch, not once per k-step
+  constexpr int KB = (KS * RB <= 8) ? KS : (8 / RB < 1 ? 1 : 8 / RB);
+  static_assert(KS % KB == 0, "whole batches");
   const int lane = threadIdx.x % 64, wave = threadIdx.x / 64;
   w4_f32x4 acc[BPW][RB];
 #pragma unroll
@@ -263,26 +268,33 @@ __device__ __forceinline__ void w4_rank_partial(const __bf16* lds, const __bf16*
 #pragma unroll
     for (int rb = 0; rb < RB; ++rb) acc[i][rb] = w4_f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-  for (int ks = 0; ks < KCOLS / 32; ++ks) {
-    const int k = ks * 32 + (lane / 16) * 8;
-    bf16x8 b[RB];
+  for (int kb = 0; kb < KS; kb += KB) {
+    bf16x8 b[KB][RB];
 #pragma unroll
-    for (int rb = 0; rb < RB; ++rb) {
-      const int j = rb * 16 + lane % 16;
-      if (j < r && n0 + k + 8 <= N) {
-        b[rb] = *reinterpret_cast<const bf16x8*>(bt + (int64_t)j * ldbt + n0 + k);
-      } else {
+    for (int u = 0; u < KB; ++u) {
+      const int k = (kb + u) * 32 + (lane / 16) * 8;
 #pragma unroll
-        for (int t = 0; t < 8; ++t) b[rb][t] = (__bf16)0.f;
+      for (int rb = 0; rb < RB; ++rb) {
+        const int j = rb * 16 + lane % 16;
+        if (j < r && n0 + k + 8 <= N) {
+          b[u][rb] = *reinterpret_cast<const bf16x8*>(bt + (int64_t)j * ldbt + n0 + k);
+        } else {
+#pragma unroll
+          for (int t = 0; t < 8; ++t) b[u][rb][t] = (__bf16)0.f;
+        }
       }
     }
 #pragma unroll
-    for (int i = 0; i < BPW; ++i) {
-      const int row = (wave * BPW + i) * 16 + lane % 16;
-      const bf16x8 a = *reinterpret_cast<const bf16x8*>(lds + row * PITCH + k);
+    for (int u = 0; u < KB; ++u) {
+      const int k = (kb + u) * 32 + (lane / 16) * 8;
 #pragma unroll
-      for (int rb = 0; rb < RB; ++rb)
-        acc[i][rb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(b[rb], a, acc[i][rb], 0, 0, 0);
+      for (int i = 0; i < BPW; ++i) {
+        const int row = (wave * BPW + i) * 16 + lane % 16;
+        const bf16x8 a = *reinterpret_cast<const bf16x8*>(lds + row * PITCH + k);
+#pragma unroll
+        for (int rb = 0; rb < RB; ++rb)
+          acc[i][rb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(b[u][rb], a, acc[i][rb], 0, 0, 0);
+      }
     }
   }
 #pragma unroll
