@@ -433,10 +433,21 @@ int forge_lora_mlp_down_bwd(int64_t M, int64_t H, int64_t I, int64_t r,
  * with b_up_t = B_u^T, b_gate_t = B_g^T ([rv][I], pitch ld_bt).  v_part is
  * fp32 [ceil(I / 256)][M][2 rv]; forge_splitk_reduce over its ceil(I / 256)
  * slices (fixed order) gives [df B_u | de B_g], scaled and rounded once.
+ * With w_part (may be NULL) it also forms the LoRA B gradients' token
+ * reductions:
+ *   w_part[t][i][j]      = sum over the rows m of row tile t (256 tall)
+ *                          of df[m, i] xa_up[m, j]        (j < rv)
+ *   w_part[t][i][rv + j] = the same of de[m, i] xa_gate[m, j]
+ * with xa_t_up = xa_up^T, xa_t_gate = xa_gate^T ([rv][M], pitch ld_xat >= M,
+ * a multiple of 8).  w_part is fp32 [ceil(M / 256)][I][2 rv];
+ * forge_splitk_reduce over its ceil(M / 256) slices gives [df^T xa_up |
+ * de^T xa_gate] = [dB_up | dB_gate] when xa holds the scaled products
+ * s X A^T.
  * rv: 8..64, a multiple of 8; I a multiple of 8; every buffer 16-byte aligned
  * and ld a multiple of 8 (else an error, no launch).
  * Replaces the rank-r products of the LoRA up / gate backward that re-read df
- * and de (kernels/lora_mlp/experiments/v6/lora_mlp_kernel_v6.py:643-653). */
+ * and de (kernels/lora_mlp/experiments/v6/lora_mlp_kernel_v6.py:643-653), and
+ * with w_part their B-gradient products (:646, :648). */
 int forge_lora_mlp_down_bwd_v(int64_t M, int64_t H, int64_t I, int64_t r,
                               const void* dy, int64_t lddy,
                               const void* w_down_t, int64_t ldwd,
@@ -444,7 +455,8 @@ int forge_lora_mlp_down_bwd_v(int64_t M, int64_t H, int64_t I, int64_t r,
                               const void* a_down_t, int64_t ld_ad,
                               void* h_out, void* e_df, void* g_de, int64_t ld, int activation,
                               const void* b_up_t, const void* b_gate_t, int64_t ld_bt, int64_t rv,
-                              float* v_part, void* stream);
+                              float* v_part, const void* xa_t_up, const void* xa_t_gate,
+                              int64_t ld_xat, float* w_part, void* stream);
 
 /* The gated-activation backward of forge_lora_mlp_down_bwd on its own:
  * (D, e, g) -> h [M, I] (pitch ld_h), df over e and de over g (pitch ld_eg)

@@ -128,6 +128,15 @@ struct EpiArgs {
   const __bf16* vbt[2];
   int64_t vbt_ld;
   int vr;
+  // Token-reduction LoRA products of the GLU backward epilogue (wpart ==
+  // nullptr: off), fp32 partial sums with one slice per 256-row tile:
+  // wpart[(m0 / 256) * wpart_stride + n * 2 vr + j] = sum over the tile's rows
+  // m of df[m][n] xa_u[m][j] (j < vr), of de[m][n] xa_g[m][j - vr] (vr <= j <
+  // 2 vr); wxt = {xa_u^T, xa_g^T}, each [vr][M] with pitch wxt_ld.
+  float* wpart;
+  int64_t wpart_stride;
+  const __bf16* wxt[2];
+  int64_t wxt_ld;
 };
 
 // Activations of the STORE epilogues, applied to alpha * acc + beta * C.

@@ -309,6 +309,86 @@ __device__ __forceinline__ void w4_rank_partial(const __bf16* lds, const __bf16*
   }
 }
 
+// ---------------------------------------------------------------------------
+// Token-reduction partial product of a staged bf16 tile of 256 rows (tokens)
+// x 256 columns (row pitch PITCH elements):
+//   wp[c * ldw + col0 + j] = sum over the tile's rows t of lds[t][c] xt[j][m0 + t]
+// for j < r and the tile's columns c with n0 + c < N, with
+// v_mfma_f32_16x16x32_bf16.  The column operand (8 consecutive rows of one
+// column per lane) is read with ds_read_b64_tr_b16, which transposes within
+// each 16-lane group: lane L of group g supplies the 8 bytes at row
+// 32 ks + 8 g + L / 4 (+ 4 for the second read), columns 16 cb + 4 (L % 4),
+// and result lane 16 g + i receives (row 32 ks + 8 g + q, column 16 cb + i).
+// xt is token-contiguous ([r][tokens], pitch ldxt); tokens at or past M read
+// zeros.  Each wave takes 4 of the 16 column blocks; each lane then holds four
+// consecutive j of one column, stored as one 16-byte vector.  Used for the
+// LoRA B gradients of the GLU backward epilogue: df^T xa_u and de^T xa_g.
+// ---------------------------------------------------------------------------
+template <int RB, int PITCH>
+__device__ __forceinline__ void w4_token_partial(const __bf16* lds, const __bf16* xt, int64_t ldxt, int r,
+                                                 int64_t N, int64_t n0, int64_t M, int64_t m0, float* wp,
+                                                 int64_t ldw, int col0) {
+  constexpr int BPW = 4;  // column blocks of 16 per wave
+  constexpr int KS = 8;   // 32-row k-steps
+  constexpr int KB = (RB == 1) ? 8 : (RB == 2 ? 4 : 2);  // xt fragments loaded per batch
+  const int lane = threadIdx.x % 64, wave = threadIdx.x / 64;
+  const int g = lane / 16, L = lane % 16;
+  w4_f32x4 acc[BPW][RB];
+#pragma unroll
+  for (int i = 0; i < BPW; ++i)
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb) acc[i][rb] = w4_f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int kb = 0; kb < KS; kb += KB) {
+    bf16x8 b[KB][RB];
+#pragma unroll
+    for (int u = 0; u < KB; ++u) {
+      const int64_t m = m0 + (kb + u) * 32 + 8 * g;
+#pragma unroll
+      for (int rb = 0; rb < RB; ++rb) {
+        const int j = rb * 16 + L;
+        if (j < r && m + 8 <= M) {
+          b[u][rb] = *reinterpret_cast<const bf16x8*>(xt + (int64_t)j * ldxt + m);
+        } else {
+#pragma unroll
+          for (int t = 0; t < 8; ++t) b[u][rb][t] = (j < r && m + t < M) ? xt[(int64_t)j * ldxt + m + t] : (__bf16)0.f;
+        }
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < KB; ++u) {
+      const int row = (kb + u) * 32 + 8 * g + L / 4;
+#pragma unroll
+      for (int i = 0; i < BPW; ++i) {
+        const __bf16* p0 = lds + row * PITCH + (wave * BPW + i) * 16 + 4 * (L % 4);
+        const bf16x8 a = tr_frag((const char*)p0, (const char*)(p0 + 4 * PITCH));
+#pragma unroll
+        for (int rb = 0; rb < RB; ++rb)
+          acc[i][rb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(b[u][rb], a, acc[i][rb], 0, 0, 0);
+      }
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < BPW; ++i) {
+    const int64_t n = n0 + (wave * BPW + i) * 16 + L;
+    if (n >= N) continue;
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb) {
+      const int j0 = rb * 16 + 4 * g;
+      if (j0 < r) *reinterpret_cast<w4_f32x4*>(wp + (n - n0) * ldw + col0 + j0) = acc[i][rb];
+    }
+  }
+}
+
+template <int PITCH>
+__device__ __forceinline__ void w4_token_partial_any(const __bf16* lds, const __bf16* xt, int64_t ldxt, int r,
+                                                     int64_t N, int64_t n0, int64_t M, int64_t m0, float* wp,
+                                                     int64_t ldw, int col0) {
+  if (r <= 16) w4_token_partial<1, PITCH>(lds, xt, ldxt, r, N, n0, M, m0, wp, ldw, col0);
+  else if (r <= 32) w4_token_partial<2, PITCH>(lds, xt, ldxt, r, N, n0, M, m0, wp, ldw, col0);
+  else w4_token_partial<4, PITCH>(lds, xt, ldxt, r, N, n0, M, m0, wp, ldw, col0);
+}
+
 template <int ROWS, int KCOLS, int PITCH>
 __device__ __forceinline__ void w4_rank_partial_any(const __bf16* lds, const __bf16* bt, int64_t ldbt, int r,
                                                     int64_t N, int64_t n0, int64_t M, int64_t m0, float* vp,
@@ -368,8 +448,9 @@ __device__ __forceinline__ void w4_epilogue_staged(const GemmArgs& args, f32x16 
     }
   } else if constexpr (glu_bwd_epi(EPI)) {
     // With ep.vpart the rank-r products [df B_u | de B_g] of this tile's
-    // columns are formed here from df and de as they are produced, instead of
-    // by a later pass that streams both [M, I] tensors again: df goes into
+    // columns (and with ep.wpart the token products df^T xa_u, de^T xa_g of
+    // its rows) are formed here from df and de as they are produced, instead
+    // of by later passes that stream both [M, I] tensors again: df goes into
     // the staged tile in place of DW (each thread overwrites only the chunk it
     // read), de stays in registers until the df product is done and then
     // replaces df.
@@ -432,6 +513,8 @@ __device__ __forceinline__ void w4_epilogue_staged(const GemmArgs& args, f32x16 
       const int r = ep.vr;
       lds_barrier();  // df of the whole tile staged
       w4_rank_partial_any<256, 256, W4_SP>(lds, ep.vbt[0], ep.vbt_ld, r, N, n0, M, m0, part, 2 * r, 0);
+      float* wpart = ep.wpart ? ep.wpart + (m0 / 256) * ep.wpart_stride + n0 * 2 * r : nullptr;
+      if (wpart) w4_token_partial_any<W4_SP>(lds, ep.wxt[0], ep.wxt_ld, r, N, n0, M, m0, wpart, 2 * r, 0);
       lds_barrier();  // every wave is done reading df
 #pragma unroll
       for (int it = 0; it < IT; ++it) {
@@ -440,6 +523,7 @@ __device__ __forceinline__ void w4_epilogue_staged(const GemmArgs& args, f32x16 
       }
       lds_barrier();
       w4_rank_partial_any<256, 256, W4_SP>(lds, ep.vbt[1], ep.vbt_ld, r, N, n0, M, m0, part, 2 * r, r);
+      if (wpart) w4_token_partial_any<W4_SP>(lds, ep.wxt[1], ep.wxt_ld, r, N, n0, M, m0, wpart, 2 * r, r);
     }
   } else {  // EPI_ROPE
     // Q / K tiles (the host launches the RoPE epilogue only when Q and K are

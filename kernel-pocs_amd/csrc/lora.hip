@@ -142,7 +142,8 @@ extern "C" int forge_lora_mlp_gate_up_v(int64_t M, int64_t H, int64_t I, int64_t
 static int down_bwd(int64_t M, int64_t H, int64_t I, int64_t r, const void* dy, int64_t lddy, const void* w_down,
                     int64_t ldwd, const void* t_d, int64_t ld_t, const void* a_down, int64_t ld_ad, int w_layout,
                     void* h_out, void* e_df, void* g_de, int64_t ld, int activation, const void* bu_t,
-                    const void* bg_t, int64_t ld_bt, int64_t rv, float* v_part, void* stream) {
+                    const void* bg_t, int64_t ld_bt, int64_t rv, float* v_part, const void* xat_up,
+                    const void* xat_gate, int64_t ld_xat, float* w_part, void* stream) {
   if (M < 0 || H < 0 || I < 0 || r < 0) return forge_set_error(FORGE_ERR_INVALID, "lora_mlp_down_bwd: shape");
   const int epi = glu_epi(activation, true);
   if (epi < 0) return forge_set_error(FORGE_ERR_INVALID, "lora_mlp_down_bwd: activation %d", activation);
@@ -181,6 +182,17 @@ static int down_bwd(int64_t M, int64_t H, int64_t I, int64_t r, const void* dy, 
     a.ep.vbt[1] = (const __bf16*)bg_t;
     a.ep.vbt_ld = ld_bt;
     a.ep.vr = (int)rv;
+    if (w_part) {
+      if (!xat_up || !xat_gate || !aligned16(xat_up) || !aligned16(xat_gate) || !aligned16(w_part) ||
+          ld_xat % 8 != 0 || ld_xat < M)
+        return forge_set_error(FORGE_ERR_INVALID, "lora_mlp_down_bwd_v: xa^T operands must be 16-byte aligned "
+                               "with ld_xat (%lld) >= M and a multiple of 8", (long long)ld_xat);
+      a.ep.wpart = w_part;
+      a.ep.wpart_stride = I * 2 * rv;
+      a.ep.wxt[0] = (const __bf16*)xat_up;
+      a.ep.wxt[1] = (const __bf16*)xat_gate;
+      a.ep.wxt_ld = ld_xat;
+    }
   }
   return run(-1, ROW, w_layout, epi, a, (hipStream_t)stream);
 }
@@ -193,7 +205,7 @@ extern "C" int forge_lora_mlp_down_bwd(int64_t M, int64_t H, int64_t I, int64_t 
                                        void* h_out, void* e_df, void* g_de, int64_t ld, int activation,
                                        void* stream) {
   return down_bwd(M, H, I, r, dy, lddy, w_down, ldwd, t_d, ld_t, a_down, ld_ad, w_layout, h_out, e_df, g_de, ld,
-                  activation, nullptr, nullptr, 0, 0, nullptr, stream);
+                  activation, nullptr, nullptr, 0, 0, nullptr, nullptr, nullptr, 0, nullptr, stream);
 }
 
 extern "C" int forge_lora_mlp_down_bwd_v(int64_t M, int64_t H, int64_t I, int64_t r,
@@ -203,10 +215,11 @@ extern "C" int forge_lora_mlp_down_bwd_v(int64_t M, int64_t H, int64_t I, int64_
                                          const void* a_down_t, int64_t ld_ad,
                                          void* h_out, void* e_df, void* g_de, int64_t ld, int activation,
                                          const void* b_up_t, const void* b_gate_t, int64_t ld_bt, int64_t rv,
-                                         float* v_part, void* stream) {
+                                         float* v_part, const void* xa_t_up, const void* xa_t_gate,
+                                         int64_t ld_xat, float* w_part, void* stream) {
   if (!v_part) return forge_set_error(FORGE_ERR_INVALID, "lora_mlp_down_bwd_v: v_part is NULL");
   return down_bwd(M, H, I, r, dy, lddy, w_down_t, ldwd, t_d, ld_t, a_down_t, ld_ad, COL, h_out, e_df, g_de, ld,
-                  activation, b_up_t, b_gate_t, ld_bt, rv, v_part, stream);
+                  activation, b_up_t, b_gate_t, ld_bt, rv, v_part, xa_t_up, xa_t_gate, ld_xat, w_part, stream);
 }
 
 extern "C" int forge_lora_mlp_glu_bwd(int64_t M, int64_t I, const void* d, int64_t ld_d, void* e_df, void* g_de,

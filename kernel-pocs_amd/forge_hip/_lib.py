@@ -173,7 +173,7 @@ forge_lora_mlp_gate_up_v = _decl(
 forge_lora_mlp_down_bwd_v = _decl(
     "forge_lora_mlp_down_bwd_v",
     [c_i64, c_i64, c_i64, c_i64, c_vp, c_i64, c_vp, c_i64, c_vp, c_i64, c_vp, c_i64, c_vp, c_vp, c_vp, c_i64, c_int,
-     c_vp, c_vp, c_i64, c_i64, c_vp, c_vp])
+     c_vp, c_vp, c_i64, c_i64, c_vp, c_vp, c_vp, c_i64, c_vp, c_vp])
 forge_lora_mlp_glu_bwd = _decl("forge_lora_mlp_glu_bwd", [c_i64, c_i64, c_vp, c_i64, c_vp, c_vp, c_i64, c_vp, c_i64,
                                                           c_int, c_vp])
 forge_rmsnorm_bwd_workspace = _decl("forge_rmsnorm_bwd_workspace", [c_int, c_i64, c_i64], c_i64)

@@ -21,11 +21,14 @@ math of kernels/lora_mlp/reference/lora_mlp_pytorch.py:145-225):
   2. DW = dY Wd + td Ad, fused in-place SwiGLU backward:
      (DW, e, g) -> (h, df, de)                       forge_lora_mlp_down_bwd_v
      (ranks up to 64: its epilogue also forms step 4's [df Bu | de Bg] as fp32
-     partial sums per 256-column tile from the df, de it holds)
+     partial sums per 256-column tile from the df, de it holds, and with the
+     forward's xa step 4's dBu, dBg as fp32 partial sums per 256-row tile)
   3. dAd = td^T h,  dBd = sd dY^T (h Ad^T)           split-K forge_gemm
   4. vu = su df Bu, vg = sg de Bg                    forge_splitk_reduce of those
                                                      partials (else forge_gemm)  [M, r]
      dAu = vu^T X, dAg = vg^T X, dBu = su df^T (X Au^T), dBg = sg de^T (X Ag^T)
+                                                     (dBu, dBg: forge_splitk_reduce of
+                                                     step 2's row-tile partials)
   5. dX = df Wu + de Wg + vu Au + vg Ag              forge_gemm, 4 K segments over the
                                                      cached W^T and the small A^T
 The saved e/g buffers are overwritten by df/de in step 2 (the reference's
@@ -65,6 +68,12 @@ def _w(t):
 # 5.22 -> 5.27 ms, its epilogue's GELU derivative holding enough registers
 # that de's stay spills to scratch, so GeGLU keeps the GEMM there.
 RANK_IN_EPILOGUE = True
+# With RANK_IN_EPILOGUE and the forward's xa, the down-projection backward's
+# epilogue also forms the B gradients' token reductions df^T xa_u and
+# de^T xa_g (fp32 partial sums per 256-row tile) from the df and de tiles it
+# stages for [df Bu | de Bg], instead of a product that re-reads both [M, I]
+# tensors (False).
+TOKEN_IN_EPILOGUE = True
 
 ACTIVATIONS = {"silu": L.ACT_SILU, "gelu_tanh": L.ACT_GELU_TANH, "gelu_exact": L.ACT_GELU_ERF}
 
@@ -179,7 +188,16 @@ def mlp_backward(dY2, X2, e, g, W_gate, A_gate, B_gate, s_gate, W_up, A_up, B_up
     # 8 here) put the three big GEMMs of the backward on the 4-wave engine.
     # The six small transposes (B^T for the dY B products, A^T for the LoRA
     # segments) are one launch.
-    BdT, AdT, BuT, BgT, AuT, AgT = small_t_batch([Bd, Ad, Bu, Bg, Au, Ag])
+    act_ok = RANK_IN_EPILOGUE and act == L.ACT_SILU and r <= 64 and I % 8 == 0
+    dt = A_gate.dtype
+    # the B gradients' token reductions in the epilogue need xa^T [2r, M]
+    # (token-contiguous): one more matrix in the batch of transposes
+    tok_epi = (TOKEN_IN_EPILOGUE and act_ok and aux is not None and "xa" in aux and dt == torch.bfloat16
+               and M % 8 == 0)
+    if tok_epi:
+        BdT, AdT, BuT, BgT, AuT, AgT, xaT = small_t_batch([Bd, Ad, Bu, Bg, Au, Ag, aux["xa"]])
+    else:
+        BdT, AdT, BuT, BgT, AuT, AgT = small_t_batch([Bd, Ad, Bu, Bg, Au, Ag])
 
     # h, e, g share one pitch
     e, g = as_operand(e), as_operand(g)
@@ -194,15 +212,20 @@ def mlp_backward(dY2, X2, e, g, W_gate, A_gate, B_gate, s_gate, W_up, A_up, B_up
     WdT = frozen_t(W_down)
     # with ranks up to 64 the epilogue also forms [df Bu | de Bg] (step 4) as
     # fp32 partial sums per 256-column tile, from df and de in its registers
-    in_epi = RANK_IN_EPILOGUE and act == L.ACT_SILU and r <= 64 and I % 8 == 0 and lde % 8 == 0
+    in_epi = act_ok and lde % 8 == 0
+    tok_epi = tok_epi and in_epi
     if in_epi:
         n_ct = (I + 255) // 256
         vpart = torch.empty(n_ct, M, 2 * r, dtype=torch.float32, device=dev)
+        # [dBu | dBg] partials per 256-row tile: xa^T rows r..2r are su X Au^T, rows 0..r sg X Ag^T
+        n_rt = (M + 255) // 256
+        wpart = torch.empty(n_rt, I, 2 * r, dtype=torch.float32, device=dev) if tok_epi else None
         L.check(
             L.forge_lora_mlp_down_bwd_v(M, H, I, r, dY2.data_ptr(), ld(dY2), WdT.data_ptr(), ld(WdT), td.data_ptr(),
                                         r, AdT.data_ptr(), ld(AdT), h.data_ptr(), e.data_ptr(), g.data_ptr(), lde,
                                         act, BuT.data_ptr(), BgT.data_ptr(), ld(BuT), r, vpart.data_ptr(),
-                                        L.stream_of(X2)),
+                                        L.ptr(xaT[r:]) if tok_epi else None, L.ptr(xaT[:r]) if tok_epi else None,
+                                        M, L.ptr(wpart), L.stream_of(X2)),
             "forge_lora_mlp_down_bwd_v",
         )
     else:
@@ -215,11 +238,10 @@ def mlp_backward(dY2, X2, e, g, W_gate, A_gate, B_gate, s_gate, W_up, A_up, B_up
     df, de = e, g
 
     # 3: down-projection LoRA grads
-    dt = A_gate.dtype
     dAd = grad_at_b(td, r, h, lde, r, I, M, out_dtype=dt)          # [r, I] = (sd dY Bd)^T h
     # with the forward's scaled products the three B gradients are one
     # launch (step 4); otherwise each is its own
-    grouped = aux is not None and "xd" in aux and "xa" in aux and dt == torch.bfloat16
+    grouped = aux is not None and "xd" in aux and "xa" in aux and dt == torch.bfloat16 and not tok_epi
     if grouped:
         dBd = None
     elif aux is not None and "xd" in aux:
@@ -243,7 +265,14 @@ def mlp_backward(dY2, X2, e, g, W_gate, A_gate, B_gate, s_gate, W_up, A_up, B_up
         times_b(df, lde, Bu, I, out=v[:, :r], alpha=s_up, b_t=BuT)
         times_b(de, lde, Bg, I, out=v[:, r:], alpha=s_gate, b_t=BgT)
     dA_ug = grad_at_b(v, ld(v), X2, ld(X2), 2 * r, H, M, out_dtype=dt)  # [2r, H]: rows [dAu; dAg]
-    if grouped:
+    if tok_epi:  # the row tiles' partial sums, in a fixed order, rounded once (xa holds the scales)
+        st = L.stream_of(X2)
+        dBu = torch.empty(I, r, dtype=dt, device=dev)
+        dBg = torch.empty(I, r, dtype=dt, device=dev)
+        for c0, out in ((0, dBu), (r, dBg)):
+            L.check(L.forge_splitk_reduce(wpart.data_ptr() + 4 * c0, I * 2 * r, n_rt, I, r, 2 * r,
+                                          out.data_ptr(), r, L.DTYPE_BF16, 1.0, st), "forge_splitk_reduce")
+    elif grouped:
         xa = aux["xa"]                                            # [sg X Ag^T | su X Au^T]
         dBd, dBu, dBg = grad_at_b_group([(aux["xd"], ld(aux["xd"]), dY2, ld(dY2), H), (xa[:, r:], 2 * r, df, lde, I),
                                          (xa[:, :r], 2 * r, de, lde, I)], r, M)

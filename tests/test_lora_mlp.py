@@ -273,10 +273,12 @@ def test_unsloth_helpers_match_oracle():
                                        (130, 264, 24, "silu"), (256, 512, 16, "gelu_tanh"), (130, 264, 24, "gelu_exact")])
 def test_down_bwd_rank_partials(M, I, r, act):
     """forge_lora_mlp_down_bwd_v: the same h, df, de as forge_lora_mlp_down_bwd
-    (bit for bit), and partial sums over its column tiles that add up to
-    [df B_u | de B_g] (fp32 reference on the GPU from the df, de it wrote;
-    ragged M, I not a multiple of 256, ranks 8..64, SiLU and both GELU
-    forms)."""
+    (bit for bit), partial sums over its column tiles that add up to
+    [df B_u | de B_g], and with w_part partial sums over its row tiles that add
+    up to [df^T xa_u | de^T xa_g] (fp32 references on the GPU from the df, de
+    it wrote; ragged M, I not a multiple of 256, ranks 8..64, SiLU and both
+    GELU forms).  xa^T's pitch is padded past M with NaN, which a read of a
+    token outside the tile would carry into the sums."""
     from forge_hip import _lib as L
     from kernels.lora_mlp._impl import ACTIVATIONS
 
@@ -293,25 +295,33 @@ def test_down_bwd_rank_partials(M, I, r, act):
     g0 = torch.randn(M, I, device=dev).to(bf)
     BuT = (torch.randn(r, I, device=dev) * 0.1).to(bf)
     BgT = (torch.randn(r, I, device=dev) * 0.1).to(bf)
+    ldx = -(-M // 8) * 8
+    xaT = torch.full((2 * r, ldx), float("nan"), device=dev, dtype=bf)   # rows [gate; up], tokens < M valid
+    xaT[:, :M] = (torch.randn(2 * r, M, device=dev) * 0.5).to(bf)
     st = L.stream_of(dY)
     outs = []
-    for with_v in (False, True):
+    n_ct, n_rt = (I + 255) // 256, (M + 255) // 256
+    for mode in ("plain", "v", "vw"):
         e, g = e0.clone(), g0.clone()
         h = torch.empty(M, I, device=dev, dtype=bf)
-        n_ct = (I + 255) // 256
         vpart = torch.full((n_ct, M, 2 * r), float("nan"), device=dev)
-        if with_v:
-            L.check(L.forge_lora_mlp_down_bwd_v(M, H, I, r, dY.data_ptr(), H, WdT.data_ptr(), H, td.data_ptr(), r,
-                                                AdT.data_ptr(), r, h.data_ptr(), e.data_ptr(), g.data_ptr(), I,
-                                                code, BuT.data_ptr(), BgT.data_ptr(), I, r, vpart.data_ptr(),
-                                                st), "forge_lora_mlp_down_bwd_v")
-        else:
+        wpart = torch.full((n_rt, I, 2 * r), float("nan"), device=dev)
+        if mode == "plain":
             L.check(L.forge_lora_mlp_down_bwd(M, H, I, r, dY.data_ptr(), H, WdT.data_ptr(), H, td.data_ptr(), r,
                                               AdT.data_ptr(), r, L.LAYOUT_COL, h.data_ptr(), e.data_ptr(),
                                               g.data_ptr(), I, code, st), "forge_lora_mlp_down_bwd")
-        outs.append((h, e, g, vpart))
-    (h0, df0, de0, _), (h1, df1, de1, vpart) = outs
+        else:
+            w = mode == "vw"
+            L.check(L.forge_lora_mlp_down_bwd_v(M, H, I, r, dY.data_ptr(), H, WdT.data_ptr(), H, td.data_ptr(), r,
+                                                AdT.data_ptr(), r, h.data_ptr(), e.data_ptr(), g.data_ptr(), I,
+                                                code, BuT.data_ptr(), BgT.data_ptr(), I, r, vpart.data_ptr(),
+                                                xaT[r:].data_ptr() if w else None, xaT[:r].data_ptr() if w else None,
+                                                ldx, wpart.data_ptr() if w else None, st),
+                    "forge_lora_mlp_down_bwd_v")
+        outs.append((h, e, g, vpart, wpart))
+    (h0, df0, de0, _, _), (h1, df1, de1, vpart, _), (h2, df2, de2, vpart2, wpart) = outs
     assert torch.equal(h0, h1) and torch.equal(df0, df1) and torch.equal(de0, de1)
+    assert torch.equal(h0, h2) and torch.equal(df0, df2) and torch.equal(de0, de2) and torch.equal(vpart, vpart2)
     assert not torch.isnan(vpart).any()
     got = vpart.sum(0)
     want = torch.cat([df1.float() @ BuT.float().t(), de1.float() @ BgT.float().t()], 1)
@@ -320,6 +330,15 @@ def test_down_bwd_rank_partials(M, I, r, act):
     L.check(L.forge_splitk_reduce(vpart.data_ptr(), M * 2 * r, vpart.shape[0], M, 2 * r, 2 * r, v.data_ptr(), 2 * r,
                                   L.DTYPE_BF16, 1.0, st), "forge_splitk_reduce")
     torch.testing.assert_close(v.float(), want, rtol=1e-2, atol=1e-2 * want.abs().max().item())
+    # B gradients' token reductions
+    assert not torch.isnan(wpart).any()
+    xa = xaT[:, :M].float().t()                                  # [M, 2r]: [xa_g | xa_u]
+    want_w = torch.cat([df1.float().t() @ xa[:, r:], de1.float().t() @ xa[:, :r]], 1)   # [I, 2r]
+    torch.testing.assert_close(wpart.sum(0), want_w, rtol=1e-4, atol=1e-3 * want_w.abs().max().item())
+    dB = torch.empty(I, r, device=dev, dtype=bf)
+    L.check(L.forge_splitk_reduce(wpart.data_ptr() + 4 * r, I * 2 * r, n_rt, I, r, 2 * r, dB.data_ptr(), r,
+                                  L.DTYPE_BF16, 1.0, st), "forge_splitk_reduce")
+    torch.testing.assert_close(dB.float(), want_w[:, r:], rtol=1e-2, atol=1e-2 * want_w.abs().max().item())
 
 
 @pytest.mark.gpu
