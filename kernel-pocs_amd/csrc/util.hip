@@ -159,6 +159,67 @@ __global__ __launch_bounds__(256) void transpose2_kernel(const uint16_t* in, int
   transpose_tile(in, ld_in, rows, cols, out, ld_out, tiles_c, vec, blockIdx.x, tile);
 }
 
+// out[c, r] = in[r, c] for larger 2-byte matrices with 16-byte aligned bases
+// and pitches that are multiples of 8: 64 x 256 tiles, so that each input row
+// segment read is 512 bytes and each output row segment written 128 bytes,
+// eight 16-byte loads per thread in flight before the tile goes to LDS, and
+// the columns read back with ds_read_b64_tr_b16, which transposes within each
+// 16-lane group: lane L supplies the 8 bytes at tile row k0 + L / 4, columns
+// cb + 4 (L % 4), and receives rows k0 .. k0+3 of column cb + L; two reads
+// (k0, k0 + 4) give a lane the 8 consecutive input rows of one output row
+// chunk.  Partial tiles are zero-filled in LDS and their stores bounds-checked.
+constexpr int TW_R = 64, TW_C = 256, TW_P = TW_C + 8;  // pitch: rows 16 bytes apart in the bank cycle
+typedef short tw_i16x4 __attribute__((ext_vector_type(4)));
+
+__global__ __launch_bounds__(256) void transpose2_wide_kernel(const uint16_t* in, int64_t ld_in, int64_t rows,
+                                                              int64_t cols, uint16_t* out, int64_t ld_out,
+                                                              int64_t tiles_c) {
+  __shared__ __attribute__((aligned(16))) uint16_t tile[TW_R * TW_P];
+  const int64_t r0 = ((int64_t)blockIdx.x / tiles_c) * TW_R, c0 = ((int64_t)blockIdx.x % tiles_c) * TW_C;
+  const int t = threadIdx.x;
+  uint4 q[8];
+#pragma unroll
+  for (int it = 0; it < 8; ++it) {
+    const int row = t / 32 + 8 * it, cc = (t % 32) * 8;
+    const int64_t r = r0 + row, c = c0 + cc;
+    if (r < rows && c + 8 <= cols) {
+      q[it] = *reinterpret_cast<const uint4*>(in + r * ld_in + c);
+    } else {
+      uint16_t e[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) e[j] = (r < rows && c + j < cols) ? in[r * ld_in + c + j] : 0;
+      q[it] = make_uint4(e[0] | ((uint32_t)e[1] << 16), e[2] | ((uint32_t)e[3] << 16), e[4] | ((uint32_t)e[5] << 16),
+                         e[6] | ((uint32_t)e[7] << 16));
+    }
+  }
+#pragma unroll
+  for (int it = 0; it < 8; ++it)
+    *reinterpret_cast<uint4*>(tile + (t / 32 + 8 * it) * TW_P + (t % 32) * 8) = q[it];
+  __syncthreads();
+  const int lane = t % 64, w = t / 64, g = lane / 16, L = lane % 16;
+#pragma unroll
+  for (int it = 0; it < 8; ++it) {
+    // (column block, row chunk) of this 16-lane group: the four groups of a
+    // wave take four consecutive row chunks of one column block
+    const int pidx = it * 16 + w * 4 + g, cb = (pidx / 8) * 16, rc = (pidx % 8) * 8;
+    const uint16_t* a0 = tile + (rc + L / 4) * TW_P + cb + 4 * (L % 4);
+    const tw_i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) tw_i16x4*)a0);
+    const tw_i16x4 hi =
+        __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) tw_i16x4*)(a0 + 4 * TW_P));
+    const int64_t oc = c0 + cb + L, r = r0 + rc;
+    if (oc >= cols || r >= rows) continue;
+    const uint16_t e[8] = {(uint16_t)lo[0], (uint16_t)lo[1], (uint16_t)lo[2], (uint16_t)lo[3],
+                           (uint16_t)hi[0], (uint16_t)hi[1], (uint16_t)hi[2], (uint16_t)hi[3]};
+    if (r + 8 <= rows) {
+      *reinterpret_cast<uint4*>(out + oc * ld_out + r) =
+          make_uint4(e[0] | ((uint32_t)e[1] << 16), e[2] | ((uint32_t)e[3] << 16), e[4] | ((uint32_t)e[5] << 16),
+                     e[6] | ((uint32_t)e[7] << 16));
+    } else {
+      for (int j = 0; j < 8 && r + j < rows; ++j) out[oc * ld_out + r + j] = e[j];
+    }
+  }
+}
+
 // Up to FORGE_TRANSPOSE_BATCH_MAX transposes in one launch: workgroup b takes
 // tile b - first[i] of matrix i, first[i] <= b < first[i + 1].
 struct TransposeBatch {
@@ -192,8 +253,17 @@ extern "C" int forge_transpose_2b(const void* src, int64_t ld_src, int64_t rows,
   const int64_t tr = (rows + 63) / 64, tc = (cols + 63) / 64;
   if (tr * tc > 0x7fffffffLL) return forge_set_error(FORGE_ERR_INVALID, "transpose_2b: too many tiles");
   const int vec = aligned16(src) && aligned16(dst) && ld_src % 8 == 0 && ld_dst % 8 == 0;
-  transpose2_kernel<<<(unsigned)(tr * tc), 256, 0, (hipStream_t)stream>>>(
-      (const uint16_t*)src, ld_src, rows, cols, (uint16_t*)dst, ld_dst, tc, vec);
+  if (vec && rows * cols >= (int64_t(1) << 16)) {
+    // (measured on MI355X, bf16 [8192, 128256]: 64 x 64 tiles 864 us, these
+    // 843 us; 64 to 256 rows x 128 or 256 columns 847-904 us: about 5 TB/s
+    // whatever the tile shape)
+    const int64_t wr = (rows + TW_R - 1) / TW_R, wc = (cols + TW_C - 1) / TW_C;
+    transpose2_wide_kernel<<<(unsigned)(wr * wc), 256, 0, (hipStream_t)stream>>>(
+        (const uint16_t*)src, ld_src, rows, cols, (uint16_t*)dst, ld_dst, wc);
+  } else {
+    transpose2_kernel<<<(unsigned)(tr * tc), 256, 0, (hipStream_t)stream>>>(
+        (const uint16_t*)src, ld_src, rows, cols, (uint16_t*)dst, ld_dst, tc, vec);
+  }
   FORGE_CHECK_LAUNCH();
   return FORGE_OK;
 }

@@ -180,8 +180,13 @@ def test_gemm_fp32_beta_epilogue(a_layout, b_layout, N, ldc):
 
 @pytest.mark.gpu
 @pytest.mark.parametrize("rows,cols,ld_in,ld_out", [(64, 64, 64, 64), (300, 1003, 1008, 304), (7, 129, 129, 9),
-                                                    (4096, 1024, 1024, 4096)])
+                                                    (4096, 1024, 1024, 4096), (130, 1000, 1000, 136),
+                                                    (200, 1030, 1040, 208), (1024, 4096, 4104, 1032)])
 def test_transpose_2b(rows, cols, ld_in, ld_out):
+    """dst = src^T for 2-byte elements: the 64 x 64 tile kernel (small or
+    unaligned cases) and the 64 x 256 one with transposing LDS reads (aligned
+    cases of 2^16 elements and more, partial tiles in both dimensions and
+    rows not a multiple of 8); pitch padding untouched."""
     gen = torch.Generator().manual_seed(4)
     src = torch.randn(rows, ld_in, generator=gen).to(torch.bfloat16).cuda()
     dst = torch.full((cols, ld_out), 7.0, dtype=torch.bfloat16).cuda()
