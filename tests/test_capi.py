@@ -78,6 +78,31 @@ def test_status_codes_and_messages():
     assert rc == 1 and b"activation -1" in L.forge_last_error()
 
 
+def test_lora_mlp_rank_product_argument_errors():
+    """The entry points whose epilogues also form LoRA products check their
+    partial-sum buffers, ranks, pitches and alignment before any launch."""
+    # forge_lora_mlp_gate_up_v(M, H, I, r, x, ldx, wg, wu, ldw, xa, ld_xa, bg, bu, ldb, e, g, h, ld_out, act,
+    #                          a_down, ld_ad, rd, v_part, stream)
+    gate_up = [16, 64, 64, 0, 16, 64, 32, 48, 64, None, 0, None, None, 0, 64, 80, 96, 64, 0]
+    assert L.forge_lora_mlp_gate_up_v(*gate_up, 112, 64, 16, None, None) == 1
+    assert b"v_part is NULL" in L.forge_last_error()
+    assert L.forge_lora_mlp_gate_up_v(*gate_up, 112, 64, 4, 128, None) == 1      # rank 4
+    assert b"rank 4" in L.forge_last_error()
+    assert L.forge_lora_mlp_gate_up_v(*gate_up, 120, 64, 16, 128, None) == 1     # A_down misaligned
+    assert b"16-byte aligned" in L.forge_last_error()
+    # forge_lora_mlp_down_bwd_v(M, H, I, r, dy, lddy, wd_t, ldwd, t_d, ld_t, ad_t, ld_ad, h, e, g, ld, act,
+    #                           bu_t, bg_t, ld_bt, rv, v_part, xa_t_up, xa_t_gate, ld_xat, w_part, stream)
+    down = [16, 64, 64, 0, 16, 64, 32, 64, None, 0, None, 0, 48, 64, 80, 64, 0, 96, 112, 64]
+    assert L.forge_lora_mlp_down_bwd_v(*down, 16, None, None, None, 0, None, None) == 1
+    assert b"v_part is NULL" in L.forge_last_error()
+    assert L.forge_lora_mlp_down_bwd_v(*down, 72, 128, None, None, 0, None, None) == 1   # rank 72
+    assert b"rank 72" in L.forge_last_error()
+    assert L.forge_lora_mlp_down_bwd_v(*down, 16, 128, 152, 176, 16, 200, None) == 1  # xa_t_up misaligned
+    assert b"xa^T" in L.forge_last_error()
+    assert L.forge_lora_mlp_down_bwd_v(*down, 16, 128, 144, 176, 8, 192, None) == 1   # ld_xat < M
+    assert b"ld_xat (8)" in L.forge_last_error()
+
+
 def test_zero_size_calls_are_noops():
     assert L.forge_swiglu_fwd(0, None, None, 0, None, 0, 0, 0, 1.0, 1.0, None) == 0
     assert L.forge_ce_fwd(2, None, 0, 0, 0, None, 1, None, None, None, None, None, -100, *([0.0] * 6), 0, None, None) == 0
