@@ -435,14 +435,14 @@ int forge_lora_mlp_down_bwd(int64_t M, int64_t H, int64_t I, int64_t r,
  * slices (fixed order) gives [df B_u | de B_g], scaled and rounded once.
  * With w_part (may be NULL) it also forms the LoRA B gradients' token
  * reductions:
- *   w_part[t][i][j]      = sum over the rows m of row tile t (256 tall)
- *                          of df[m, i] xa_up[m, j]        (j < rv)
- *   w_part[t][i][rv + j] = the same of de[m, i] xa_gate[m, j]
+ *   w_part[t][0][i][j] = sum over the rows m of row tile t (256 tall)
+ *                        of df[m, i] xa_up[m, j]        (j < rv)
+ *   w_part[t][1][i][j] = the same of de[m, i] xa_gate[m, j]
  * with xa_t_up = xa_up^T, xa_t_gate = xa_gate^T ([rv][M], pitch ld_xat >= M,
- * a multiple of 8).  w_part is fp32 [ceil(M / 256)][I][2 rv];
- * forge_splitk_reduce over its ceil(M / 256) slices gives [df^T xa_up |
- * de^T xa_gate] = [dB_up | dB_gate] when xa holds the scaled products
- * s X A^T.
+ * a multiple of 8).  w_part is fp32 [ceil(M / 256)][2][I][rv];
+ * forge_splitk_reduce over its ceil(M / 256) slices (stride 2 I rv) from
+ * block 0 or 1 gives df^T xa_up = dB_up or de^T xa_gate = dB_gate when xa
+ * holds the scaled products s X A^T.
  * rv: 8..64, a multiple of 8; I a multiple of 8; every buffer 16-byte aligned
  * and ld a multiple of 8 (else an error, no launch).
  * Replaces the rank-r products of the LoRA up / gate backward that re-read df

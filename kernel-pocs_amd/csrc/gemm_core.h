@@ -129,10 +129,11 @@ struct EpiArgs {
   int64_t vbt_ld;
   int vr;
   // Token-reduction LoRA products of the GLU backward epilogue (wpart ==
-  // nullptr: off), fp32 partial sums with one slice per 256-row tile:
-  // wpart[(m0 / 256) * wpart_stride + n * 2 vr + j] = sum over the tile's rows
-  // m of df[m][n] xa_u[m][j] (j < vr), of de[m][n] xa_g[m][j - vr] (vr <= j <
-  // 2 vr); wxt = {xa_u^T, xa_g^T}, each [vr][M] with pitch wxt_ld.
+  // nullptr: off), fp32 partial sums with one slice of two [N][vr] blocks per
+  // 256-row tile: wpart[(m0 / 256) * wpart_stride + p * N * vr + n * vr + j]
+  // = sum over the tile's rows m of df[m][n] xa_u[m][j] (p = 0), of
+  // de[m][n] xa_g[m][j] (p = 1); wxt = {xa_u^T, xa_g^T}, each [vr][M] with
+  // pitch wxt_ld.
   float* wpart;
   int64_t wpart_stride;
   const __bf16* wxt[2];

@@ -513,8 +513,8 @@ __device__ __forceinline__ void w4_epilogue_staged(const GemmArgs& args, f32x16 
       const int r = ep.vr;
       lds_barrier();  // df of the whole tile staged
       w4_rank_partial_any<256, 256, W4_SP>(lds, ep.vbt[0], ep.vbt_ld, r, N, n0, M, m0, part, 2 * r, 0);
-      float* wpart = ep.wpart ? ep.wpart + (m0 / 256) * ep.wpart_stride + n0 * 2 * r : nullptr;
-      if (wpart) w4_token_partial_any<W4_SP>(lds, ep.wxt[0], ep.wxt_ld, r, N, n0, M, m0, wpart, 2 * r, 0);
+      float* wpart = ep.wpart ? ep.wpart + (m0 / 256) * ep.wpart_stride + n0 * r : nullptr;
+      if (wpart) w4_token_partial_any<W4_SP>(lds, ep.wxt[0], ep.wxt_ld, r, N, n0, M, m0, wpart, r, 0);
       lds_barrier();  // every wave is done reading df
 #pragma unroll
       for (int it = 0; it < IT; ++it) {
@@ -523,7 +523,7 @@ __device__ __forceinline__ void w4_epilogue_staged(const GemmArgs& args, f32x16 
       }
       lds_barrier();
       w4_rank_partial_any<256, 256, W4_SP>(lds, ep.vbt[1], ep.vbt_ld, r, N, n0, M, m0, part, 2 * r, r);
-      if (wpart) w4_token_partial_any<W4_SP>(lds, ep.wxt[1], ep.wxt_ld, r, N, n0, M, m0, wpart, 2 * r, r);
+      if (wpart) w4_token_partial_any<W4_SP>(lds, ep.wxt[1], ep.wxt_ld, r, N, n0, M, m0, wpart + N * r, r, 0);
     }
   } else {  // EPI_ROPE
     // Q / K tiles (the host launches the RoPE epilogue only when Q and K are

@@ -188,7 +188,7 @@ static int down_bwd(int64_t M, int64_t H, int64_t I, int64_t r, const void* dy, 
         return forge_set_error(FORGE_ERR_INVALID, "lora_mlp_down_bwd_v: xa^T operands must be 16-byte aligned "
                                "with ld_xat (%lld) >= M and a multiple of 8", (long long)ld_xat);
       a.ep.wpart = w_part;
-      a.ep.wpart_stride = I * 2 * rv;
+      a.ep.wpart_stride = 2 * I * rv;
       a.ep.wxt[0] = (const __bf16*)xat_up;
       a.ep.wxt[1] = (const __bf16*)xat_gate;
       a.ep.wxt_ld = ld_xat;

@@ -217,9 +217,9 @@ def mlp_backward(dY2, X2, e, g, W_gate, A_gate, B_gate, s_gate, W_up, A_up, B_up
     if in_epi:
         n_ct = (I + 255) // 256
         vpart = torch.empty(n_ct, M, 2 * r, dtype=torch.float32, device=dev)
-        # [dBu | dBg] partials per 256-row tile: xa^T rows r..2r are su X Au^T, rows 0..r sg X Ag^T
+        # dBu, dBg partials per 256-row tile: xa^T rows r..2r are su X Au^T, rows 0..r sg X Ag^T
         n_rt = (M + 255) // 256
-        wpart = torch.empty(n_rt, I, 2 * r, dtype=torch.float32, device=dev) if tok_epi else None
+        wpart = torch.empty(n_rt, 2, I, r, dtype=torch.float32, device=dev) if tok_epi else None
         L.check(
             L.forge_lora_mlp_down_bwd_v(M, H, I, r, dY2.data_ptr(), ld(dY2), WdT.data_ptr(), ld(WdT), td.data_ptr(),
                                         r, AdT.data_ptr(), ld(AdT), h.data_ptr(), e.data_ptr(), g.data_ptr(), lde,
@@ -269,8 +269,8 @@ def mlp_backward(dY2, X2, e, g, W_gate, A_gate, B_gate, s_gate, W_up, A_up, B_up
         st = L.stream_of(X2)
         dBu = torch.empty(I, r, dtype=dt, device=dev)
         dBg = torch.empty(I, r, dtype=dt, device=dev)
-        for c0, out in ((0, dBu), (r, dBg)):
-            L.check(L.forge_splitk_reduce(wpart.data_ptr() + 4 * c0, I * 2 * r, n_rt, I, r, 2 * r,
+        for blk, out in ((0, dBu), (1, dBg)):  # each block's slices are contiguous [I, r] rows
+            L.check(L.forge_splitk_reduce(wpart[0, blk].data_ptr(), 2 * I * r, n_rt, I, r, r,
                                           out.data_ptr(), r, L.DTYPE_BF16, 1.0, st), "forge_splitk_reduce")
     elif grouped:
         xa = aux["xa"]                                            # [sg X Ag^T | su X Au^T]

@@ -305,7 +305,7 @@ def test_down_bwd_rank_partials(M, I, r, act):
         e, g = e0.clone(), g0.clone()
         h = torch.empty(M, I, device=dev, dtype=bf)
         vpart = torch.full((n_ct, M, 2 * r), float("nan"), device=dev)
-        wpart = torch.full((n_rt, I, 2 * r), float("nan"), device=dev)
+        wpart = torch.full((n_rt, 2, I, r), float("nan"), device=dev)
         if mode == "plain":
             L.check(L.forge_lora_mlp_down_bwd(M, H, I, r, dY.data_ptr(), H, WdT.data_ptr(), H, td.data_ptr(), r,
                                               AdT.data_ptr(), r, L.LAYOUT_COL, h.data_ptr(), e.data_ptr(),
@@ -334,9 +334,10 @@ def test_down_bwd_rank_partials(M, I, r, act):
     assert not torch.isnan(wpart).any()
     xa = xaT[:, :M].float().t()                                  # [M, 2r]: [xa_g | xa_u]
     want_w = torch.cat([df1.float().t() @ xa[:, r:], de1.float().t() @ xa[:, :r]], 1)   # [I, 2r]
-    torch.testing.assert_close(wpart.sum(0), want_w, rtol=1e-4, atol=1e-3 * want_w.abs().max().item())
+    torch.testing.assert_close(torch.cat([wpart[:, 0].sum(0), wpart[:, 1].sum(0)], 1), want_w, rtol=1e-4,
+                               atol=1e-3 * want_w.abs().max().item())
     dB = torch.empty(I, r, device=dev, dtype=bf)
-    L.check(L.forge_splitk_reduce(wpart.data_ptr() + 4 * r, I * 2 * r, n_rt, I, r, 2 * r, dB.data_ptr(), r,
+    L.check(L.forge_splitk_reduce(wpart[0, 1].data_ptr(), 2 * I * r, n_rt, I, r, r, dB.data_ptr(), r,
                                   L.DTYPE_BF16, 1.0, st), "forge_splitk_reduce")
     torch.testing.assert_close(dB.float(), want_w[:, r:], rtol=1e-2, atol=1e-2 * want_w.abs().max().item())
 
