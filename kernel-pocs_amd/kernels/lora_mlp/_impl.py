@@ -211,7 +211,8 @@ def mlp_backward(dY2, X2, e, g, W_gate, A_gate, B_gate, s_gate, W_up, A_up, B_up
         torch.empty(M, I, dtype=torch.bfloat16, device=dev)
     WdT = frozen_t(W_down)
     # with ranks up to 64 the epilogue also forms [df Bu | de Bg] (step 4) as
-    # fp32 partial sums per 256-column tile, from df and de in its registers
+    # fp32 partial sums per 256-column tile from the df and de it produces
+    # (and, with tok_epi, step 4's dBu, dBg partials per 256-row tile)
     in_epi = act_ok and lde % 8 == 0
     tok_epi = tok_epi and in_epi
     if in_epi:
