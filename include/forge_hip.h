@@ -493,6 +493,31 @@ int forge_lora_qkv_rope(int64_t M, int64_t K, int64_t hq, int64_t hkv, int64_t r
                         const int64_t* positions, int64_t head_dim, int apply_rope,
                         void* stream);
 
+/* LoRA-QKV backward through RoPE with the LoRA-B products of its outputs, in
+ * one pass over the gradients (head_dim 128, an even number of Q and of KV
+ * heads; 32/8, 32/32, 64/8, 16/8, 8/2 and 4/2 Q/KV heads are built):
+ *   dq_out = rotate(dq, -theta), dk_out = rotate(dk, -theta)   (forge_rope's
+ *            backward: the same formula and rounding, bitwise equal)
+ *   t[m]   = alpha [dq_out[m] B_q | dk_out[m] B_k | dv[m] B_v]   (bf16 [M, 3r],
+ *            fp32 sums rounded once)
+ * dq [M, hq], dk / dv [M, hkv] (row pitches ld_*); cos / sin bf16 [cs_rows,
+ * >= 64] with row pitch cs_ld, read at the token's position (positions
+ * int64 [M], or the row index when NULL); b*_t = B^T [r][width] (pitch ld_b*).
+ * r: 16, 32, 48 or 64.  Every buffer 16-byte aligned, pitches multiples of 8
+ * (ld_t of 4), else an error and no launch.  Replaces the RoPE backward
+ * (kernels/rope/forge_rope_v3.py:32-132) and the three LoRA-B products of the
+ * QKV backward (kernels/lora_qkv/experiments/v4/lora_qkv_kernel_v4.py:264-266),
+ * which read the gradients a second time. */
+int forge_lora_qkv_rope_bwd(int64_t M, int64_t hq, int64_t hkv, int64_t r, int64_t head_dim,
+                            const void* dq, int64_t ld_dq, const void* dk, int64_t ld_dk,
+                            const void* dv, int64_t ld_dv,
+                            const void* cos, const void* sin, int64_t cs_ld, int64_t cs_rows,
+                            const int64_t* positions,
+                            void* dq_out, int64_t ld_qo, void* dk_out, int64_t ld_ko,
+                            const void* bq_t, const void* bk_t, const void* bv_t,
+                            int64_t ld_bq, int64_t ld_bk, int64_t ld_bv,
+                            void* t, int64_t ld_t, float alpha, void* stream);
+
 /* Rank-r LoRA-A projections of one input, one GEMM:
  *   out[:, p*r:(p+1)*r] = scales[p] * X @ A_p^T     for p < n_proj (<= 4)
  * X [M, K] (row pitch ldx), A_p [r, K] (pitch lda), out [M, n_proj*r] bf16.

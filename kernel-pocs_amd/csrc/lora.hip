@@ -18,6 +18,7 @@
 // caller (computed with forge_gemm); the LoRA-B product rides along the base
 // GEMM as one more K segment.
 #include <mutex>
+#include <type_traits>
 
 #include "gemm_core.h"
 
@@ -65,6 +66,190 @@ __global__ __launch_bounds__(kGluBlock) void lora_glu_bwd_kernel(const __bf16* d
     store16(h + r * ld_h + c, hv);
     store16(e + r * ld_eg + c, dfv);
     store16(g + r * ld_eg + c, dev);
+  }
+}
+
+// LoRA-QKV backward through RoPE with the LoRA-B products of its outputs, in
+// one pass over the gradients: dQ and dK rotated back by -theta per token
+// (forge_rope's backward: the same per-element formula and rounding) into
+// dq_out / dk_out, and
+//   t[m] = alpha [dQu[m] B_q | dKu[m] B_k | dV[m] B_v]     (bf16, one rounding)
+// from the rotated rows while they are on chip, instead of a second pass
+// that reads dQu, dKu and dV again.  A workgroup takes 32 tokens and walks
+// every head, Q, then K, then V (head_dim 128): thread (row, c) owns token
+// row m0 + row and the 8-column chunks 8c.. and 64 + 8c.. of each head; the
+// rotated head goes to a double-buffered LDS slab, and the four waves
+// multiply it by the head's slice of B^T ([r][width], read from L2) with
+// v_mfma_f32_16x16x32_bf16: wave w takes the 16-wide j block w (r <= 64) for
+// all 32 tokens.  Each head's
+// chunks are loaded four heads ahead, its B^T fragments one head ahead.
+constexpr int kQrTok = 32, kQrD = 128, kQrP = kQrD + 8;
+
+struct QkvRopeBwdArgs {
+  int64_t M;
+  int nq, nkv, r;
+  const __bf16* src[3];   // dQ, dK, dV
+  int64_t ld_src[3];
+  __bf16* dst[2];         // dQu, dKu
+  int64_t ld_dst[2];
+  const __bf16* cos;
+  const __bf16* sin;
+  int64_t cs_ld, cs_rows;
+  const int64_t* positions;
+  const __bf16* bt[3];    // B_q^T, B_k^T, B_v^T
+  int64_t ld_bt[3];
+  __bf16* t;
+  int64_t ld_t;
+  float alpha;
+};
+
+typedef float qr_f32x4 __attribute__((ext_vector_type(4)));
+
+// Barrier that leaves global loads in flight: this wave's LDS writes are
+// done (lgkmcnt 0) before it, vmcnt is not waited on.
+__device__ __forceinline__ void qr_barrier() {
+  __builtin_amdgcn_s_waitcnt(15 | (7 << 4) | (3 << 14));
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
+template <int NQ, int NKV>
+__global__ __launch_bounds__(256) void qkv_rope_bwd_rank_kernel(QkvRopeBwdArgs a) {
+  __shared__ __attribute__((aligned(16))) __bf16 slab[2][kQrTok * kQrP];
+  const int tid = threadIdx.x, lane = tid % 64, w = tid / 64;
+  const int row = tid / 8, c = tid % 8;
+  const int64_t m0 = (int64_t)blockIdx.x * kQrTok, m = m0 + row;
+  const bool mok = m < a.M;
+  constexpr int nh = NQ + 2 * NKV;
+  // cos / sin of this token's position at dims 8c .. 8c+7; the backward
+  // rotates by -theta (sin scaled by -1, as forge_rope's backward does)
+  float cs[8], sn[8];
+  {
+    const int64_t pos = mok ? (a.positions ? a.positions[m] : m) : 0;
+    if (mok && pos >= 0 && pos < a.cs_rows) {
+      const Vec16<__bf16> cv = load16(a.cos + pos * a.cs_ld + 8 * c);
+      const Vec16<__bf16> sv = load16(a.sin + pos * a.cs_ld + 8 * c);
+#pragma unroll
+      for (int q = 0; q < 8; ++q) {
+        cs[q] = 1.0f * (float)cv.v[q];
+        sn[q] = -1.0f * (float)sv.v[q];
+      }
+    } else {
+#pragma unroll
+      for (int q = 0; q < 8; ++q) cs[q] = sn[q] = __builtin_nanf("");
+    }
+  }
+  // Loads and stores go through buffer instructions with out-of-range offsets
+  // for rows past M (zeros read, writes dropped): no branch around them, so
+  // the compiler counts the loads in flight exactly.
+  auto load_head = [&](int h, uint4& lo, uint4& hi) {
+    if (h >= nh) return;  // (h is a compile-time index)
+    const int p = h < NQ ? 0 : (h < NQ + NKV ? 1 : 2);
+    const int hh = p == 0 ? h : (p == 1 ? h - NQ : h - NQ - NKV);
+    const __amdgpu_buffer_rsrc_t rs = make_rsrc(a.src[p] + m0 * a.ld_src[p] + (int64_t)hh * kQrD);
+    const uint32_t off = mok ? (uint32_t)((row * a.ld_src[p] + 8 * c) * 2) : OOB;
+    lo = buf_load16(rs, off);
+    hi = buf_load16(rs, mok ? off + kQrD : OOB);
+  };
+  constexpr int PD = 4;  // heads whose chunks are in flight ahead of the one in use
+  uint4 nlo[PD] = {}, nhi[PD] = {};
+#pragma unroll
+  for (int i = 0; i < PD; ++i) load_head(i, nlo[i], nhi[i]);
+  const int r = a.r;
+  // the B^T fragments of head h (this wave's j block w, 4 k-steps of 32)
+  auto load_b = [&](int h, bf16x8 (&dst)[4]) {
+    if (h >= nh) return;  // (h is a compile-time index)
+    const int p = h < NQ ? 0 : (h < NQ + NKV ? 1 : 2);
+    const int hh = p == 0 ? h : (p == 1 ? h - NQ : h - NQ - NKV);
+    const __amdgpu_buffer_rsrc_t rb = make_rsrc(a.bt[p] + (int64_t)hh * kQrD);
+    const int j = 16 * w + lane % 16;
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+      const uint32_t off = j < r ? (uint32_t)((j * a.ld_bt[p] + 32 * ks + 8 * (lane / 16)) * 2) : OOB;
+      dst[ks] = __builtin_bit_cast(bf16x8, buf_load16(rb, off));
+    }
+  };
+  bf16x8 bslot[2][4];  // head h's fragments in slot h % 2, loaded one head ahead
+  load_b(0, bslot[0]);
+  qr_f32x4 acc[3][2];
+#pragma unroll
+  for (int p = 0; p < 3; ++p)
+#pragma unroll
+    for (int u = 0; u < 2; ++u) acc[p][u] = qr_f32x4{0.f, 0.f, 0.f, 0.f};
+
+  // head h (projection P, register slot S = h % 2)
+  // (every head loop is unrolled, so h, and with it every slot index below, is
+  // a compile-time constant)
+  auto head = [&](int h, auto pc) {
+    constexpr int P = decltype(pc)::value;
+    const int S = h % 2, SD = h % PD;
+    const int hh = P == 0 ? h : (P == 1 ? h - NQ : h - NQ - NKV);
+    // the next head's B^T fragments (this head's were loaded one head ago)
+    load_b(h + 1, bslot[1 - S]);
+    uint4 lo = nlo[SD], hi = nhi[SD];
+    load_head(h + PD, nlo[SD], nhi[SD]);
+    if constexpr (P < 2) {
+      Vec16<__bf16> l, u, ol, oh;
+      l.raw = lo;
+      u.raw = hi;
+#pragma unroll
+      for (int q = 0; q < 8; ++q) {
+        const float x0 = (float)l.v[q], x1 = (float)u.v[q];
+        ol.v[q] = (__bf16)(x0 * cs[q] - x1 * sn[q]);
+        oh.v[q] = (__bf16)(x1 * cs[q] + x0 * sn[q]);
+      }
+      {
+        const __amdgpu_buffer_rsrc_t rd = make_rsrc(a.dst[P] + m0 * a.ld_dst[P] + (int64_t)hh * kQrD);
+        const uint32_t off = mok ? (uint32_t)((row * a.ld_dst[P] + 8 * c) * 2) : OOB;
+        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(i32x4, ol.raw), rd, (int)off, 0, 0);
+        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(i32x4, oh.raw), rd, (int)(mok ? off + kQrD : OOB), 0,
+                                               0);
+      }
+      lo = ol.raw;
+      hi = oh.raw;
+    }
+    __bf16* sb = slab[h & 1];
+    *reinterpret_cast<uint4*>(sb + row * kQrP + 8 * c) = lo;
+    *reinterpret_cast<uint4*>(sb + row * kQrP + kQrD / 2 + 8 * c) = hi;
+    qr_barrier();  // the slab is whole; the slab of head h - 1 is no longer read
+    if (16 * w < r) {
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks)
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+          const bf16x8 af =
+              *reinterpret_cast<const bf16x8*>(sb + (16 * u + lane % 16) * kQrP + 32 * ks + 8 * (lane / 16));
+          acc[P][u] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(bslot[S][ks], af, acc[P][u], 0, 0, 0);
+        }
+    }
+  };
+  using I0 = std::integral_constant<int, 0>;
+  using I1 = std::integral_constant<int, 1>;
+  using I2 = std::integral_constant<int, 2>;
+  // every head unrolled: the compiler then counts the loads in flight
+  // exactly (across a loop's back edge it waited for all of them, the
+  // prefetch included)
+#pragma unroll
+  for (int h = 0; h < NQ; ++h) head(h, I0{});
+#pragma unroll
+  for (int h = NQ; h < NQ + NKV; ++h) head(h, I1{});
+#pragma unroll
+  for (int h = NQ + NKV; h < nh; ++h) head(h, I2{});
+  // acc[p][u][q] = sum for j = 16 w + 4 (lane / 16) + q, token 16 u + lane % 16
+  const int j0 = 16 * w + 4 * (lane / 16);
+#pragma unroll
+  for (int u = 0; u < 2; ++u) {
+    const int64_t tok = m0 + 16 * u + lane % 16;
+    if (tok >= a.M || j0 >= r) continue;
+#pragma unroll
+    for (int p = 0; p < 3; ++p) {
+      const uint32_t w0 = (uint32_t)__builtin_bit_cast(uint16_t, (__bf16)(a.alpha * acc[p][u][0])) |
+                          ((uint32_t)__builtin_bit_cast(uint16_t, (__bf16)(a.alpha * acc[p][u][1])) << 16);
+      const uint32_t w1 = (uint32_t)__builtin_bit_cast(uint16_t, (__bf16)(a.alpha * acc[p][u][2])) |
+                          ((uint32_t)__builtin_bit_cast(uint16_t, (__bf16)(a.alpha * acc[p][u][3])) << 16);
+      *reinterpret_cast<uint2*>(a.t + tok * a.ld_t + p * r + j0) = make_uint2(w0, w1);
+    }
   }
 }
 
@@ -299,6 +484,81 @@ extern "C" int forge_lora_qkv_rope(int64_t M, int64_t K, int64_t hq, int64_t hkv
   a.ep.head_dim = (int)(head_dim > 0 ? head_dim : 128);
   if (!apply_rope) return run(-1, ROW, COL, EPI_STORE_BF16, a, (hipStream_t)stream);
   return run(-1, ROW, COL, EPI_ROPE, a, (hipStream_t)stream);
+}
+
+
+extern "C" int forge_lora_qkv_rope_bwd(int64_t M, int64_t hq, int64_t hkv, int64_t r, int64_t head_dim,
+                                       const void* dq, int64_t ld_dq, const void* dk, int64_t ld_dk,
+                                       const void* dv, int64_t ld_dv,
+                                       const void* cos, const void* sin, int64_t cs_ld, int64_t cs_rows,
+                                       const int64_t* positions,
+                                       void* dq_out, int64_t ld_qo, void* dk_out, int64_t ld_ko,
+                                       const void* bq_t, const void* bk_t, const void* bv_t,
+                                       int64_t ld_bq, int64_t ld_bk, int64_t ld_bv,
+                                       void* t, int64_t ld_t, float alpha, void* stream) {
+  if (M < 0 || hq < 0 || hkv < 0) return forge_set_error(FORGE_ERR_INVALID, "lora_qkv_rope_bwd: shape");
+  if (head_dim != kQrD || hq % (2 * kQrD) != 0 || hkv % (2 * kQrD) != 0 || hkv == 0)
+    return forge_set_error(FORGE_ERR_UNSUPPORTED,
+                           "lora_qkv_rope_bwd: head_dim 128 and even head counts (hq %lld, hkv %lld, head_dim %lld)",
+                           (long long)hq, (long long)hkv, (long long)head_dim);
+  if (r <= 0 || r > 64 || r % 16 != 0)
+    return forge_set_error(FORGE_ERR_UNSUPPORTED, "lora_qkv_rope_bwd: rank %lld (16, 32, 48 or 64)", (long long)r);
+  if (M == 0) return FORGE_OK;
+  const void* ptrs[] = {dq, dk, dv, cos, sin, dq_out, dk_out, bq_t, bk_t, bv_t, t};
+  for (const void* p : ptrs)
+    if (!p || !aligned16(p)) return forge_set_error(FORGE_ERR_INVALID, "lora_qkv_rope_bwd: null or unaligned operand");
+  if (ld_dq < hq || ld_dk < hkv || ld_dv < hkv || ld_qo < hq || ld_ko < hkv || ld_bq < hq || ld_bk < hkv ||
+      ld_bv < hkv || ld_t < 3 * r || cs_ld < head_dim)
+    return forge_set_error(FORGE_ERR_INVALID, "lora_qkv_rope_bwd: pitch below the row width");
+  if (ld_dq % 8 || ld_dk % 8 || ld_dv % 8 || ld_qo % 8 || ld_ko % 8 || ld_bq % 8 || ld_bk % 8 || ld_bv % 8 ||
+      ld_t % 4 || cs_ld % 8)
+    return forge_set_error(FORGE_ERR_INVALID, "lora_qkv_rope_bwd: pitches must be multiples of 8 (ld_t of 4)");
+  if (!positions && cs_rows < M)
+    return forge_set_error(FORGE_ERR_INVALID, "lora_qkv_rope_bwd: cos/sin have %lld rows for %lld tokens",
+                           (long long)cs_rows, (long long)M);
+  QkvRopeBwdArgs a = {};
+  a.M = M;
+  a.nq = (int)(hq / kQrD);
+  a.nkv = (int)(hkv / kQrD);
+  a.r = (int)r;
+  a.src[0] = (const __bf16*)dq;
+  a.src[1] = (const __bf16*)dk;
+  a.src[2] = (const __bf16*)dv;
+  a.ld_src[0] = ld_dq;
+  a.ld_src[1] = ld_dk;
+  a.ld_src[2] = ld_dv;
+  a.dst[0] = (__bf16*)dq_out;
+  a.dst[1] = (__bf16*)dk_out;
+  a.ld_dst[0] = ld_qo;
+  a.ld_dst[1] = ld_ko;
+  a.cos = (const __bf16*)cos;
+  a.sin = (const __bf16*)sin;
+  a.cs_ld = cs_ld;
+  a.cs_rows = cs_rows;
+  a.positions = positions;
+  a.bt[0] = (const __bf16*)bq_t;
+  a.bt[1] = (const __bf16*)bk_t;
+  a.bt[2] = (const __bf16*)bv_t;
+  a.ld_bt[0] = ld_bq;
+  a.ld_bt[1] = ld_bk;
+  a.ld_bt[2] = ld_bv;
+  a.t = (__bf16*)t;
+  a.ld_t = ld_t;
+  a.alpha = alpha;
+  const int64_t grid = (M + kQrTok - 1) / kQrTok;
+  if (grid > 0x7fffffffLL) return forge_set_error(FORGE_ERR_INVALID, "lora_qkv_rope_bwd: too many tokens");
+  hipStream_t s = (hipStream_t)stream;
+  if (a.nq == 32 && a.nkv == 8) qkv_rope_bwd_rank_kernel<32, 8><<<(unsigned)grid, 256, 0, s>>>(a);
+  else if (a.nq == 32 && a.nkv == 32) qkv_rope_bwd_rank_kernel<32, 32><<<(unsigned)grid, 256, 0, s>>>(a);
+  else if (a.nq == 64 && a.nkv == 8) qkv_rope_bwd_rank_kernel<64, 8><<<(unsigned)grid, 256, 0, s>>>(a);
+  else if (a.nq == 16 && a.nkv == 8) qkv_rope_bwd_rank_kernel<16, 8><<<(unsigned)grid, 256, 0, s>>>(a);
+  else if (a.nq == 8 && a.nkv == 2) qkv_rope_bwd_rank_kernel<8, 2><<<(unsigned)grid, 256, 0, s>>>(a);
+  else if (a.nq == 4 && a.nkv == 2) qkv_rope_bwd_rank_kernel<4, 2><<<(unsigned)grid, 256, 0, s>>>(a);
+  else
+    return forge_set_error(FORGE_ERR_UNSUPPORTED, "lora_qkv_rope_bwd: %d Q / %d KV heads not instantiated", a.nq,
+                           a.nkv);
+  FORGE_CHECK_LAUNCH();
+  return FORGE_OK;
 }
 
 extern "C" int forge_lora_a(int64_t M, int64_t K, int64_t r, int n_proj, const void* x, int64_t ldx,

@@ -174,6 +174,10 @@ forge_lora_mlp_down_bwd_v = _decl(
     "forge_lora_mlp_down_bwd_v",
     [c_i64, c_i64, c_i64, c_i64, c_vp, c_i64, c_vp, c_i64, c_vp, c_i64, c_vp, c_i64, c_vp, c_vp, c_vp, c_i64, c_int,
      c_vp, c_vp, c_i64, c_i64, c_vp, c_vp, c_vp, c_i64, c_vp, c_vp])
+forge_lora_qkv_rope_bwd = _decl(
+    "forge_lora_qkv_rope_bwd",
+    [c_i64, c_i64, c_i64, c_i64, c_i64, c_vp, c_i64, c_vp, c_i64, c_vp, c_i64, c_vp, c_vp, c_i64, c_i64, c_vp,
+     c_vp, c_i64, c_vp, c_i64, c_vp, c_vp, c_vp, c_i64, c_i64, c_i64, c_vp, c_i64, c_f32, c_vp])
 forge_lora_mlp_glu_bwd = _decl("forge_lora_mlp_glu_bwd", [c_i64, c_i64, c_vp, c_i64, c_vp, c_vp, c_i64, c_vp, c_i64,
                                                           c_int, c_vp])
 forge_rmsnorm_bwd_workspace = _decl("forge_rmsnorm_bwd_workspace", [c_int, c_i64, c_i64], c_i64)
@@ -191,7 +195,7 @@ EXPORTED = [
     "forge_ce_fwd", "forge_ce_target_stats", "forge_ce_fwd_reduce", "forge_ce_stats_wait", "forge_ce_scale",
     "forge_sum_f32",
     "forge_gemm", "forge_lora_mlp_gate_up", "forge_lora_mlp_gate_up_v", "forge_lora_mlp_down_bwd", "forge_lora_mlp_down_bwd_v", "forge_lora_mlp_glu_bwd",
-    "forge_lora_qkv_rope",
+    "forge_lora_qkv_rope", "forge_lora_qkv_rope_bwd",
     "forge_lora_a", "forge_lora_a_noalloc", "forge_zero", "forge_copy", "forge_cast_f32_bf16", "forge_splitk_reduce",
     "forge_ce_target_prob", "forge_row_scale", "forge_gemm_generic", "forge_transpose_2b", "forge_transpose_2b_batch",
     "forge_rmsnorm_fwd", "forge_rmsnorm_bwd", "forge_rmsnorm_bwd_workspace",

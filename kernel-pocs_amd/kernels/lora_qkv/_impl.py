@@ -151,9 +151,12 @@ def rope_qk_inplace(out, Hq, Hkv, rope, backward=False):
 
 
 def qkv_backward(dQ, dK, dV, X2, W_q, W_k, W_v, A_q, B_q, s_q, A_k, B_k, s_k, A_v, B_v, s_v,
-                 aux: Optional[dict] = None):
+                 aux: Optional[dict] = None, pre: Optional[tuple] = None):
     """Returns (dX, dA_q, dB_q, dA_k, dB_k, dA_v, dB_v).  With the forward's
-    aux the B gradients reuse its scaled xa instead of re-reading X."""
+    aux the B gradients reuse its scaled xa instead of re-reading X.  pre =
+    (t, B_q^T, B_k^T, B_v^T, A_q^T, A_k^T, A_v^T) from a caller that already
+    formed t = s [dQ B_q | dK B_k | dV B_v] (forge_lora_qkv_rope_bwd) and the
+    small transposes (rank a multiple of 8)."""
     if X2.dtype in G.GENERIC_DTYPES:
         return G.qkv_backward(dQ, dK, dV, X2, W_q, W_k, W_v, A_q, B_q, s_q, A_k, B_k, s_k, A_v, B_v, s_v, aux=aux)
     if A_q.shape[0] % 8:  # rank padded to a multiple of 8 (exact); the padding's gradients are dropped
@@ -173,9 +176,14 @@ def qkv_backward(dQ, dK, dV, X2, W_q, W_k, W_v, A_q, B_q, s_q, A_k, B_k, s_k, A_
     Aq, Bq, Ak, Bk, Av, Bv = (_w(t) for t in (A_q, B_q, A_k, B_k, A_v, B_v))
     # K-contiguous operands for the 4-wave engine (cached W^T, small A^T / B^T;
     # the rank is a multiple of 8 here): the six small transposes in one launch
-    BqT, BkT, BvT, AqT, AkT, AvT = small_t_batch([Bq, Bk, Bv, Aq, Ak, Av])
-    t = torch.empty(M, 3 * r, dtype=torch.bfloat16, device=dev)
-    if s_q == s_k == s_v:  # [dQ Bq | dK Bk | dV Bv] in one launch (column-ranged segments)
+    if pre is not None:  # t formed by the caller
+        t, BqT, BkT, BvT, AqT, AkT, AvT = pre
+    else:
+        BqT, BkT, BvT, AqT, AkT, AvT = small_t_batch([Bq, Bk, Bv, Aq, Ak, Av])
+        t = torch.empty(M, 3 * r, dtype=torch.bfloat16, device=dev)
+    if pre is not None:
+        pass
+    elif s_q == s_k == s_v:  # [dQ Bq | dK Bk | dV Bv] in one launch (column-ranged segments)
         gemm(M, 3 * r, [(dQ, ld(dQ), BqT, Hq, Hq, 0, r), (dK, ld(dK), BkT, Hkv, Hkv, r, 2 * r),
                         (dV, ld(dV), BvT, Hkv, Hkv, 2 * r, 3 * r)], ROW, COL, out=t, alpha=s_q)
     else:

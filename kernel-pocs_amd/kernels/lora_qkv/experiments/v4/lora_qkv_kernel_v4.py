@@ -21,7 +21,7 @@ from __future__ import annotations
 import torch
 
 from forge_hip import _lib as L
-from kernels._lora_ops import frozen_cat
+from kernels._lora_ops import frozen_cat, small_t_batch
 from kernels._positions import check_positions
 from kernels.lora_qkv._impl import (  # noqa: F401
     pack_lora_a,
@@ -36,6 +36,47 @@ from kernels.lora_qkv._impl import (  # noqa: F401
 
 def _flat(t):
     return t.reshape(-1, t.shape[-1])
+
+
+# The backward's RoPE pass and its LoRA-B products [dQ B_q | dK B_k | dV B_v]
+# in one kernel (forge_lora_qkv_rope_bwd) when the shapes allow (True), else
+# a forge_rope pass and a GEMM that reads the gradients again (False).
+ROPE_BWD_FUSED = True
+_ROPE_BWD_HEADS = {(32, 8), (32, 32), (64, 8), (16, 8), (8, 2), (4, 2)}  # (Q, KV) head counts built
+
+
+def _rope_bwd_fused(dQ2, dK2, dV2, X2, A_q, B_q, s_q, A_k, B_k, s_k, A_v, B_v, s_v, D, cos2, sin2, pos):
+    """(dQu, dKu, pre) from forge_lora_qkv_rope_bwd, or None when the shapes,
+    dtypes or scales rule it out; pre is qkv_backward's precomputed t and
+    small transposes."""
+    from kernels.lora_qkv._impl import _w
+
+    r = A_q.shape[0]
+    M, Hq, Hkv = dQ2.shape[0], dQ2.shape[1], dK2.shape[1]
+    bf = torch.bfloat16
+    tens = (dQ2, dK2, dV2, cos2, sin2)
+    if not (ROPE_BWD_FUSED and D == 128 and (Hq // D, Hkv // D) in _ROPE_BWD_HEADS and Hq % D == 0
+            and Hkv % D == 0 and r in (16, 32, 48, 64) and s_q == s_k == s_v and M > 0
+            and all(t.dtype == bf and t.stride(-1) == 1 and t.stride(0) % 8 == 0 and t.data_ptr() % 16 == 0
+                    for t in tens)
+            and A_q.dtype == bf and B_q.dtype == bf):
+        return None
+    Bq, Bk, Bv, Aq, Ak, Av = (_w(t) for t in (B_q, B_k, B_v, A_q, A_k, A_v))
+    BqT, BkT, BvT, AqT, AkT, AvT = small_t_batch([Bq, Bk, Bv, Aq, Ak, Av])
+    dev = dQ2.device
+    dQu = torch.empty(M, Hq, dtype=bf, device=dev)
+    dKu = torch.empty(M, Hkv, dtype=bf, device=dev)
+    t = torch.empty(M, 3 * r, dtype=bf, device=dev)
+    L.check(
+        L.forge_lora_qkv_rope_bwd(M, Hq, Hkv, r, D, dQ2.data_ptr(), dQ2.stride(0), dK2.data_ptr(), dK2.stride(0),
+                                  dV2.data_ptr(), dV2.stride(0), cos2.data_ptr(), sin2.data_ptr(), cos2.stride(0),
+                                  cos2.shape[0], pos.data_ptr() if pos is not None else None,
+                                  dQu.data_ptr(), Hq, dKu.data_ptr(), Hkv, BqT.data_ptr(), BkT.data_ptr(),
+                                  BvT.data_ptr(), BqT.stride(0), BkT.stride(0), BvT.stride(0), t.data_ptr(), 3 * r,
+                                  float(s_q), L.stream_of(dQ2)),
+        "forge_lora_qkv_rope_bwd",
+    )
+    return dQu, dKu, (t, BqT, BkT, BvT, AqT, AkT, AvT)
 
 
 class LoRAQKVv4Function(torch.autograd.Function):
@@ -198,10 +239,16 @@ class LoRAQKVRoPEFunction(torch.autograd.Function):
         dQ2, dK2 = _flat(dQ), _flat(dK)
         dQ2 = dQ2 if dQ2.stride(-1) == 1 else dQ2.contiguous()
         dK2 = dK2 if dK2.stride(-1) == 1 else dK2.contiguous()
-        dQu, dKu = _rope_qk_backward(dQ2, dK2, D, cos2, sin2, pos)
+        fused = _rope_bwd_fused(dQ2, dK2, _flat(dV), _flat(X), A_q, B_q, s_q, A_k, B_k, s_k, A_v, B_v, s_v, D,
+                                cos2, sin2, pos)
+        if fused is not None:
+            dQu, dKu, pre = fused
+        else:
+            dQu, dKu = _rope_qk_backward(dQ2, dK2, D, cos2, sin2, pos)
+            pre = None
         dX, dAq, dBq, dAk, dBk, dAv, dBv = qkv_backward(dQu, dKu, _flat(dV), _flat(X), W_q, W_k, W_v,
                                                         A_q, B_q, s_q, A_k, B_k, s_k, A_v, B_v, s_v,
-                                                        aux=ctx.lora_aux)
+                                                        aux=ctx.lora_aux, pre=pre)
         if X.dim() == 3:
             dX = dX.reshape(X.shape)
         return (dX, None, None, None, dAq, dBq, None, dAk, dBk, None, dAv, dBv, None, None, None, None, None)

@@ -143,6 +143,85 @@ def test_qkv_rope_epilogue_paths_agree(head_dim):
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("M,nq,nkv,r,with_pos", [(300, 32, 8, 64, True), (64, 8, 2, 16, False), (1000, 4, 2, 32, True),
+                                                 (31, 8, 2, 48, True), (97, 16, 8, 64, False)])
+def test_rope_bwd_rank_kernel(M, nq, nkv, r, with_pos):
+    """forge_lora_qkv_rope_bwd: dQ and dK rotated back equal the forge_rope
+    backward bit for bit, and t = s [dQu B_q | dKu B_k | dV B_v] matches the
+    fp32 product of those rotated rows (one bf16 rounding).  Row pitches are
+    padded with NaN past the head columns, which a read outside the heads
+    would carry into t; ragged M (partial 32-token tiles), ranks 16..64."""
+    from forge_hip import _lib as L
+    from kernels.lora_qkv.experiments.v4.lora_qkv_kernel_v4 import _rope_qk_backward
+
+    torch.manual_seed(M + nq + r)
+    D, dev, bf = 128, "cuda", torch.bfloat16
+    Hq, Hkv = nq * D, nkv * D
+
+    def padded(w):
+        t = torch.full((M, w + 8), float("nan"), device=dev, dtype=bf)
+        t[:, :w] = torch.randn(M, w, device=dev).to(bf)
+        return t
+
+    dq, dk, dv = padded(Hq), padded(Hkv), padded(Hkv)
+    P = M + 50
+    c, s_ = cos_sin(torch.arange(P), D, 500000.0, bf)
+    c, s_ = c.to(dev).contiguous(), s_.to(dev).contiguous()
+    pos = torch.randint(0, P, (M,), device=dev, dtype=torch.int64) if with_pos else None
+    bt = [(torch.randn(r, w, device=dev) * 0.05).to(bf) for w in (Hq, Hkv, Hkv)]
+    dq_out = torch.empty(M, Hq, device=dev, dtype=bf)
+    dk_out = torch.empty(M, Hkv, device=dev, dtype=bf)
+    t = torch.empty(M, 3 * r, device=dev, dtype=bf)
+    scale = 2.0
+    L.check(L.forge_lora_qkv_rope_bwd(M, Hq, Hkv, r, D, dq.data_ptr(), Hq + 8, dk.data_ptr(), Hkv + 8,
+                                      dv.data_ptr(), Hkv + 8, c.data_ptr(), s_.data_ptr(), D, P,
+                                      pos.data_ptr() if pos is not None else None, dq_out.data_ptr(), Hq,
+                                      dk_out.data_ptr(), Hkv, bt[0].data_ptr(), bt[1].data_ptr(), bt[2].data_ptr(),
+                                      Hq, Hkv, Hkv, t.data_ptr(), 3 * r, scale, L.stream_of(dq)),
+            "forge_lora_qkv_rope_bwd")
+    ref_q, ref_k = _rope_qk_backward(dq[:, :Hq], dk[:, :Hkv], D, c, s_, pos)
+    assert torch.equal(dq_out, ref_q) and torch.equal(dk_out, ref_k)
+    want = scale * torch.cat([ref_q.float() @ bt[0].float().t(), ref_k.float() @ bt[1].float().t(),
+                              dv[:, :Hkv].float() @ bt[2].float().t()], 1)
+    assert not torch.isnan(t).any()
+    torch.testing.assert_close(t.float(), want, rtol=1e-2, atol=1e-2 * want.abs().max().item())
+
+
+@pytest.mark.gpu
+def test_lora_qkv_rope_backward_fused_and_unfused_agree():
+    """The RoPE autograd backward with the fused RoPE / LoRA-B kernel and
+    with the forge_rope pass plus the GEMM: the same gradients within one
+    bf16 rounding of t (its products are summed in another order)."""
+    import kernels.lora_qkv.experiments.v4.lora_qkv_kernel_v4 as v4
+
+    gen = torch.Generator().manual_seed(11)
+    lens = [150, 77, 200]
+    pos = orc.positions_for(lens)
+    T, K, Hq, Hkv, r, D = int(pos.numel()), 512, 1024, 256, 16, 128
+    params = orc.make_params(K, Hq, Hkv, r, 32, gen)
+    X = torch.randn(T, K, generator=gen).to(torch.bfloat16)
+    dQ = torch.randn(T, Hq, generator=gen).to(torch.bfloat16).cuda()
+    dK = torch.randn(T, Hkv, generator=gen).to(torch.bfloat16).cuda()
+    dV = torch.randn(T, Hkv, generator=gen).to(torch.bfloat16).cuda()
+    c, s = cos_sin(torch.arange(256), D, 500000.0, torch.bfloat16)
+    grads = []
+    for fused in (True, False):
+        v4.ROPE_BWD_FUSED = fused
+        try:
+            p = _cuda(params)
+            x = X.cuda().requires_grad_(True)
+            Q, K_, V = lora_qkv_rope(x, p[0], p[3], p[4], p[5], p[1], p[6], p[7], p[8], p[2], p[9], p[10], p[11],
+                                     c.cuda(), s.cuda(), pos.cuda(), D)
+            torch.autograd.backward((Q, K_, V), (dQ, dK, dV))
+            grads.append([x.grad, p[3].grad, p[4].grad, p[6].grad, p[7].grad, p[9].grad, p[10].grad])
+        finally:
+            v4.ROPE_BWD_FUSED = True
+    for n, a, b in zip(NAMES, grads[0], grads[1]):
+        torch.testing.assert_close(a.float(), b.float(), rtol=2e-2, atol=2e-2 * b.float().abs().max().item(),
+                                   msg=lambda m: f"{n}: {m}")
+
+
+@pytest.mark.gpu
 def test_lora_qkv_fp64_gradcheck_uses_reference_torch_path():
     gen = torch.Generator().manual_seed(9)
     K, Hq, Hkv, r = 8, 8, 4, 2
