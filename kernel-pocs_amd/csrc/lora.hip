@@ -149,8 +149,10 @@ __global__ __launch_bounds__(256) void qkv_rope_bwd_rank_kernel(QkvRopeBwdArgs a
     const int hh = p == 0 ? h : (p == 1 ? h - NQ : h - NQ - NKV);
     const __amdgpu_buffer_rsrc_t rs = make_rsrc(a.src[p] + m0 * a.ld_src[p] + (int64_t)hh * kQrD);
     const uint32_t off = mok ? (uint32_t)((row * a.ld_src[p] + 8 * c) * 2) : OOB;
-    lo = buf_load16(rs, off);
-    hi = buf_load16(rs, mok ? off + kQrD : OOB);
+    // (nontemporal: each gradient chunk is read once; the B^T slices that every
+    // workgroup reads stay in L2)
+    lo = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rs, (int)off, 0, 2));
+    hi = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rs, (int)(mok ? off + kQrD : OOB), 0, 2));
   };
   constexpr int PD = 4;  // heads whose chunks are in flight ahead of the one in use
   uint4 nlo[PD] = {}, nhi[PD] = {};
@@ -202,9 +204,9 @@ __global__ __launch_bounds__(256) void qkv_rope_bwd_rank_kernel(QkvRopeBwdArgs a
       {
         const __amdgpu_buffer_rsrc_t rd = make_rsrc(a.dst[P] + m0 * a.ld_dst[P] + (int64_t)hh * kQrD);
         const uint32_t off = mok ? (uint32_t)((row * a.ld_dst[P] + 8 * c) * 2) : OOB;
-        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(i32x4, ol.raw), rd, (int)off, 0, 0);
+        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(i32x4, ol.raw), rd, (int)off, 0, 2);
         __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(i32x4, oh.raw), rd, (int)(mok ? off + kQrD : OOB), 0,
-                                               0);
+                                               2);
       }
       lo = ol.raw;
       hi = oh.raw;
